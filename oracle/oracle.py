@@ -1,0 +1,279 @@
+"""ctypes binding for the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker (or the timed
+CPU baseline) -- never as the thing measured or shipped.  The product path in
+torchburn_amd/ never imports it.
+
+Every function mirrors one C function in tb_oracle.c, which cites the
+reference file:line it restates.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+_vp = C.c_void_p
+
+
+def build() -> None:
+    """Compile liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            build()
+        L = C.CDLL(_SO)
+        L.orc_pack_int4.argtypes = [_i8p, _u8p, _i64, _i64]
+        L.orc_unpack_int4.argtypes = [_u8p, _i8p, _i64, _i64]
+        L.orc_quantize_int4_grouped.argtypes = [_f32p, _u8p, _f32p, _i64, _i64, _i64]
+        L.orc_gemv_w4.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64]
+        L.orc_gemm_w4.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64]
+        L.orc_gemv_w4_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64]
+        L.orc_swiglu_h_w4.argtypes = [_vp] * 8 + [_i64, _i64, _i64]
+        L.orc_swiglu_mlp_w4.argtypes = [_vp] * 11 + [_i64] * 5
+        L.orc_gemv_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64]
+        L.orc_quantize_int8.argtypes = [_f32p, _i8p, _f32p, _i64, _i64]
+        L.orc_swiglu_h_w8.argtypes = [_vp] * 6 + [_i64, _i64]
+        L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
+        L.orc_gemv_f32.argtypes = [_vp, _vp, _vp, _i64, _i64]
+        L.orc_rope_tables.argtypes = [_f32p, _f32p, _i64, _i64, C.c_double]
+        L.orc_rope_apply.argtypes = [_f32p, _f32p, _f32p, _i64]
+        L.orc_attention.argtypes = [_f32p, _vp, _vp, _f32p, _i64, _i64, _i64, _i64, _i64]
+        L.orc_argmax.argtypes = [_f32p, _i64]
+        L.orc_argmax.restype = _i64
+        L.orc_decoder_create.argtypes = [_i64] * 9 + [C.c_double, C.c_float, C.c_int, C.c_int,
+                                                      _vp, _vp, _vp, _vp]
+        L.orc_decoder_create.restype = _vp
+        L.orc_decoder_set_layer.argtypes = [_vp, _i64] + [_vp] * 13
+        L.orc_decoder_destroy.argtypes = [_vp]
+        L.orc_decoder_step.argtypes = [_vp, _i64, _i64]
+        L.orc_decoder_logits.argtypes = [_vp]
+        L.orc_decoder_logits.restype = C.POINTER(C.c_float)
+        L.orc_decoder_k_cache.argtypes = [_vp, _i64]
+        L.orc_decoder_k_cache.restype = C.POINTER(C.c_float)
+        L.orc_decoder_v_cache.argtypes = [_vp, _i64]
+        L.orc_decoder_v_cache.restype = C.POINTER(C.c_float)
+        L.orc_decoder_kv_len.argtypes = [_vp]
+        L.orc_decoder_kv_len.restype = _i64
+        L.orc_decoder_copy_kv.argtypes = [_vp, _i64, _vp, _vp, _i64, _i64]
+        L.orc_decoder_copy_kv.restype = C.c_int
+        L.orc_num_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dt):
+    return None if a is None else np.ascontiguousarray(a, dtype=dt)
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    q = _c(q, np.int8)
+    n, k = q.shape
+    out = np.empty((n, (k + 1) // 2), np.uint8)
+    lib().orc_pack_int4(q, out, n, k)
+    return out
+
+
+def unpack_int4(w: np.ndarray, k: int) -> np.ndarray:
+    w = _c(w, np.uint8)
+    n = w.shape[0]
+    out = np.empty((n, k), np.int8)
+    lib().orc_unpack_int4(w, out, n, k)
+    return out
+
+
+def quantize_int4_grouped(w: np.ndarray, group_size: int):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    packed = np.empty((n, (k + 1) // 2), np.uint8)
+    scales = np.empty((n, k // group_size), np.float32)
+    lib().orc_quantize_int4_grouped(w, packed, scales, n, k, group_size)
+    return packed, scales
+
+
+def gemm_w4(x, w, s, bias=None, group_size=32) -> np.ndarray:
+    """y[M, N] of the reference's gemm_w4a32_grouped (gemv.rs:1690-1725)."""
+    x = _c(x, np.float32)
+    w, s, bias = _c(w, np.uint8), _c(s, np.float32), _c(bias, np.float32)
+    k = x.shape[-1]
+    m = x.size // k
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().orc_gemm_w4(_p(x), _p(w), _p(s), _p(bias), _p(y), m, n, k, group_size)
+    return y.reshape(*x.shape[:-1], n)
+
+
+def gemv_w4_f64(x, w, s, bias=None, group_size=32) -> np.ndarray:
+    x = _c(x, np.float32).reshape(-1)
+    w, s, bias = _c(w, np.uint8), _c(s, np.float32), _c(bias, np.float32)
+    n = w.shape[0]
+    y = np.empty(n, np.float64)
+    lib().orc_gemv_w4_f64(_p(x), _p(w), _p(s), _p(bias), _p(y), n, x.size, group_size)
+    return y
+
+
+def swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None, group_size=32):
+    """fused_swiglu_mlp_w4a32 (fused_ops.rs:138-424); no residual."""
+    x = _c(x, np.float32)
+    k = x.shape[-1]
+    m = x.size // k
+    inter, nout = gw.shape[0], dw.shape[0]
+    arrs = [_c(a, dt) for a, dt in ((gw, np.uint8), (gsc, np.float32), (gb, np.float32),
+                                    (uw, np.uint8), (usc, np.float32), (ub, np.float32),
+                                    (dw, np.uint8), (dsc, np.float32), (db, np.float32))]
+    out = np.empty((m, nout), np.float32)
+    lib().orc_swiglu_mlp_w4(_p(x), *[_p(a) for a in arrs], _p(out), m, k, inter, nout,
+                            group_size)
+    return out.reshape(*x.shape[:-1], nout)
+
+
+def swiglu_h_w4(x, gw, gsc, uw, usc, gb=None, ub=None, group_size=32):
+    x = _c(x, np.float32).reshape(-1)
+    inter = gw.shape[0]
+    h = np.empty(inter, np.float32)
+    a = [_c(gw, np.uint8), _c(gsc, np.float32), _c(gb, np.float32), _c(uw, np.uint8),
+         _c(usc, np.float32), _c(ub, np.float32)]
+    lib().orc_swiglu_h_w4(_p(x), *[_p(t) for t in a], _p(h), inter, x.size, group_size)
+    return h
+
+
+def gemv_w8(x, w, s, bias=None) -> np.ndarray:
+    """w8a32_linear (gemv.rs:974-1061), any number of x rows."""
+    x = _c(x, np.float32)
+    w, s, bias = _c(w, np.int8), _c(s, np.float32).reshape(-1), _c(bias, np.float32)
+    k = x.shape[-1]
+    m = x.size // k
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    xf = x.reshape(m, k)
+    for i in range(m):
+        row = np.ascontiguousarray(xf[i])
+        lib().orc_gemv_w8(_p(row), _p(w), _p(s), s.size, _p(bias), y[i].ctypes.data, n, k)
+    return y.reshape(*x.shape[:-1], n)
+
+
+def quantize_int8(w: np.ndarray):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty(n, np.float32)
+    lib().orc_quantize_int8(w, q, s, n, k)
+    return q, s
+
+
+def rms_norm(x, w, eps) -> np.ndarray:
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rms_norm(x, w, out, x.size, eps)
+    return out
+
+
+def gemv_f32(x, w) -> np.ndarray:
+    x, w = _c(x, np.float32).reshape(-1), _c(w, np.float32)
+    y = np.empty(w.shape[0], np.float32)
+    lib().orc_gemv_f32(_p(x), _p(w), _p(y), w.shape[0], w.shape[1])
+    return y
+
+
+def rope_tables(max_seq: int, head_dim: int, theta: float):
+    c = np.empty((max_seq, head_dim), np.float32)
+    s = np.empty((max_seq, head_dim), np.float32)
+    lib().orc_rope_tables(c, s, max_seq, head_dim, theta)
+    return c, s
+
+
+def rope_apply(head, cos_row, sin_row) -> np.ndarray:
+    h = np.array(head, dtype=np.float32, copy=True)
+    lib().orc_rope_apply(h, _c(cos_row, np.float32), _c(sin_row, np.float32), h.size // 2)
+    return h
+
+
+def attention(q, k_cache, v_cache, seq_len: int) -> np.ndarray:
+    """q [hq, hd]; caches [hkv, max_seq, hd]."""
+    q = _c(q, np.float32)
+    k_cache, v_cache = _c(k_cache, np.float32), _c(v_cache, np.float32)
+    hq, hd = q.shape
+    hkv, max_seq, _ = k_cache.shape
+    out = np.empty_like(q)
+    lib().orc_attention(q, _p(k_cache), _p(v_cache), out, hq, hkv, hd, max_seq, seq_len)
+    return out
+
+
+def argmax(v) -> int:
+    return int(lib().orc_argmax(_c(v, np.float32), np.asarray(v).size))
+
+
+class Decoder:
+    """The reference's RustQwenDecoder step (decoder.rs:1051-1374) on the CPU.
+
+    Borrows the numpy weight arrays held in ``weights`` (kept alive here).
+    wkind: 4 (INT4 grouped) or 8 (INT8 per-channel); lmkind: 4, 8 or 32 (fp32).
+    """
+
+    def __init__(self, weights: dict, cfg: dict):
+        self.cfg = cfg
+        self.w = weights
+        L = lib()
+        lm_s = weights.get("lm_head_s")
+        self.h = L.orc_decoder_create(
+            cfg["num_layers"], cfg["hidden"], cfg["intermediate"], cfg["num_heads"],
+            cfg["num_kv_heads"], cfg["head_dim"], cfg["vocab"], cfg["group_size"],
+            cfg["max_seq"], float(cfg["rope_theta"]), float(cfg["eps"]), cfg["wkind"],
+            cfg["lmkind"], _p(weights["embed"]), _p(weights["final_norm"]),
+            _p(weights["lm_head_w"]), _p(lm_s))
+        for li, lw in enumerate(weights["layers"]):
+            L.orc_decoder_set_layer(
+                self.h, li, _p(lw["in_norm"]), _p(lw["qkv_w"]), _p(lw["qkv_s"]), _p(lw["o_w"]),
+                _p(lw["o_s"]), _p(lw["post_norm"]), _p(lw["gate_w"]), _p(lw["gate_s"]),
+                _p(lw["up_w"]), _p(lw["up_s"]), _p(lw["down_w"]), _p(lw["down_s"]),
+                _p(lw.get("qkv_b")))
+
+    def step(self, token: int, offset: int) -> np.ndarray:
+        L = lib()
+        L.orc_decoder_step(self.h, token, offset)
+        ptr = L.orc_decoder_logits(self.h)
+        return np.ctypeslib.as_array(ptr, shape=(self.cfg["vocab"],)).copy()
+
+    def copy_kv(self, layer: int, k: np.ndarray, v: np.ndarray, seq_len: int) -> None:
+        k, v = _c(k, np.float32), _c(v, np.float32)
+        rc = lib().orc_decoder_copy_kv(self.h, layer, _p(k), _p(v), k.shape[-2], seq_len)
+        if rc != 0:
+            raise ValueError("KV cache copy out of bounds")
+
+    def kv_len(self) -> int:
+        return int(lib().orc_decoder_kv_len(self.h))
+
+    def close(self):
+        if self.h:
+            lib().orc_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

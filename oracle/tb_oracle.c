@@ -1,0 +1,649 @@
+/*
+ * tb_oracle.c -- CPU restatement of TorchBurn's quantized decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels in
+ * torchburn_amd/csrc are compared against, and the CPU baseline that bench.py
+ * times beside the GPU.  Nothing in the product path may call it.
+ *
+ * Every function restates the algorithm of the Rust reference at
+ * /root/reference (kuntal-devrat/torchburn), cited as file:line.  The SIMD
+ * kernels of the reference are restated lane by lane in plain C: a 16-float
+ * array stands for one __m512 register, fmaf() for _mm512_fmadd_ps (single
+ * rounding), and tree16() for _mm512_reduce_add_ps.  The file is built with
+ * -ffp-contract=off so that every "a * b + c" that the reference writes as two
+ * operations stays two operations.
+ *
+ * Hot loops carry target_clones so one .so runs on AVX-512, AVX2 or plain
+ * x86-64 hosts (the GPU box's CPU is not this container's CPU).
+ *
+ * Parity status of each function is listed in the header of tests/test_oracle.py
+ * (what pins it) -- every function here has at least one pinning check.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_API __attribute__((visibility("default")))
+#define HOT __attribute__((target_clones("avx512f", "avx2", "default")))
+
+enum { L16 = 16 };
+
+/* Rayon's minimum task length for row loops, gemv.rs:1535-1536:           */
+/* max(N / (4 * threads), 8).  Only scheduling -- no cross-row reduction.   */
+static int64_t rayon_chunk(int64_t n) {
+#ifdef _OPENMP
+    int64_t t = omp_get_max_threads();
+#else
+    int64_t t = 1;
+#endif
+    int64_t c = n / (4 * t);
+    return c > 8 ? c : 8;
+}
+
+/* _mm512_reduce_add_ps: halves added pairwise, 512 -> 256 -> 128 -> 64 -> 32.
+ * The exact order is LLVM's and is not pinned at the bit level (see the
+ * tolerance-based tests); this is the natural tree. */
+static inline float tree16(const float *a) {
+    float t8[8], t4[4];
+    for (int i = 0; i < 8; ++i) t8[i] = a[i] + a[i + 8];
+    for (int i = 0; i < 4; ++i) t4[i] = t8[i] + t8[i + 4];
+    float t0 = t4[0] + t4[2], t1 = t4[1] + t4[3];
+    return t0 + t1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a1: INT4 v1 packing.  python/torchburn/quantization.py:89-94 packs          */
+/*   byte[n, j] = (q[n,2j] + 8) | ((q[n,2j+1] + 8) << 4),  q in [-8, 7];      */
+/* unpack (gemv.rs:1486-1502) is nib - 8.  Odd K: the last byte's high nibble */
+/* is element K which does not exist; it is written as 0 (q = -8 is never     */
+/* read back).                                                                */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_pack_int4(const int8_t *q, uint8_t *out, int64_t n, int64_t k) {
+    int64_t bpr = (k + 1) / 2;
+    for (int64_t r = 0; r < n; ++r) {
+        const int8_t *qr = q + r * k;
+        uint8_t *o = out + r * bpr;
+        for (int64_t j = 0; j < bpr; ++j) {
+            uint8_t lo = (uint8_t)((qr[2 * j] + 8) & 0x0F);
+            uint8_t hi = (2 * j + 1 < k) ? (uint8_t)((qr[2 * j + 1] + 8) & 0x0F) : 0;
+            o[j] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+}
+
+ORC_API void orc_unpack_int4(const uint8_t *w, int8_t *q, int64_t n, int64_t k) {
+    int64_t bpr = (k + 1) / 2;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t i = 0; i < k; ++i) {
+            uint8_t b = w[r * bpr + i / 2];
+            q[r * k + i] = (int8_t)(((i & 1) ? (b >> 4) : (b & 0x0F)) - 8);
+        }
+}
+
+/* Grouped quantizer, quantization.py:53-118: s = max(amax/7, 1e-8) per group, */
+/* q = clamp(round_half_even(w / s), -8, 7).  nearbyintf rounds half to even  */
+/* in the default rounding mode, as torch.round does.                         */
+ORC_API void orc_quantize_int4_grouped(const float *w, uint8_t *packed, float *scales,
+                                       int64_t n, int64_t k, int64_t gs) {
+    int64_t ng = k / gs, bpr = (k + 1) / 2;
+    int8_t *q = (int8_t *)malloc((size_t)k);
+    for (int64_t r = 0; r < n; ++r) {
+        for (int64_t g = 0; g < ng; ++g) {
+            float amax = 0.f;
+            for (int64_t i = 0; i < gs; ++i) {
+                float a = fabsf(w[r * k + g * gs + i]);
+                amax = a > amax ? a : amax;
+            }
+            float s = amax / 7.0f;
+            if (s < 1e-8f) s = 1e-8f;
+            scales[r * ng + g] = s;
+            for (int64_t i = 0; i < gs; ++i) {
+                float v = nearbyintf(w[r * k + g * gs + i] / s);
+                v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
+                q[g * gs + i] = (int8_t)v;
+            }
+        }
+        orc_pack_int4(q, packed + r * bpr, 1, k);
+    }
+    free(q);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a2: scalar exact group dot, gemv.rs:1486-1502 (sequential f32 sum).        */
+/* ------------------------------------------------------------------------ */
+static float dot_u4_group_scalar(const float *x, const uint8_t *w, int64_t len) {
+    float t = 0.f;
+    for (int64_t i = 0; i < len; ++i) {
+        uint8_t b = w[i / 2];
+        int q = ((i & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+        t += x[i] * (float)q;
+    }
+    return t;
+}
+
+/* a3: unpack_and_fma_32_avx512, gemv.rs:1190-1211.  16 bytes -> elements     */
+/* 0..15 (lane i) and 16..31 (lane i); result lane i = fma(w1, x1, w0 * x0).   */
+static inline void unpack_fma32(const float *x, const uint8_t *w, float *out16) {
+    for (int i = 0; i < L16; ++i) {
+        int e0 = i, e1 = 16 + i;
+        int q0 = ((e0 & 1) ? (w[e0 / 2] >> 4) : (w[e0 / 2] & 0x0F)) - 8;
+        int q1 = ((e1 & 1) ? (w[e1 / 2] >> 4) : (w[e1 / 2] & 0x0F)) - 8;
+        float m0 = (float)q0 * x[e0];
+        out16[i] = fmaf((float)q1, x[e1], m0);
+    }
+}
+
+/* a4: one output row.  group 32: gemv.rs:1279-1299; group 64: 1253-1275;     */
+/* other group sizes: the scalar per-group fallback at gemv.rs:1650-1660.     */
+static inline float w4_row(const float *x, const uint8_t *wr, const float *sr, int64_t k,
+                           int64_t gs) {
+    int64_t ng = (k + gs - 1) / gs;
+    if ((gs == 32 || gs == 64) && k % gs == 0) {
+        float acc[L16] = {0}, p0[L16], p1[L16];
+        for (int64_t g = 0; g < ng; ++g) {
+            float s = sr[g];
+            if (gs == 32) {
+                unpack_fma32(x + g * 32, wr + g * 16, p0);
+                for (int i = 0; i < L16; ++i) acc[i] = fmaf(p0[i], s, acc[i]);
+            } else {
+                unpack_fma32(x + g * 64, wr + g * 32, p0);
+                unpack_fma32(x + g * 64 + 32, wr + g * 32 + 16, p1);
+                for (int i = 0; i < L16; ++i) acc[i] = fmaf(p0[i] + p1[i], s, acc[i]);
+            }
+        }
+        return tree16(acc);
+    }
+    float t = 0.f;
+    for (int64_t g = 0; g < ng; ++g) {
+        int64_t len = (k - g * gs) < gs ? (k - g * gs) : gs;
+        t += dot_u4_group_scalar(x + g * gs, wr + g * (gs / 2), len) * sr[g];
+    }
+    return t;
+}
+
+/* a5: gemv_w4a32_grouped, gemv.rs:1514-1684.  One task per output row       */
+/* (Rayon par_iter, min chunk max(N/(4T), 8)); no cross-row reduction.        */
+HOT static void w4_rows(const float *x, const uint8_t *w, const float *s, const float *bias,
+                        float *y, int64_t r0, int64_t r1, int64_t k, int64_t gs) {
+    int64_t ng = (k + gs - 1) / gs, bpr = (k + 1) / 2;
+    for (int64_t r = r0; r < r1; ++r) {
+        float v = w4_row(x, w + r * bpr, s + r * ng, k, gs);
+        y[r] = v + (bias ? bias[r] : 0.f);
+    }
+}
+
+ORC_API void orc_gemv_w4(const float *x, const uint8_t *w, const float *s, const float *bias,
+                         float *y, int64_t n, int64_t k, int64_t gs) {
+    int64_t ch = rayon_chunk(n);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (n + ch - 1) / ch; ++c)
+        w4_rows(x, w, s, bias, y, c * ch, (c + 1) * ch < n ? (c + 1) * ch : n, k, gs);
+}
+
+/* a6: gemm_w4a32_grouped, gemv.rs:1690-1725: M independent GEMVs.          */
+ORC_API void orc_gemm_w4(const float *x, const uint8_t *w, const float *s, const float *bias,
+                         float *y, int64_t m, int64_t n, int64_t k, int64_t gs) {
+    for (int64_t i = 0; i < m; ++i) orc_gemv_w4(x + i * k, w, s, bias, y + i * n, n, k, gs);
+}
+
+/* Float64 brute force of the same contraction (the "exact dequant-dot" of   */
+/* tests/parity/int4.rs:109-126), used to pin the lane restatement above.     */
+ORC_API void orc_gemv_w4_f64(const float *x, const uint8_t *w, const float *s,
+                             const float *bias, double *y, int64_t n, int64_t k, int64_t gs) {
+    int64_t ng = (k + gs - 1) / gs, bpr = (k + 1) / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n; ++r) {
+        double t = 0.0;
+        for (int64_t g = 0; g < ng; ++g) {
+            double p = 0.0;
+            for (int64_t i = g * gs; i < k && i < (g + 1) * gs; ++i) {
+                uint8_t b = w[r * bpr + i / 2];
+                int q = ((i & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+                p += (double)q * (double)x[i];
+            }
+            t += p * (double)s[r * ng + g];
+        }
+        y[r] = t + (bias ? (double)bias[r] : 0.0);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a7/a8: SwiGLU.  Neuron pair swiglu.rs:205-255 (g32) / 85-163 (g64) is the   */
+/* a4 row kernel applied to the gate and the up row with shared x;           */
+/* h = silu(g + gb) * (u + ub), silu(g) = g / (1 + exp(-g))                  */
+/* (fused_ops.rs:404-406).  Then down = gemv_w4a32_grouped(h)                 */
+/* (fused_ops.rs:409-421).  The residual is the caller's (decoder.rs:1344).   */
+/* ------------------------------------------------------------------------ */
+HOT static void swiglu_w4_rows(const float *x, const uint8_t *gw, const float *gsc,
+                               const float *gb, const uint8_t *uw, const float *usc,
+                               const float *ub, float *h, int64_t j0, int64_t j1, int64_t k,
+                               int64_t gs) {
+    int64_t ng = (k + gs - 1) / gs, bpr = (k + 1) / 2;
+    for (int64_t j = j0; j < j1; ++j) {
+        float g = w4_row(x, gw + j * bpr, gsc + j * ng, k, gs) + (gb ? gb[j] : 0.f);
+        float u = w4_row(x, uw + j * bpr, usc + j * ng, k, gs) + (ub ? ub[j] : 0.f);
+        float silu = g / (1.0f + expf(-g));
+        h[j] = silu * u;
+    }
+}
+
+ORC_API void orc_swiglu_h_w4(const float *x, const uint8_t *gw, const float *gsc,
+                             const float *gb, const uint8_t *uw, const float *usc,
+                             const float *ub, float *h, int64_t inter, int64_t k, int64_t gs) {
+    int64_t ch = rayon_chunk(inter);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (inter + ch - 1) / ch; ++c)
+        swiglu_w4_rows(x, gw, gsc, gb, uw, usc, ub, h, c * ch,
+                       (c + 1) * ch < inter ? (c + 1) * ch : inter, k, gs);
+}
+
+ORC_API void orc_swiglu_mlp_w4(const float *x, const uint8_t *gw, const float *gsc,
+                               const float *gb, const uint8_t *uw, const float *usc,
+                               const float *ub, const uint8_t *dw, const float *dsc,
+                               const float *db, float *out, int64_t m, int64_t k,
+                               int64_t inter, int64_t nout, int64_t gs) {
+    float *h = (float *)malloc((size_t)inter * sizeof(float));
+    for (int64_t t = 0; t < m; ++t) {
+        orc_swiglu_h_w4(x + t * k, gw, gsc, gb, uw, usc, ub, h, inter, k, gs);
+        orc_gemv_w4(h, dw, dsc, db, out + t * nout, nout, inter, gs);
+    }
+    free(h);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a18: INT8 W8A32.  dot_f32_i8_avx512 gemv.rs:280-324 and the 8-row kernel   */
+/* gemv.rs:147-270 share one per-row structure: two 16-lane accumulators over */
+/* 32-element chunks, summed, then 16-element chunks, lane reduce, scalar     */
+/* tail.  Row result = dot * s + b (gemv.rs:777-785; s_len == 1 means one     */
+/* per-tensor scale).                                                          */
+/* ------------------------------------------------------------------------ */
+static inline float dot_i8_row(const float *x, const int8_t *w, int64_t len) {
+    float a0[L16] = {0}, a1[L16] = {0};
+    int64_t off = 0;
+    for (; off + 32 <= len; off += 32)
+        for (int i = 0; i < L16; ++i) {
+            a0[i] = fmaf((float)w[off + i], x[off + i], a0[i]);
+            a1[i] = fmaf((float)w[off + 16 + i], x[off + 16 + i], a1[i]);
+        }
+    float sm[L16];
+    for (int i = 0; i < L16; ++i) sm[i] = a0[i] + a1[i];
+    for (; off + 16 <= len; off += 16)
+        for (int i = 0; i < L16; ++i) sm[i] = fmaf((float)w[off + i], x[off + i], sm[i]);
+    float t = tree16(sm);
+    for (; off < len; ++off) t += x[off] * (float)w[off];
+    return t;
+}
+
+HOT static void w8_rows(const float *x, const int8_t *w, const float *s, int64_t s_len,
+                        const float *bias, float *y, int64_t r0, int64_t r1, int64_t k) {
+    for (int64_t r = r0; r < r1; ++r) {
+        float d = dot_i8_row(x, w + r * k, k);
+        float sc = s_len > 1 ? s[r] : s[0];
+        y[r] = d * sc + (bias ? bias[r] : 0.f);
+    }
+}
+
+ORC_API void orc_gemv_w8(const float *x, const int8_t *w, const float *s, int64_t s_len,
+                         const float *bias, float *y, int64_t n, int64_t k) {
+    int64_t ch = rayon_chunk(n);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (n + ch - 1) / ch; ++c)
+        w8_rows(x, w, s, s_len, bias, y, c * ch, (c + 1) * ch < n ? (c + 1) * ch : n, k);
+}
+
+/* Per-channel INT8 quantizer, fused_ops.rs:554-589: s = amax/127 (1 when    */
+/* amax == 0), q = clamp(round_half_away(w * (1/s)), -127, 127).             */
+ORC_API void orc_quantize_int8(const float *w, int8_t *q, float *s, int64_t n, int64_t k) {
+    for (int64_t r = 0; r < n; ++r) {
+        float amax = 0.f;
+        for (int64_t i = 0; i < k; ++i) {
+            float a = fabsf(w[r * k + i]);
+            amax = a > amax ? a : amax;
+        }
+        float sc = amax > 0.f ? amax / 127.0f : 1.0f;
+        float inv = 1.0f / sc;
+        s[r] = sc;
+        for (int64_t i = 0; i < k; ++i) {
+            float v = roundf(w[r * k + i] * inv);
+            v = v < -127.f ? -127.f : (v > 127.f ? 127.f : v);
+            q[r * k + i] = (int8_t)v;
+        }
+    }
+}
+
+/* SwiGLU MLP with INT8 weights, fused_ops.rs:8-133: the same neuron formula  */
+/* with the a18 row dot, then the INT8 down GEMV.                             */
+HOT static void swiglu_w8_rows(const float *x, const int8_t *gw, const float *gsc,
+                               const int8_t *uw, const float *usc, float *h, int64_t j0,
+                               int64_t j1, int64_t k) {
+    for (int64_t j = j0; j < j1; ++j) {
+        float g = dot_i8_row(x, gw + j * k, k) * gsc[j];
+        float u = dot_i8_row(x, uw + j * k, k) * usc[j];
+        float silu = g / (1.0f + expf(-g));
+        h[j] = silu * u;
+    }
+}
+
+ORC_API void orc_swiglu_h_w8(const float *x, const int8_t *gw, const float *gsc,
+                             const int8_t *uw, const float *usc, float *h, int64_t inter,
+                             int64_t k) {
+    int64_t ch = rayon_chunk(inter);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (inter + ch - 1) / ch; ++c)
+        swiglu_w8_rows(x, gw, gsc, uw, usc, h, c * ch, (c + 1) * ch < inter ? (c + 1) * ch : inter,
+                       k);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a9: fast_rms_norm AVX-512 tier, fused_ops.rs:1066-1089.                    */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_rms_norm(const float *x, const float *w, float *out, int64_t n, float eps) {
+    float acc[L16] = {0};
+    int64_t nc = n / 16;
+    for (int64_t c = 0; c < nc; ++c)
+        for (int i = 0; i < L16; ++i) acc[i] = fmaf(x[c * 16 + i], x[c * 16 + i], acc[i]);
+    float tot = tree16(acc);
+    for (int64_t i = nc * 16; i < n; ++i) tot += x[i] * x[i];
+    float rms = sqrtf(tot / (float)n + eps);
+    float inv = 1.0f / rms;
+    for (int64_t i = 0; i < nc * 16; ++i) out[i] = (x[i] * inv) * w[i];
+    for (int64_t i = nc * 16; i < n; ++i) out[i] = (x[i] / rms) * w[i];
+}
+
+/* dot_f32_f32 AVX-512 tier, fused_ops.rs:646-664 (len >= 16), else scalar.  */
+static inline float dot_f32(const float *a, const float *b, int64_t len) {
+    if (len >= 16) {
+        float acc[L16] = {0};
+        int64_t i = 0;
+        for (; i + 16 <= len; i += 16)
+            for (int l = 0; l < L16; ++l) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+        float s = tree16(acc);
+        for (; i < len; ++i) s += a[i] * b[i];
+        return s;
+    }
+    float s = 0.f;
+    for (int64_t i = 0; i < len; ++i) s += a[i] * b[i];
+    return s;
+}
+
+/* FP32 linear (the fp32 lm_head of the per-layer Python path,               */
+/* python/torchburn/llm/model.py:499-500): y[r] = dot(W[r], x).  torch's CPU  */
+/* sgemv order is not pinned; the row dot above stands for it.               */
+HOT static void f32_rows(const float *x, const float *w, float *y, int64_t r0, int64_t r1,
+                         int64_t k) {
+    for (int64_t r = r0; r < r1; ++r) y[r] = dot_f32(w + r * k, x, k);
+}
+
+ORC_API void orc_gemv_f32(const float *x, const float *w, float *y, int64_t n, int64_t k) {
+    int64_t ch = rayon_chunk(n);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (n + ch - 1) / ch; ++c)
+        f32_rows(x, w, y, c * ch, (c + 1) * ch < n ? (c + 1) * ch : n, k);
+}
+
+/* ------------------------------------------------------------------------ */
+/* a10: RoPE.  Tables decoder.rs:334-350 (f64 math, cast to f32, both halves  */
+/* duplicated); rotate-half apply decoder.rs:28-68 (mul and sub separately).  */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_rope_tables(float *cos_t, float *sin_t, int64_t max_seq, int64_t hd,
+                             double theta) {
+    int64_t half = hd / 2;
+    for (int64_t p = 0; p < max_seq; ++p)
+        for (int64_t i = 0; i < half; ++i) {
+            double freq = 1.0 / pow(theta, (2.0 * (double)i) / (double)hd);
+            double val = (double)p * freq;
+            float c = (float)cos(val), s = (float)sin(val);
+            cos_t[p * hd + i] = cos_t[p * hd + i + half] = c;
+            sin_t[p * hd + i] = sin_t[p * hd + i + half] = s;
+        }
+}
+
+ORC_API void orc_rope_apply(float *head, const float *c, const float *s, int64_t half) {
+    for (int64_t i = 0; i < half; ++i) {
+        float x1 = head[i], x2 = head[i + half];
+        head[i] = x1 * c[i] - x2 * s[i];
+        head[i + half] = x2 * c[i + half] + x1 * s[i + half];
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* a12: GQA decode attention for one query head, decoder.rs:1148-1213.        */
+/* kv_base points at [seq, hd] rows of this head's KV.                       */
+/* ------------------------------------------------------------------------ */
+static void attend_head(const float *q, const float *kb, const float *vb, float *out,
+                        float *scores, int64_t seq_len, int64_t hd) {
+    for (int64_t d = 0; d < hd; ++d) out[d] = 0.f;
+    if (seq_len == 1) {
+        memcpy(out, vb, (size_t)hd * sizeof(float));
+        return;
+    }
+    int64_t cap = seq_len < 32768 ? seq_len : 32768;
+    float scale = 1.0f / sqrtf((float)hd);
+    float mx = -INFINITY;
+    for (int64_t t = 0; t < cap; ++t) {
+        float sc = dot_f32(q, kb + t * hd, hd) * scale;
+        scores[t] = sc;
+        if (sc > mx) mx = sc;
+    }
+    float sum = 0.f;
+    for (int64_t t = 0; t < cap; ++t) {
+        float e = expf(scores[t] - mx);
+        scores[t] = e;
+        sum += e;
+    }
+    float inv = 1.0f / (sum > 1e-30f ? sum : 1e-30f);
+    for (int64_t t = 0; t < cap; ++t) {
+        float wt = scores[t] * inv;
+        const float *v = vb + t * hd;
+        /* fast_vector_fma AVX-512 tier, fused_ops.rs:1189-1202 */
+        int64_t nc = hd / 16;
+        for (int64_t i = 0; i < nc * 16; ++i) out[i] = fmaf(wt, v[i], out[i]);
+        for (int64_t i = nc * 16; i < hd; ++i) out[i] += wt * v[i];
+    }
+}
+
+/* q: [hq, hd]; k_cache/v_cache: [hkv, max_seq, hd]; out: [hq, hd]. */
+ORC_API void orc_attention(const float *q, const float *k_cache, const float *v_cache,
+                           float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
+                           int64_t seq_len) {
+    int64_t per = hq / (hkv > 0 ? hkv : 1);
+    if (per < 1) per = 1;
+#pragma omp parallel
+    {
+        float *scores = (float *)malloc((size_t)(seq_len > 0 ? seq_len : 1) * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t h = 0; h < hq; ++h) {
+            int64_t kvh = h / per;
+            attend_head(q + h * hd, k_cache + kvh * max_seq * hd, v_cache + kvh * max_seq * hd,
+                        out + h * hd, scores, seq_len, hd);
+        }
+        free(scores);
+    }
+}
+
+/* a17: greedy argmax, decoder.rs:914-925 (strict >, lowest index wins).      */
+ORC_API int64_t orc_argmax(const float *v, int64_t n) {
+    if (n <= 0) return 0;
+    int64_t bi = 0;
+    float bv = v[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (v[i] > bv) {
+            bv = v[i];
+            bi = i;
+        }
+    return bi;
+}
+
+/* ------------------------------------------------------------------------ */
+/* a16: RustQwenDecoder::step_internal, decoder.rs:1051-1374.                 */
+/* The oracle borrows every weight pointer (the caller keeps them alive) and */
+/* owns its KV cache [L][hkv, max_seq, hd], RoPE tables and scratch, as the  */
+/* reference does (decoder.rs:334-359).                                      */
+/* wkind: 4 = INT4 grouped (the native decoder), 8 = INT8 per-channel        */
+/*   projections with the same step structure (the reference has no native   */
+/*   INT8 decoder; engine.py:133-151 routes INT8 through the per-layer path  */
+/*   whose GEMVs are the a18 kernels).                                        */
+/* lmkind: 4 = INT4 grouped, 8 = INT8 per-channel, 32 = fp32.                 */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    const float *in_norm, *post_norm;
+    const void *qkv_w, *o_w, *gate_w, *up_w, *down_w;
+    const float *qkv_s, *o_s, *gate_s, *up_s, *down_s;
+    const float *qkv_b; /* may be NULL */
+} orc_layer;
+
+typedef struct {
+    int64_t L, H, I, hq, hkv, hd, V, gs, max_seq;
+    int wkind, lmkind;
+    float eps;
+    const float *embed, *final_norm;
+    const void *lm_w;
+    const float *lm_s;
+    orc_layer *layers;
+    float *kc, *vc, *cos_t, *sin_t;
+    float *x, *xn, *qkv, *att, *o, *h, *dn, *logits;
+    int64_t kv_used;
+} orc_decoder;
+
+ORC_API orc_decoder *orc_decoder_create(int64_t L, int64_t H, int64_t I, int64_t hq,
+                                        int64_t hkv, int64_t hd, int64_t V, int64_t gs,
+                                        int64_t max_seq, double theta, float eps, int wkind,
+                                        int lmkind, const float *embed,
+                                        const float *final_norm, const void *lm_w,
+                                        const float *lm_s) {
+    orc_decoder *d = (orc_decoder *)calloc(1, sizeof(orc_decoder));
+    d->L = L; d->H = H; d->I = I; d->hq = hq; d->hkv = hkv; d->hd = hd; d->V = V;
+    d->gs = gs; d->max_seq = max_seq; d->eps = eps; d->wkind = wkind; d->lmkind = lmkind;
+    d->embed = embed; d->final_norm = final_norm; d->lm_w = lm_w; d->lm_s = lm_s;
+    d->layers = (orc_layer *)calloc((size_t)L, sizeof(orc_layer));
+    size_t kvn = (size_t)L * (size_t)hkv * (size_t)max_seq * (size_t)hd;
+    d->kc = (float *)calloc(kvn, sizeof(float));
+    d->vc = (float *)calloc(kvn, sizeof(float));
+    d->cos_t = (float *)malloc((size_t)(max_seq * hd) * sizeof(float));
+    d->sin_t = (float *)malloc((size_t)(max_seq * hd) * sizeof(float));
+    orc_rope_tables(d->cos_t, d->sin_t, max_seq, hd, theta);
+    int64_t tq = (hq + 2 * hkv) * hd;
+    d->x = (float *)calloc((size_t)H, 4);
+    d->xn = (float *)calloc((size_t)H, 4);
+    d->qkv = (float *)calloc((size_t)tq, 4);
+    d->att = (float *)calloc((size_t)(hq * hd), 4);
+    d->o = (float *)calloc((size_t)H, 4);
+    d->h = (float *)calloc((size_t)I, 4);
+    d->dn = (float *)calloc((size_t)H, 4);
+    d->logits = (float *)calloc((size_t)V, 4);
+    return d;
+}
+
+ORC_API void orc_decoder_set_layer(orc_decoder *d, int64_t l, const float *in_norm,
+                                   const void *qkv_w, const float *qkv_s, const void *o_w,
+                                   const float *o_s, const float *post_norm,
+                                   const void *gate_w, const float *gate_s, const void *up_w,
+                                   const float *up_s, const void *down_w, const float *down_s,
+                                   const float *qkv_b) {
+    orc_layer *y = &d->layers[l];
+    y->in_norm = in_norm; y->qkv_w = qkv_w; y->qkv_s = qkv_s; y->o_w = o_w; y->o_s = o_s;
+    y->post_norm = post_norm; y->gate_w = gate_w; y->gate_s = gate_s; y->up_w = up_w;
+    y->up_s = up_s; y->down_w = down_w; y->down_s = down_s; y->qkv_b = qkv_b;
+}
+
+ORC_API void orc_decoder_destroy(orc_decoder *d) {
+    if (!d) return;
+    free(d->layers); free(d->kc); free(d->vc); free(d->cos_t); free(d->sin_t);
+    free(d->x); free(d->xn); free(d->qkv); free(d->att); free(d->o); free(d->h);
+    free(d->dn); free(d->logits); free(d);
+}
+
+ORC_API float *orc_decoder_logits(orc_decoder *d) { return d->logits; }
+ORC_API float *orc_decoder_k_cache(orc_decoder *d, int64_t l) {
+    return d->kc + l * d->hkv * d->max_seq * d->hd;
+}
+ORC_API float *orc_decoder_v_cache(orc_decoder *d, int64_t l) {
+    return d->vc + l * d->hkv * d->max_seq * d->hd;
+}
+ORC_API int64_t orc_decoder_kv_len(orc_decoder *d) { return d->kv_used; }
+ORC_API void orc_decoder_set_kv_len(orc_decoder *d, int64_t n) {
+    if (n > d->kv_used) d->kv_used = n;
+}
+
+/* projection_gemv, decoder.rs:1029-1049 (v1 path). */
+static void proj(const orc_decoder *d, int kind, const float *x, const void *w, const float *s,
+                 const float *b, float *y, int64_t n, int64_t k) {
+    if (kind == 4)
+        orc_gemv_w4(x, (const uint8_t *)w, s, b, y, n, k, d->gs);
+    else if (kind == 8)
+        orc_gemv_w8(x, (const int8_t *)w, s, n, b, y, n, k);
+    else {
+        orc_gemv_f32(x, (const float *)w, y, n, k);
+        if (b)
+            for (int64_t i = 0; i < n; ++i) y[i] += b[i];
+    }
+}
+
+ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
+    int64_t H = d->H, hd = d->hd, hq = d->hq, hkv = d->hkv;
+    int64_t qd = hq * hd, kvd = hkv * hd, tq = qd + 2 * kvd, half = hd / 2;
+    /* decoder.rs:1066-1089: out-of-range token or offset -> zeroed step. */
+    if (token < 0 || token >= d->V || offset < 0 || offset >= d->max_seq) {
+        memset(d->x, 0, (size_t)H * 4);
+        memset(d->logits, 0, (size_t)d->V * 4);
+        return;
+    }
+    memcpy(d->x, d->embed + token * H, (size_t)H * 4);
+    const float *cp = d->cos_t + offset * hd, *sp = d->sin_t + offset * hd;
+    if (offset + 1 > d->kv_used) d->kv_used = offset + 1;
+    for (int64_t l = 0; l < d->L; ++l) {
+        const orc_layer *y = &d->layers[l];
+        orc_rms_norm(d->x, y->in_norm, d->xn, H, d->eps);
+        proj(d, d->wkind, d->xn, y->qkv_w, y->qkv_s, y->qkv_b, d->qkv, tq, H);
+        float *q = d->qkv, *k = d->qkv + qd, *v = d->qkv + qd + kvd;
+        for (int64_t h = 0; h < hq; ++h) orc_rope_apply(q + h * hd, cp, sp, half);
+        for (int64_t h = 0; h < hkv; ++h) orc_rope_apply(k + h * hd, cp, sp, half);
+        float *kc = orc_decoder_k_cache(d, l), *vc = orc_decoder_v_cache(d, l);
+        for (int64_t h = 0; h < hkv; ++h) {
+            memcpy(kc + (h * d->max_seq + offset) * hd, k + h * hd, (size_t)hd * 4);
+            memcpy(vc + (h * d->max_seq + offset) * hd, v + h * hd, (size_t)hd * 4);
+        }
+        orc_attention(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1);
+        proj(d, d->wkind, d->att, y->o_w, y->o_s, NULL, d->o, H, qd);
+        for (int64_t i = 0; i < H; ++i) d->x[i] += d->o[i];
+        orc_rms_norm(d->x, y->post_norm, d->xn, H, d->eps);
+        if (d->wkind == 4)
+            orc_swiglu_h_w4(d->xn, (const uint8_t *)y->gate_w, y->gate_s, NULL,
+                            (const uint8_t *)y->up_w, y->up_s, NULL, d->h, d->I, H, d->gs);
+        else
+            orc_swiglu_h_w8(d->xn, (const int8_t *)y->gate_w, y->gate_s,
+                            (const int8_t *)y->up_w, y->up_s, d->h, d->I, H);
+        proj(d, d->wkind, d->h, y->down_w, y->down_s, NULL, d->dn, H, d->I);
+        for (int64_t i = 0; i < H; ++i) d->x[i] += d->dn[i];
+    }
+    orc_rms_norm(d->x, d->final_norm, d->xn, H, d->eps);
+    proj(d, d->lmkind, d->xn, d->lm_w, d->lm_s, NULL, d->logits, d->V, H);
+}
+
+/* Copy a prefilled KV prefix, decoder.rs:479-523: src is [hkv, src_max, hd]. */
+ORC_API int orc_decoder_copy_kv(orc_decoder *d, int64_t l, const float *k, const float *v,
+                                int64_t src_max, int64_t seq_len) {
+    if (l < 0 || l >= d->L || seq_len > d->max_seq || seq_len > src_max) return -1;
+    float *kc = orc_decoder_k_cache(d, l), *vc = orc_decoder_v_cache(d, l);
+    for (int64_t h = 0; h < d->hkv; ++h)
+        for (int64_t t = 0; t < seq_len; ++t) {
+            memcpy(kc + (h * d->max_seq + t) * d->hd, k + (h * src_max + t) * d->hd,
+                   (size_t)d->hd * 4);
+            memcpy(vc + (h * d->max_seq + t) * d->hd, v + (h * src_max + t) * d->hd,
+                   (size_t)d->hd * 4);
+        }
+    if (seq_len > d->kv_used) d->kv_used = seq_len;
+    return 0;
+}
+
+ORC_API int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,131 @@
+"""Parity of the gfx950 INT4 GEMV / SwiGLU kernels with the CPU oracle.
+
+The oracle (oracle/tb_oracle.c) restates the reference's gemv_w4a32_grouped
+(src/quantization/gemv.rs:1514-1725) and fused_swiglu_mlp_w4a32
+(src/quantization/fused_ops.rs:138-424).  Metric: max|d| / max|ref|, the
+reference's own (tests/parity/int4.rs:131-141); bar 1e-4 (fp32 accumulate).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from torchburn_amd import synth
+import torchburn_amd as tb
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+SHAPES = [
+    # (m, n, k, gs)
+    (1, 4864, 896, 32),      # config 1 (Qwen2.5-0.5B MLP up-proj)
+    (1, 64, 896, 64),        # the reference's own KAT shape (group 64)
+    (1, 1152, 896, 32),      # Qwen qkv
+    (1, 896, 4864, 32),      # Qwen down (K = 4864, 152 groups)
+    (1, 14336, 4096, 32),    # Llama gate/up
+    (1, 4096, 14336, 32),    # Llama down
+    (2, 4096, 4096, 32),
+    (3, 1000, 2048, 32),     # ragged N, odd M
+    (4, 517, 1024, 64),
+    (8, 4096, 4096, 32),     # config 2 batch 8
+    (1, 7, 32, 32),          # one group per row
+    (5, 33, 64, 32),
+]
+
+
+@pytest.mark.parametrize("m,n,k,gs", SHAPES)
+def test_w4_linear_matches_oracle(cuda, m, n, k, gs):
+    print(f"case w4a32_grouped_linear m={m} n={n} k={k} gs={gs}", flush=True)
+    g = synth.rng(11, m, n, k, gs)
+    x = synth.activations(g, m, k)
+    w, s = synth.int4_weight(g, n, k, gs)
+    bias = g.normal(0, 0.1, n).astype(np.float32)
+    ref = O.gemm_w4(x, w, s, bias, group_size=gs)
+    y = tb.w4a32_grouped_linear(torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda),
+                                torch.from_numpy(s).to(cuda), torch.from_numpy(bias).to(cuda),
+                                group_size=gs)
+    torch.cuda.synchronize()
+    assert rel(y.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("m,k,inter,gs", [(1, 896, 4864, 32), (1, 4096, 14336, 32),
+                                          (4, 4096, 14336, 32), (8, 4096, 14336, 32),
+                                          (2, 512, 1024, 64)])
+def test_swiglu_mlp_residual_matches_oracle(cuda, m, k, inter, gs):
+    print(f"case fused_swiglu_mlp m={m} k={k} inter={inter} gs={gs}", flush=True)
+    g = synth.rng(12, m, k, inter)
+    x = synth.activations(g, m, k)
+    r = synth.activations(g, m, k)
+    gw, gsc = synth.int4_weight(g, inter, k, gs)
+    uw, usc = synth.int4_weight(g, inter, k, gs)
+    dw, dsc = synth.int4_weight(g, k, inter, gs)
+    ref = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, group_size=gs) + r
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    out = tb.fused_swiglu_mlp_w4a32(T(x), T(gw), T(gsc), None, T(uw), T(usc), None, T(dw),
+                                    T(dsc), None, group_size=gs, residual=T(r))
+    torch.cuda.synchronize()
+    assert rel(out.cpu().numpy(), ref) < TOL
+
+
+def test_residual_in_place(cuda):
+    g = synth.rng(13)
+    x = synth.activations(g, 1, 4096)
+    w, s = synth.int4_weight(g, 4096, 4096, 32)
+    r = synth.activations(g, 1, 4096)
+    ref = O.gemm_w4(x, w, s, None, group_size=32) + r
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    rt = T(r)
+    from torchburn_amd import _lib
+    xt, wt, st = T(x), T(w), T(s)
+    _lib.call("tb_w4a32_grouped_linear_residual", xt.data_ptr(), wt.data_ptr(), st.data_ptr(),
+              None, rt.data_ptr(), rt.data_ptr(), 1, 4096, 4096, 32,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rel(rt.cpu().numpy(), ref) < TOL
+
+
+def test_special_cases(cuda):
+    """Closed forms: x == 0 -> bias; q == c with unit scales -> c * sum(x);
+    one-hot x -> a column of the dequantized matrix."""
+    n, k = 96, 256
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    bias = np.arange(n, dtype=np.float32)
+    w = np.random.default_rng(0).integers(0, 256, (n, k // 2), dtype=np.uint8)
+    s = np.ones((n, k // 32), np.float32)
+    y = tb.w4a32_grouped_linear(T(np.zeros((1, k), np.float32)), T(w), T(s), T(bias), 32)
+    assert np.array_equal(y.cpu().numpy()[0], bias)
+    x = np.random.default_rng(1).standard_normal((1, k)).astype(np.float32)
+    for c in (-8, -3, 0, 7):
+        wc = np.full((n, k // 2), (c + 8) | ((c + 8) << 4), np.uint8)
+        y = tb.w4a32_grouped_linear(T(x), T(wc), T(s), None, 32).cpu().numpy()[0]
+        np.testing.assert_allclose(y, np.full(n, c * x.astype(np.float64).sum()), rtol=1e-5,
+                                   atol=1e-4)
+    s2 = np.random.default_rng(2).uniform(0.5, 2, (n, k // 32)).astype(np.float32)
+    q = O.unpack_int4(w, k)
+    for col in (0, 1, 31, 32, 255):
+        e = np.zeros((1, k), np.float32)
+        e[0, col] = 1.0
+        y = tb.w4a32_grouped_linear(T(e), T(w), T(s2), None, 32).cpu().numpy()[0]
+        np.testing.assert_array_equal(y, q[:, col].astype(np.float32) * s2[:, col // 32])
+
+
+def test_errors_match_reference_contract(cuda):
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    x = T(np.zeros((1, 64), np.float32))
+    w = T(np.zeros((8, 31), np.uint8))
+    s = T(np.ones((8, 2), np.float32))
+    with pytest.raises(tb.UnsupportedOpError, match="TB_UNSUPPORTED"):
+        tb.w4a32_grouped_linear(x, w, s, group_size=32)
+    w = T(np.zeros((8, 32), np.uint8))
+    with pytest.raises(tb.UnsupportedOpError, match="scales mismatch"):
+        tb.w4a32_grouped_linear(x, w, T(np.ones((8, 3), np.float32)), group_size=32)
+    with pytest.raises(tb.UnsupportedOpError, match="group_size"):
+        tb.w4a32_grouped_linear(x, w, T(np.ones((8, 4), np.float32)), group_size=16)

@@ -1,0 +1,30 @@
+"""torchburn_amd: TorchBurn's quantized decode hot path, rebuilt for AMD MI355X (gfx950).
+
+The compute lives in libtbhip.so (hand-written HIP kernels behind a C ABI,
+include/tbhip.h).  This package is the host-side mirror of the reference's
+Python operator API (python/torchburn/quantization.py): same names, argument
+meaning and error behaviour.
+"""
+from ._lib import UnsupportedOpError
+from .quantization import (
+    QuantizedLinear,
+    fused_swiglu_mlp,
+    fused_swiglu_mlp_w4a32,
+    quantize_model,
+    quantize_weight_int4_grouped,
+    quantize_weight_int8,
+    w4a32_grouped_linear,
+    w4a32_grouped_linear_residual,
+)
+
+__all__ = [
+    "UnsupportedOpError",
+    "QuantizedLinear",
+    "fused_swiglu_mlp",
+    "fused_swiglu_mlp_w4a32",
+    "quantize_model",
+    "quantize_weight_int4_grouped",
+    "quantize_weight_int8",
+    "w4a32_grouped_linear",
+    "w4a32_grouped_linear_residual",
+]

@@ -1,0 +1,87 @@
+"""Loader for libtbhip.so and the status-code -> exception mapping.
+
+The library is built in-tree by ``python -m torchburn_amd.build``.  There is no
+CPU fallback: if the library or a GPU is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtbhip.so")
+
+TB_OK = 0
+TB_ERR_UNSUPPORTED = 1
+TB_ERR_VALUE = 2
+TB_ERR_MEMORY = 3
+TB_ERR_HIP = 4
+
+UNSUPPORTED_MARKER = "TB_UNSUPPORTED:"
+
+
+class UnsupportedOpError(RuntimeError):
+    """Raised for shapes, dtypes or devices the kernels do not support.
+
+    Mirrors the reference's UnsupportedOpError (src/dlpack.rs:35-53): a
+    RuntimeError subclass whose message carries the "TB_UNSUPPORTED:" marker.
+    """
+
+
+_lock = threading.Lock()
+_lib = None
+
+_p = C.c_void_p
+_i64 = C.c_int64
+
+# name -> argtypes; every function returns int (status).
+_SIGS = {
+    "tb_w4a32_grouped_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "tb_w4a32_grouped_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+    "tb_swiglu_w4a32": [_p] * 8 + [_i64] * 4 + [_p],
+    "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
+}
+
+
+def declared_symbols() -> list:
+    """Every entry point the Python layer binds (all are declared in include/tbhip.h)."""
+    return ["tb_last_error", "tb_version", *_SIGS.keys()]
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise ImportError(
+                    f"{LIB_PATH} is missing; build it with `python -m torchburn_amd.build` "
+                    "(there is no CPU fallback for the HIP path)")
+            L = C.CDLL(LIB_PATH)
+            L.tb_last_error.restype = C.c_char_p
+            L.tb_version.restype = C.c_char_p
+            for name, args in _SIGS.items():
+                fn = getattr(L, name)
+                fn.argtypes = args
+                fn.restype = C.c_int
+            _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc == TB_OK:
+        return
+    msg = lib().tb_last_error().decode(errors="replace")
+    if rc == TB_ERR_UNSUPPORTED:
+        raise UnsupportedOpError(msg if UNSUPPORTED_MARKER in msg else f"{UNSUPPORTED_MARKER} {msg}")
+    if rc == TB_ERR_VALUE:
+        raise ValueError(msg)
+    if rc == TB_ERR_MEMORY:
+        raise MemoryError(msg)
+    raise RuntimeError(f"HIP error: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

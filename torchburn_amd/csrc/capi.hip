@@ -1,0 +1,179 @@
+// extern "C" entry points of libtbhip.so (declared in include/tbhip.h).
+//
+// Argument validation mirrors the reference's shape checks
+// (src/quantization/packed_v2.rs:565-596) and returns TB_ERR_UNSUPPORTED with
+// the reference's "TB_UNSUPPORTED:" marker, which the Python layer maps to
+// UnsupportedOpError.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "tb_common.hpp"
+#include "w4_gemv.hpp"
+
+namespace tb {
+
+namespace {
+thread_local std::string g_last_error;
+
+// Device workspace (grow-only, one per device) for intermediates of fused ops.
+std::mutex g_ws_mu;
+std::vector<std::pair<void *, size_t>> g_ws;
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int gshift_of(int64_t gs) { return gs == 32 ? 5 : (gs == 64 ? 6 : -1); }
+}  // namespace
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int workspace(size_t bytes, void **out) {
+    int dev = 0;
+    TB_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
+    auto &slot = g_ws[dev];
+    if (slot.second < bytes) {
+        // A stream may still be using the old buffer; free it only after the
+        // device is idle.
+        if (slot.first) {
+            TB_HIP(hipDeviceSynchronize());
+            TB_HIP(hipFree(slot.first));
+            slot = {nullptr, 0};
+        }
+        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
+        TB_HIP(hipMalloc(&slot.first, sz));
+        slot.second = sz;
+    }
+    *out = slot.first;
+    return TB_OK;
+}
+
+// Validates a grouped INT4 projection and fills the common W4Params fields.
+static int check_w4(const float *x, const uint8_t *w, const float *s, int64_t m, int64_t n,
+                    int64_t k, int64_t gs, const char *what) {
+    const std::string op(what);
+    TB_REQUIRE(x && w && s, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": null pointer");
+    TB_REQUIRE(m >= 0 && n >= 0 && k > 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": negative or empty dimension");
+    TB_REQUIRE(gshift_of(gs) > 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": group_size must be 32 or 64, got " + std::to_string(gs));
+    TB_REQUIRE(k % gs == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": K=" + std::to_string(k) +
+                   " must be a multiple of group_size=" + std::to_string(gs));
+    TB_REQUIRE(k <= (1 << 20) && n < (1ll << 31) && m < (1ll << 31), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": dimension too large");
+    TB_REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(s, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": x and w must be 16-byte aligned device pointers");
+    return TB_OK;
+}
+
+static W4Params w4_params(const float *x, const uint8_t *w, const float *s, const float *b,
+                          float *y, int64_t m, int64_t n, int64_t k, int64_t gs) {
+    W4Params p{};
+    p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
+    return p;
+}
+
+// M rows in passes of at most kMaxRowsPerPass (the GEMV keeps x in VGPRs).
+static int w4_rows(W4Params p, int epi, int64_t m, hipStream_t st) {
+    for (int64_t r0 = 0; r0 < m; r0 += kMaxRowsPerPass) {
+        W4Params q = p;
+        q.m = (int)((m - r0) < kMaxRowsPerPass ? (m - r0) : kMaxRowsPerPass);
+        q.x = p.x + r0 * p.k;
+        q.y = p.y + r0 * (int64_t)p.n;
+        if (p.res) q.res = p.res + r0 * (int64_t)p.n;
+        int rc = w4_gemv(q, epi, st);
+        if (rc) return rc;
+    }
+    return TB_OK;
+}
+
+}  // namespace tb
+
+using namespace tb;
+
+extern "C" {
+
+const char *tb_last_error(void) { return g_last_error.c_str(); }
+
+const char *tb_version(void) { return "torchburn_amd 0.1.0 gfx950"; }
+
+int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float *scales,
+                            const float *bias, float *out, int64_t m, int64_t n, int64_t k,
+                            int64_t group_size, void *stream) {
+    int rc = check_w4(x, w_packed, scales, m, n, k, group_size, "w4a32_grouped_linear");
+    if (rc) return rc;
+    TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_grouped_linear: null output");
+    if (m == 0 || n == 0) return TB_OK;
+    W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
+    return w4_rows(p, EPI_PLAIN, m, (hipStream_t)stream);
+}
+
+int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
+                                     const float *scales, const float *bias,
+                                     const float *residual, float *out, int64_t m, int64_t n,
+                                     int64_t k, int64_t group_size, void *stream) {
+    int rc = check_w4(x, w_packed, scales, m, n, k, group_size, "w4a32_grouped_linear_residual");
+    if (rc) return rc;
+    TB_REQUIRE(out && residual, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4a32_grouped_linear_residual: null output or residual");
+    if (m == 0 || n == 0) return TB_OK;
+    W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
+    p.res = residual;
+    return w4_rows(p, EPI_RESID, m, (hipStream_t)stream);
+}
+
+int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
+                    const float *gate_b, const uint8_t *up_w, const float *up_s,
+                    const float *up_b, float *h, int64_t m, int64_t k, int64_t inter,
+                    int64_t group_size, void *stream) {
+    int rc = check_w4(x, gate_w, gate_s, m, inter, k, group_size, "swiglu_w4a32");
+    if (rc) return rc;
+    rc = check_w4(x, up_w, up_s, m, inter, k, group_size, "swiglu_w4a32");
+    if (rc) return rc;
+    TB_REQUIRE(h, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: swiglu_w4a32: null output");
+    if (m == 0 || inter == 0) return TB_OK;
+    W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+    p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
+    return w4_rows(p, EPI_SWIGLU, m, (hipStream_t)stream);
+}
+
+int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
+                              const float *gate_b, const uint8_t *up_w, const float *up_s,
+                              const float *up_b, const uint8_t *down_w, const float *down_s,
+                              const float *down_b, const float *residual, float *out,
+                              int64_t m, int64_t k, int64_t inter, int64_t n_out,
+                              int64_t group_size, void *stream) {
+    int rc = check_w4(x, gate_w, gate_s, m, inter, k, group_size, "fused_swiglu_mlp_w4a32");
+    if (rc) return rc;
+    rc = check_w4(x, up_w, up_s, m, inter, k, group_size, "fused_swiglu_mlp_w4a32");
+    if (rc) return rc;
+    TB_REQUIRE(inter % group_size == 0 && inter % 32 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: intermediate size must be a multiple "
+               "of group_size");
+    TB_REQUIRE(down_w && down_s && out, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: null down weight or output");
+    if (m == 0 || n_out == 0) return TB_OK;
+    void *ws = nullptr;
+    rc = workspace((size_t)m * (size_t)inter * sizeof(float), &ws);
+    if (rc) return rc;
+    float *h = static_cast<float *>(ws);
+    hipStream_t st = (hipStream_t)stream;
+    W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+    p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
+    rc = w4_rows(p, EPI_SWIGLU, m, st);
+    if (rc) return rc;
+    W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
+    if (residual) {
+        d.res = residual;
+        return w4_rows(d, EPI_RESID, m, st);
+    }
+    return w4_rows(d, EPI_PLAIN, m, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,34 @@
+// Internal launchers of the INT4 GEMV kernels (w4_gemv.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tb {
+
+enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+
+// Activation rows per GEMV pass (x is held in VGPRs).
+constexpr int kMaxRowsPerPass = 2;
+
+struct W4Params {
+    const float *x;    // [m, k] activations
+    const uint8_t *w0; // [n, k/2] packed nibbles (gate when dual)
+    const float *s0;   // [n, k/group] scales
+    const float *b0;   // [n] bias or null
+    const uint8_t *w1; // up projection of a SwiGLU pair, or null
+    const float *s1;
+    const float *b1;
+    const float *res;  // [m, n] residual for EPI_RESID
+    float *y;          // [m, n] output
+    int m, n, k;
+    int gshift;        // log2(group_size)
+    // Filled in by the launcher.
+    int c, sw, b, rows_per_step, rows_per_block;
+};
+
+// One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
+// p.w1 is set.  Shapes are validated by the caller.
+int w4_gemv(W4Params p, int epi, hipStream_t st);
+
+}  // namespace tb
