@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (FETCH_SIZE / "
+                         "WRITE_SIZE calibration for rocprofv3 --pmc), then exit")
     return ap.parse_args()
 
 
@@ -68,6 +71,15 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": n, "copies": 5}))
+        return
     M, K, I, GS = args.m, 4096, 14336, 32
 
     # Weights: `copies` independent sets generated on the device.

@@ -4,6 +4,8 @@
 // (src/quantization/packed_v2.rs:565-596) and returns TB_ERR_UNSUPPORTED with
 // the reference's "TB_UNSUPPORTED:" marker, which the Python layer maps to
 // UnsupportedOpError.
+#include <stdlib.h>
+
 #include <mutex>
 #include <string>
 #include <vector>
@@ -23,6 +25,16 @@ std::vector<std::pair<void *, size_t>> g_ws;
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int gshift_of(int64_t gs) { return gs == 32 ? 5 : (gs == 64 ? 6 : -1); }
+
+// Row batches per GEMV block (TB_W4_BATCHES overrides, for tuning sweeps).
+int batches_env() {
+    static int v = [] {
+        const char *e = getenv("TB_W4_BATCHES");
+        int b = e ? atoi(e) : 1;
+        return b < 1 ? 1 : b;
+    }();
+    return v;
+}
 }  // namespace
 
 int fail(int code, const std::string &msg) {
@@ -76,6 +88,7 @@ static W4Params w4_params(const float *x, const uint8_t *w, const float *s, cons
     W4Params p{};
     p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
     p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
+    p.batches_per_block = batches_env();
     return p;
 }
 

@@ -57,6 +57,23 @@ struct Chunk<32> {
     }
 };
 
+// q & mask, opaque to the optimiser.  With the mask visible, the compiler folds
+// "(float)((q & 0x0F0F0F0F) >> 8 & 0xFF)" into v_bfe_u32 + v_cvt_f32_ubyte0 (two
+// instructions per nibble); behind this AND each byte converts with a single
+// v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t q, uint32_t mask) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(q), "v"(mask));
+    return r;
+}
+
+// a if !pick_b else b, as bit operations: a plain `pick ? v[i + h] : v[i]` on a
+// register array is rewritten by the compiler into a dynamically indexed
+// access (a cmp/cndmask chain over the whole array).
+__device__ __forceinline__ float select_bits(float a, float b, uint32_t mask_b) {
+    return __uint_as_float((__float_as_uint(a) & ~mask_b) | (__float_as_uint(b) & mask_b));
+}
+
 // Reduce V per-lane values over the lanes of bits [0, b) of the lane id.
 // After the call, lane l holds in v[0] the full sum of value index
 // (l >> (b - log2 V)) & (V - 1) over its 2^b-lane span.  Requires V <= 2^b.
@@ -67,11 +84,12 @@ __device__ __forceinline__ void transpose_reduce(float (&v)[V], int lane, int b)
     for (int s = 0; s < LOGV; ++s) {
         const int h = (V >> s) >> 1;
         const int mask = 1 << (b - 1 - s);
-        const bool upper = (lane & mask) != 0;
+        const uint32_t up = (lane & mask) ? 0xFFFFFFFFu : 0u;
 #pragma unroll
         for (int i = 0; i < h; ++i) {
-            float keep = upper ? v[i + h] : v[i];
-            float send = upper ? v[i] : v[i + h];
+            const float lo = v[i], hi = v[i + h];
+            const float keep = select_bits(lo, hi, up);
+            const float send = select_bits(hi, lo, up);
             v[i] = keep + __shfl_xor(send, mask);
         }
     }
@@ -86,6 +104,7 @@ __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p) {
     constexpr int V = D * J * M;
     constexpr int NDW = Chunk<E>::ndw;
     constexpr int LOGV = Log2<V>::value;
+    constexpr int OUT = J * M;
     __shared__ float red[kMaxWaves * 64];
 
     const int lane = threadIdx.x & 63;
@@ -93,9 +112,10 @@ __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p) {
     const int nwaves = blockDim.x >> 6;
     const int rr = lane >> p.b;
     const int cl = lane & ((1 << p.b) - 1);
-    const int chunk = wave * p.sw + cl;
-    const bool act = (cl < p.sw) && (chunk < p.c);
-    const int row0 = blockIdx.x * p.rows_per_block;
+    const int chunk_raw = wave * p.sw + cl;
+    const bool act = (cl < p.sw) && (chunk_raw < p.c);
+    // Idle lanes read a valid chunk and contribute zero (scale forced to 0).
+    const int chunk = act ? chunk_raw : 0;
 
     // This lane's slice of every activation row, odd elements pre-divided by 16.
     float xr[M][E];
@@ -121,80 +141,89 @@ __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p) {
     const int sg = (chunk * E) >> p.gshift;     // this chunk's scale column
     const size_t bpr = (size_t)(p.k >> 1);
     const size_t boff = (size_t)chunk * (E / 2);
+    const int nblk = (p.n + p.rows_per_block - 1) / p.rows_per_block;
 
-    float v[V];
+    for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+        const int row0 = blk * p.rows_per_block;
+        // Issue every load of the batch first (J*D 16-byte chunks + scales in
+        // flight per lane), then unpack and accumulate.
+        uint32_t q[D][J][NDW];
+        float sc[D][J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int row = row0 + j * p.rows_per_step + rr;
-        const bool ok = act && row < p.n;
+        for (int j = 0; j < J; ++j) {
+            const int row_raw = row0 + j * p.rows_per_step + rr;
+            const bool ok = act && row_raw < p.n;
+            const int row = ok ? row_raw : 0;   // out-of-range rows re-read row 0, weight 0
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const uint8_t *w = d ? p.w1 : p.w0;
-            const float *s = d ? p.s1 : p.s0;
-            uint32_t q[NDW];
-            float sc = 0.f;
-            if (ok) {
-                Chunk<E>::load(w + (size_t)row * bpr + boff, q);
-                sc = s[(size_t)row * gcols + sg];
-            } else {
-#pragma unroll
-                for (int i = 0; i < NDW; ++i) q[i] = 0u;
+            for (int d = 0; d < D; ++d) {
+                const uint8_t *w = d ? p.w1 : p.w0;
+                const float *s = d ? p.s1 : p.s0;
+                Chunk<E>::load(w + (size_t)row * bpr + boff, q[d][j]);
+                const float sv = s[(size_t)row * gcols + sg];
+                sc[d][j] = ok ? sv : 0.f;
             }
-            float acc[M];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        float v[V];
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[m] = 0.f;
+        for (int j = 0; j < J; ++j) {
 #pragma unroll
-            for (int dw = 0; dw < NDW; ++dw) {
-                const uint32_t lo = q[dw] & 0x0F0F0F0Fu;
-                const uint32_t hi = q[dw] & 0xF0F0F0F0u;
+            for (int d = 0; d < D; ++d) {
+                float acc[M];
 #pragma unroll
-                for (int bb = 0; bb < 4; ++bb) {
-                    const float f0 = (float)((lo >> (8 * bb)) & 0xFFu);
-                    const float f1 = (float)((hi >> (8 * bb)) & 0xFFu);
+                for (int m = 0; m < M; ++m) acc[m] = 0.f;
 #pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        acc[m] = fmaf(f0, xr[m][8 * dw + 2 * bb], acc[m]);
-                        acc[m] = fmaf(f1, xr[m][8 * dw + 2 * bb + 1], acc[m]);
-                    }
+                for (int dw = 0; dw < NDW; ++dw) {
+                    const uint32_t lo = and_opaque(q[d][j][dw], 0x0F0F0F0Fu);
+                    const uint32_t hi = and_opaque(q[d][j][dw], 0xF0F0F0F0u);
+                    const float f[8] = {(float)(lo & 0xFFu),         (float)(hi & 0xFFu),
+                                        (float)((lo >> 8) & 0xFFu),  (float)((hi >> 8) & 0xFFu),
+                                        (float)((lo >> 16) & 0xFFu), (float)((hi >> 16) & 0xFFu),
+                                        (float)(lo >> 24),           (float)(hi >> 24)};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+#pragma unroll
+                        for (int m = 0; m < M; ++m) acc[m] = fmaf(f[e], xr[m][8 * dw + e], acc[m]);
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) v[(d * J + j) * M + m] = sc[d][j] * (acc[m] - xs8[m]);
+            }
+        }
+
+        transpose_reduce<V>(v, lane, p.b);
+        const int low = p.b - LOGV;
+        if ((cl & ((1 << low) - 1)) == 0) {
+            const int idx = (cl >> low) & (V - 1);
+            red[(wave * p.rows_per_step + rr) * V + idx] = v[0];
+        }
+        __syncthreads();
+
+        // Epilogue: one thread per (sub-row, row step, activation row).
+        const int t = threadIdx.x;
+        if (t < p.rows_per_step * OUT) {
+            const int r2 = t / OUT, jm = t - r2 * OUT;
+            const int j = jm / M, m = jm - j * M;
+            const int row = row0 + j * p.rows_per_step + r2;
+            if (row < p.n && m < p.m) {
+                float a0 = 0.f, a1 = 0.f;
+                for (int w = 0; w < nwaves; ++w) {
+                    const float *rw = red + (w * p.rows_per_step + r2) * V;
+                    a0 += rw[j * M + m];
+                    if (DUAL) a1 += rw[(J + j) * M + m];
+                }
+                const size_t o = (size_t)m * p.n + row;
+                if (EPI == EPI_SWIGLU) {
+                    const float g = a0 + (p.b0 ? p.b0[row] : 0.f);
+                    const float u = a1 + (p.b1 ? p.b1[row] : 0.f);
+                    p.y[o] = silu(g) * u;
+                } else {
+                    const float val = a0 + (p.b0 ? p.b0[row] : 0.f);
+                    p.y[o] = (EPI == EPI_RESID) ? p.res[o] + val : val;
                 }
             }
-#pragma unroll
-            for (int m = 0; m < M; ++m) v[(d * J + j) * M + m] = sc * (acc[m] - xs8[m]);
         }
-    }
-
-    transpose_reduce<V>(v, lane, p.b);
-    const int low = p.b - LOGV;
-    if ((cl & ((1 << low) - 1)) == 0) {
-        const int idx = (cl >> low) & (V - 1);
-        red[(wave * p.rows_per_step + rr) * V + idx] = v[0];
-    }
-    __syncthreads();
-
-    // Epilogue: one thread per (sub-row, row step, activation row).
-    constexpr int OUT = J * M;
-    const int t = threadIdx.x;
-    if (t < p.rows_per_step * OUT) {
-        const int r2 = t / OUT, jm = t - r2 * OUT;
-        const int j = jm / M, m = jm - j * M;
-        const int row = row0 + j * p.rows_per_step + r2;
-        if (row < p.n && m < p.m) {
-            float a0 = 0.f, a1 = 0.f;
-            for (int w = 0; w < nwaves; ++w) {
-                const float *rw = red + (w * p.rows_per_step + r2) * V;
-                a0 += rw[j * M + m];
-                if (DUAL) a1 += rw[(J + j) * M + m];
-            }
-            const size_t o = (size_t)m * p.n + row;
-            if (EPI == EPI_SWIGLU) {
-                const float g = a0 + (p.b0 ? p.b0[row] : 0.f);
-                const float u = a1 + (p.b1 ? p.b1[row] : 0.f);
-                p.y[o] = silu(g) * u;
-            } else {
-                const float val = a0 + (p.b0 ? p.b0[row] : 0.f);
-                p.y[o] = (EPI == EPI_RESID) ? p.res[o] + val : val;
-            }
-        }
+        __syncthreads();   // red is rewritten by the next batch
     }
 }
 
@@ -225,7 +254,8 @@ int launch(W4Params p, hipStream_t st) {
     p.b = bnat > LOGV ? bnat : LOGV;
     p.rows_per_step = 64 >> p.b;
     p.rows_per_block = J * p.rows_per_step;
-    const int grid = (int)((p.n + p.rows_per_block - 1) / p.rows_per_block);
+    const int nblk = (int)((p.n + p.rows_per_block - 1) / p.rows_per_block);
+    const int grid = (nblk + p.batches_per_block - 1) / p.batches_per_block;
     hipLaunchKernelGGL((k_w4_gemv<M, E, J, DUAL, EPI>), dim3(grid), dim3(ks * 64), 0, st, p);
     TB_LAUNCHED();
     return TB_OK;
@@ -234,8 +264,8 @@ int launch(W4Params p, hipStream_t st) {
 template <bool DUAL, int EPI>
 int dispatch_m(const W4Params &p, hipStream_t st) {
     // x stays in VGPRs (32 per activation row), so one pass takes <= 2 rows.
-    if (p.m <= 1) return launch<1, 32, 16, DUAL, EPI>(p, st);
-    return launch<2, 32, 8, DUAL, EPI>(p, st);
+    if (p.m <= 1) return launch<1, 32, DUAL ? 8 : 16, DUAL, EPI>(p, st);
+    return launch<2, 32, DUAL ? 4 : 8, DUAL, EPI>(p, st);
 }
 
 }  // namespace

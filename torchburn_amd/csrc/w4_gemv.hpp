@@ -23,6 +23,7 @@ struct W4Params {
     float *y;          // [m, n] output
     int m, n, k;
     int gshift;        // log2(group_size)
+    int batches_per_block;  // row batches each block streams with x held in VGPRs
     // Filled in by the launcher.
     int c, sw, b, rows_per_step, rows_per_block;
 };
