@@ -129,3 +129,37 @@ def test_errors_match_reference_contract(cuda):
         tb.w4a32_grouped_linear(x, w, T(np.ones((8, 3), np.float32)), group_size=32)
     with pytest.raises(tb.UnsupportedOpError, match="group_size"):
         tb.w4a32_grouped_linear(x, w, T(np.ones((8, 4), np.float32)), group_size=16)
+
+
+def test_non_finite_activations_propagate(cuda):
+    """NaN / Inf in x propagate as in the reference's f32 arithmetic."""
+    g = synth.rng(14)
+    n, k = 300, 4096
+    w, s = synth.int4_weight(g, n, k, 32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    for bad in (np.nan, np.inf):
+        x = synth.activations(g, 1, k)
+        x[0, 1234] = bad
+        ref = O.gemm_w4(x, w, s, None, group_size=32)
+        y = tb.w4a32_grouped_linear(T(x), T(w), T(s), None, 32).cpu().numpy()
+        assert np.array_equal(np.isnan(y), np.isnan(ref))
+        assert np.array_equal(np.isinf(y), np.isinf(ref))
+        fin = np.isfinite(ref)
+        if fin.any():
+            assert rel(y[fin], ref[fin]) < TOL
+
+
+def test_extreme_activation_ranges(cuda):
+    """Chunks mixing magnitudes 1e-30..1e30 and all-zero chunks."""
+    g = synth.rng(15)
+    n, k = 256, 2048
+    w, s = synth.int4_weight(g, n, k, 32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    x = synth.activations(g, 1, k)
+    x[0, :32] = 0.0
+    x[0, 32:64] *= 1e-30
+    x[0, 64:96] *= 1e30
+    x[0, 100] = 1e20
+    ref = O.gemm_w4(x, w, s, None, group_size=32)
+    y = tb.w4a32_grouped_linear(T(x), T(w), T(s), None, 32).cpu().numpy()
+    assert rel(y, ref) < TOL

@@ -26,13 +26,14 @@ bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 int gshift_of(int64_t gs) { return gs == 32 ? 5 : (gs == 64 ? 6 : -1); }
 
-// Row batches per GEMV block (TB_W4_BATCHES overrides, for tuning sweeps).
-int batches_env() {
-    static int v = [] {
-        const char *e = getenv("TB_W4_BATCHES");
-        int b = e ? atoi(e) : 1;
-        return b < 1 ? 1 : b;
-    }();
+// GEMV rows per block; TB_W4_J overrides the default (tuning sweeps only).
+int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    int v = e ? atoi(e) : dflt;
+    return v < 0 ? dflt : v;
+}
+int rows_j_env() {
+    static int v = env_int("TB_W4_J", 0);
     return v;
 }
 }  // namespace
@@ -88,16 +89,28 @@ static W4Params w4_params(const float *x, const uint8_t *w, const float *s, cons
     W4Params p{};
     p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
     p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
-    p.batches_per_block = batches_env();
+    p.rows_j = rows_j_env();
     return p;
 }
 
+static size_t xq_bytes(int64_t m, int64_t k) {
+    return (size_t)m * (size_t)(k / 32) * kXRecDwords * sizeof(uint32_t);
+}
+
 // M rows in passes of at most kMaxRowsPerPass (the GEMV keeps x in VGPRs).
-static int w4_rows(W4Params p, int epi, int64_t m, hipStream_t st) {
+// xq: chunk records of all m rows of p.x (built here when build_xq is set).
+static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
+                   hipStream_t st) {
+    if (build_xq) {
+        int rc = xquant(p.x, xq, (int)m, p.k, st);
+        if (rc) return rc;
+    }
+    const int64_t rec = (int64_t)(p.k / 32) * kXRecDwords;
     for (int64_t r0 = 0; r0 < m; r0 += kMaxRowsPerPass) {
         W4Params q = p;
         q.m = (int)((m - r0) < kMaxRowsPerPass ? (m - r0) : kMaxRowsPerPass);
         q.x = p.x + r0 * p.k;
+        q.xq = xq + r0 * rec;
         q.y = p.y + r0 * (int64_t)p.n;
         if (p.res) q.res = p.res + r0 * (int64_t)p.n;
         int rc = w4_gemv(q, epi, st);
@@ -123,8 +136,11 @@ int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float
     if (rc) return rc;
     TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_grouped_linear: null output");
     if (m == 0 || n == 0) return TB_OK;
+    void *ws = nullptr;
+    rc = workspace(xq_bytes(m, k), &ws);
+    if (rc) return rc;
     W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
-    return w4_rows(p, EPI_PLAIN, m, (hipStream_t)stream);
+    return w4_rows(p, EPI_PLAIN, m, (uint32_t *)ws, true, (hipStream_t)stream);
 }
 
 int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
@@ -136,9 +152,12 @@ int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
     TB_REQUIRE(out && residual, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32_grouped_linear_residual: null output or residual");
     if (m == 0 || n == 0) return TB_OK;
+    void *ws = nullptr;
+    rc = workspace(xq_bytes(m, k), &ws);
+    if (rc) return rc;
     W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
     p.res = residual;
-    return w4_rows(p, EPI_RESID, m, (hipStream_t)stream);
+    return w4_rows(p, EPI_RESID, m, (uint32_t *)ws, true, (hipStream_t)stream);
 }
 
 int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
@@ -151,9 +170,12 @@ int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
     if (rc) return rc;
     TB_REQUIRE(h, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: swiglu_w4a32: null output");
     if (m == 0 || inter == 0) return TB_OK;
+    void *ws = nullptr;
+    rc = workspace(xq_bytes(m, k), &ws);
+    if (rc) return rc;
     W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
     p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
-    return w4_rows(p, EPI_SWIGLU, m, (hipStream_t)stream);
+    return w4_rows(p, EPI_SWIGLU, m, (uint32_t *)ws, true, (hipStream_t)stream);
 }
 
 int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
@@ -172,21 +194,26 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
     TB_REQUIRE(down_w && down_s && out, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: null down weight or output");
     if (m == 0 || n_out == 0) return TB_OK;
+    // Workspace: h [m, inter] f32 | chunk records of x | chunk records of h.
+    const size_t hb = ((size_t)m * (size_t)inter * sizeof(float) + 255) & ~(size_t)255;
+    const size_t xb = (xq_bytes(m, k) + 255) & ~(size_t)255;
     void *ws = nullptr;
-    rc = workspace((size_t)m * (size_t)inter * sizeof(float), &ws);
+    rc = workspace(hb + xb + xq_bytes(m, inter), &ws);
     if (rc) return rc;
     float *h = static_cast<float *>(ws);
+    uint32_t *xq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb);
+    uint32_t *hq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb + xb);
     hipStream_t st = (hipStream_t)stream;
     W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
     p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
-    rc = w4_rows(p, EPI_SWIGLU, m, st);
+    rc = w4_rows(p, EPI_SWIGLU, m, xq, true, st);
     if (rc) return rc;
     W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
     if (residual) {
         d.res = residual;
-        return w4_rows(d, EPI_RESID, m, st);
+        return w4_rows(d, EPI_RESID, m, hq, true, st);
     }
-    return w4_rows(d, EPI_PLAIN, m, st);
+    return w4_rows(d, EPI_PLAIN, m, hq, true, st);
 }
 
 }  // extern "C"

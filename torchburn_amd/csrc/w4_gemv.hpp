@@ -11,8 +11,15 @@ enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 // Activation rows per GEMV pass (x is held in VGPRs).
 constexpr int kMaxRowsPerPass = 2;
 
+// An x chunk record: 32 activations as a 24-bit fixed-point integer per element
+// in six 4-bit limb planes (24 dwords), then {step (f32 bits; NaN when the chunk
+// holds NaN/Inf), sum of the integers, 0, 0} (112 bytes, 16-byte aligned).  Built once per activation vector by xquant()
+// and read by every block of the GEMV.
+constexpr int kXRecDwords = 28;
+
 struct W4Params {
-    const float *x;    // [m, k] activations
+    const float *x;    // [m, k] activations (read only by the NaN/Inf path)
+    const uint32_t *xq; // [m, k/32, kXRecDwords] chunk records of x (xquant)
     const uint8_t *w0; // [n, k/2] packed nibbles (gate when dual)
     const float *s0;   // [n, k/group] scales
     const float *b0;   // [n] bias or null
@@ -23,7 +30,7 @@ struct W4Params {
     float *y;          // [m, n] output
     int m, n, k;
     int gshift;        // log2(group_size)
-    int batches_per_block;  // row batches each block streams with x held in VGPRs
+    int rows_j;             // rows per batch (tuning: 4, 8 or 16; 0 = default)
     // Filled in by the launcher.
     int c, sw, b, rows_per_step, rows_per_block;
 };
@@ -31,5 +38,8 @@ struct W4Params {
 // One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
 // p.w1 is set.  Shapes are validated by the caller.
 int w4_gemv(W4Params p, int epi, hipStream_t st);
+
+// Chunk records of x [m, k] (k % 32 == 0) into xq [m, k/32, kXRecDwords].
+int xquant(const float *x, uint32_t *xq, int m, int k, hipStream_t st);
 
 }  // namespace tb
