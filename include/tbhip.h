@@ -108,6 +108,110 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
                               int64_t m, int64_t k, int64_t inter, int64_t n_out,
                               int64_t group_size, void *stream);
 
+/*
+ * out[m, n] = (sum_k x[m, k] * w[n, k]) * s[n] + bias[n]: the reference's
+ * w8a32_linear (binding src/ffi/quantization_ffi.rs:8-30, kernel
+ * src/quantization/gemv.rs:733-1061).  w i8 [N, K]; s_len 1 (one per-tensor
+ * scale) or N; K must be a multiple of 32.
+ */
+TB_API int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_t s_len,
+                           const float *bias, float *out, int64_t m, int64_t n, int64_t k,
+                           void *stream);
+
+/*
+ * INT8 SwiGLU MLP, fused_swiglu_mlp_w8a32 (binding src/ffi/quantization_ffi.rs:150-201,
+ * kernel src/quantization/fused_ops.rs:8-133), with an optional residual add.
+ * Per-channel scales [I] / [n_out]; h [M, I] in the library workspace.
+ */
+TB_API int tb_fused_swiglu_mlp_w8a32(const float *x, const int8_t *gate_w, const float *gate_s,
+                                     const float *gate_b, const int8_t *up_w, const float *up_s,
+                                     const float *up_b, const int8_t *down_w,
+                                     const float *down_s, const float *down_b,
+                                     const float *residual, float *out, int64_t m, int64_t k,
+                                     int64_t inter, int64_t n_out, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Decoder (replaces RustQwenDecoder, reference src/llm/decoder.rs:176-1374)   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct tb_decoder tb_decoder;
+
+/* Constructor arguments of RustQwenDecoder::new (decoder.rs:176-212), plus the
+ * weight formats: weight_bits 4 = INT4 grouped projections (the reference's
+ * native decoder), 8 = INT8 per-channel projections (the reference runs INT8
+ * through its per-layer path, python/torchburn/llm/model.py:214-239, 334-344);
+ * lm_head_bits 4, 8 or 32 (fp32 nn.Linear lm_head, model.py:499-500). */
+typedef struct {
+    int64_t num_layers, hidden_size, intermediate_size, num_heads, num_kv_heads, head_dim;
+    int64_t vocab_size, group_size, max_seq_len;
+    double rms_norm_eps, rope_theta;
+    int32_t weight_bits, lm_head_bits;
+} tb_decoder_config;
+
+/* RustQwenDecoder::new (decoder.rs:193-424): validates the configuration
+ * (TB_ERR_VALUE), copies the embedding table [V, H], final norm [H] and lm_head
+ * (w, s; s unused for fp32) to the device, builds the f64 RoPE tables and a
+ * zeroed KV cache [L][num_kv_heads, max_seq_len, head_dim].  Pointers may be
+ * host or device memory. */
+TB_API int tb_decoder_create(const tb_decoder_config *cfg, const float *embed,
+                             const float *final_norm, const void *lm_head_w,
+                             const float *lm_head_s, tb_decoder **out);
+
+/* One layer, in the reference's capsule order (decoder.rs:260-308); qkv_b may be
+ * NULL.  Every layer must be set once before the first step. */
+TB_API int tb_decoder_set_layer(tb_decoder *d, int64_t layer, const float *in_norm,
+                                const void *qkv_w, const float *qkv_s, const void *o_w,
+                                const float *o_s, const float *post_norm, const void *gate_w,
+                                const float *gate_s, const void *up_w, const float *up_s,
+                                const void *down_w, const float *down_s, const float *qkv_b);
+
+/* step_internal + decode_step (decoder.rs:729-750, 1051-1374): logits_out (host,
+ * vocab_size floats) and argmax_out may be NULL.  An out-of-range token or
+ * offset >= max_seq_len gives zeroed logits and changes nothing else. */
+TB_API int tb_decoder_step(tb_decoder *d, int64_t token, int64_t offset, float *logits_out,
+                           int64_t *argmax_out);
+
+/* decode_and_sample (decoder.rs:752-777, 878-1020): repetition penalty over
+ * `recent`, then greedy (temperature <= 0 or not finite, or top_k == 1) or
+ * top-k / top-p sampling from the decoder's seeded generator. */
+TB_API int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t offset,
+                                        float temperature, int64_t top_k,
+                                        float repetition_penalty, const int64_t *recent,
+                                        int64_t n_recent, float top_p, int64_t *token_out);
+
+/* Greedy generate_loop (decoder.rs:788-832): tokens_out receives up to
+ * max_new_tokens ids (the first is first_token); *seq_len_out = seq_len + n.
+ * eos_token_id < 0 means none.  Without an EOS the steps run as device-driven
+ * graph replays with no host round trip. */
+TB_API int tb_decoder_generate(tb_decoder *d, int64_t first_token, int64_t seq_len,
+                               int64_t max_new_tokens, int64_t eos_token_id,
+                               int64_t *tokens_out, int64_t *n_out, int64_t *seq_len_out);
+
+/* prefill_tokens (decoder.rs:431-447): TB_ERR_VALUE when start_offset + n >
+ * max_seq_len. */
+TB_API int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n,
+                              int64_t start_offset, int64_t *offset_out);
+
+/* reset_kv_cache / copy_kv_cache_from_tensors / kv_len / get_logits
+ * (decoder.rs:449-533).  copy_kv sources are [num_kv_heads, src_max, head_dim]. */
+TB_API int tb_decoder_reset_kv(tb_decoder *d);
+TB_API int tb_decoder_copy_kv(tb_decoder *d, int64_t layer, const float *k, const float *v,
+                              int64_t src_max, int64_t seq_len);
+TB_API int tb_decoder_kv_len(tb_decoder *d, int64_t *out);
+TB_API int tb_decoder_get_logits(tb_decoder *d, float *out);
+
+/* Seed of the sampling generator (no reference counterpart: the reference draws
+ * from an unseeded rand::random). */
+TB_API int tb_decoder_set_seed(tb_decoder *d, uint64_t seed);
+
+/* Benchmark helper (no reference counterpart): n_steps greedy steps from
+ * (first_token, offset) as back-to-back graph replays, timed with HIP events on
+ * the decoder's stream. */
+TB_API int tb_decoder_time_greedy(tb_decoder *d, int64_t first_token, int64_t offset,
+                                  int64_t n_steps, float *ms_out);
+
+TB_API int tb_decoder_destroy(tb_decoder *d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,81 @@
+"""The C-ABI library (libtbhip.so): loads on a GPU-less host, exports every
+entry point include/tbhip.h declares, and maps argument errors to the
+reference's exception split without touching the GPU."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from torchburn_amd import _lib
+from torchburn_amd import decoder as tbdec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "tbhip.h")).read()
+    return sorted(set(re.findall(r"TB_API\s+[\w\s\*]*?\b(tb_\w+)\s*\(", txt)))
+
+
+def test_header_declares_entry_points():
+    syms = header_symbols()
+    assert "tb_w4a32_grouped_linear" in syms and "tb_decoder_step" in syms
+    assert len(syms) >= 21
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for s in header_symbols():
+        assert hasattr(L, s), s
+    for s in _lib.declared_symbols() + tbdec.decoder_symbols():
+        assert s in header_symbols(), s
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.lib().tb_version()
+
+
+def test_argument_errors_before_any_gpu_call():
+    L = _lib.lib()
+    buf = (C.c_float * 64)()
+    p = C.cast(buf, C.c_void_p).value
+    # group size 16 is not supported by the kernels -> UnsupportedOpError
+    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, 1, 1, 64, 16, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED
+    with pytest.raises(_lib.UnsupportedOpError, match="TB_UNSUPPORTED"):
+        _lib.check(rc)
+    # K not a multiple of the group
+    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, 1, 1, 48, 32, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"multiple" in L.tb_last_error()
+    # misaligned pointers
+    rc = L.tb_w4a32_grouped_linear(p + 4, p, p, None, p, 1, 1, 64, 32, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("hidden_size", 898, "divisible by 4"),
+    ("head_dim", 63, "even"),
+    ("num_heads", 7, "divisible by num_kv_heads"),
+    ("group_size", 48, "group_size"),
+])
+def test_decoder_config_errors_are_value_errors(field, value, msg):
+    L = tbdec._bind()
+    cfg = tbdec._Config(2, 256, 512, 4, 2, 64, 1000, 32, 128, 1e-6, 1e6, 4, 4)
+    setattr(cfg, field, value)
+    buf = (C.c_float * 16)()
+    h = C.c_void_p()
+    rc = L.tb_decoder_create(C.byref(cfg), buf, buf, buf, buf, C.byref(h))
+    assert rc == _lib.TB_ERR_VALUE
+    with pytest.raises(ValueError, match=msg):
+        _lib.check(rc)
+
+
+def test_product_path_never_touches_the_oracle():
+    pkg = os.path.join(ROOT, "torchburn_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                txt = open(os.path.join(dirpath, f)).read()
+                for needle in ("import oracle", "from oracle", "liboracle", "orc_", "tb_oracle"):
+                    assert needle not in txt, (f, needle)

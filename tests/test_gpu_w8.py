@@ -1,0 +1,60 @@
+"""Parity of the gfx950 INT8 per-channel GEMV / SwiGLU MLP with the CPU oracle
+(gemv_w8a32, src/quantization/gemv.rs:733-1061; fused_swiglu_mlp_w8a32,
+src/quantization/fused_ops.rs:8-133).  Metric max|d| / max|ref| < 1e-4."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from torchburn_amd import synth
+import torchburn_amd as tb
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 128256, 4096), (2, 1000, 896),
+                                   (3, 77, 64), (1, 4096, 14336)])
+def test_w8_linear_matches_oracle(cuda, m, n, k):
+    print(f"case w8a32_linear m={m} n={n} k={k}", flush=True)
+    g = synth.rng(21, m, n, k)
+    x = synth.activations(g, m, k)
+    w, s = synth.int8_weight(g, n, k)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    ref = O.gemv_w8(x, w, s, b)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    y = tb.w8a32_linear(T(x), T(w), T(s), T(b)).cpu().numpy()
+    assert rel(y, ref) < 1e-4
+
+
+def test_w8_per_tensor_scale(cuda):
+    g = synth.rng(22)
+    x = synth.activations(g, 1, 512)
+    w, _ = synth.int8_weight(g, 64, 512)
+    s = np.array([0.03], np.float32)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    y = tb.w8a32_linear(T(x), T(w), T(s)).cpu().numpy()
+    assert rel(y, O.gemv_w8(x, w, s)) < 1e-4
+
+
+def test_w8_swiglu_mlp_matches_oracle(cuda):
+    g = synth.rng(23)
+    m, k, inter = 1, 1024, 2048
+    x = synth.activations(g, m, k)
+    gw, gsc = synth.int8_weight(g, inter, k)
+    uw, usc = synth.int8_weight(g, inter, k)
+    dw, dsc = synth.int8_weight(g, k, inter)
+    h = O.lib()  # noqa: F841  (loads the oracle)
+    hh = np.empty(inter, np.float32)
+    O.lib().orc_swiglu_h_w8(x.ctypes.data, gw.ctypes.data, gsc.ctypes.data, uw.ctypes.data,
+                            usc.ctypes.data, hh.ctypes.data, inter, k)
+    ref = O.gemv_w8(hh[None], dw, dsc)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    out = tb.fused_swiglu_mlp_w8a32(T(x), T(gw), T(gsc), None, T(uw), T(usc), None, T(dw),
+                                    T(dsc), None).cpu().numpy()
+    assert rel(out, ref) < 1e-4

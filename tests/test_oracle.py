@@ -1,0 +1,341 @@
+"""Pins the CPU oracle (oracle/tb_oracle.c) before it is trusted as the checker.
+
+What pins each oracle function (no golden-vector files exist in the reference;
+its own tests recompute expectations in-test, so their deterministic inputs and
+budgets are reproduced here):
+
+  pack / unpack      all 256 byte values; random round trips; the reference's
+                     quantize_grouped KAT (tests/parity/int4.rs:12-38)
+  quantizer          numpy closed form with half-to-even rounding
+                     (python/torchburn/quantization.py:53-118)
+  gemv_w4 / gemm_w4  float64 brute force (tests/parity/int4.rs:109-126), the
+                     reference's KAT inputs and budgets (int4.rs:172-255, 303-329),
+                     special cases (x = 0, constant q, one-hot x)
+  swiglu             float64 closed form via torch.nn.functional.silu
+  gemv_w8            the dot_f32_i8 KAT (tests/parity/int8.rs:24-37), float64,
+                     quality budget (int8.rs:41-67)
+  rms_norm           the reference's KAT (tests/parity/decoder.rs:14-29) and
+                     torch.nn.functional.rms_norm in float64
+  rope               RoPE as a complex rotation in float64 (a different formula),
+                     pos 0 is the identity, pair norms preserved
+  attention          torch scaled_dot_product_attention(enable_gqa) in float64;
+                     seq_len 1 returns v; identical keys give mean(V)
+  argmax             decoder.rs:32-40 KAT, ties -> lowest index
+  decoder step       an independent float64 torch model built from library ops
+                     (rms_norm, complex RoPE, SDPA, silu) on a small config
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+from torchburn_amd import synth
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-6))
+
+
+def dequant(w, s, k, gs):
+    q = O.unpack_int4(w, k).astype(np.float64)
+    return q * np.repeat(s.astype(np.float64), gs, axis=1)[:, :k]
+
+
+# ---------------------------------------------------------------- packing ---
+
+def test_unpack_all_bytes():
+    w = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    q = O.unpack_int4(w, 512)[0]
+    b = np.arange(256)
+    assert np.array_equal(q[0::2], (b & 15) - 8)
+    assert np.array_equal(q[1::2], (b >> 4) - 8)
+
+
+@pytest.mark.parametrize("k", [2, 31, 32, 896, 1001])
+def test_pack_round_trip(k):
+    q = np.random.default_rng(k).integers(-8, 8, size=(7, k), dtype=np.int8)
+    w = O.pack_int4(q)
+    assert w.shape == (7, (k + 1) // 2)
+    assert np.array_equal(O.unpack_int4(w, k), q)
+    # byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4
+    assert int(w[0, 0]) == (int(q[0, 0]) + 8) | ((int(q[0, 1]) + 8) << 4)
+
+
+def test_quantizer_matches_closed_form():
+    g = np.random.default_rng(3)
+    w = g.normal(0, 1, (9, 128)).astype(np.float32)
+    w[0, :32] = 0.0                      # all-zero group -> scale 1e-8
+    w[1, 5] = 3.5 * (np.abs(w[1, :32]).max() / 7.0)   # an exact .5 tie
+    packed, scales = O.quantize_int4_grouped(w, 32)
+    wg = w.reshape(9, 4, 32)
+    s = np.maximum(np.abs(wg).max(-1) / np.float32(7.0), np.float32(1e-8)).astype(np.float32)
+    q = np.clip(np.round(wg / s[..., None]), -8, 7).astype(np.int8).reshape(9, 128)
+    assert np.array_equal(scales, s)
+    assert np.array_equal(packed, O.pack_int4(q))
+
+
+def reference_quantize_grouped(w, k, gs):
+    """tests/parity/int4.rs:12-38: scale = max_abs/7 (1.0 if <= 1e-8), q = round-half-away."""
+    n = w.size // k
+    wg = w.reshape(n, k // gs, gs)
+    mx = np.abs(wg).max(-1)
+    s = np.where(mx > 1e-8, mx / np.float32(7.0), np.float32(1.0)).astype(np.float32)
+    v = wg * (np.float32(1.0) / s)[..., None]
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) + 0.5), -8, 7).astype(np.int8)
+    return O.pack_int4(q.reshape(n, k)), s
+
+
+# ------------------------------------------------------------------- gemv ---
+
+@pytest.mark.parametrize("n,k,gs", [(64, 896, 32), (64, 896, 64), (33, 4096, 32),
+                                    (5, 96, 32), (8, 48, 16), (3, 40, 8)])
+def test_gemv_w4_vs_float64(n, k, gs):
+    g = np.random.default_rng(n * k + gs)
+    x = g.standard_normal((2, k), dtype=np.float32)
+    w = g.integers(0, 256, (n, (k + 1) // 2), dtype=np.uint8)
+    s = (np.abs(g.normal(0, 0.02, (n, k // gs))) + 1e-3).astype(np.float32)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    y = O.gemm_w4(x, w, s, b, group_size=gs)
+    ref = x.astype(np.float64) @ dequant(w, s, k, gs).T + b
+    assert rel(y, ref) < 1e-6
+    assert np.allclose(O.gemv_w4_f64(x[0], w, s, b, gs), ref[0], rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_w4_reference_kat():
+    """tests/parity/int4.rs:172-215 inputs; the oracle is the exact-W4A32 tier."""
+    n, k, gs = 64, 896, 64
+    x = (np.sin(np.arange(k, dtype=np.float32) * np.float32(0.13)) * 2).astype(np.float32)
+    w = (np.cos(np.arange(n * k, dtype=np.float32) * np.float32(0.29)) * 1.5).astype(np.float32)
+    packed, scales = reference_quantize_grouped(w, k, gs)
+    y = O.gemm_w4(x[None], packed, scales, group_size=gs)[0]
+    ref = x.astype(np.float64) @ dequant(packed, scales, k, gs).T
+    assert rel(y, ref) < 1e-3          # the reference's budget
+    assert rel(y, ref) < 1e-6          # and the oracle's own
+
+
+def test_gemv_w4_quality_budget():
+    """tests/parity/int4.rs:221-255: int4-g64 vs unquantized f32 < 0.2."""
+    n, k = 32, 512
+    x = (np.cos(np.arange(k, dtype=np.float32) * np.float32(0.07)) * 1.2).astype(np.float32)
+    w = (np.sin(np.arange(n * k, dtype=np.float32) * np.float32(0.17)) * 2).astype(np.float32)
+    packed, scales = reference_quantize_grouped(w, k, 64)
+    y = O.gemm_w4(x[None], packed, scales, group_size=64)[0]
+    assert rel(y, w.reshape(n, k).astype(np.float64) @ x) < 0.2
+
+
+def test_gemv_w4_bias_kat():
+    """tests/parity/int4.rs:303-329."""
+    n, k = 16, 64
+    x = np.full(k, 0.5, np.float32)
+    w = (np.sin(np.arange(n * k, dtype=np.float32) * np.float32(0.23)) * 0.5).astype(np.float32)
+    packed, scales = reference_quantize_grouped(w, k, 64)
+    bias = (np.arange(n) * 0.01 + 0.1).astype(np.float32)
+    y = O.gemm_w4(x[None], packed, scales, bias, group_size=64)[0]
+    want = x.astype(np.float64) @ dequant(packed, scales, k, 64).T + bias
+    assert np.all(np.abs(y - want) / np.maximum(np.abs(want), 1e-4) < 1e-2)
+
+
+def test_gemv_w4_special_cases():
+    n, k = 24, 128
+    g = np.random.default_rng(1)
+    w = g.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    s = g.uniform(0.5, 2, (n, k // 32)).astype(np.float32)
+    b = g.normal(0, 1, n).astype(np.float32)
+    assert np.array_equal(O.gemm_w4(np.zeros((1, k), np.float32), w, s, b, group_size=32)[0], b)
+    x = g.standard_normal((1, k), dtype=np.float32)
+    for c in (-8, 0, 7):
+        wc = np.full((n, k // 2), (c + 8) | ((c + 8) << 4), np.uint8)
+        y = O.gemm_w4(x, wc, np.ones((n, k // 32), np.float32), group_size=32)[0]
+        assert np.allclose(y, c * x.astype(np.float64).sum(), rtol=1e-5, atol=1e-5)
+    q = O.unpack_int4(w, k)
+    for col in (0, 1, 63, 127):
+        e = np.zeros((1, k), np.float32)
+        e[0, col] = 1
+        y = O.gemm_w4(e, w, s, group_size=32)[0]
+        assert np.array_equal(y, q[:, col].astype(np.float32) * s[:, col // 32])
+
+
+def test_swiglu_mlp_vs_float64():
+    g = np.random.default_rng(4)
+    m, k, inter = 2, 128, 96
+    x = g.standard_normal((m, k), dtype=np.float32)
+    gw, gsc = synth.int4_weight(g, inter, k, 32)
+    uw, usc = synth.int4_weight(g, inter, k, 32)
+    dw, dsc = synth.int4_weight(g, k, inter, 32)
+    gb = g.normal(0, 0.1, inter).astype(np.float32)
+    out = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb=gb, group_size=32)
+    xd = torch.from_numpy(x.astype(np.float64))
+    gg = xd @ torch.from_numpy(dequant(gw, gsc, k, 32)).T + torch.from_numpy(gb.astype(np.float64))
+    uu = xd @ torch.from_numpy(dequant(uw, usc, k, 32)).T
+    h = F.silu(gg) * uu
+    ref = (h @ torch.from_numpy(dequant(dw, dsc, inter, 32)).T).numpy()
+    assert rel(out, ref) < 1e-5
+
+
+# ------------------------------------------------------------------- int8 ---
+
+def test_dot_i8_reference_kat():
+    """tests/parity/int8.rs:24-37 (row dot with unit scale)."""
+    i = np.arange(2048)
+    x = (np.cos(i.astype(np.float32) * np.float32(0.041)) * 2).astype(np.float32)
+    w = (((i * 31) % 251) - 125).astype(np.int8)[None]
+    got = O.gemv_w8(x[None], w, np.ones(1, np.float32))[0, 0]
+    want = float(np.dot(x.astype(np.float64), w[0].astype(np.float64)))
+    assert abs(got - want) / max(abs(want), 1e-6) < 1e-3
+    assert abs(got - want) / max(abs(want), 1e-6) < 1e-5
+
+
+def test_gemv_w8_vs_float64_and_quality():
+    g = np.random.default_rng(5)
+    n, k = 40, 1000       # k % 32 != 0 exercises the 16-wide and scalar tails
+    x = g.standard_normal((1, k), dtype=np.float32)
+    q, s = synth.int8_weight(g, n, k)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    y = O.gemv_w8(x, q, s, b)[0]
+    ref = (q.astype(np.float64) @ x[0].astype(np.float64)) * s + b
+    assert rel(y, ref) < 1e-6
+    # int8.rs:41-67 quality budget, with the oracle's quantizer
+    n, k = 32, 512
+    xx = (np.cos(np.arange(k, dtype=np.float32) * np.float32(0.051)) * 1.1).astype(np.float32)
+    ww = (np.sin(np.arange(n * k, dtype=np.float32) * np.float32(0.19)) * 1.8).astype(np.float32)
+    qq, ss = O.quantize_int8(ww.reshape(n, k))
+    y = O.gemv_w8(xx[None], qq, ss)[0]
+    assert rel(y, ww.reshape(n, k).astype(np.float64) @ xx) < 0.05
+
+
+# -------------------------------------------------------- norm, rope, attn ---
+
+def test_rms_norm_reference_kat():
+    """tests/parity/decoder.rs:14-29 inputs and budget."""
+    n = 896
+    x = (np.sin(np.arange(n, dtype=np.float32) * np.float32(0.31)) * 3).astype(np.float32)
+    w = (1 + np.arange(n, dtype=np.float32) * np.float32(0.001)).astype(np.float32)
+    out = O.rms_norm(x, w, 1e-6)
+    want = F.rms_norm(torch.from_numpy(x.astype(np.float64)), (n,),
+                      torch.from_numpy(w.astype(np.float64)), eps=1e-6).numpy()
+    assert np.max(np.abs(out - want) / np.maximum(np.abs(want), 1e-6)) < 1e-4
+    assert rel(out, want) < 1e-6
+
+
+@pytest.mark.parametrize("hd,theta", [(64, 1e6), (128, 5e5)])
+def test_rope_vs_complex_rotation(hd, theta):
+    c, s = O.rope_tables(300, hd, theta)
+    assert np.array_equal(c[0], np.ones(hd, np.float32)) and not s[0].any()
+    half = hd // 2
+    g = np.random.default_rng(hd)
+    head = g.standard_normal(hd, dtype=np.float32)
+    assert np.array_equal(O.rope_apply(head, c[0], s[0]), head)
+    for pos in (1, 17, 299):
+        out = O.rope_apply(head, c[pos], s[pos])
+        freq = theta ** (-(2.0 * np.arange(half)) / hd)
+        z = (head[:half] + 1j * head[half:]).astype(np.complex128) * np.exp(1j * pos * freq)
+        assert np.allclose(out[:half], z.real, atol=2e-5) and np.allclose(out[half:], z.imag, atol=2e-5)
+        assert np.allclose(np.hypot(out[:half], out[half:]), np.hypot(head[:half], head[half:]),
+                           rtol=1e-5)
+
+
+@pytest.mark.parametrize("hq,hkv,hd,seq", [(14, 2, 64, 300), (32, 8, 128, 97), (4, 4, 64, 2)])
+def test_attention_vs_sdpa(hq, hkv, hd, seq):
+    g = np.random.default_rng(seq)
+    max_seq = seq + 5
+    q = g.standard_normal((hq, hd), dtype=np.float32)
+    kc = g.standard_normal((hkv, max_seq, hd), dtype=np.float32)
+    vc = g.standard_normal((hkv, max_seq, hd), dtype=np.float32)
+    out = O.attention(q, kc, vc, seq)
+    T = lambda a: torch.from_numpy(a.astype(np.float64))
+    ref = F.scaled_dot_product_attention(T(q)[None, :, None], T(kc[:, :seq])[None],
+                                         T(vc[:, :seq])[None], enable_gqa=True)[0, :, 0].numpy()
+    assert rel(out, ref) < 1e-5
+
+
+def test_attention_special_cases():
+    g = np.random.default_rng(0)
+    q = g.standard_normal((4, 64), dtype=np.float32)
+    kc = g.standard_normal((2, 16, 64), dtype=np.float32)
+    vc = g.standard_normal((2, 16, 64), dtype=np.float32)
+    out = O.attention(q, kc, vc, 1)
+    assert np.array_equal(out[:2], np.repeat(vc[0, :1], 2, 0))
+    assert np.array_equal(out[2:], np.repeat(vc[1, :1], 2, 0))
+    kc[:] = kc[:, :1]
+    out = O.attention(q, kc, vc, 10)
+    assert np.allclose(out[0], vc[0, :10].mean(0), atol=1e-6)
+
+
+def test_argmax_kat_and_ties():
+    lg = np.sin(np.arange(4096, dtype=np.float32) * np.float32(0.013)).astype(np.float32)
+    lg[1234] = 100.0
+    assert O.argmax(lg) == 1234
+    lg = np.zeros(10, np.float32)
+    lg[[3, 7]] = 5.0
+    assert O.argmax(lg) == 3
+
+
+# ------------------------------------------------------------ decoder step ---
+
+def torch_step(w, cfg, kv, tok, pos, gs):
+    """One decoder step in float64 from torch library ops (independent of the
+    oracle's C code): rms_norm, complex RoPE, SDPA with GQA, silu."""
+    D = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    H, hq, hkv, hd = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    half = hd // 2
+    freq = D(cfg["rope_theta"] ** (-(2.0 * np.arange(half)) / hd))
+    rot = torch.exp(1j * pos * freq)
+
+    def rope(t):   # [heads, hd]
+        z = torch.complex(t[:, :half], t[:, half:]) * rot
+        return torch.cat([z.real, z.imag], -1)
+
+    x = D(w["embed"][tok])
+    for li, lw in enumerate(w["layers"]):
+        xn = F.rms_norm(x, (H,), D(lw["in_norm"]), eps=cfg["eps"])
+        qkv = D(dequant(lw["qkv_w"], lw["qkv_s"], H, gs)) @ xn
+        if lw.get("qkv_b") is not None:
+            qkv = qkv + D(lw["qkv_b"])
+        q = rope(qkv[:hq * hd].reshape(hq, hd))
+        k = rope(qkv[hq * hd:(hq + hkv) * hd].reshape(hkv, hd))
+        v = qkv[(hq + hkv) * hd:].reshape(hkv, hd)
+        kc, vc = kv[li]
+        kc[:, pos] = k
+        vc[:, pos] = v
+        att = F.scaled_dot_product_attention(q[None, :, None], kc[None, :, :pos + 1],
+                                             vc[None, :, :pos + 1], enable_gqa=True)[0, :, 0]
+        x = x + D(dequant(lw["o_w"], lw["o_s"], hq * hd, gs)) @ att.reshape(-1)
+        xn = F.rms_norm(x, (H,), D(lw["post_norm"]), eps=cfg["eps"])
+        h = F.silu(D(dequant(lw["gate_w"], lw["gate_s"], H, gs)) @ xn) * \
+            (D(dequant(lw["up_w"], lw["up_s"], H, gs)) @ xn)
+        x = x + D(dequant(lw["down_w"], lw["down_s"], cfg["intermediate"], gs)) @ h
+    xn = F.rms_norm(x, (H,), D(w["final_norm"]), eps=cfg["eps"])
+    return (D(dequant(w["lm_head_w"], w["lm_head_s"], H, gs)) @ xn).numpy()
+
+
+def test_decoder_step_vs_torch_float64():
+    cfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
+               head_dim=32 * 2, vocab=300, eps=1e-6, rope_theta=1e6, qkv_bias=True)
+    gs, max_seq, pre = 32, 24, 9
+    w = synth.decoder_weights(cfg, 21, 4, 4, gs)
+    ocfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
+                head_dim=64, vocab=300, group_size=gs, max_seq=max_seq, rope_theta=1e6,
+                eps=1e-6, wkind=4, lmkind=4)
+    dec = O.Decoder(w, ocfg)
+    kvp = synth.kv_prefill(cfg, 21, pre, max_seq)
+    tkv = []
+    for li, (k, v) in enumerate(kvp):
+        dec.copy_kv(li, k, v, pre)
+        tkv.append((torch.from_numpy(k.astype(np.float64)), torch.from_numpy(v.astype(np.float64))))
+    tok = 17
+    for step in range(4):
+        pos = pre + step
+        lo = dec.step(tok, pos)
+        lt = torch_step(w, cfg, tkv, tok, pos, gs)
+        assert rel(lo, lt) < 1e-5, f"step {step}"
+        assert O.argmax(lo) == int(np.argmax(lt))
+        tok = O.argmax(lo)
+    assert dec.kv_len() == pre + 4
+    # out-of-range token / position -> zeroed logits (decoder.rs:1066-1089)
+    assert not dec.step(300, 3).any() and not dec.step(1, max_seq).any()
+    dec.close()

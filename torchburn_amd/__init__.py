@@ -6,18 +6,25 @@ Python operator API (python/torchburn/quantization.py): same names, argument
 meaning and error behaviour.
 """
 from ._lib import UnsupportedOpError
+from .decoder import RustQwenDecoder, create_rust_qwen_decoder
 from .quantization import (
     QuantizedLinear,
     fused_swiglu_mlp,
     fused_swiglu_mlp_w4a32,
+    fused_swiglu_mlp_w8a32,
     quantize_model,
     quantize_weight_int4_grouped,
     quantize_weight_int8,
     w4a32_grouped_linear,
     w4a32_grouped_linear_residual,
+    w8a32_linear,
 )
 
 __all__ = [
+    "RustQwenDecoder",
+    "create_rust_qwen_decoder",
+    "fused_swiglu_mlp_w8a32",
+    "w8a32_linear",
     "UnsupportedOpError",
     "QuantizedLinear",
     "fused_swiglu_mlp",

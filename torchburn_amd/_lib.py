@@ -41,6 +41,8 @@ _SIGS = {
     "tb_w4a32_grouped_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "tb_swiglu_w4a32": [_p] * 8 + [_i64] * 4 + [_p],
     "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
+    "tb_w8a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
+    "tb_fused_swiglu_mlp_w8a32": [_p] * 12 + [_i64] * 4 + [_p],
 }
 
 

@@ -10,6 +10,7 @@
 #include <string>
 #include <vector>
 
+#include "gemv_dense.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
 
@@ -119,6 +120,34 @@ static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
     return TB_OK;
 }
 
+static int check_w8(const float *x, const int8_t *w, const float *s, int64_t s_len, int64_t m,
+                    int64_t n, int64_t k, const char *what) {
+    const std::string op(what);
+    TB_REQUIRE(x && w && s, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": null pointer");
+    TB_REQUIRE(m >= 0 && n >= 0 && k > 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": negative or empty dimension");
+    TB_REQUIRE(s_len == 1 || s_len == n, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": scales must have 1 or N elements");
+    TB_REQUIRE(k % 32 == 0 && k <= (1 << 20) && n < (1ll << 31), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": K must be a multiple of 32");
+    TB_REQUIRE(aligned(x, 16) && aligned(w, 16), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": x and w must be 16-byte aligned device pointers");
+    return TB_OK;
+}
+
+static int dense_rows(DenseParams p, int wt, int epi, int64_t m, hipStream_t st) {
+    for (int64_t r0 = 0; r0 < m; r0 += kMaxRowsPerPass) {
+        DenseParams q = p;
+        q.m = (int)((m - r0) < kMaxRowsPerPass ? (m - r0) : kMaxRowsPerPass);
+        q.x = p.x + r0 * p.k;
+        q.y = p.y + r0 * (int64_t)p.n;
+        if (p.res) q.res = p.res + r0 * (int64_t)p.n;
+        int rc = dense_gemv(q, wt, epi, st);
+        if (rc) return rc;
+    }
+    return TB_OK;
+}
+
 }  // namespace tb
 
 using namespace tb;
@@ -214,6 +243,49 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
         return w4_rows(d, EPI_RESID, m, hq, true, st);
     }
     return w4_rows(d, EPI_PLAIN, m, hq, true, st);
+}
+
+int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_t s_len,
+                    const float *bias, float *out, int64_t m, int64_t n, int64_t k,
+                    void *stream) {
+    int rc = check_w8(x, w, scales, s_len, m, n, k, "w8a32_linear");
+    if (rc) return rc;
+    TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w8a32_linear: null output");
+    if (m == 0 || n == 0) return TB_OK;
+    DenseParams p{};
+    p.x = x; p.w0 = w; p.rs0 = scales; p.rs0_len = (int)s_len; p.b0 = bias; p.y = out;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k;
+    return dense_rows(p, W_I8, EPI_PLAIN, m, (hipStream_t)stream);
+}
+
+int tb_fused_swiglu_mlp_w8a32(const float *x, const int8_t *gate_w, const float *gate_s,
+                              const float *gate_b, const int8_t *up_w, const float *up_s,
+                              const float *up_b, const int8_t *down_w, const float *down_s,
+                              const float *down_b, const float *residual, float *out,
+                              int64_t m, int64_t k, int64_t inter, int64_t n_out,
+                              void *stream) {
+    int rc = check_w8(x, gate_w, gate_s, inter, m, inter, k, "fused_swiglu_mlp_w8a32");
+    if (rc) return rc;
+    rc = check_w8(x, up_w, up_s, inter, m, inter, k, "fused_swiglu_mlp_w8a32");
+    if (rc) return rc;
+    TB_REQUIRE(down_w && down_s && out && inter % 32 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused_swiglu_mlp_w8a32: bad down projection or output");
+    if (m == 0 || n_out == 0) return TB_OK;
+    void *ws = nullptr;
+    rc = workspace((size_t)m * (size_t)inter * sizeof(float), &ws);
+    if (rc) return rc;
+    float *h = static_cast<float *>(ws);
+    hipStream_t st = (hipStream_t)stream;
+    DenseParams p{};
+    p.x = x; p.w0 = gate_w; p.rs0 = gate_s; p.rs0_len = (int)inter; p.b0 = gate_b;
+    p.w1 = up_w; p.rs1 = up_s; p.rs1_len = (int)inter; p.b1 = up_b;
+    p.y = h; p.m = (int)m; p.n = (int)inter; p.k = (int)k;
+    rc = dense_rows(p, W_I8, EPI_SWIGLU, m, st);
+    if (rc) return rc;
+    DenseParams d{};
+    d.x = h; d.w0 = down_w; d.rs0 = down_s; d.rs0_len = (int)n_out; d.b0 = down_b;
+    d.res = residual; d.y = out; d.m = (int)m; d.n = (int)n_out; d.k = (int)inter;
+    return dense_rows(d, W_I8, residual ? EPI_RESID : EPI_PLAIN, m, st);
 }
 
 }  // extern "C"

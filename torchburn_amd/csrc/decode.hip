@@ -1,0 +1,400 @@
+// Single-token decoder-step kernels for gfx950: everything in the reference's
+// RustQwenDecoder::step_internal (src/llm/decoder.rs:1051-1374) except the
+// GEMVs (w4_gemv.hip, gemv_dense.hip).
+//
+// All kernels read the token id and position from a small device state block
+// (DecState), so one captured hipGraph serves every step, and the greedy argmax
+// writes the next token and advances the position on the device.
+#include <float.h>
+
+#include "decode.hpp"
+#include "gemv_common.hpp"
+#include "tb_common.hpp"
+
+namespace tb {
+
+using namespace gemv;
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Block-wide sum; every thread gets the total.  `scratch` holds >= 16 floats.
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_sum(v);
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < nw; ++w) t += scratch[w];
+    __syncthreads();
+    return t;
+}
+
+// x = embed[token] (when embed != null), then
+//   xn = (x * (1 / sqrt(sum(x^2) / H + eps))) * w
+// (fast_rms_norm, src/quantization/fused_ops.rs:1066-1089; the AVX-512 tier's
+// x * inv_rms * w order), and the chunk records of xn for the next INT4 GEMV.
+// One block; H <= kMaxHidden.
+__global__ __launch_bounds__(1024) void k_rmsnorm(const DecState *__restrict__ st,
+                                                  const float *__restrict__ embed,
+                                                  float *__restrict__ x,
+                                                  const float *__restrict__ w,
+                                                  float *__restrict__ xn,
+                                                  uint32_t *__restrict__ xq, int H, float eps) {
+    __shared__ float sxn[kMaxHidden];
+    __shared__ float scratch[16];
+    const int tid = threadIdx.x;
+    float ss = 0.f;
+    if (embed) {
+        const float *e = embed + (size_t)st->token * H;
+        for (int i = tid; i < H; i += blockDim.x) {
+            const float v = e[i];
+            x[i] = v;
+            sxn[i] = v;
+            ss = fmaf(v, v, ss);
+        }
+    } else {
+        for (int i = tid; i < H; i += blockDim.x) {
+            const float v = x[i];
+            sxn[i] = v;
+            ss = fmaf(v, v, ss);
+        }
+    }
+    const float tot = block_sum(ss, scratch);
+    const float rms = sqrtf(tot / (float)H + eps);
+    const float inv = 1.0f / rms;
+    for (int i = tid; i < H; i += blockDim.x) {
+        const float v = __fmul_rn(__fmul_rn(sxn[i], inv), w[i]);
+        sxn[i] = v;
+        xn[i] = v;
+    }
+    __syncthreads();
+    if (xq) {
+        const int c = H / 32;
+        for (int base = 0; base < c * 8; base += blockDim.x) {
+            const int t = base + tid;
+            const int rec = t >> 3, sub = t & 7;
+            const bool live = rec < c;
+            const float4 v = live ? reinterpret_cast<const float4 *>(sxn + rec * 32)[sub]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            build_xrec8(v, sub, live, xq + (size_t)rec * kXRecDwords);
+        }
+    }
+}
+
+// Rotate-half RoPE on the q and k heads of qkv and the KV-cache append at the
+// current position (src/llm/decoder.rs:28-68, 1115-1146):
+//   x1' = x1*c1 - x2*s1,  x2' = x2*c2 + x1*s2   (products rounded separately)
+// Block b < hq rotates q head b in place; hq <= b < hq+hkv rotates k head
+// b - hq into the cache; the rest copy v heads.  blockDim = hd / 2.
+__global__ void k_rope_kv(const DecState *__restrict__ st, float *__restrict__ qkv,
+                          const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                          float *__restrict__ kc, float *__restrict__ vc, int hq, int hkv, int hd,
+                          int max_seq) {
+    const int b = blockIdx.x, i = threadIdx.x, half = hd / 2;
+    const int pos = st->pos;
+    const float *cp = cos_t + (size_t)pos * hd, *sp = sin_t + (size_t)pos * hd;
+    if (b < hq + hkv) {
+        float *head = qkv + (size_t)b * hd;
+        const float x1 = head[i], x2 = head[i + half];
+        const float o1 = __fsub_rn(__fmul_rn(x1, cp[i]), __fmul_rn(x2, sp[i]));
+        const float o2 = __fadd_rn(__fmul_rn(x2, cp[i + half]), __fmul_rn(x1, sp[i + half]));
+        if (b < hq) {
+            head[i] = o1;
+            head[i + half] = o2;
+        } else {
+            float *dst = kc + ((size_t)(b - hq) * max_seq + pos) * hd;
+            dst[i] = o1;
+            dst[i + half] = o2;
+        }
+    } else {
+        const int h = b - hq - hkv;
+        const float *src = qkv + (size_t)(hq + hkv + h) * hd;
+        float *dst = vc + ((size_t)h * max_seq + pos) * hd;
+        dst[i] = src[i];
+        dst[i + half] = src[i + half];
+    }
+}
+
+// Split-KV decode attention (flash-decoding), one block per (kv head, tile of
+// kAttnTile positions), all G = hq/hkv query heads of the group together so
+// each K/V row is read from HBM once.  The tile of K and V is staged through
+// LDS; scores s = (q . k_t) * (1/sqrt(hd)); per head the tile's max m, the sum
+// l = sum exp(s - m) and o = sum exp(s - m) v_t go to `part`, combined across
+// tiles by k_attn_combine (the online-softmax merge).  Math of the reference:
+// src/llm/decoder.rs:1148-1213.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_split(const DecState *__restrict__ st,
+                                                    const float *__restrict__ qkv,
+                                                    const float *__restrict__ kc,
+                                                    const float *__restrict__ vc,
+                                                    float *__restrict__ part, int hq, int hkv,
+                                                    int max_seq, int nsplit, float scale) {
+    constexpr int T = kAttnTile, KP = HD + 4;
+    extern __shared__ float sm[];
+    const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
+    const int G = hq / hkv;
+    const int seq = st->pos + 1;
+    const int t0 = sp * T;
+    float *sq = sm;                 // [G][HD]
+    float *sk = sq + G * HD;        // [T][KP]
+    float *sv = sk + T * KP;        // [T][HD]
+    float *ss = sv + T * HD;        // [G][T]
+    float *sml = ss + G * T;        // [G][2]
+    const size_t rec = HD + 2;
+    if (t0 >= seq) {   // empty tile: neutral element of the merge
+        for (int i = tid; i < G * (HD + 2); i += blockDim.x) {
+            const int g = i / (HD + 2), d = i - g * (HD + 2);
+            part[((size_t)(kvh * G + g) * nsplit + sp) * rec + d] = d == HD ? -FLT_MAX : 0.f;
+        }
+        return;
+    }
+    const int tn = min(T, seq - t0);
+    for (int i = tid; i < G * HD; i += blockDim.x) sq[i] = qkv[(size_t)kvh * G * HD + i];
+    const float4 *kb = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + t0) * HD);
+    const float4 *vb = reinterpret_cast<const float4 *>(vc + ((size_t)kvh * max_seq + t0) * HD);
+    for (int i = tid; i < tn * (HD / 4); i += blockDim.x) {
+        const int r = i / (HD / 4), c = i - r * (HD / 4);
+        *reinterpret_cast<float4 *>(sk + r * KP + 4 * c) = kb[i];
+        *reinterpret_cast<float4 *>(sv + r * HD + 4 * c) = vb[i];
+    }
+    __syncthreads();
+    for (int i = tid; i < G * T; i += blockDim.x) {
+        const int g = i / T, t = i - g * T;
+        float s = -FLT_MAX;
+        if (t < tn) {
+            const float4 *qa = reinterpret_cast<const float4 *>(sq + g * HD);
+            const float4 *ka = reinterpret_cast<const float4 *>(sk + t * KP);
+            float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+            for (int c = 0; c < HD / 4; c += 2) {
+                const float4 a = qa[c], b = ka[c], a2 = qa[c + 1], b2 = ka[c + 1];
+                d0 = fmaf(a.x, b.x, fmaf(a.y, b.y, fmaf(a.z, b.z, fmaf(a.w, b.w, d0))));
+                d1 = fmaf(a2.x, b2.x, fmaf(a2.y, b2.y, fmaf(a2.z, b2.z, fmaf(a2.w, b2.w, d1))));
+            }
+            s = (d0 + d1) * scale;
+        }
+        ss[i] = s;
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    for (int g = wave; g < G; g += nw) {
+        const float s = ss[g * T + lane];
+        const float m = wave_max(s);
+        const float p = lane < tn ? expf(s - m) : 0.f;
+        const float l = wave_sum(p);
+        ss[g * T + lane] = p;
+        if (lane == 0) {
+            sml[2 * g] = m;
+            sml[2 * g + 1] = l;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < G * HD; i += blockDim.x) {
+        const int g = i / HD, d = i - g * HD;
+        const float *pg = ss + g * T;
+        float a0 = 0.f, a1 = 0.f;
+        int t = 0;
+        for (; t + 1 < tn; t += 2) {
+            a0 = fmaf(pg[t], sv[t * HD + d], a0);
+            a1 = fmaf(pg[t + 1], sv[(t + 1) * HD + d], a1);
+        }
+        if (t < tn) a0 = fmaf(pg[t], sv[t * HD + d], a0);
+        float *o = part + ((size_t)(kvh * G + g) * nsplit + sp) * rec;
+        o[d] = a0 + a1;
+        if (d == 0) {
+            o[HD] = sml[2 * g];
+            o[HD + 1] = sml[2 * g + 1];
+        }
+    }
+}
+
+// Merge of the per-tile partials of one query head:
+//   M = max m_s,  L = sum_s e^(m_s - M) l_s,  o = sum_s e^(m_s - M) o_s / L
+// then the chunk records of the head's output for the O-projection GEMV.
+// blockDim = hd.
+__global__ void k_attn_combine(const DecState *__restrict__ st, const float *__restrict__ part,
+                               float *__restrict__ out, uint32_t *__restrict__ xq, int hd,
+                               int nsplit) {
+    extern __shared__ float sm[];
+    float *so = sm;            // [hd]
+    float *sw = sm + hd;       // [nsplit] tile weights
+    const int h = blockIdx.x, d = threadIdx.x;
+    const size_t rec = hd + 2;
+    const float *ph = part + (size_t)h * nsplit * rec;
+    const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;   // tiles holding positions
+    float M = -FLT_MAX;
+    for (int s = 0; s < used; ++s) M = fmaxf(M, ph[s * rec + hd]);
+    for (int s = d; s < used; s += blockDim.x) sw[s] = expf(ph[s * rec + hd] - M);
+    __syncthreads();
+    float L = 0.f, acc = 0.f;
+    for (int s = 0; s < used; ++s) {
+        const float wgt = sw[s];
+        L = fmaf(wgt, ph[s * rec + hd + 1], L);
+        acc = fmaf(wgt, ph[s * rec + d], acc);
+    }
+    const float v = acc * (1.0f / fmaxf(L, 1e-30f));
+    out[(size_t)h * hd + d] = v;
+    so[d] = v;
+    __syncthreads();
+    if (xq) {
+        const int c = hd / 32;
+        const int t = threadIdx.x, rc = t >> 3, sub = t & 7;
+        if (rc < c || (t >> 3) < (int)(blockDim.x >> 3)) {
+            const bool live = rc < c;
+            const float4 vv = live ? reinterpret_cast<const float4 *>(so + rc * 32)[sub]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            build_xrec8(vv, sub, live, xq + ((size_t)h * c + rc) * kXRecDwords);
+        }
+    }
+}
+
+// Greedy argmax, stage 1: per block the largest logit, lowest index on ties
+// (the reference's strict `>` scan, src/llm/decoder.rs:914-925).  NaN at index 0
+// wins outright (the scan never replaces a NaN best); NaN elsewhere never wins.
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const float *__restrict__ logits, int n,
+                                                        float *__restrict__ pv,
+                                                        int *__restrict__ pi) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float v = logits[i];
+        if (__builtin_isnan(v)) v = (i == 0) ? INFINITY : -INFINITY;
+        better(bv, bi, v, i);
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            float v = sv[threadIdx.x + s];
+            int i = si[threadIdx.x + s];
+            float b = sv[threadIdx.x];
+            int j = si[threadIdx.x];
+            better(b, j, v, i);
+            sv[threadIdx.x] = b;
+            si[threadIdx.x] = j;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = sv[0];
+        pi[blockIdx.x] = si[0];
+    }
+}
+
+// Stage 2: final argmax, then the greedy loop's state update on the device:
+// history[step] = token; token = argmax; pos += 1; step += 1.
+__global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ pv,
+                                                      const int *__restrict__ pi, int nb, int n,
+                                                      DecState *__restrict__ st,
+                                                      int *__restrict__ history, int hist_cap) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) better(bv, bi, pv[i], pi[i]);
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            float b = sv[threadIdx.x];
+            int j = si[threadIdx.x];
+            better(b, j, sv[threadIdx.x + s], si[threadIdx.x + s]);
+            sv[threadIdx.x] = b;
+            si[threadIdx.x] = j;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        int tok = si[0];
+        if (tok < 0 || tok >= n) tok = 0;
+        const int step = st->step;
+        if (history && step < hist_cap) history[step] = tok;
+        st->argmax = tok;
+        st->token = tok;
+        st->pos = st->pos + 1;
+        st->step = step + 1;
+    }
+}
+
+}  // namespace
+
+int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
+                   uint32_t *xq, int H, float eps, hipStream_t s) {
+    TB_REQUIRE(H <= kMaxHidden && H % 32 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: hidden size must be a multiple of 32 and <= " +
+                   std::to_string(kMaxHidden));
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, s, st, embed, x, w, xn, xq, H, eps);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_rope_kv(const DecState *st, float *qkv, const float *cos_t, const float *sin_t,
+                   float *kc, float *vc, int hq, int hkv, int hd, int max_seq, hipStream_t s) {
+    hipLaunchKernelGGL(k_rope_kv, dim3(hq + 2 * hkv), dim3(hd / 2), 0, s, st, qkv, cos_t, sin_t,
+                       kc, vc, hq, hkv, hd, max_seq);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int attn_nsplit(int max_seq) { return (max_seq + kAttnTile - 1) / kAttnTile; }
+
+int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
+                     float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
+                     hipStream_t s) {
+    const int ns = attn_nsplit(max_seq);
+    const int G = hq / hkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (hd == 128) {
+        const size_t lds = sizeof(float) * (G * 128 + kAttnTile * 132 + kAttnTile * 128 +
+                                            G * kAttnTile + 2 * G);
+        hipLaunchKernelGGL(k_attn_split<128>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc,
+                           part, hq, hkv, max_seq, ns, scale);
+    } else if (hd == 64) {
+        const size_t lds = sizeof(float) * (G * 64 + kAttnTile * 68 + kAttnTile * 64 +
+                                            G * kAttnTile + 2 * G);
+        hipLaunchKernelGGL(k_attn_split<64>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc,
+                           part, hq, hkv, max_seq, ns, scale);
+    } else {
+        return fail(TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: head_dim must be 64 or 128");
+    }
+    TB_LAUNCHED();
+    hipLaunchKernelGGL(k_attn_combine, dim3(hq), dim3(hd), sizeof(float) * (hd + ns), s, st, part,
+                       out, xq, hd, ns);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_argmax(const float *logits, int n, float *pv, int *pi, DecState *st, int *history,
+                  int hist_cap, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_partial, dim3(kArgmaxBlocks), dim3(256), 0, s, logits, n, pv, pi);
+    TB_LAUNCHED();
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, pv, pi, kArgmaxBlocks, n, st,
+                       history, hist_cap);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+}  // namespace tb

@@ -1,0 +1,33 @@
+// Launchers of the decoder-step kernels (decode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tb {
+
+// Device-resident step state: every step kernel reads token / pos from here,
+// and the greedy argmax writes the next token and advances pos and step.
+struct DecState {
+    int token;    // input token of the step
+    int pos;      // its position (offset); the step attends over 0..pos
+    int step;     // index into the greedy history
+    int argmax;   // argmax of the last step's logits
+};
+
+constexpr int kMaxHidden = 8192;   // RMSNorm keeps one hidden vector in LDS
+constexpr int kAttnTile = 64;      // KV positions per attention block
+constexpr int kArgmaxBlocks = 256;
+
+int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
+                   uint32_t *xq, int H, float eps, hipStream_t s);
+int launch_rope_kv(const DecState *st, float *qkv, const float *cos_t, const float *sin_t,
+                   float *kc, float *vc, int hq, int hkv, int hd, int max_seq, hipStream_t s);
+int attn_nsplit(int max_seq);
+int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
+                     float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
+                     hipStream_t s);
+int launch_argmax(const float *logits, int n, float *pv, int *pi, DecState *st, int *history,
+                  int hist_cap, hipStream_t s);
+
+}  // namespace tb

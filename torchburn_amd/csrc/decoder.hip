@@ -1,0 +1,621 @@
+// The decoder handle: device-resident weights, KV cache and RoPE tables, and one
+// captured hipGraph per token step.
+//
+// Replaces RustQwenDecoder (reference src/llm/decoder.rs:176-1374): `new`
+// (193-424) -> tb_decoder_create / tb_decoder_set_layer, `step_internal`
+// (1051-1374) -> the captured step, `decode_step` / `decode_and_sample` /
+// `generate_loop` / `prefill_tokens` / `reset_kv_cache` /
+// `copy_kv_cache_from_tensors` / `kv_len` / `get_logits` -> the tb_decoder_*
+// entry points below.
+//
+// Step = embed -> L x [RMSNorm(+x records) -> QKV GEMV(+bias) -> RoPE + KV
+// append -> split-KV attention (+x records) -> O GEMV (+residual) -> RMSNorm
+// -> gate/up GEMV with silu*up -> x records of h -> down GEMV (+residual)] ->
+// final RMSNorm -> lm_head GEMV -> device argmax.  Token and position live in a
+// device state block, so the same graph replays for every step and a greedy
+// generation runs without host round trips.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "decode.hpp"
+#include "gemv_dense.hpp"
+#include "tb_common.hpp"
+#include "w4_gemv.hpp"
+
+struct tb_decoder;
+
+namespace tb {
+
+namespace {
+
+struct Layer {
+    float *in_norm = nullptr, *post_norm = nullptr;
+    void *qkv_w = nullptr, *o_w = nullptr, *gate_w = nullptr, *up_w = nullptr, *down_w = nullptr;
+    float *qkv_s = nullptr, *o_s = nullptr, *gate_s = nullptr, *up_s = nullptr, *down_s = nullptr;
+    float *qkv_b = nullptr;
+    bool set = false;
+};
+
+int gshift(int64_t gs) { return gs == 32 ? 5 : 6; }
+
+}  // namespace
+
+struct Decoder {
+    tb_decoder_config cfg{};
+    int H = 0, I = 0, hq = 0, hkv = 0, hd = 0, V = 0, L = 0, max_seq = 0, tq = 0, nsplit = 0;
+    int wbits = 4, lmbits = 4, gs = 32;
+    float eps = 1e-6f;
+    int device = 0;
+    hipStream_t st = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::vector<void *> allocs;
+    std::vector<Layer> layers;
+    float *embed = nullptr, *final_norm = nullptr;
+    void *lm_w = nullptr;
+    float *lm_s = nullptr;
+    float *kc = nullptr, *vc = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *attn = nullptr, *h = nullptr;
+    float *logits = nullptr, *part = nullptr, *am_v = nullptr;
+    int *am_i = nullptr, *history = nullptr;
+    uint32_t *xq_h = nullptr, *xq_a = nullptr, *xq_i = nullptr;
+    DecState *state = nullptr;    // device
+    DecState *hstate = nullptr;   // pinned host staging
+    int hist_cap = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int64_t kv_used = 0;
+    std::vector<float> host_logits;
+    std::mt19937_64 rng{0x7B};
+
+    ~Decoder() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (st) (void)hipStreamSynchronize(st);
+        for (void *p : allocs) (void)hipFree(p);
+        if (hstate) (void)hipHostFree(hstate);
+        if (ev0) (void)hipEventDestroy(ev0);
+        if (ev1) (void)hipEventDestroy(ev1);
+        if (st) (void)hipStreamDestroy(st);
+    }
+
+    template <class T>
+    int alloc(T **p, size_t bytes) {
+        void *q = nullptr;
+        hipError_t e = hipMalloc(&q, bytes < 256 ? 256 : bytes);
+        if (e != hipSuccess)
+            return fail(e == hipErrorOutOfMemory ? TB_ERR_MEMORY : TB_ERR_HIP,
+                        "Out of memory allocating " + std::to_string(bytes >> 20) +
+                            " MB for the decoder on the GPU: " + hipGetErrorString(e));
+        allocs.push_back(q);
+        *p = static_cast<T *>(q);
+        return TB_OK;
+    }
+
+    // Device copy of a caller buffer (host or device memory).
+    template <class T>
+    int upload(T **dst, const void *src, size_t bytes) {
+        int rc = alloc(dst, bytes);
+        if (rc) return rc;
+        TB_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyDefault));
+        return TB_OK;
+    }
+
+    size_t wbytes(int bits, int64_t n, int64_t k) const {
+        return bits == 4 ? (size_t)n * (size_t)((k + 1) / 2)
+                         : (size_t)n * (size_t)k * (bits == 8 ? 1 : 4);
+    }
+    size_t sbytes(int bits, int64_t n, int64_t k) const {
+        return bits == 4 ? (size_t)n * (size_t)(k / gs) * 4 : (bits == 8 ? (size_t)n * 4 : 0);
+    }
+
+    // One projection y = W x [+ bias] [+ residual] or the gate/up pair.
+    int proj(int bits, const float *xin, const uint32_t *xq, const void *w, const float *s,
+             const float *b, const void *w2, const float *s2, const float *res, float *y,
+             int n, int k, int epi) {
+        if (bits == 4) {
+            W4Params p{};
+            p.x = xin; p.xq = xq;
+            p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
+            p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
+            p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k; p.gshift = gshift(gs);
+            return w4_gemv(p, epi, st);
+        }
+        DenseParams p{};
+        p.x = xin; p.w0 = w; p.rs0 = s; p.rs0_len = s ? n : 0; p.b0 = b;
+        p.w1 = w2; p.rs1 = s2; p.rs1_len = s2 ? n : 0;
+        p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k;
+        return dense_gemv(p, bits == 8 ? W_I8 : W_F32, epi, st);
+    }
+
+    // Enqueues one decoder step (reference step_internal) on `st`.
+    int enqueue_step() {
+        const bool q4 = wbits == 4;
+        int rc;
+        for (int l = 0; l < L; ++l) {
+            const Layer &y = layers[l];
+            float *kcl = kc + (size_t)l * hkv * max_seq * hd;
+            float *vcl = vc + (size_t)l * hkv * max_seq * hd;
+            rc = launch_rmsnorm(state, l == 0 ? embed : nullptr, x, y.in_norm, xn,
+                                q4 ? xq_h : nullptr, H, eps, st);
+            if (rc) return rc;
+            rc = proj(wbits, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv,
+                      tq, H, EPI_PLAIN);
+            if (rc) return rc;
+            rc = launch_rope_kv(state, qkv, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, st);
+            if (rc) return rc;
+            rc = launch_attention(state, qkv, kcl, vcl, part, attn, q4 ? xq_a : nullptr, hq, hkv,
+                                  hd, max_seq, st);
+            if (rc) return rc;
+            rc = proj(wbits, attn, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H,
+                      hq * hd, EPI_RESID);
+            if (rc) return rc;
+            rc = launch_rmsnorm(state, nullptr, x, y.post_norm, xn, q4 ? xq_h : nullptr, H, eps,
+                                st);
+            if (rc) return rc;
+            rc = proj(wbits, xn, xq_h, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, h, I,
+                      H, EPI_SWIGLU);
+            if (rc) return rc;
+            if (q4) {
+                rc = xquant(h, xq_i, 1, I, st);
+                if (rc) return rc;
+            }
+            rc = proj(wbits, h, xq_i, y.down_w, y.down_s, nullptr, nullptr, nullptr, x, x, H, I,
+                      EPI_RESID);
+            if (rc) return rc;
+        }
+        rc = launch_rmsnorm(state, nullptr, x, final_norm, xn, lmbits == 4 ? xq_h : nullptr, H,
+                            eps, st);
+        if (rc) return rc;
+        rc = proj(lmbits, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V, H,
+                  EPI_PLAIN);
+        if (rc) return rc;
+        return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
+    }
+
+    int ensure_graph() {
+        if (exec) return TB_OK;
+        for (int l = 0; l < L; ++l)
+            TB_REQUIRE(layers[l].set, TB_ERR_VALUE,
+                       "decoder layer " + std::to_string(l) + " was never set");
+        TB_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_step();
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return fail(TB_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+        graph = g;
+        TB_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        return TB_OK;
+    }
+
+    int set_state(int token, int pos) {
+        hstate->token = token;
+        hstate->pos = pos;
+        hstate->step = 0;
+        hstate->argmax = 0;
+        TB_HIP(hipMemcpyAsync(state, hstate, sizeof(DecState), hipMemcpyHostToDevice, st));
+        return TB_OK;
+    }
+
+    bool in_range(int64_t token, int64_t pos) const {
+        return token >= 0 && token < V && pos >= 0 && pos < max_seq;
+    }
+
+    // One step; out-of-range token or position gives zero logits and touches
+    // nothing else (decoder.rs:1066-1089).
+    int step(int64_t token, int64_t pos, bool want_logits, int64_t *argmax) {
+        int rc = ensure_graph();
+        if (rc) return rc;
+        if (!in_range(token, pos)) {
+            TB_HIP(hipMemsetAsync(logits, 0, (size_t)V * 4, st));
+            TB_HIP(hipStreamSynchronize(st));
+            if (want_logits) std::fill(host_logits.begin(), host_logits.end(), 0.f);
+            if (argmax) *argmax = 0;
+            return TB_OK;
+        }
+        kv_used = std::max<int64_t>(kv_used, pos + 1);
+        rc = set_state((int)token, (int)pos);
+        if (rc) return rc;
+        TB_HIP(hipGraphLaunch(exec, st));
+        if (want_logits)
+            TB_HIP(hipMemcpyAsync(host_logits.data(), logits, (size_t)V * 4, hipMemcpyDeviceToHost,
+                                  st));
+        if (argmax) TB_HIP(hipMemcpyAsync(hstate, state, sizeof(DecState), hipMemcpyDeviceToHost, st));
+        TB_HIP(hipStreamSynchronize(st));
+        if (argmax) *argmax = hstate->argmax;
+        return TB_OK;
+    }
+};
+
+// Repetition penalty (src/llm/decoder.rs:878-899): each distinct recent token's
+// logit is divided by the penalty when positive, multiplied when not.
+static void repetition_penalty(std::vector<float> &lg, const int64_t *recent, int64_t n,
+                               float penalty) {
+    if (penalty <= 1.0f || n <= 0) return;
+    std::vector<int64_t> seen;
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t t = recent[i];
+        if (t < 0 || t >= (int64_t)lg.size()) continue;
+        if (std::find(seen.begin(), seen.end(), t) != seen.end()) continue;
+        seen.push_back(t);
+        const float l = lg[t];
+        lg[t] = l > 0.f ? l / penalty : l * penalty;
+    }
+}
+
+// Sampling of src/llm/decoder.rs:908-1020: greedy (strict >, lowest index) when
+// temperature is not finite or <= 0 or top_k == 1; otherwise the top-k
+// candidates (non-finite logits as -inf), softmax at `temperature`, optional
+// nucleus cut at top_p, then one multinomial draw.  The reference draws from
+// rand::random (unseeded); this draws from the decoder's seeded generator.
+static int64_t sample(const std::vector<float> &lg, float temperature, int64_t top_k, float top_p,
+                      std::mt19937_64 &rng) {
+    const int64_t V = (int64_t)lg.size();
+    if (V == 0) return 0;
+    if (!std::isfinite(temperature) || temperature <= 0.f || top_k == 1) {
+        int64_t bi = 0;
+        float bv = lg[0];
+        for (int64_t i = 1; i < V; ++i)
+            if (lg[i] > bv) {
+                bv = lg[i];
+                bi = i;
+            }
+        return bi;
+    }
+    const int64_t k = std::max<int64_t>(1, std::min<int64_t>(top_k, V));
+    std::vector<std::pair<int64_t, float>> items((size_t)V);
+    for (int64_t i = 0; i < V; ++i) items[i] = {i, std::isfinite(lg[i]) ? lg[i] : -INFINITY};
+    std::partial_sort(items.begin(), items.begin() + k, items.end(),
+                      [](const auto &a, const auto &b) { return a.second > b.second; });
+    items.resize((size_t)k);
+    const float mx = items[0].second;
+    const float inv_t = 1.0f / temperature;
+    float sum = 0.f;
+    for (auto &it : items) {
+        it.second = expf((it.second - mx) * inv_t);
+        sum += it.second;
+    }
+    size_t kept = items.size();
+    if (top_p > 0.f && top_p < 1.f && kept > 1 && sum > 0.f) {
+        float cum = 0.f;
+        for (size_t i = 0; i < items.size(); ++i) {
+            if (cum > top_p) {
+                kept = i;
+                break;
+            }
+            cum += items[i].second / sum;
+        }
+    }
+    float ksum = 0.f;
+    for (size_t i = 0; i < kept; ++i) ksum += items[i].second;
+    std::uniform_real_distribution<float> U(0.f, 1.f);
+    const float r = U(rng) * ksum;
+    float acc = 0.f;
+    for (size_t i = 0; i < kept; ++i) {
+        acc += items[i].second;
+        if (acc >= r) return items[i].first;
+    }
+    return items[0].first;
+}
+
+}  // namespace tb
+
+struct tb_decoder : tb::Decoder {};
+
+using namespace tb;
+
+// RoPE tables as the reference builds them (src/llm/decoder.rs:334-350): f64
+// freq = 1 / theta^(2i / hd), angle = pos * freq, cos/sin rounded to f32 and
+// duplicated into both halves of each row.
+static void rope_tables(std::vector<float> &c, std::vector<float> &s, int max_seq, int hd,
+                        double theta) {
+    const int half = hd / 2;
+    c.assign((size_t)max_seq * hd, 0.f);
+    s.assign((size_t)max_seq * hd, 0.f);
+    for (int p = 0; p < max_seq; ++p)
+        for (int i = 0; i < half; ++i) {
+            const double freq = 1.0 / pow(theta, (2.0 * (double)i) / (double)hd);
+            const double v = (double)p * freq;
+            const float cv = (float)cos(v), sv = (float)sin(v);
+            c[(size_t)p * hd + i] = c[(size_t)p * hd + i + half] = cv;
+            s[(size_t)p * hd + i] = s[(size_t)p * hd + i + half] = sv;
+        }
+}
+
+extern "C" {
+
+int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const float *final_norm,
+                      const void *lm_head_w, const float *lm_head_s, tb_decoder **out) {
+    TB_REQUIRE(cfg && out && embed && final_norm && lm_head_w, TB_ERR_VALUE,
+               "tb_decoder_create: null argument");
+    *out = nullptr;
+    const tb_decoder_config &c = *cfg;
+    // Configuration checks of RustQwenDecoder::new (decoder.rs:214-233).
+    TB_REQUIRE(c.hidden_size > 0 && c.hidden_size % 4 == 0, TB_ERR_VALUE,
+               "hidden_size (" + std::to_string(c.hidden_size) + ") must be divisible by 4");
+    TB_REQUIRE(c.group_size == 32 || c.group_size == 64 || c.weight_bits == 8, TB_ERR_VALUE,
+               "group_size must be 32 or 64");
+    TB_REQUIRE(c.weight_bits == 8 || c.hidden_size % c.group_size == 0, TB_ERR_VALUE,
+               "hidden_size (" + std::to_string(c.hidden_size) +
+                   ") must be divisible by group_size (" + std::to_string(c.group_size) + ")");
+    TB_REQUIRE(c.head_dim > 0 && c.head_dim % 2 == 0, TB_ERR_VALUE,
+               "head_dim (" + std::to_string(c.head_dim) + ") must be even");
+    TB_REQUIRE(c.num_kv_heads > 0 && c.num_heads % c.num_kv_heads == 0, TB_ERR_VALUE,
+               "num_heads (" + std::to_string(c.num_heads) +
+                   ") must be divisible by num_kv_heads (" + std::to_string(c.num_kv_heads) + ")");
+    TB_REQUIRE(c.weight_bits == 4 || c.weight_bits == 8, TB_ERR_VALUE, "weight_bits must be 4 or 8");
+    TB_REQUIRE(c.lm_head_bits == 4 || c.lm_head_bits == 8 || c.lm_head_bits == 32, TB_ERR_VALUE,
+               "lm_head_bits must be 4, 8 or 32");
+    TB_REQUIRE(c.head_dim == 64 || c.head_dim == 128, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: head_dim must be 64 or 128");
+    TB_REQUIRE(c.hidden_size % 32 == 0 && c.intermediate_size % 32 == 0 &&
+                   (c.num_heads * c.head_dim) % 32 == 0,
+               TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: hidden, intermediate and num_heads*head_dim must be multiples of 32");
+    TB_REQUIRE(c.hidden_size <= kMaxHidden, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: hidden_size > " + std::to_string(kMaxHidden));
+    TB_REQUIRE(c.max_seq_len > 0 && c.max_seq_len < (1 << 24) && c.vocab_size > 0 &&
+                   c.num_layers > 0,
+               TB_ERR_VALUE, "max_seq_len, vocab_size and num_layers must be positive");
+
+    auto *d = new (std::nothrow) tb_decoder();
+    TB_REQUIRE(d, TB_ERR_MEMORY, "Out of memory allocating the decoder");
+    d->cfg = c;
+    d->H = (int)c.hidden_size; d->I = (int)c.intermediate_size; d->hq = (int)c.num_heads;
+    d->hkv = (int)c.num_kv_heads; d->hd = (int)c.head_dim; d->V = (int)c.vocab_size;
+    d->L = (int)c.num_layers; d->max_seq = (int)c.max_seq_len; d->gs = (int)c.group_size;
+    d->wbits = c.weight_bits; d->lmbits = c.lm_head_bits; d->eps = (float)c.rms_norm_eps;
+    d->tq = (d->hq + 2 * d->hkv) * d->hd;
+    d->nsplit = attn_nsplit(d->max_seq);
+    d->hist_cap = d->max_seq;
+    d->layers.resize(d->L);
+    d->host_logits.assign(d->V, 0.f);
+    int rc = TB_OK;
+    auto bail = [&](int code) {
+        delete d;
+        return code;
+    };
+    if (hipGetDevice(&d->device) != hipSuccess) return bail(fail(TB_ERR_HIP, "no HIP device"));
+    if (hipStreamCreateWithFlags(&d->st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&d->ev0) != hipSuccess || hipEventCreate(&d->ev1) != hipSuccess)
+        return bail(fail(TB_ERR_HIP, "stream/event creation failed"));
+    if (hipHostMalloc((void **)&d->hstate, sizeof(DecState)) != hipSuccess)
+        return bail(fail(TB_ERR_MEMORY, "pinned host allocation failed"));
+    const size_t kv = (size_t)d->L * d->hkv * d->max_seq * d->hd * sizeof(float);
+    if ((rc = d->upload(&d->embed, embed, (size_t)d->V * d->H * 4)) ||
+        (rc = d->upload(&d->final_norm, final_norm, (size_t)d->H * 4)) ||
+        (rc = d->upload(&d->lm_w, lm_head_w, d->wbytes(d->lmbits, d->V, d->H))) ||
+        (rc = d->alloc(&d->kc, kv)) || (rc = d->alloc(&d->vc, kv)) ||
+        (rc = d->alloc(&d->x, d->H * 4)) || (rc = d->alloc(&d->xn, d->H * 4)) ||
+        (rc = d->alloc(&d->qkv, d->tq * 4)) || (rc = d->alloc(&d->attn, d->hq * d->hd * 4)) ||
+        (rc = d->alloc(&d->h, (size_t)d->I * 4)) || (rc = d->alloc(&d->logits, (size_t)d->V * 4)) ||
+        (rc = d->alloc(&d->part, (size_t)d->hq * d->nsplit * (d->hd + 2) * 4)) ||
+        (rc = d->alloc(&d->am_v, kArgmaxBlocks * 4)) || (rc = d->alloc(&d->am_i, kArgmaxBlocks * 4)) ||
+        (rc = d->alloc(&d->history, (size_t)d->hist_cap * 4)) ||
+        (rc = d->alloc(&d->state, sizeof(DecState))) ||
+        (rc = d->alloc(&d->xq_h, (size_t)(d->H / 32) * kXRecDwords * 4)) ||
+        (rc = d->alloc(&d->xq_a, (size_t)(d->hq * d->hd / 32) * kXRecDwords * 4)) ||
+        (rc = d->alloc(&d->xq_i, (size_t)(d->I / 32) * kXRecDwords * 4)))
+        return bail(rc);
+    if (d->lmbits != 32) {
+        TB_REQUIRE(lm_head_s, TB_ERR_VALUE, "lm_head scales are required for a quantized lm_head");
+        if ((rc = d->upload(&d->lm_s, lm_head_s, d->sbytes(d->lmbits, d->V, d->H)))) return bail(rc);
+    }
+    std::vector<float> ct, stb;
+    rope_tables(ct, stb, d->max_seq, d->hd, c.rope_theta);
+    if ((rc = d->upload(&d->cos_t, ct.data(), ct.size() * 4)) ||
+        (rc = d->upload(&d->sin_t, stb.data(), stb.size() * 4)))
+        return bail(rc);
+    if (hipMemset(d->kc, 0, kv) != hipSuccess || hipMemset(d->vc, 0, kv) != hipSuccess ||
+        hipMemset(d->x, 0, d->H * 4) != hipSuccess)
+        return bail(fail(TB_ERR_HIP, "initial clear failed"));
+    *out = d;
+    return TB_OK;
+}
+
+int tb_decoder_set_layer(tb_decoder *d, int64_t layer, const float *in_norm, const void *qkv_w,
+                         const float *qkv_s, const void *o_w, const float *o_s,
+                         const float *post_norm, const void *gate_w, const float *gate_s,
+                         const void *up_w, const float *up_s, const void *down_w,
+                         const float *down_s, const float *qkv_b) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    TB_REQUIRE(layer >= 0 && layer < d->L, TB_ERR_VALUE, "layer index out of range");
+    TB_REQUIRE(in_norm && qkv_w && qkv_s && o_w && o_s && post_norm && gate_w && gate_s && up_w &&
+                   up_s && down_w && down_s,
+               TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: Each layer requires 12 tensors: input_norm, qkv_w, qkv_s, o_w, "
+               "o_s, post_norm, gate_w, gate_s, up_w, up_s, down_w, down_s");
+    Layer &y = d->layers[layer];
+    TB_REQUIRE(!y.set, TB_ERR_VALUE, "decoder layer " + std::to_string(layer) + " set twice");
+    const int b = d->wbits, H = d->H, I = d->I, qd = d->hq * d->hd;
+    int rc;
+    if ((rc = d->upload(&y.in_norm, in_norm, H * 4)) ||
+        (rc = d->upload(&y.post_norm, post_norm, H * 4)) ||
+        (rc = d->upload(&y.qkv_w, qkv_w, d->wbytes(b, d->tq, H))) ||
+        (rc = d->upload(&y.qkv_s, qkv_s, d->sbytes(b, d->tq, H))) ||
+        (rc = d->upload(&y.o_w, o_w, d->wbytes(b, H, qd))) ||
+        (rc = d->upload(&y.o_s, o_s, d->sbytes(b, H, qd))) ||
+        (rc = d->upload(&y.gate_w, gate_w, d->wbytes(b, I, H))) ||
+        (rc = d->upload(&y.gate_s, gate_s, d->sbytes(b, I, H))) ||
+        (rc = d->upload(&y.up_w, up_w, d->wbytes(b, I, H))) ||
+        (rc = d->upload(&y.up_s, up_s, d->sbytes(b, I, H))) ||
+        (rc = d->upload(&y.down_w, down_w, d->wbytes(b, H, I))) ||
+        (rc = d->upload(&y.down_s, down_s, d->sbytes(b, H, I))))
+        return rc;
+    if (qkv_b && (rc = d->upload(&y.qkv_b, qkv_b, (size_t)d->tq * 4))) return rc;
+    y.set = true;
+    return TB_OK;
+}
+
+int tb_decoder_step(tb_decoder *d, int64_t token, int64_t offset, float *logits_out,
+                    int64_t *argmax_out) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    int rc = d->step(token, offset, logits_out != nullptr, argmax_out);
+    if (rc) return rc;
+    if (logits_out) memcpy(logits_out, d->host_logits.data(), (size_t)d->V * 4);
+    return TB_OK;
+}
+
+int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t offset, float temperature,
+                                 int64_t top_k, float repetition_penalty, const int64_t *recent,
+                                 int64_t n_recent, float top_p, int64_t *token_out) {
+    TB_REQUIRE(d && token_out, TB_ERR_VALUE, "null argument");
+    const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
+    if (greedy && (repetition_penalty <= 1.0f || n_recent <= 0))
+        return d->step(token, offset, false, token_out);
+    int rc = d->step(token, offset, true, nullptr);
+    if (rc) return rc;
+    tb::repetition_penalty(d->host_logits, recent, n_recent, repetition_penalty);
+    *token_out = tb::sample(d->host_logits, temperature, top_k, top_p, d->rng);
+    return TB_OK;
+}
+
+int tb_decoder_generate(tb_decoder *d, int64_t first_token, int64_t seq_len,
+                        int64_t max_new_tokens, int64_t eos_token_id, int64_t *tokens_out,
+                        int64_t *n_out, int64_t *seq_len_out) {
+    TB_REQUIRE(d && tokens_out && n_out && seq_len_out, TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(seq_len >= 0 && max_new_tokens >= 0, TB_ERR_VALUE, "negative length");
+    int rc = d->ensure_graph();
+    if (rc) return rc;
+    // Greedy generate_loop (decoder.rs:788-832): push the token, decode it at
+    // seq_len + generated - 1, take the argmax as the next token.
+    int64_t n = 0;
+    const bool device_loop = eos_token_id < 0 && d->in_range(first_token, seq_len);
+    if (device_loop) {
+        // Steps whose position is inside the cache run as back-to-back graph
+        // replays (token and position advance on the device); the reference
+        // zeroes the logits of any later step, whose argmax is token 0.
+        const int64_t valid = std::min<int64_t>(max_new_tokens, d->max_seq - seq_len);
+        if (valid > 0) {
+            rc = d->set_state((int)first_token, (int)seq_len);
+            if (rc) return rc;
+            for (int64_t i = 0; i < valid; ++i) TB_HIP(hipGraphLaunch(d->exec, d->st));
+            std::vector<int> hist((size_t)valid);
+            TB_HIP(hipMemcpyAsync(hist.data(), d->history, (size_t)valid * 4,
+                                  hipMemcpyDeviceToHost, d->st));
+            TB_HIP(hipStreamSynchronize(d->st));
+            d->kv_used = std::max<int64_t>(d->kv_used, seq_len + valid);
+            int64_t next = first_token;
+            for (int64_t i = 0; i < max_new_tokens; ++i) {
+                tokens_out[n++] = next;
+                next = i < valid ? hist[(size_t)i] : 0;
+            }
+        } else {
+            for (int64_t i = 0; i < max_new_tokens; ++i) tokens_out[n++] = i == 0 ? first_token : 0;
+        }
+    } else {
+        int64_t next = first_token;
+        while (n < max_new_tokens) {
+            if (eos_token_id >= 0 && next == eos_token_id) break;
+            tokens_out[n++] = next;
+            int64_t am = 0;
+            rc = d->step(next, seq_len + n - 1, false, &am);
+            if (rc) return rc;
+            next = am;
+        }
+    }
+    *n_out = n;
+    *seq_len_out = seq_len + n;
+    return TB_OK;
+}
+
+int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n, int64_t start_offset,
+                       int64_t *offset_out) {
+    TB_REQUIRE(d && offset_out, TB_ERR_VALUE, "null argument");
+    if (n <= 0) {
+        *offset_out = start_offset;
+        return TB_OK;
+    }
+    TB_REQUIRE(tokens, TB_ERR_VALUE, "null tokens");
+    TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
+               "prefill " + std::to_string(n) + " tokens at offset " + std::to_string(start_offset) +
+                   " exceeds max_seq_len " + std::to_string(d->max_seq));
+    for (int64_t i = 0; i < n; ++i) {
+        int rc = d->step(tokens[i], start_offset + i, i + 1 == n, nullptr);
+        if (rc) return rc;
+    }
+    *offset_out = start_offset + n;
+    return TB_OK;
+}
+
+int tb_decoder_reset_kv(tb_decoder *d) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    const size_t kv = (size_t)d->L * d->hkv * d->max_seq * d->hd * sizeof(float);
+    if (d->kv_used > 0) {
+        TB_HIP(hipMemsetAsync(d->kc, 0, kv, d->st));
+        TB_HIP(hipMemsetAsync(d->vc, 0, kv, d->st));
+        TB_HIP(hipStreamSynchronize(d->st));
+    }
+    d->kv_used = 0;
+    return TB_OK;
+}
+
+int tb_decoder_copy_kv(tb_decoder *d, int64_t layer, const float *k, const float *v,
+                       int64_t src_max, int64_t seq_len) {
+    TB_REQUIRE(d && k && v, TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(layer >= 0 && layer < d->L, TB_ERR_VALUE, "layer index out of range");
+    TB_REQUIRE(seq_len >= 0 && seq_len <= src_max && seq_len <= d->max_seq, TB_ERR_VALUE,
+               "KV cache copy out of bounds");
+    // Source [hkv, src_max, hd] per layer (decoder.rs:479-523).
+    const size_t row = (size_t)d->hd * 4;
+    for (int hh = 0; hh < d->hkv; ++hh) {
+        const size_t so = (size_t)hh * src_max * d->hd;
+        const size_t dof = ((size_t)layer * d->hkv + hh) * d->max_seq * d->hd;
+        TB_HIP(hipMemcpyAsync(d->kc + dof, k + so, row * seq_len, hipMemcpyDefault, d->st));
+        TB_HIP(hipMemcpyAsync(d->vc + dof, v + so, row * seq_len, hipMemcpyDefault, d->st));
+    }
+    TB_HIP(hipStreamSynchronize(d->st));
+    d->kv_used = std::max<int64_t>(d->kv_used, seq_len);
+    return TB_OK;
+}
+
+int tb_decoder_kv_len(tb_decoder *d, int64_t *out) {
+    TB_REQUIRE(d && out, TB_ERR_VALUE, "null argument");
+    *out = d->kv_used;
+    return TB_OK;
+}
+
+int tb_decoder_get_logits(tb_decoder *d, float *out) {
+    TB_REQUIRE(d && out, TB_ERR_VALUE, "null argument");
+    memcpy(out, d->host_logits.data(), (size_t)d->V * 4);
+    return TB_OK;
+}
+
+int tb_decoder_set_seed(tb_decoder *d, uint64_t seed) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    d->rng.seed(seed);
+    return TB_OK;
+}
+
+int tb_decoder_time_greedy(tb_decoder *d, int64_t first_token, int64_t offset, int64_t n_steps,
+                           float *ms_out) {
+    TB_REQUIRE(d && ms_out, TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(d->in_range(first_token, offset) && offset + n_steps <= d->max_seq, TB_ERR_VALUE,
+               "timed steps must stay inside the KV cache");
+    int rc = d->ensure_graph();
+    if (rc) return rc;
+    rc = d->set_state((int)first_token, (int)offset);
+    if (rc) return rc;
+    TB_HIP(hipEventRecord(d->ev0, d->st));
+    for (int64_t i = 0; i < n_steps; ++i) TB_HIP(hipGraphLaunch(d->exec, d->st));
+    TB_HIP(hipEventRecord(d->ev1, d->st));
+    TB_HIP(hipEventSynchronize(d->ev1));
+    TB_HIP(hipEventElapsedTime(ms_out, d->ev0, d->ev1));
+    d->kv_used = std::max<int64_t>(d->kv_used, offset + n_steps);
+    return TB_OK;
+}
+
+int tb_decoder_destroy(tb_decoder *d) {
+    delete d;
+    return TB_OK;
+}
+
+}  // extern "C"

@@ -30,9 +30,7 @@ struct W4Params {
     float *y;          // [m, n] output
     int m, n, k;
     int gshift;        // log2(group_size)
-    int rows_j;             // rows per batch (tuning: 4, 8 or 16; 0 = default)
-    // Filled in by the launcher.
-    int c, sw, b, rows_per_step, rows_per_block;
+    int rows_j;        // rows per block (tuning: 4, 8 or 16; 0 = default)
 };
 
 // One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when

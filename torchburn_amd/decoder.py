@@ -1,0 +1,309 @@
+"""RustQwenDecoder on MI355X: the reference's native decoder API over libtbhip.so.
+
+Mirrors the reference's RustQwenDecoder pyclass (src/llm/decoder.rs:176-1020)
+and its factory create_rust_qwen_decoder (python/torchburn/quantization.py:575-647):
+same constructor arguments, layer tensor order and method names.  Tensors may be
+torch (CPU or GPU) or numpy arrays; they are copied to the GPU once at
+construction, as the reference copies them into Rust-owned memory.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Any, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import _lib
+
+RECENT_WINDOW = 64   # repetition-penalty window (src/llm/decoder.rs:837-850)
+
+
+class _Config(C.Structure):
+    _fields_ = [("num_layers", C.c_int64), ("hidden_size", C.c_int64),
+                ("intermediate_size", C.c_int64), ("num_heads", C.c_int64),
+                ("num_kv_heads", C.c_int64), ("head_dim", C.c_int64),
+                ("vocab_size", C.c_int64), ("group_size", C.c_int64),
+                ("max_seq_len", C.c_int64), ("rms_norm_eps", C.c_double),
+                ("rope_theta", C.c_double), ("weight_bits", C.c_int32),
+                ("lm_head_bits", C.c_int32)]
+
+
+def _bind():
+    L = _lib.lib()
+    if getattr(L, "_tb_decoder_bound", False):
+        return L
+    p, i64 = C.c_void_p, C.c_int64
+    sigs = {
+        "tb_decoder_create": [C.POINTER(_Config), p, p, p, p, C.POINTER(p)],
+        "tb_decoder_set_layer": [p, i64] + [p] * 13,
+        "tb_decoder_step": [p, i64, i64, p, C.POINTER(i64)],
+        "tb_decoder_decode_and_sample": [p, i64, i64, C.c_float, i64, C.c_float, p, i64,
+                                         C.c_float, C.POINTER(i64)],
+        "tb_decoder_generate": [p, i64, i64, i64, i64, p, C.POINTER(i64), C.POINTER(i64)],
+        "tb_decoder_prefill": [p, p, i64, i64, C.POINTER(i64)],
+        "tb_decoder_reset_kv": [p],
+        "tb_decoder_copy_kv": [p, i64, p, p, i64, i64],
+        "tb_decoder_kv_len": [p, C.POINTER(i64)],
+        "tb_decoder_get_logits": [p, p],
+        "tb_decoder_set_seed": [p, C.c_uint64],
+        "tb_decoder_time_greedy": [p, i64, i64, i64, C.POINTER(C.c_float)],
+        "tb_decoder_destroy": [p],
+    }
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = C.c_int
+    L._tb_decoder_bound = True
+    return L
+
+
+def decoder_symbols() -> list:
+    return ["tb_decoder_create", "tb_decoder_set_layer", "tb_decoder_step",
+            "tb_decoder_decode_and_sample", "tb_decoder_generate", "tb_decoder_prefill",
+            "tb_decoder_reset_kv", "tb_decoder_copy_kv", "tb_decoder_kv_len",
+            "tb_decoder_get_logits", "tb_decoder_set_seed", "tb_decoder_time_greedy",
+            "tb_decoder_destroy"]
+
+
+def _as_buffer(t: Any, dtype=None):
+    """(pointer, keep-alive object, numpy dtype) of a contiguous tensor/array."""
+    if t is None:
+        return None, None, None
+    try:
+        import torch
+        if isinstance(t, torch.Tensor):
+            t = t.detach().contiguous()
+            return t.data_ptr(), t, str(t.dtype).replace("torch.", "")
+    except ImportError:
+        pass
+    a = np.ascontiguousarray(t if dtype is None else np.asarray(t, dtype=dtype))
+    return a.ctypes.data, a, str(a.dtype)
+
+
+def _bits_of(dtype: str) -> int:
+    return {"uint8": 4, "int8": 8, "float32": 32}[dtype]
+
+
+class RustQwenDecoder:
+    """Device-resident INT4 (or INT8) decoder with the reference's API.
+
+    Constructor arguments are those of RustQwenDecoder::new (decoder.rs:176-212);
+    each entry of ``layers_data`` is the reference's 12 (+1 bias) tensors:
+    [in_norm, qkv_w, qkv_s, o_w, o_s, post_norm, gate_w, gate_s, up_w, up_s,
+    down_w, down_s, (qkv_b)].  Projection format follows the weight dtype
+    (uint8 packed nibbles = INT4 grouped, int8 = INT8 per-channel); the lm_head
+    may be INT4, INT8 or float32 (``lm_head_s`` None).
+    """
+
+    def __init__(self, embed_tokens, layers_data: Sequence[Sequence[Any]], final_norm_w,
+                 lm_head_w, lm_head_s, num_layers: int, hidden_size: int,
+                 intermediate_size: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                 group_size: int = 64, rms_norm_eps: float = 1e-6, max_seq_len: int = 2048,
+                 rope_theta: float = 1e6):
+        L = _bind()
+        self._h = None
+        emb_p, emb_k, _ = _as_buffer(embed_tokens, np.float32)
+        fn_p, fn_k, _ = _as_buffer(final_norm_w, np.float32)
+        lm_p, lm_k, lm_dt = _as_buffer(lm_head_w)
+        ls_p, ls_k, _ = _as_buffer(lm_head_s, np.float32) if lm_head_s is not None else (None, None, None)
+        vocab = int(embed_tokens.shape[0])
+        if len(layers_data) != num_layers:
+            raise ValueError(f"expected {num_layers} layers, got {len(layers_data)}")
+        wdt = _as_buffer(layers_data[0][1])[2] if num_layers else "uint8"
+        cfg = _Config(num_layers, hidden_size, intermediate_size, num_heads, num_kv_heads,
+                      head_dim, vocab, group_size, max_seq_len, float(rms_norm_eps),
+                      float(rope_theta), _bits_of(wdt), _bits_of(lm_dt))
+        h = C.c_void_p()
+        _lib.check(L.tb_decoder_create(C.byref(cfg), emb_p, fn_p, lm_p, ls_p, C.byref(h)))
+        self._h = h
+        self.vocab_size = vocab
+        self.hidden_size = hidden_size
+        self.num_layers = num_layers
+        self.max_seq_len = max_seq_len
+        self.weight_bits = cfg.weight_bits
+        self.lm_head_bits = cfg.lm_head_bits
+        del emb_k, fn_k, lm_k, ls_k
+        for li, caps in enumerate(layers_data):
+            if len(caps) < 12:
+                raise _lib.UnsupportedOpError(
+                    f"{_lib.UNSUPPORTED_MARKER} Each layer requires 12 capsules: input_norm, "
+                    "qkv_w, qkv_s, o_w, o_s, post_norm, gate_w, gate_s, up_w, up_s, down_w, down_s")
+            bufs = [_as_buffer(caps[i]) for i in range(12)]
+            qkv_b = _as_buffer(caps[12], np.float32) if len(caps) >= 13 and caps[12] is not None \
+                else (None, None, None)
+            _lib.check(L.tb_decoder_set_layer(self._h, li, *[b[0] for b in bufs], qkv_b[0]))
+
+    # -- stepping -----------------------------------------------------------
+
+    def _step(self, token_id: int, offset: int, want_logits: bool):
+        out = np.empty(self.vocab_size, np.float32) if want_logits else None
+        am = C.c_int64()
+        _lib.check(_bind().tb_decoder_step(self._h, int(token_id), int(offset),
+                                           out.ctypes.data if want_logits else None,
+                                           C.byref(am)))
+        return out, int(am.value)
+
+    def decode_step(self, token_id: int, offset: int):
+        """Logits of one step as a float32 tensor [1, vocab] (decoder.rs:729-750)."""
+        import torch
+        out, _ = self._step(token_id, offset, True)
+        return torch.from_numpy(out).reshape(1, -1)
+
+    def step(self, token_id: int, offset: int) -> List[float]:
+        out, _ = self._step(token_id, offset, True)
+        return out.tolist()
+
+    def decode_and_sample(self, token_id: int, offset: int, temperature: float = 0.7,
+                          top_k: int = 40, repetition_penalty: float = 1.0,
+                          recent_tokens: Optional[Sequence[int]] = None,
+                          top_p: float = 1.0) -> int:
+        rec = np.asarray(list(recent_tokens or []), dtype=np.int64)
+        out = C.c_int64()
+        _lib.check(_bind().tb_decoder_decode_and_sample(
+            self._h, int(token_id), int(offset), float(temperature), int(top_k),
+            float(repetition_penalty), rec.ctypes.data if rec.size else None, rec.size,
+            float(top_p), C.byref(out)))
+        return int(out.value)
+
+    def generate_loop(self, first_token: int, seq_len: int, max_new_tokens: int,
+                      temperature: float = 0.7, top_k: int = 40,
+                      repetition_penalty: float = 1.0, top_p: float = 1.0,
+                      eos_token_id: Optional[int] = None,
+                      recent_seed: Optional[Sequence[int]] = None) -> Tuple[List[int], int]:
+        """Whole decode loop in one call (decoder.rs:788-832)."""
+        greedy = not np.isfinite(temperature) or temperature <= 0 or top_k == 1
+        if greedy and repetition_penalty <= 1.0:
+            toks = np.empty(max(int(max_new_tokens), 1), np.int64)
+            n, sl = C.c_int64(), C.c_int64()
+            _lib.check(_bind().tb_decoder_generate(
+                self._h, int(first_token), int(seq_len), int(max_new_tokens),
+                -1 if eos_token_id is None else int(eos_token_id), toks.ctypes.data,
+                C.byref(n), C.byref(sl)))
+            return toks[:n.value].tolist(), int(sl.value)
+        tokens: List[int] = []
+        recent = list(recent_seed or [])
+        nxt, generated = int(first_token), 0
+        while generated < max_new_tokens:
+            if eos_token_id is not None and nxt == eos_token_id:
+                break
+            tokens.append(nxt)
+            generated += 1
+            recent.append(nxt)
+            if len(recent) > RECENT_WINDOW:
+                del recent[:len(recent) - RECENT_WINDOW]
+            nxt = self.decode_and_sample(nxt, seq_len + generated - 1, temperature, top_k,
+                                         repetition_penalty, recent, top_p)
+        return tokens, seq_len + generated
+
+    def prefill_tokens(self, tokens: Sequence[int], start_offset: int) -> int:
+        arr = np.asarray(list(tokens), dtype=np.int64)
+        off = C.c_int64()
+        _lib.check(_bind().tb_decoder_prefill(self._h, arr.ctypes.data if arr.size else None,
+                                              arr.size, int(start_offset), C.byref(off)))
+        return int(off.value)
+
+    def prefill(self, tokens: Sequence[int]) -> List[float]:
+        if len(tokens) == 0:
+            raise ValueError("empty prefill")
+        if len(tokens) > self.max_seq_len:
+            raise ValueError("prefill exceeds max_seq_len")
+        self.prefill_tokens(tokens, 0)
+        return self.get_logits()
+
+    def verify_tokens(self, start_offset: int, tokens: Sequence[int]) -> List[List[float]]:
+        if start_offset + len(tokens) > self.max_seq_len:
+            raise ValueError("verify exceeds max_seq_len")
+        return [self.step(t, start_offset + i) for i, t in enumerate(tokens)]
+
+    # -- KV cache -------------------------------------------------------------
+
+    def reset_kv_cache(self) -> None:
+        _lib.check(_bind().tb_decoder_reset_kv(self._h))
+
+    def copy_kv_cache_from_tensors(self, k_tensors, v_tensors, seq_len: int) -> None:
+        """Per-layer [.., kv_heads, src_max, head_dim] f32 tensors (decoder.rs:479-523)."""
+        L = _bind()
+        for li in range(min(self.num_layers, len(k_tensors))):
+            kp, kk, _ = _as_buffer(k_tensors[li], np.float32)
+            vp, vk, _ = _as_buffer(v_tensors[li], np.float32)
+            src_max = int(k_tensors[li].shape[-2]) if len(k_tensors[li].shape) >= 2 else seq_len
+            _lib.check(L.tb_decoder_copy_kv(self._h, li, kp, vp, src_max, int(seq_len)))
+            del kk, vk
+
+    def kv_len(self) -> int:
+        out = C.c_int64()
+        _lib.check(_bind().tb_decoder_kv_len(self._h, C.byref(out)))
+        return int(out.value)
+
+    def get_logits(self) -> List[float]:
+        out = np.empty(self.vocab_size, np.float32)
+        _lib.check(_bind().tb_decoder_get_logits(self._h, out.ctypes.data))
+        return out.tolist()
+
+    def set_seed(self, seed: int) -> None:
+        _lib.check(_bind().tb_decoder_set_seed(self._h, int(seed) & (2 ** 64 - 1)))
+
+    def time_greedy(self, first_token: int, offset: int, n_steps: int) -> float:
+        """Milliseconds for n_steps device-driven greedy steps (benchmark helper)."""
+        ms = C.c_float()
+        _lib.check(_bind().tb_decoder_time_greedy(self._h, int(first_token), int(offset),
+                                                  int(n_steps), C.byref(ms)))
+        return float(ms.value)
+
+    def close(self) -> None:
+        if self._h:
+            _bind().tb_decoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def decoder_from_weights(w: dict, cfg: dict, group_size: int = 32,
+                         max_seq_len: int = 2048) -> RustQwenDecoder:
+    """RustQwenDecoder from a synthetic weight dict (torchburn_amd.synth.decoder_weights)."""
+    layers = []
+    for lw in w["layers"]:
+        caps = [lw["in_norm"], lw["qkv_w"], lw["qkv_s"], lw["o_w"], lw["o_s"], lw["post_norm"],
+                lw["gate_w"], lw["gate_s"], lw["up_w"], lw["up_s"], lw["down_w"], lw["down_s"]]
+        if lw.get("qkv_b") is not None:
+            caps.append(lw["qkv_b"])
+        layers.append(caps)
+    return RustQwenDecoder(w["embed"], layers, w["final_norm"], w["lm_head_w"], w["lm_head_s"],
+                           cfg["num_layers"], cfg["hidden"], cfg["intermediate"],
+                           cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], group_size,
+                           cfg["eps"], max_seq_len, cfg["rope_theta"])
+
+
+def create_rust_qwen_decoder(model: Any, max_seq_len: int = 4096,
+                             group_size: Optional[int] = None) -> RustQwenDecoder:
+    """From a quantized model with the reference's module layout
+    (python/torchburn/quantization.py:575-647): embed_tokens, layers[i].
+    {input_layernorm, self_attn.{qkv_proj,o_proj}, post_attention_layernorm,
+    mlp.{gate,up,down}_proj}, norm, lm_head (QuantizedLinear or nn.Linear)."""
+    layers = []
+    for layer in model.layers:
+        at, mlp = layer.self_attn, layer.mlp
+        caps = [layer.input_layernorm.weight, at.qkv_proj.qweight, at.qkv_proj.scales,
+                at.o_proj.qweight, at.o_proj.scales, layer.post_attention_layernorm.weight,
+                mlp.gate_proj.qweight, mlp.gate_proj.scales, mlp.up_proj.qweight,
+                mlp.up_proj.scales, mlp.down_proj.qweight, mlp.down_proj.scales]
+        if getattr(at.qkv_proj, "bias", None) is not None:
+            caps.append(at.qkv_proj.bias)
+        layers.append([c.detach().float() if c.dtype.is_floating_point else c.detach()
+                       for c in caps])
+    cfg = model.config
+    lm = model.lm_head
+    if hasattr(lm, "qweight"):
+        lm_w, lm_s = lm.qweight.detach(), lm.scales.detach().float()
+    else:
+        lm_w, lm_s = lm.weight.detach().float(), None
+    gs = group_size or getattr(model.layers[0].mlp.gate_proj, "group_size", 64)
+    return RustQwenDecoder(model.embed_tokens.weight.detach().float(), layers,
+                           model.norm.weight.detach().float(), lm_w, lm_s, len(model.layers),
+                           cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads,
+                           cfg.num_key_value_heads, cfg.head_dim, gs, cfg.rms_norm_eps,
+                           max_seq_len, cfg.rope_theta)

@@ -207,8 +207,61 @@ def fused_swiglu_mlp_w4a32(
     return out.reshape(*x.shape[:-1], n_out).to(x.device)
 
 
+def w8a32_linear(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """out = (x @ w.T) * scales + bias for int8 w (reference quantization.py:193-216)."""
+    dev = _target(x)
+    k = x.shape[-1]
+    x2 = _on_gpu(x.reshape(-1, k), torch.float32, dev)
+    m = x2.shape[0]
+    wt = _on_gpu(w, torch.int8, dev)
+    s = _on_gpu(scales, torch.float32, dev).reshape(-1)
+    b = _on_gpu(bias, torch.float32, dev)
+    if wt.ndim != 2 or wt.shape[1] != k:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w8a32_linear dimension mismatch: x K={k}, "
+            f"w {list(wt.shape)}")
+    n = wt.shape[0]
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _lib.call("tb_w8a32_linear", _ptr(x2), _ptr(wt), _ptr(s), s.numel(), _ptr(b), _ptr(out),
+              m, n, k, _stream(dev))
+    return out.reshape(*x.shape[:-1], n).to(x.device)
+
+
+def fused_swiglu_mlp_w8a32(
+    x: torch.Tensor,
+    gate_w: torch.Tensor, gate_s: torch.Tensor, gate_b: Optional[torch.Tensor],
+    up_w: torch.Tensor, up_s: torch.Tensor, up_b: Optional[torch.Tensor],
+    down_w: torch.Tensor, down_s: torch.Tensor, down_b: Optional[torch.Tensor],
+    residual: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """INT8 down(silu(gate(x)) * up(x)) [+ residual] (reference fused_ops.rs:8-133)."""
+    dev = _target(x)
+    k = x.shape[-1]
+    x2 = _on_gpu(x.reshape(-1, k), torch.float32, dev)
+    m = x2.shape[0]
+    gw, uw, dw = (_on_gpu(t, torch.int8, dev) for t in (gate_w, up_w, down_w))
+    gs, us, ds = (_on_gpu(t, torch.float32, dev).reshape(-1) for t in (gate_s, up_s, down_s))
+    gb, ub, db = (_on_gpu(t, torch.float32, dev) for t in (gate_b, up_b, down_b))
+    inter, n_out = gw.shape[0], dw.shape[0]
+    r = None if residual is None else _on_gpu(residual.reshape(m, n_out), torch.float32, dev)
+    out = torch.empty((m, n_out), dtype=torch.float32, device=dev)
+    _lib.call("tb_fused_swiglu_mlp_w8a32", _ptr(x2), _ptr(gw), _ptr(gs), _ptr(gb), _ptr(uw),
+              _ptr(us), _ptr(ub), _ptr(dw), _ptr(ds), _ptr(db), _ptr(r), _ptr(out),
+              m, k, inter, n_out, _stream(dev))
+    return out.reshape(*x.shape[:-1], n_out).to(x.device)
+
+
 def fused_swiglu_mlp(x: torch.Tensor, gate: Any, up: Any, down: Any) -> torch.Tensor:
     """Fused SwiGLU MLP over three QuantizedLinear modules (reference quantization.py:299-355)."""
+    if gate.bits == 8:
+        return fused_swiglu_mlp_w8a32(
+            x, gate.qweight, gate.scales, gate.bias, up.qweight, up.scales, up.bias,
+            down.qweight, down.scales, down.bias)
     if gate.bits == 4:
         return fused_swiglu_mlp_w4a32(
             x, gate.qweight, gate.scales, gate.bias, up.qweight, up.scales, up.bias,
@@ -270,7 +323,6 @@ class QuantizedLinear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.bits == 8:
-            from .w8 import w8a32_linear
             return w8a32_linear(x, self.qweight, self.scales, self.bias)
         return w4a32_grouped_linear(x, self.qweight, self.scales, self.bias,
                                     group_size=self.group_size)
