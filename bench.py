@@ -1,16 +1,25 @@
-"""Benchmark of the gfx950 INT4 decode hot path.
+"""Benchmark of the gfx950 INT4 decode hot path (one MI355X).
 
-Default workload: the Llama-3-8B-shape INT4 (group 32)
-SwiGLU MLP at batch M = 1 -- gate/up [14336, 4096] fused with silu*up, then down
-[4096, 14336] with the residual add -- on one MI355X.  One "step" is one pass of
-that MLP over one synthetic activation row; inputs are resident in HBM before
-the timed region.  Four distinct weight copies (4 x 110 MB) are rotated so the
-256 MB Infinity Cache cannot serve the weights.
+Headline (BASELINE metric "INT4 GEMV HBM GB/s (% of 8 TB/s); decode tokens/sec
+at 8B shape, 1 GPU"):
 
-Prints one JSON line (rank 0): metric/value = whole-step algorithmic bytes per
-second (GB/s), plus the roofline of the dominant kernel (the fused gate/up
-GEMV, timed with HIP events on its own stream) and the CPU-oracle baseline
-timed on this host's cores.
+  * value: whole-step throughput of the Llama-3-8B-shape INT4 (group 32) SwiGLU
+    MLP at batch M (default M = 1): x records -> fused
+    gate/up GEMV with silu*up -> h records -> down GEMV with the residual add.
+    One step = one pass over one synthetic activation row, weights resident in
+    HBM.  Four distinct weight copies (4 x 110 MB > the 256 MB Infinity Cache)
+    rotate, and the steps replay from one captured hipGraph, timed with HIP
+    events on the capture stream.
+  * roofline: the dominant kernel (fused gate/up GEMV, 73.5 MB per launch)
+    timed alone the same way.
+  * decode: Llama-3-8B INT4 (config 5), its INT8 repeat and Qwen2.5-0.5B with
+    an fp32 lm_head (config 4): greedy steps as device-driven graph replays at
+    KV length 4096 / 4096 / 2048, tokens/s and the fraction of the step's
+    weight + KV byte roofline.
+  * cpu_baseline: the C oracle (a restatement of the reference's CPU path) on
+    this host's cores, on a bounded sample of the same MLP workload.
+
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -23,19 +32,20 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
-ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=400, help="timed MLP steps")
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--m", type=int, default=1, help="activation rows (config 2: 1, 4, 8)")
     ap.add_argument("--copies", type=int, default=4, help="weight copies rotated (> 256 MB)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="budget of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode", default="llama4,llama8,qwen",
+                    help="decode runs: comma list of llama4, llama8, qwen, or 'none'")
+    ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (FETCH_SIZE / "
                          "WRITE_SIZE calibration for rocprofv3 --pmc), then exit")
@@ -53,22 +63,169 @@ def cpu_info():
                     flags = set(line.split(":", 1)[1].split())
     except OSError:
         pass
-    return model, sorted(f for f in flags if f in ("avx2", "fma", "avx512f", "avx512bw",
-                                                    "avx512_vnni"))
+    keep = ("avx2", "fma", "avx512f", "avx512bw", "avx512_vnni")
+    return model, sorted(f for f in flags if f in keep)
+
+
+def graph_time(torch, fn, reps, warmup):
+    """Capture fn() once, replay it `reps` times; returns ms per replay."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fn()                      # allocate workspaces outside the capture
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps, g
+
+
+def mlp_section(torch, args, dev):
+    from torchburn_amd import _lib
+    M, K, I, GS = args.m, 4096, 14336, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x7B + 2)
+
+    def int4(n, k):
+        w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
+        s = torch.randn((n, k // GS), device=dev, generator=gen).mul_(0.02).abs_().add_(1e-3)
+        return w, s
+
+    sets = [(*int4(I, K), *int4(I, K), *int4(K, I)) for _ in range(args.copies)]
+    x = torch.randn((M, K), device=dev, generator=gen)
+    r = torch.randn((M, K), device=dev, generator=gen)
+    out = torch.empty((M, K), device=dev)
+    h = torch.empty((M, I), device=dev)
+    xq = torch.empty(_lib.lib().tb_x_records_bytes(M, K) // 4, dtype=torch.int32, device=dev)
+    hq = torch.empty(_lib.lib().tb_x_records_bytes(M, I) // 4, dtype=torch.int32, device=dev)
+    P = lambda t: t.data_ptr()
+    S = lambda: torch.cuda.current_stream(dev).cuda_stream
+
+    def mlp(ws):
+        gw, gs, uw, us, dw, ds = ws
+        _lib.call("tb_xquant", P(x), P(xq), M, K, S())
+        _lib.call("tb_swiglu_w4a32_xq", P(x), P(xq), P(gw), P(gs), None, P(uw), P(us), None,
+                  P(h), M, K, I, GS, S())
+        _lib.call("tb_xquant", P(h), P(hq), M, I, S())
+        _lib.call("tb_w4a32_gemv_xq", P(h), P(hq), P(dw), P(ds), None, P(r), P(out), M, K, I,
+                  GS, S())
+
+    def all_steps():
+        for ws in sets:
+            mlp(ws)
+
+    reps = max(1, args.steps // len(sets))
+    ms_graph, _ = graph_time(torch, all_steps, reps, max(1, args.warmup // len(sets)))
+    ms = ms_graph / len(sets)
+    w_bytes = 3 * (I * K // 2 + 4 * I * (K // GS))
+    act_bytes = 4 * (M * K + 2 * M * I + 2 * M * K)
+    step_bytes = w_bytes + act_bytes
+
+    # Dominant kernel alone: fused gate/up GEMV over the rotation (records prebuilt).
+    _lib.call("tb_xquant", P(x), P(xq), M, K, S())
+    _lib.call("tb_xquant", P(h), P(hq), M, I, S())
+
+    def gateups():
+        for gw, gs, uw, us, _, _ in sets:
+            _lib.call("tb_swiglu_w4a32_xq", P(x), P(xq), P(gw), P(gs), None, P(uw), P(us), None,
+                      P(h), M, K, I, GS, S())
+
+    def downs():
+        for _, _, _, _, dw, ds in sets:
+            _lib.call("tb_w4a32_gemv_xq", P(h), P(hq), P(dw), P(ds), None, P(r), P(out), M, K,
+                      I, GS, S())
+
+    gu_ms, _ = graph_time(torch, gateups, reps, 4)
+    dn_ms, _ = graph_time(torch, downs, reps, 4)
+    gu_us = gu_ms * 1e3 / len(sets)
+    dn_us = dn_ms * 1e3 / len(sets)
+    gu_bytes = 2 * (I * K // 2 + 4 * I * (K // GS)) + 4 * M * K + 4 * M * I
+    dn_bytes = K * I // 2 + 4 * K * (I // GS) + 4 * M * I + 8 * M * K
+
+    # Parity guard on the measured data against the CPU oracle (set 0).
+    from oracle import oracle as O
+    torch.cuda.synchronize()
+    mlp(sets[0])
+    torch.cuda.synchronize()
+    ws = [t.cpu().numpy() for t in sets[0]]
+    xs, rs = x.cpu().numpy(), r.cpu().numpy()
+    ref = O.swiglu_mlp_w4(xs, ws[0], ws[1], ws[2], ws[3], ws[4], ws[5], group_size=GS) + rs
+    max_rel = float(np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max())
+
+    cpu = None
+    if not args.no_cpu:
+        n, t0 = 0, time.perf_counter()
+        while True:
+            O.swiglu_mlp_w4(xs, ws[0], ws[1], ws[2], ws[3], ws[4], ws[5], group_size=GS)
+            n += 1
+            el = time.perf_counter() - t0
+            if el > args.cpu_seconds:
+                break
+        model, flags = cpu_info()
+        cpu = {"value": round(step_bytes * n / el / 1e9, 3), "unit": "GB/s",
+               "cores": O.num_threads(), "kind": "port",
+               "sample": f"{n} M={M} MLP passes of the C oracle (restated reference CPU path) "
+                         f"in {el:.1f} s on {model} [{' '.join(flags)}]",
+               "ms_per_step": round(el / n * 1e3, 3)}
+    del sets
+    return dict(ms=ms, step_bytes=step_bytes, gu_us=gu_us, gu_bytes=gu_bytes, dn_us=dn_us,
+                dn_bytes=dn_bytes, max_rel=max_rel, cpu=cpu)
+
+
+def decode_run(torch, name, steps):
+    from torchburn_amd import synth
+    from torchburn_amd.decoder import decoder_from_weights
+    cfg, wk, lk, kvlen, seed = {
+        "llama4": (synth.LLAMA3_8B, 4, 4, 4096, 0x7B + 5),
+        "llama8": (synth.LLAMA3_8B, 8, 8, 4096, 0x7B + 5),
+        "qwen": (synth.QWEN_0_5B, 4, 32, 2048, 0x7B + 4),
+    }[name]
+    max_seq = kvlen + steps
+    w = synth.decoder_weights_torch(cfg, seed, wk, lk, 32)
+    dec = decoder_from_weights(w, cfg, group_size=32, max_seq_len=max_seq)
+    del w
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    hkv, hd = cfg["num_kv_heads"], cfg["head_dim"]
+    ks, vs = [], []
+    for _ in range(cfg["num_layers"]):
+        ks.append(torch.randn((hkv, kvlen, hd), device="cuda", generator=g))
+        vs.append(torch.randn((hkv, kvlen, hd), device="cuda", generator=g))
+    dec.copy_kv_cache_from_tensors(ks, vs, kvlen)
+    del ks, vs
+    torch.cuda.empty_cache()
+    first = seed % cfg["vocab"]
+    dec.time_greedy(first, kvlen, min(8, steps))          # warm-up (same positions)
+    ms = dec.time_greedy(first, kvlen, steps)
+    dec.close()
+    torch.cuda.empty_cache()
+    byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk) for i in range(steps)) / steps
+    sec = ms / 1e3 / steps
+    return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(ms / steps, 4),
+            "bytes_per_token": int(byts), "kv_len": kvlen,
+            "roofline_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / byts, 1)}
 
 
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is "
-                                   "design-only (see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
+                          "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
-    import torchburn_amd as tb
-    from torchburn_amd import synth
-
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.calib_copy_mib:
@@ -80,125 +237,42 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calib_copy_bytes": n, "copies": 5}))
         return
-    M, K, I, GS = args.m, 4096, 14336, 32
 
-    # Weights: `copies` independent sets generated on the device.
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0x7B + 2)
-
-    def int4(n, k):
-        w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
-        s = torch.randn((n, k // GS), device=dev, generator=gen).mul_(0.02).abs_().add_(1e-3)
-        return w, s
-
-    sets = []
-    for _ in range(args.copies):
-        gw, gs = int4(I, K)
-        uw, us = int4(I, K)
-        dw, ds = int4(K, I)
-        sets.append((gw, gs, uw, us, dw, ds))
-    x = torch.randn((M, K), device=dev, generator=gen)
-    r = torch.randn((M, K), device=dev, generator=gen)
-    out = torch.empty((M, K), device=dev)
-    h = torch.empty((M, I), device=dev)
-    torch.cuda.synchronize()
-
-    from torchburn_amd import _lib
-    st = torch.cuda.current_stream(dev).cuda_stream
-    P = lambda t: t.data_ptr()
-
-    def gateup(ws):
-        gw, gs, uw, us, _, _ = ws
-        _lib.call("tb_swiglu_w4a32", P(x), P(gw), P(gs), None, P(uw), P(us), None, P(h),
-                  M, K, I, GS, st)
-
-    def down(ws):
-        _, _, _, _, dw, ds = ws
-        _lib.call("tb_w4a32_grouped_linear_residual", P(h), P(dw), P(ds), None, P(r), P(out),
-                  M, K, I, GS, st)
-
-    def step(i):
-        ws = sets[i % len(sets)]
-        gateup(ws)
-        down(ws)
-
-    w_bytes = 3 * (I * K // 2 + 4 * I * (K // GS))
-    act_bytes = 4 * (M * K + 2 * M * I + 2 * M * K)  # x; h written+read; r; out
-    step_bytes = w_bytes + act_bytes
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(args.steps):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
-    gbs = step_bytes / (ms * 1e-3) / 1e9
-
-    # Dominant kernel: the fused gate/up GEMV, timed alone over the same rotation.
-    gu_bytes = 2 * (I * K // 2 + 4 * I * (K // GS)) + 4 * M * K + 4 * M * I
-    for i in range(args.warmup):
-        gateup(sets[i % len(sets)])
-    e0.record()
-    for i in range(args.steps):
-        gateup(sets[i % len(sets)])
-    e1.record()
-    torch.cuda.synchronize()
-    gu_us = e0.elapsed_time(e1) * 1e3 / args.steps
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-
-    # Correctness guard on the measured data (oracle, CPU): one row of set 0.
-    from oracle import oracle as O
-    ws = [t.cpu().numpy() for t in sets[0]]
-    xs, rs = x.cpu().numpy(), r.cpu().numpy()
-    step(0)
-    torch.cuda.synchronize()
-    ref = O.swiglu_mlp_w4(xs, ws[0], ws[1], ws[2], ws[3], ws[4], ws[5], group_size=GS) + rs
-    got = out.cpu().numpy()
-    max_rel = float(np.abs(got - ref).max() / np.abs(ref).max())
-
-    cpu = None
-    if not args.no_cpu:
-        n, t_start = 0, time.perf_counter()
-        while True:
-            O.swiglu_mlp_w4(xs, ws[0], ws[1], ws[2], ws[3], ws[4], ws[5], group_size=GS)
-            n += 1
-            el = time.perf_counter() - t_start
-            if el > args.cpu_seconds:
-                break
-        model, flags = cpu_info()
-        cpu = {"value": round(step_bytes * n / el / 1e9, 3), "unit": "GB/s",
-               "cores": O.num_threads(), "kind": "port",
-               "sample": f"{n} MLP passes (M={M}) of the C oracle in {el:.1f} s on {model} "
-                         f"[{' '.join(flags)}]",
-               "ms_per_step": round(el / n * 1e3, 3)}
-
+    t_start = time.perf_counter()
+    r = mlp_section(torch, args, dev)
+    gbs = r["step_bytes"] / (r["ms"] * 1e-3) / 1e9
+    gu_gbs = r["gu_bytes"] / (r["gu_us"] * 1e-6) / 1e9
+    decode = {}
+    if args.decode != "none":
+        for name in args.decode.split(","):
+            decode[name] = decode_run(torch, name.strip(), args.decode_steps)
     line = {
-        "metric": "INT4 GEMV HBM GB/s (Llama-3-8B SwiGLU MLP, group 32)",
+        "metric": "INT4 GEMV HBM GB/s (% of 8 TB/s); decode tokens/sec at 8B shape, 1 GPU",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": round(r["ms"], 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4-w/f32-a (fp32 accumulate)", "data": "synthetic",
-        "config": {"workload": f"llama3-8b int4-g32 swiglu mlp (gate/up+down+residual), M={M}",
-                   "m": M, "hidden": K, "intermediate": I, "group_size": GS,
-                   "weight_copies_rotated": args.copies, "step_bytes": step_bytes,
-                   "parallelism": "single-gpu"},
-        "roofline": {"bound": "hbm", "kernel": "k_w4_gemv<dual swiglu>",
+        "dtype": "int4 weights, f32 activations, f32 accumulate",
+        "data": "synthetic (seeded random weights and activations)",
+        "config": {"workload": f"llama3-8b int4-g32 SwiGLU MLP step (gate/up + down + residual), "
+                               f"M={args.m}", "m": args.m, "hidden": 4096,
+                   "intermediate": 14336, "group_size": 32, "weight_copies_rotated": args.copies,
+                   "step_bytes": r["step_bytes"], "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "kernel": "k_w4_gemv (gate/up pair, silu*up epilogue)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_us": round(gu_us, 3), "bytes_per_launch": gu_bytes},
-        "cpu_baseline": cpu,
-        "parity_max_rel": max_rel,
-        "wall_s": round(wall, 3),
+                     "avg_us": round(r["gu_us"], 3), "bytes_per_launch": r["gu_bytes"],
+                     "down_kernel_avg_us": round(r["dn_us"], 3),
+                     "down_kernel_gbs": round(r["dn_bytes"] / (r["dn_us"] * 1e-6) / 1e9, 1)},
+        "decode": decode,
+        "cpu_baseline": r["cpu"],
+        "parity_max_rel": r["max_rel"],
+        "wall_s": round(time.perf_counter() - t_start, 1),
     }
+    if "llama4" in decode:
+        line["decode_tok_s"] = decode["llama4"]["tok_s"]
     print(json.dumps(line), flush=True)
 
 

@@ -109,6 +109,26 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
                               int64_t group_size, void *stream);
 
 /*
+ * Activation chunk records, for callers that reuse one x across several INT4
+ * projections (no reference counterpart: the reference converts x inside each
+ * GEMV).  A record holds 32 activations as 24-bit fixed-point integers in six
+ * 4-bit limb planes plus a power-of-two step: 112 bytes per 32 elements,
+ * tb_x_records_bytes(m, k) in total.  tb_xquant builds them from x [M, K];
+ * the *_xq GEMVs read them instead of building their own (x itself is still
+ * read when a chunk holds NaN/Inf).  residual may be NULL.
+ */
+TB_API int64_t tb_x_records_bytes(int64_t m, int64_t k);
+TB_API int tb_xquant(const float *x, uint32_t *xq, int64_t m, int64_t k, void *stream);
+TB_API int tb_w4a32_gemv_xq(const float *x, const uint32_t *xq, const uint8_t *w_packed,
+                            const float *scales, const float *bias, const float *residual,
+                            float *out, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                            void *stream);
+TB_API int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t *gate_w,
+                              const float *gate_s, const float *gate_b, const uint8_t *up_w,
+                              const float *up_s, const float *up_b, float *h, int64_t m,
+                              int64_t k, int64_t inter, int64_t group_size, void *stream);
+
+/*
  * out[m, n] = (sum_k x[m, k] * w[n, k]) * s[n] + bias[n]: the reference's
  * w8a32_linear (binding src/ffi/quantization_ffi.rs:8-30, kernel
  * src/quantization/gemv.rs:733-1061).  w i8 [N, K]; s_len 1 (one per-tensor

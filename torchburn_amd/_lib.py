@@ -43,12 +43,15 @@ _SIGS = {
     "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
     "tb_w8a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "tb_fused_swiglu_mlp_w8a32": [_p] * 12 + [_i64] * 4 + [_p],
+    "tb_xquant": [_p, _p, _i64, _i64, _p],
+    "tb_w4a32_gemv_xq": [_p] * 7 + [_i64] * 4 + [_p],
+    "tb_swiglu_w4a32_xq": [_p] * 9 + [_i64] * 4 + [_p],
 }
 
 
 def declared_symbols() -> list:
     """Every entry point the Python layer binds (all are declared in include/tbhip.h)."""
-    return ["tb_last_error", "tb_version", *_SIGS.keys()]
+    return ["tb_last_error", "tb_version", "tb_x_records_bytes", *_SIGS.keys()]
 
 
 def lib():
@@ -64,6 +67,8 @@ def lib():
             L = C.CDLL(LIB_PATH)
             L.tb_last_error.restype = C.c_char_p
             L.tb_version.restype = C.c_char_p
+            L.tb_x_records_bytes.restype = C.c_int64
+            L.tb_x_records_bytes.argtypes = [C.c_int64, C.c_int64]
             for name, args in _SIGS.items():
                 fn = getattr(L, name)
                 fn.argtypes = args

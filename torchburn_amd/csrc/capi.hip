@@ -245,6 +245,49 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
     return w4_rows(d, EPI_PLAIN, m, hq, true, st);
 }
 
+int64_t tb_x_records_bytes(int64_t m, int64_t k) {
+    return (m < 0 || k < 0) ? 0 : (int64_t)xq_bytes(m, k);
+}
+
+int tb_xquant(const float *x, uint32_t *xq, int64_t m, int64_t k, void *stream) {
+    TB_REQUIRE(x && xq, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: xquant: null pointer");
+    TB_REQUIRE(m >= 0 && k > 0 && k % 32 == 0 && k <= (1 << 20) && m < (1 << 24),
+               TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: xquant: K must be a positive multiple of 32");
+    TB_REQUIRE(aligned(x, 16) && aligned(xq, 16), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: xquant: 16-byte aligned device pointers required");
+    return xquant(x, xq, (int)m, (int)k, (hipStream_t)stream);
+}
+
+int tb_w4a32_gemv_xq(const float *x, const uint32_t *xq, const uint8_t *w_packed,
+                     const float *scales, const float *bias, const float *residual, float *out,
+                     int64_t m, int64_t n, int64_t k, int64_t group_size, void *stream) {
+    int rc = check_w4(x, w_packed, scales, m, n, k, group_size, "w4a32_gemv_xq");
+    if (rc) return rc;
+    TB_REQUIRE(out && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4a32_gemv_xq: null output or unaligned records");
+    if (m == 0 || n == 0) return TB_OK;
+    W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
+    p.res = residual;
+    return w4_rows(p, residual ? EPI_RESID : EPI_PLAIN, m, const_cast<uint32_t *>(xq), false,
+                   (hipStream_t)stream);
+}
+
+int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t *gate_w,
+                       const float *gate_s, const float *gate_b, const uint8_t *up_w,
+                       const float *up_s, const float *up_b, float *h, int64_t m, int64_t k,
+                       int64_t inter, int64_t group_size, void *stream) {
+    int rc = check_w4(x, gate_w, gate_s, m, inter, k, group_size, "swiglu_w4a32_xq");
+    if (rc) return rc;
+    rc = check_w4(x, up_w, up_s, m, inter, k, group_size, "swiglu_w4a32_xq");
+    if (rc) return rc;
+    TB_REQUIRE(h && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: swiglu_w4a32_xq: null output or unaligned records");
+    if (m == 0 || inter == 0) return TB_OK;
+    W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+    p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
+    return w4_rows(p, EPI_SWIGLU, m, const_cast<uint32_t *>(xq), false, (hipStream_t)stream);
+}
+
 int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_t s_len,
                     const float *bias, float *out, int64_t m, int64_t n, int64_t k,
                     void *stream) {

@@ -97,3 +97,68 @@ def kv_prefill(cfg: dict, seed: int, seq_len: int, max_seq: int):
         v[:, :seq_len] = g.standard_normal((hkv, seq_len, hd), dtype=np.float32)
         out.append((k, v))
     return out
+
+
+def decoder_weights_torch(cfg: dict, seed: int, wkind: int = 4, lmkind: int = 4,
+                          group_size: int = 32, device: str = "cuda") -> dict:
+    """decoder_weights() generated directly on a torch device (same layout and
+    distributions, torch's generator) -- for multi-GB benchmark models."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    H, I = cfg["hidden"], cfg["intermediate"]
+    hq, hkv, hd = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    V = cfg["vocab"]
+    tq = (hq + 2 * hkv) * hd
+
+    def normal(shape, std):
+        return torch.randn(shape, device=device, generator=g).mul_(std)
+
+    def proj(n, k, bits):
+        if bits == 4:
+            w = torch.randint(0, 256, (n, (k + 1) // 2), dtype=torch.uint8, device=device,
+                              generator=g)
+            return w, normal((n, k // group_size), 0.02).abs_().add_(1e-3)
+        if bits == 8:
+            w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=device, generator=g)
+            return w, normal((n,), 0.02).abs_().div_(16).add_(1e-4)
+        return normal((n, k), 0.02), None
+
+    layers = []
+    for _ in range(cfg["num_layers"]):
+        qkv_w, qkv_s = proj(tq, H, wkind)
+        o_w, o_s = proj(H, hq * hd, wkind)
+        gate_w, gate_s = proj(I, H, wkind)
+        up_w, up_s = proj(I, H, wkind)
+        down_w, down_s = proj(H, I, wkind)
+        lw = dict(in_norm=torch.ones(H, device=device), post_norm=torch.ones(H, device=device),
+                  qkv_w=qkv_w, qkv_s=qkv_s, o_w=o_w, o_s=o_s, gate_w=gate_w, gate_s=gate_s,
+                  up_w=up_w, up_s=up_s, down_w=down_w, down_s=down_s)
+        if cfg.get("qkv_bias"):
+            lw["qkv_b"] = normal((tq,), 0.02)
+        layers.append(lw)
+    lm_w, lm_s = proj(V, H, lmkind)
+    return dict(embed=normal((V, H), 0.02), final_norm=torch.ones(H, device=device),
+                lm_head_w=lm_w, lm_head_s=lm_s, layers=layers)
+
+
+def decode_bytes_per_token(cfg: dict, pos: int, wkind: int, lmkind: int,
+                           group_size: int = 32) -> int:
+    """Algorithmic HBM bytes of one decoder step at position `pos`: every weight
+    byte once (projections, norms, lm_head, one embedding row) plus the KV rows
+    0..pos read and the new K/V row written."""
+    H, I = cfg["hidden"], cfg["intermediate"]
+    hq, hkv, hd = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    tq = (hq + 2 * hkv) * hd
+
+    def proj(n, k, bits):
+        if bits == 4:
+            return n * ((k + 1) // 2) + 4 * n * (k // group_size)
+        if bits == 8:
+            return n * k + 4 * n
+        return 4 * n * k
+
+    layer = (proj(tq, H, wkind) + proj(H, hq * hd, wkind) + 2 * proj(I, H, wkind) +
+             proj(H, I, wkind) + 2 * 4 * H + (4 * tq if cfg.get("qkv_bias") else 0))
+    kv = 2 * hkv * (pos + 1) * hd * 4 + 2 * hkv * hd * 4
+    return (cfg["num_layers"] * (layer + kv) + proj(cfg["vocab"], H, lmkind) + 4 * H + 4 * H)
