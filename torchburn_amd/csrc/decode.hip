@@ -129,45 +129,53 @@ __global__ void k_rope_kv(const DecState *__restrict__ st, float *__restrict__ q
 
 // Split-KV decode attention (flash-decoding), one block per (kv head, tile of
 // kAttnTile positions), all G = hq/hkv query heads of the group together so
-// each K/V row is read from HBM once.  The tile of K and V is staged through
-// LDS; scores s = (q . k_t) * (1/sqrt(hd)); per head the tile's max m, the sum
-// l = sum exp(s - m) and o = sum exp(s - m) v_t go to `part`, combined across
-// tiles by k_attn_combine (the online-softmax merge).  Math of the reference:
-// src/llm/decoder.rs:1148-1213.
+// each K/V row is read from HBM once.  The tile of K and V is loaded into
+// registers (every load in flight at once), then staged through LDS; scores
+// s = (q . k_t) * (1/sqrt(hd)); per head the tile's max m, l = sum exp(s - m)
+// and o = sum exp(s - m) v_t go to `part` ([hq][nsplit][hd + 4], o then m, l).
+// Math of the reference: src/llm/decoder.rs:1148-1213.  (A last-block merge
+// inside this kernel was measured slower: the device-scope fence every block
+// needs before the hand-off writes back its XCD's L2.)
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_split(const DecState *__restrict__ st,
-                                                    const float *__restrict__ qkv,
-                                                    const float *__restrict__ kc,
-                                                    const float *__restrict__ vc,
-                                                    float *__restrict__ part, int hq, int hkv,
-                                                    int max_seq, int nsplit, float scale) {
-    constexpr int T = kAttnTile, KP = HD + 4;
+__global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
+                                              const float *__restrict__ qkv,
+                                              const float *__restrict__ kc,
+                                              const float *__restrict__ vc,
+                                              float *__restrict__ part, int hq, int hkv,
+                                              int max_seq, int nsplit, float scale) {
+    constexpr int T = kAttnTile, KP = HD + 4, C4 = HD / 4;
+    constexpr int NV = T * C4 / 256;   // float4 of K (and of V) per thread
     extern __shared__ float sm[];
     const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
     const int G = hq / hkv;
     const int seq = st->pos + 1;
     const int t0 = sp * T;
+    if (t0 >= seq) return;   // tile past the sequence: the merge never reads it
+    const int tn = min(T, seq - t0);
     float *sq = sm;                 // [G][HD]
     float *sk = sq + G * HD;        // [T][KP]
     float *sv = sk + T * KP;        // [T][HD]
     float *ss = sv + T * HD;        // [G][T]
     float *sml = ss + G * T;        // [G][2]
-    const size_t rec = HD + 2;
-    if (t0 >= seq) {   // empty tile: neutral element of the merge
-        for (int i = tid; i < G * (HD + 2); i += blockDim.x) {
-            const int g = i / (HD + 2), d = i - g * (HD + 2);
-            part[((size_t)(kvh * G + g) * nsplit + sp) * rec + d] = d == HD ? -FLT_MAX : 0.f;
-        }
-        return;
-    }
-    const int tn = min(T, seq - t0);
-    for (int i = tid; i < G * HD; i += blockDim.x) sq[i] = qkv[(size_t)kvh * G * HD + i];
+    const size_t rec = HD + 4;
+
     const float4 *kb = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + t0) * HD);
     const float4 *vb = reinterpret_cast<const float4 *>(vc + ((size_t)kvh * max_seq + t0) * HD);
-    for (int i = tid; i < tn * (HD / 4); i += blockDim.x) {
-        const int r = i / (HD / 4), c = i - r * (HD / 4);
-        *reinterpret_cast<float4 *>(sk + r * KP + 4 * c) = kb[i];
-        *reinterpret_cast<float4 *>(sv + r * HD + 4 * c) = vb[i];
+    float4 kr[NV], vr[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int idx = tid + i * 256;
+        const bool ok = idx / C4 < tn;
+        kr[i] = ok ? kb[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        vr[i] = ok ? vb[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int i = tid; i < G * HD; i += blockDim.x) sq[i] = qkv[(size_t)kvh * G * HD + i];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int idx = tid + i * 256;
+        const int r = idx / C4, c = idx - r * C4;
+        *reinterpret_cast<float4 *>(sk + r * KP + 4 * c) = kr[i];
+        *reinterpret_cast<float4 *>(sv + r * HD + 4 * c) = vr[i];
     }
     __syncthreads();
     for (int i = tid; i < G * T; i += blockDim.x) {
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const DecState *__restrict__
             const float4 *ka = reinterpret_cast<const float4 *>(sk + t * KP);
             float d0 = 0.f, d1 = 0.f;
 #pragma unroll
-            for (int c = 0; c < HD / 4; c += 2) {
+            for (int c = 0; c < C4; c += 2) {
                 const float4 a = qa[c], b = ka[c], a2 = qa[c + 1], b2 = ka[c + 1];
                 d0 = fmaf(a.x, b.x, fmaf(a.y, b.y, fmaf(a.z, b.z, fmaf(a.w, b.w, d0))));
                 d1 = fmaf(a2.x, b2.x, fmaf(a2.y, b2.y, fmaf(a2.z, b2.z, fmaf(a2.w, b2.w, d1))));
@@ -220,43 +228,73 @@ __global__ __launch_bounds__(256) void k_attn_split(const DecState *__restrict__
     }
 }
 
-// Merge of the per-tile partials of one query head:
-//   M = max m_s,  L = sum_s e^(m_s - M) l_s,  o = sum_s e^(m_s - M) o_s / L
-// then the chunk records of the head's output for the O-projection GEMV.
-// blockDim = hd.
-__global__ void k_attn_combine(const DecState *__restrict__ st, const float *__restrict__ part,
-                               float *__restrict__ out, uint32_t *__restrict__ xq, int hd,
-                               int nsplit) {
-    extern __shared__ float sm[];
-    float *so = sm;            // [hd]
-    float *sw = sm + hd;       // [nsplit] tile weights
-    const int h = blockIdx.x, d = threadIdx.x;
-    const size_t rec = hd + 2;
+// Merge of one query head's tiles: M = max m_s, L = sum e^(m_s - M) l_s,
+// o = sum e^(m_s - M) o_s / L; then the head's x chunk records for the O
+// projection.  blockDim = 64: thread = (half of the tiles, float4 column).
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_merge(const DecState *__restrict__ st,
+                                                   const float *__restrict__ part,
+                                                   float *__restrict__ out,
+                                                   uint32_t *__restrict__ xq, int nsplit) {
+    constexpr int C4 = HD / 4;
+    constexpr size_t rec = HD + 4;
+    __shared__ float sw[kMaxTiles];
+    __shared__ float sacc[2 * HD];
+    __shared__ float so[HD];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;
     const float *ph = part + (size_t)h * nsplit * rec;
-    const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;   // tiles holding positions
     float M = -FLT_MAX;
-    for (int s = 0; s < used; ++s) M = fmaxf(M, ph[s * rec + hd]);
-    for (int s = d; s < used; s += blockDim.x) sw[s] = expf(ph[s * rec + hd] - M);
-    __syncthreads();
-    float L = 0.f, acc = 0.f;
-    for (int s = 0; s < used; ++s) {
-        const float wgt = sw[s];
-        L = fmaf(wgt, ph[s * rec + hd + 1], L);
-        acc = fmaf(wgt, ph[s * rec + d], acc);
+    for (int s = tid; s < used; s += 64) M = fmaxf(M, ph[s * rec + HD]);
+    M = wave_max(M);
+    float L = 0.f;
+    for (int s = tid; s < used; s += 64) {
+        const float w = expf(ph[s * rec + HD] - M);
+        sw[s] = w;
+        L = fmaf(w, ph[s * rec + HD + 1], L);
     }
-    const float v = acc * (1.0f / fmaxf(L, 1e-30f));
-    out[(size_t)h * hd + d] = v;
-    so[d] = v;
+    L = wave_sum(L);
+    __syncthreads();
+    if (tid < 2 * C4) {
+        const int half = tid / C4, c = tid - half * C4;
+        const float *pc = ph + 4 * c;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = half; s0 < used; s0 += 32) {
+            float4 v[16];
+            float w[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int s = s0 + 2 * u;
+                const bool ok = s < used;
+                v[u] = ok ? *reinterpret_cast<const float4 *>(pc + s * rec)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                w[u] = ok ? sw[s] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                acc.x = fmaf(w[u], v[u].x, acc.x);
+                acc.y = fmaf(w[u], v[u].y, acc.y);
+                acc.z = fmaf(w[u], v[u].z, acc.z);
+                acc.w = fmaf(w[u], v[u].w, acc.w);
+            }
+        }
+        *reinterpret_cast<float4 *>(sacc + half * HD + 4 * c) = acc;
+    }
+    __syncthreads();
+    const float inv = 1.0f / fmaxf(L, 1e-30f);
+    for (int d = tid; d < HD; d += 64) {
+        const float v = (sacc[d] + sacc[HD + d]) * inv;
+        so[d] = v;
+        out[(size_t)h * HD + d] = v;
+    }
     __syncthreads();
     if (xq) {
-        const int c = hd / 32;
-        const int t = threadIdx.x, rc = t >> 3, sub = t & 7;
-        if (rc < c || (t >> 3) < (int)(blockDim.x >> 3)) {
-            const bool live = rc < c;
-            const float4 vv = live ? reinterpret_cast<const float4 *>(so + rc * 32)[sub]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            build_xrec8(vv, sub, live, xq + ((size_t)h * c + rc) * kXRecDwords);
-        }
+        constexpr int NREC = HD / 32;   // records of this head: 8 lanes each
+        const int rc = tid >> 3, sub = tid & 7;
+        const bool live = rc < NREC;
+        const float4 vv = live ? reinterpret_cast<const float4 *>(so + rc * 32)[sub]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        build_xrec8(vv, sub, live, xq + ((size_t)h * NREC + rc) * kXRecDwords);
     }
 }
 
@@ -365,24 +403,27 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
                      float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
                      hipStream_t s) {
     const int ns = attn_nsplit(max_seq);
+    TB_REQUIRE(ns <= kMaxTiles, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: max_seq_len above " + std::to_string(kMaxTiles * kAttnTile));
     const int G = hq / hkv;
     const float scale = 1.0f / sqrtf((float)hd);
+    const size_t lds = sizeof(float) * ((size_t)G * hd + kAttnTile * (hd + 4) + kAttnTile * hd +
+                                        G * kAttnTile + 2 * G);
+    TB_REQUIRE(lds <= 160 * 1024, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: attention tile does not fit in LDS for this head layout");
     if (hd == 128) {
-        const size_t lds = sizeof(float) * (G * 128 + kAttnTile * 132 + kAttnTile * 128 +
-                                            G * kAttnTile + 2 * G);
-        hipLaunchKernelGGL(k_attn_split<128>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc,
-                           part, hq, hkv, max_seq, ns, scale);
+        hipLaunchKernelGGL(k_attn<128>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc, part,
+                           hq, hkv, max_seq, ns, scale);
+        TB_LAUNCHED();
+        hipLaunchKernelGGL(k_attn_merge<128>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
     } else if (hd == 64) {
-        const size_t lds = sizeof(float) * (G * 64 + kAttnTile * 68 + kAttnTile * 64 +
-                                            G * kAttnTile + 2 * G);
-        hipLaunchKernelGGL(k_attn_split<64>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc,
-                           part, hq, hkv, max_seq, ns, scale);
+        hipLaunchKernelGGL(k_attn<64>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc, part,
+                           hq, hkv, max_seq, ns, scale);
+        TB_LAUNCHED();
+        hipLaunchKernelGGL(k_attn_merge<64>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
     } else {
         return fail(TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: head_dim must be 64 or 128");
     }
-    TB_LAUNCHED();
-    hipLaunchKernelGGL(k_attn_combine, dim3(hq), dim3(hd), sizeof(float) * (hd + ns), s, st, part,
-                       out, xq, hd, ns);
     TB_LAUNCHED();
     return TB_OK;
 }

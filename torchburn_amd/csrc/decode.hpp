@@ -18,12 +18,14 @@ struct DecState {
 constexpr int kMaxHidden = 8192;   // RMSNorm keeps one hidden vector in LDS
 constexpr int kAttnTile = 64;      // KV positions per attention block
 constexpr int kArgmaxBlocks = 256;
+constexpr int kMaxTiles = 1024;     // max_seq_len <= kMaxTiles * kAttnTile
 
 int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
                    uint32_t *xq, int H, float eps, hipStream_t s);
 int launch_rope_kv(const DecState *st, float *qkv, const float *cos_t, const float *sin_t,
                    float *kc, float *vc, int hq, int hkv, int hd, int max_seq, hipStream_t s);
 int attn_nsplit(int max_seq);
+// part: [hq][attn_nsplit(max_seq)][hd + 4] floats of scratch.
 int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
                      float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
                      hipStream_t s);

@@ -362,7 +362,7 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
                "TB_UNSUPPORTED: hidden, intermediate and num_heads*head_dim must be multiples of 32");
     TB_REQUIRE(c.hidden_size <= kMaxHidden, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: hidden_size > " + std::to_string(kMaxHidden));
-    TB_REQUIRE(c.max_seq_len > 0 && c.max_seq_len < (1 << 24) && c.vocab_size > 0 &&
+    TB_REQUIRE(c.max_seq_len > 0 && c.max_seq_len <= kMaxTiles * kAttnTile && c.vocab_size > 0 &&
                    c.num_layers > 0,
                TB_ERR_VALUE, "max_seq_len, vocab_size and num_layers must be positive");
 
@@ -397,7 +397,7 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
         (rc = d->alloc(&d->x, d->H * 4)) || (rc = d->alloc(&d->xn, d->H * 4)) ||
         (rc = d->alloc(&d->qkv, d->tq * 4)) || (rc = d->alloc(&d->attn, d->hq * d->hd * 4)) ||
         (rc = d->alloc(&d->h, (size_t)d->I * 4)) || (rc = d->alloc(&d->logits, (size_t)d->V * 4)) ||
-        (rc = d->alloc(&d->part, (size_t)d->hq * d->nsplit * (d->hd + 2) * 4)) ||
+        (rc = d->alloc(&d->part, (size_t)d->hq * d->nsplit * (d->hd + 4) * 4)) ||
         (rc = d->alloc(&d->am_v, kArgmaxBlocks * 4)) || (rc = d->alloc(&d->am_i, kArgmaxBlocks * 4)) ||
         (rc = d->alloc(&d->history, (size_t)d->hist_cap * 4)) ||
         (rc = d->alloc(&d->state, sizeof(DecState))) ||
