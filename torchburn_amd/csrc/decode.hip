@@ -45,52 +45,46 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
 //   xn = (x * (1 / sqrt(sum(x^2) / H + eps))) * w
 // (fast_rms_norm, src/quantization/fused_ops.rs:1066-1089; the AVX-512 tier's
 // x * inv_rms * w order), and the chunk records of xn for the next INT4 GEMV.
-// One block; H <= kMaxHidden.
-__global__ __launch_bounds__(1024) void k_rmsnorm(const DecState *__restrict__ st,
-                                                  const float *__restrict__ embed,
-                                                  float *__restrict__ x,
-                                                  const float *__restrict__ w,
-                                                  float *__restrict__ xn,
-                                                  uint32_t *__restrict__ xq, int H, float eps) {
-    __shared__ float sxn[kMaxHidden];
+// Each block recomputes the whole sum of squares (H floats from L2, the same
+// order in every block, so every block gets the same inverse) and normalises
+// and records kNormChunks 32-element chunks of its own.
+__global__ __launch_bounds__(256) void k_rmsnorm(const DecState *__restrict__ st,
+                                                 const float *__restrict__ embed,
+                                                 float *__restrict__ x,
+                                                 const float *__restrict__ w,
+                                                 float *__restrict__ xn,
+                                                 uint32_t *__restrict__ xq, int H, float eps) {
     __shared__ float scratch[16];
     const int tid = threadIdx.x;
+    const float *src = embed ? embed + (size_t)st->token * H : x;
+    const float4 *s4 = reinterpret_cast<const float4 *>(src);
     float ss = 0.f;
-    if (embed) {
-        const float *e = embed + (size_t)st->token * H;
-        for (int i = tid; i < H; i += blockDim.x) {
-            const float v = e[i];
-            x[i] = v;
-            sxn[i] = v;
-            ss = fmaf(v, v, ss);
-        }
-    } else {
-        for (int i = tid; i < H; i += blockDim.x) {
-            const float v = x[i];
-            sxn[i] = v;
-            ss = fmaf(v, v, ss);
-        }
+    for (int i = tid; i < H / 4; i += blockDim.x) {
+        const float4 v = s4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
     }
     const float tot = block_sum(ss, scratch);
     const float rms = sqrtf(tot / (float)H + eps);
     const float inv = 1.0f / rms;
-    for (int i = tid; i < H; i += blockDim.x) {
-        const float v = __fmul_rn(__fmul_rn(sxn[i], inv), w[i]);
-        sxn[i] = v;
-        xn[i] = v;
+    const int c = H / 32;
+    const int rec = blockIdx.x * kNormChunks + (tid >> 3), sub = tid & 7;
+    const bool live = rec < c && (tid >> 3) < kNormChunks;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+        const int i4 = rec * 8 + sub;
+        const float4 v = s4[i4];
+        if (embed) reinterpret_cast<float4 *>(x)[i4] = v;
+        const float4 ww = reinterpret_cast<const float4 *>(w)[i4];
+        o.x = __fmul_rn(__fmul_rn(v.x, inv), ww.x);
+        o.y = __fmul_rn(__fmul_rn(v.y, inv), ww.y);
+        o.z = __fmul_rn(__fmul_rn(v.z, inv), ww.z);
+        o.w = __fmul_rn(__fmul_rn(v.w, inv), ww.w);
+        reinterpret_cast<float4 *>(xn)[i4] = o;
     }
-    __syncthreads();
-    if (xq) {
-        const int c = H / 32;
-        for (int base = 0; base < c * 8; base += blockDim.x) {
-            const int t = base + tid;
-            const int rec = t >> 3, sub = t & 7;
-            const bool live = rec < c;
-            const float4 v = live ? reinterpret_cast<const float4 *>(sxn + rec * 32)[sub]
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-            build_xrec8(v, sub, live, xq + (size_t)rec * kXRecDwords);
-        }
-    }
+    if (xq) build_xrec8(o, sub, live, xq + (size_t)rec * kXRecDwords);
 }
 
 // Rotate-half RoPE on the q and k heads of qkv and the KV-cache append at the
@@ -384,7 +378,8 @@ int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float
     TB_REQUIRE(H <= kMaxHidden && H % 32 == 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: hidden size must be a multiple of 32 and <= " +
                    std::to_string(kMaxHidden));
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, s, st, embed, x, w, xn, xq, H, eps);
+    const int blocks = (H / 32 + kNormChunks - 1) / kNormChunks;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(blocks), dim3(256), 0, s, st, embed, x, w, xn, xq, H, eps);
     TB_LAUNCHED();
     return TB_OK;
 }

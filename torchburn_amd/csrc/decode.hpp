@@ -15,7 +15,8 @@ struct DecState {
     int argmax;   // argmax of the last step's logits
 };
 
-constexpr int kMaxHidden = 8192;   // RMSNorm keeps one hidden vector in LDS
+constexpr int kMaxHidden = 8192;   // largest hidden size the decoder accepts
+constexpr int kNormChunks = 32;    // 32-element chunks normalised per RMSNorm block
 constexpr int kAttnTile = 64;      // KV positions per attention block
 constexpr int kArgmaxBlocks = 256;
 constexpr int kMaxTiles = 1024;     // max_seq_len <= kMaxTiles * kAttnTile

@@ -116,19 +116,21 @@ struct Decoder {
     // One projection y = W x [+ bias] [+ residual] or the gate/up pair.
     int proj(int bits, const float *xin, const uint32_t *xq, const void *w, const float *s,
              const float *b, const void *w2, const float *s2, const float *res, float *y,
-             int n, int k, int epi) {
+             int n, int k, int epi, const RopeArgs *rope = nullptr) {
         if (bits == 4) {
             W4Params p{};
             p.x = xin; p.xq = xq;
             p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
             p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
             p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k; p.gshift = gshift(gs);
+            if (rope) p.rope = *rope;
             return w4_gemv(p, epi, st);
         }
         DenseParams p{};
         p.x = xin; p.w0 = w; p.rs0 = s; p.rs0_len = s ? n : 0; p.b0 = b;
         p.w1 = w2; p.rs1 = s2; p.rs1_len = s2 ? n : 0;
         p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k;
+        if (rope) p.rope = *rope;
         return dense_gemv(p, bits == 8 ? W_I8 : W_F32, epi, st);
     }
 
@@ -143,10 +145,10 @@ struct Decoder {
             rc = launch_rmsnorm(state, l == 0 ? embed : nullptr, x, y.in_norm, xn,
                                 q4 ? xq_h : nullptr, H, eps, st);
             if (rc) return rc;
+            // QKV projection + bias + RoPE + KV-cache append in one kernel.
+            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq};
             rc = proj(wbits, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv,
-                      tq, H, EPI_PLAIN);
-            if (rc) return rc;
-            rc = launch_rope_kv(state, qkv, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, st);
+                      tq, H, EPI_ROPE, &ra);
             if (rc) return rc;
             rc = launch_attention(state, qkv, kcl, vcl, part, attn, q4 ? xq_a : nullptr, hq, hkv,
                                   hd, max_seq, st);

@@ -115,6 +115,13 @@ inline bool make_layout(int c, int logv, int j, Layout &L) {
     return true;
 }
 
+// Rotation-pair order of the rows of a head: logical rows 2i and 2i+1 of head
+// h are physical rows h*hd + i and h*hd + i + hd/2.
+__device__ __forceinline__ int rope_row(int l, int hd) {
+    const int head = l / hd, r = l - head * hd, i = r >> 1;
+    return head * hd + ((r & 1) ? i + (hd >> 1) : i);
+}
+
 // Output side of a GEMV block.  Row scales (per-channel INT8) multiply the row
 // dot before bias: y = dot * s + b, as the reference's w8a32 rows do
 // (src/quantization/gemv.rs:777-785).
@@ -125,6 +132,7 @@ struct Epi {
     const float *res;         // residual [m, n] for EPI_RESID
     float *y;                 // output [m, n]
     int n, m;
+    RopeArgs rope;            // EPI_ROPE (m == 1)
 };
 
 __device__ __forceinline__ float row_scale(const float *rs, int len, int row) {
@@ -160,7 +168,38 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, cons
                 if (DUAL) a1 += rw[(J + j) * M + m];
             }
             const size_t o = (size_t)m * e.n + row;
-            if (EPI == EPI_SWIGLU) {
+            if (EPI == EPI_ROPE) {
+                // Both rows of the rotation pair are in this block: logical rows
+                // lr and lr ^ 1 (RoPE: src/llm/decoder.rs:28-68, products
+                // rounded separately; KV append: decoder.rs:1137-1146).
+                const RopeArgs &R = e.rope;
+                const int lr = row, pl = lr ^ 1;
+                const int pj = (pl - row0) / L.rps, pr2 = (pl - row0) - pj * L.rps;
+                float ap = 0.f;
+                for (int w = 0; w < L.nwaves; ++w) ap += red[(w * L.rps + pr2) * V + pj * M];
+                const int prow = rope_row(lr, R.hd), qrow = rope_row(pl, R.hd);
+                const float own = a0 * row_scale(e.rs0, e.rs0_len, prow) + (e.b0 ? e.b0[prow] : 0.f);
+                const float oth = ap * row_scale(e.rs0, e.rs0_len, qrow) + (e.b0 ? e.b0[qrow] : 0.f);
+                const int head = prow / R.hd, r = prow - head * R.hd, half = R.hd >> 1;
+                const int pos = *R.pos;
+                float val = own;
+                if (head < R.hq + R.hkv) {
+                    const int i = r < half ? r : r - half;
+                    const float c = R.cos_t[(size_t)pos * R.hd + r];
+                    const float s = R.sin_t[(size_t)pos * R.hd + r];
+                    // r < half: own = x1, oth = x2 -> x1*c - x2*s; else own = x2 -> x2*c + x1*s
+                    val = r < half ? __fsub_rn(__fmul_rn(own, c), __fmul_rn(oth, s))
+                                   : __fadd_rn(__fmul_rn(own, c), __fmul_rn(oth, s));
+                    (void)i;
+                }
+                if (head < R.hq) {
+                    e.y[prow] = val;
+                } else if (head < R.hq + R.hkv) {
+                    R.kc[((size_t)(head - R.hq) * R.max_seq + pos) * R.hd + r] = val;
+                } else {
+                    R.vc[((size_t)(head - R.hq - R.hkv) * R.max_seq + pos) * R.hd + r] = val;
+                }
+            } else if (EPI == EPI_SWIGLU) {
                 const float g = a0 * row_scale(e.rs0, e.rs0_len, row) + (e.b0 ? e.b0[row] : 0.f);
                 const float u = a1 * row_scale(e.rs1, e.rs1_len, row) + (e.b1 ? e.b1[row] : 0.f);
                 e.y[o] = silu(g) * u;

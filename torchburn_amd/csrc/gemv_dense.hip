@@ -90,7 +90,7 @@ struct DenseGemv {
             const int row_raw = row0 + j * L.rps + rr;
             const bool ok = act && row_raw < p.n;
             bt.ok |= ok ? (1u << j) : 0u;
-            const int row = ok ? row_raw : 0;
+            const int row = !ok ? 0 : (EPI == EPI_ROPE ? rope_row(row_raw, p.rope.hd) : row_raw);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const uint8_t *w = static_cast<const uint8_t *>(d ? p.w1 : p.w0);
@@ -177,6 +177,10 @@ int launch(const DenseParams &p, hipStream_t st) {
     Epi e{};
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m;
     e.rs0 = p.rs0; e.rs1 = p.rs1; e.rs0_len = p.rs0_len; e.rs1_len = p.rs1_len;
+    e.rope = p.rope;
+    if (EPI == EPI_ROPE)
+        TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
+                   TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
     const int grid = (p.n + L.rpb - 1) / L.rpb;
     hipLaunchKernelGGL((k_dense_gemv<WT, M, J, DUAL, EPI>), dim3(grid), dim3(L.nwaves * 64), 0,
                        st, p, L, e);
@@ -200,6 +204,7 @@ template <int WT>
 int dispatch_epi(const DenseParams &p, int epi, hipStream_t st) {
     if (p.w1 != nullptr) return dispatch_m<WT, true, EPI_SWIGLU>(p, st);
     if (epi == EPI_RESID) return dispatch_m<WT, false, EPI_RESID>(p, st);
+    if (epi == EPI_ROPE) return launch<WT, 1, WT == W_I8 ? 8 : 4, false, EPI_ROPE>(p, st);
     return dispatch_m<WT, false, EPI_PLAIN>(p, st);
 }
 

@@ -23,6 +23,7 @@ struct DenseParams {
     const float *res;   // [m, n] residual for EPI_RESID
     float *y;           // [m, n]
     int m, n, k;
+    RopeArgs rope;      // EPI_ROPE only
 };
 
 // One pass over m <= kMaxRowsPerPass activation rows; shapes validated by the

@@ -137,7 +137,8 @@ struct W4Gemv {
             const int row_raw = row0 + j * L.rps + rr;
             const bool ok = act && row_raw < p.n;
             bt.ok |= ok ? (1u << j) : 0u;
-            const int row = ok ? row_raw : 0;   // rows past N re-read row 0 with weight 0
+            // rows past N re-read row 0 with weight 0
+            const int row = !ok ? 0 : (EPI == EPI_ROPE ? rope_row(row_raw, p.rope.hd) : row_raw);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const uint8_t *w = d ? p.w1 : p.w0;
@@ -240,7 +241,10 @@ int launch(const W4Params &p, hipStream_t st) {
     TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32 GEMV supports K <= " + std::to_string(kMaxWaves * 64 * 32));
     Epi e{};
-    e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m;
+    e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m; e.rope = p.rope;
+    if (EPI == EPI_ROPE)
+        TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
+                   TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
     const int grid = (p.n + L.rpb - 1) / L.rpb;
     hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI>), dim3(grid), dim3(L.nwaves * 64), 0, st, p, L,
                        e);
@@ -279,6 +283,7 @@ int w4_gemv(W4Params p, int epi, hipStream_t st) {
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4 GEMV needs K % 32 == 0");
     if (p.w1 != nullptr) return dispatch_m<true, EPI_SWIGLU>(p, st);
     if (epi == EPI_RESID) return dispatch_m<false, EPI_RESID>(p, st);
+    if (epi == EPI_ROPE) return launch<1, 16, false, EPI_ROPE>(p, st);
     return dispatch_m<false, EPI_PLAIN>(p, st);
 }
 

@@ -6,7 +6,18 @@
 
 namespace tb {
 
-enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE = 3 };
+
+// EPI_ROPE: the QKV projection of a decoder step writes rotated q into y and
+// the rotated k / plain v row of the current position into the KV cache.
+// Output rows are visited in rotation-pair order (see rope_row) so each block
+// holds both halves of every pair it rotates.
+struct RopeArgs {
+    const int *pos;           // device: current position
+    const float *cos_t, *sin_t;   // [max_seq, hd] tables
+    float *kc, *vc;           // this layer's caches [hkv, max_seq, hd]
+    int hq, hkv, hd, max_seq;
+};
 
 // Activation rows per GEMV pass (x is held in VGPRs).
 constexpr int kMaxRowsPerPass = 2;
@@ -31,6 +42,7 @@ struct W4Params {
     int m, n, k;
     int gshift;        // log2(group_size)
     int rows_j;        // rows per block (tuning: 4, 8 or 16; 0 = default)
+    RopeArgs rope;     // EPI_ROPE only
 };
 
 // One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
