@@ -139,6 +139,7 @@ __global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
                                               int max_seq, int nsplit, float scale) {
     constexpr int T = kAttnTile, KP = HD + 4, C4 = HD / 4;
     constexpr int NV = T * C4 / 256;   // float4 of K (and of V) per thread
+    static_assert(T <= 64 && NV >= 1, "tile of at most one wave of positions");
     extern __shared__ float sm[];
     const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
     const int G = hq / hkv;
@@ -192,11 +193,11 @@ __global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
     __syncthreads();
     const int lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     for (int g = wave; g < G; g += nw) {
-        const float s = ss[g * T + lane];
+        const float s = lane < T ? ss[g * T + lane] : -FLT_MAX;
         const float m = wave_max(s);
         const float p = lane < tn ? expf(s - m) : 0.f;
         const float l = wave_sum(p);
-        ss[g * T + lane] = p;
+        if (lane < T) ss[g * T + lane] = p;
         if (lane == 0) {
             sml[2 * g] = m;
             sml[2 * g + 1] = l;
