@@ -67,6 +67,29 @@ def cpu_info():
     return model, sorted(f for f in flags if f in keep)
 
 
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "k_w4_gemv_swiglu_llama8b_mlp_m1_pmc.md")
+
+
+def pmc_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc summary:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) times the scale factors that a
+    plain copy kernel of known size gives for the same counters."""
+    try:
+        kv = {}
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if ":" in line and line.split(":")[0].strip() in (
+                        "fetch_kib_per_dispatch", "write_kib_per_dispatch", "fetch_scale",
+                        "write_scale"):
+                    a, b = line.split(":", 1)
+                    kv[a.strip()] = float(b)
+        return int(round(1024 * (kv["fetch_kib_per_dispatch"] * kv["fetch_scale"] +
+                                 kv["write_kib_per_dispatch"] * kv["write_scale"])))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def graph_time(torch, fn, reps, warmup):
     """Capture fn() once, replay it `reps` times; returns ms per replay."""
     st = torch.cuda.Stream()
@@ -262,7 +285,11 @@ def main():
                    "step_bytes": r["step_bytes"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "kernel": "k_w4_gemv (gate/up pair, silu*up epilogue)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic() if args.m == 1 else None,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
+                                       "(copy-kernel calibration), "
+                                       "profiles/k_w4_gemv_swiglu_llama8b_mlp_m1_pmc.md",
                      "avg_us": round(r["gu_us"], 3), "bytes_per_launch": r["gu_bytes"],
                      "down_kernel_avg_us": round(r["dn_us"], 3),
                      "down_kernel_gbs": round(r["dn_bytes"] / (r["dn_us"] * 1e-6) / 1e9, 1)},
