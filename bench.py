@@ -32,6 +32,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK = 157.3   # TFLOP/s, dense FP32 MFMA
 
 
 def parse():
@@ -46,6 +47,10 @@ def parse():
     ap.add_argument("--decode", default="llama4,llama8,qwen",
                     help="decode runs: comma list of llama4, llama8, qwen, or 'none'")
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--batched", default="16x4096,16x14336,64x4096,64x14336",
+                    help="config 3 MxN projections (K=4096) on FP32 MFMA, or 'none'")
+    ap.add_argument("--mlp-batches", default="4,8",
+                    help="config 2 batch sizes M > 1 for the fused MLP, or 'none'")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (FETCH_SIZE / "
                          "WRITE_SIZE calibration for rocprofv3 --pmc), then exit")
@@ -205,6 +210,78 @@ def mlp_section(torch, args, dev):
                 dn_bytes=dn_bytes, max_rel=max_rel, cpu=cpu)
 
 
+def int4_set(torch, dev, gen, n, k, gs=32):
+    w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s = torch.randn((n, k // gs), device=dev, generator=gen).mul_(0.02).abs_().add_(1e-3)
+    return w, s
+
+
+def batched_section(torch, args, dev):
+    """Config 3: Y[M, N] = X[M, 4096] . deq(W)^T on FP32 MFMA, M in {16, 64}."""
+    from torchburn_amd import _lib
+    K, GS = 4096, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x7B + 3)
+    out = {}
+    S = lambda: torch.cuda.current_stream(dev).cuda_stream
+    for spec in args.batched.split(","):
+        M, N = (int(v) for v in spec.split("x"))
+        copies = max(4, -(-300 * 2**20 // (N * K * 5 // 8)))   # > 256 MB of weights rotate
+        sets = [int4_set(torch, dev, gen, N, K, GS) for _ in range(copies)]
+        x = torch.randn((M, K), device=dev, generator=gen)
+        y = torch.empty((M, N), device=dev)
+
+        def run():
+            for w, s in sets:
+                _lib.call("tb_w4a32_grouped_linear", x.data_ptr(), w.data_ptr(), s.data_ptr(),
+                          None, y.data_ptr(), M, N, K, GS, S())
+
+        reps = 20
+        ms, _ = graph_time(torch, run, reps, 3)
+        us = ms * 1e3 / len(sets)
+        flops = 2.0 * M * N * K
+        wbytes = N * K // 2 + 4 * N * (K // GS)
+        out[f"m{M}_n{N}"] = {"us": round(us, 3), "tflops": round(flops / us / 1e6, 2),
+                             "frac_fp32_mfma_peak": round(flops / us / 1e6 / MFMA_F32_PEAK, 4),
+                             "weight_gbs": round(wbytes / us / 1e3, 1),
+                             "weight_copies_rotated": copies}
+        del sets
+    torch.cuda.empty_cache()
+    return out
+
+
+def mlp_batch_section(torch, args, dev):
+    """Config 2 at M > 1: the fused SwiGLU MLP with residual through the public
+    entry point, 4 rotating weight copies; GB/s of the weight + activation bytes."""
+    from torchburn_amd import _lib
+    K, I, GS = 4096, 14336, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x7B + 2)
+    sets = [(*int4_set(torch, dev, gen, I, K), *int4_set(torch, dev, gen, I, K),
+             *int4_set(torch, dev, gen, K, I)) for _ in range(4)]
+    S = lambda: torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    for M in (int(v) for v in args.mlp_batches.split(",")):
+        x = torch.randn((M, K), device=dev, generator=gen)
+        r = torch.randn((M, K), device=dev, generator=gen)
+        o = torch.empty((M, K), device=dev)
+
+        def run():
+            for gw, gs, uw, us, dw, ds in sets:
+                _lib.call("tb_fused_swiglu_mlp_w4a32", x.data_ptr(), gw.data_ptr(), gs.data_ptr(),
+                          None, uw.data_ptr(), us.data_ptr(), None, dw.data_ptr(), ds.data_ptr(),
+                          None, r.data_ptr(), o.data_ptr(), M, K, I, K, GS, S())
+
+        ms, _ = graph_time(torch, run, 25, 3)
+        us = ms * 1e3 / len(sets)
+        byts = 3 * (I * K // 2 + 4 * I * (K // GS)) + 4 * (M * K + 2 * M * I + 2 * M * K)
+        out[f"m{M}"] = {"us": round(us, 3), "gbs": round(byts / us / 1e3, 1),
+                        "tok_s": round(M / us * 1e6, 1)}
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_run(torch, name, steps):
     from torchburn_amd import synth
     from torchburn_amd.decoder import decoder_from_weights
@@ -265,6 +342,8 @@ def main():
     r = mlp_section(torch, args, dev)
     gbs = r["step_bytes"] / (r["ms"] * 1e-3) / 1e9
     gu_gbs = r["gu_bytes"] / (r["gu_us"] * 1e-6) / 1e9
+    batched = batched_section(torch, args, dev) if args.batched != "none" else {}
+    mlp_batches = mlp_batch_section(torch, args, dev) if args.mlp_batches != "none" else {}
     decode = {}
     if args.decode != "none":
         for name in args.decode.split(","):
@@ -294,6 +373,8 @@ def main():
                      "down_kernel_avg_us": round(r["dn_us"], 3),
                      "down_kernel_gbs": round(r["dn_bytes"] / (r["dn_us"] * 1e-6) / 1e9, 1)},
         "decode": decode,
+        "batched_mfma": batched,
+        "mlp_batches": mlp_batches,
         "cpu_baseline": r["cpu"],
         "parity_max_rel": r["max_rel"],
         "wall_s": round(time.perf_counter() - t_start, 1),

@@ -13,6 +13,7 @@
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
+#include "w4_mfma.hpp"
 
 namespace tb {
 
@@ -36,6 +37,12 @@ int env_int(const char *name, int dflt) {
 int rows_j_env() {
     static int v = env_int("TB_W4_J", 0);
     return v;
+}
+// Activation rows from which INT4 projections run on FP32 MFMA instead of the
+// GEMV (TB_MFMA_MIN_M overrides; tuning sweeps only).
+int64_t mfma_min_m() {
+    static int v = env_int("TB_MFMA_MIN_M", 16);
+    return v < 1 ? 1 : v;
 }
 }  // namespace
 
@@ -92,6 +99,22 @@ static W4Params w4_params(const float *x, const uint8_t *w, const float *s, cons
     p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
     p.rows_j = rows_j_env();
     return p;
+}
+
+static MfmaParams mfma_params(const float *x, const uint8_t *w, const float *s, const float *b,
+                              float *y, int64_t m, int64_t n, int64_t k, int64_t gs) {
+    MfmaParams p{};
+    p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
+    return p;
+}
+
+// The MFMA projection with its split-K partials in the library workspace.
+static int mfma_ws(const MfmaParams &p, int epi, hipStream_t st) {
+    void *ws = nullptr;
+    int rc = workspace(w4_mfma_partials_bytes(p.m, p.n, p.k, p.w1 != nullptr), &ws);
+    if (rc) return rc;
+    return w4_mfma(p, epi, static_cast<float *>(ws), st);
 }
 
 static size_t xq_bytes(int64_t m, int64_t k) {
@@ -165,6 +188,9 @@ int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float
     if (rc) return rc;
     TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_grouped_linear: null output");
     if (m == 0 || n == 0) return TB_OK;
+    if (m >= mfma_min_m())
+        return mfma_ws(mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size),
+                       EPI_PLAIN, (hipStream_t)stream);
     void *ws = nullptr;
     rc = workspace(xq_bytes(m, k), &ws);
     if (rc) return rc;
@@ -181,6 +207,11 @@ int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
     TB_REQUIRE(out && residual, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32_grouped_linear_residual: null output or residual");
     if (m == 0 || n == 0) return TB_OK;
+    if (m >= mfma_min_m()) {
+        MfmaParams q = mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size);
+        q.res = residual;
+        return mfma_ws(q, EPI_RESID, (hipStream_t)stream);
+    }
     void *ws = nullptr;
     rc = workspace(xq_bytes(m, k), &ws);
     if (rc) return rc;
@@ -199,6 +230,11 @@ int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
     if (rc) return rc;
     TB_REQUIRE(h, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: swiglu_w4a32: null output");
     if (m == 0 || inter == 0) return TB_OK;
+    if (m >= mfma_min_m()) {
+        MfmaParams q = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+        q.w1 = up_w; q.s1 = up_s; q.b1 = up_b;
+        return mfma_ws(q, EPI_SWIGLU, (hipStream_t)stream);
+    }
     void *ws = nullptr;
     rc = workspace(xq_bytes(m, k), &ws);
     if (rc) return rc;
@@ -223,8 +259,26 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
     TB_REQUIRE(down_w && down_s && out, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: null down weight or output");
     if (m == 0 || n_out == 0) return TB_OK;
-    // Workspace: h [m, inter] f32 | chunk records of x | chunk records of h.
+    // Workspace: h [m, inter] f32 | chunk records of x | chunk records of h,
+    // or on the MFMA path h | split-K partials.
     const size_t hb = ((size_t)m * (size_t)inter * sizeof(float) + 255) & ~(size_t)255;
+    if (m >= mfma_min_m()) {
+        const size_t pg = w4_mfma_partials_bytes((int)m, (int)inter, (int)k, true);
+        const size_t pd = w4_mfma_partials_bytes((int)m, (int)n_out, (int)inter, false);
+        void *ws = nullptr;
+        rc = workspace(hb + (pg > pd ? pg : pd), &ws);
+        if (rc) return rc;
+        float *h = static_cast<float *>(ws);
+        float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + hb);
+        hipStream_t st = (hipStream_t)stream;
+        MfmaParams g = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+        g.w1 = up_w; g.s1 = up_s; g.b1 = up_b;
+        rc = w4_mfma(g, EPI_SWIGLU, part, st);
+        if (rc) return rc;
+        MfmaParams d = mfma_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
+        d.res = residual;
+        return w4_mfma(d, residual ? EPI_RESID : EPI_PLAIN, part, st);
+    }
     const size_t xb = (xq_bytes(m, k) + 255) & ~(size_t)255;
     void *ws = nullptr;
     rc = workspace(hb + xb + xq_bytes(m, inter), &ws);
@@ -266,6 +320,11 @@ int tb_w4a32_gemv_xq(const float *x, const uint32_t *xq, const uint8_t *w_packed
     TB_REQUIRE(out && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32_gemv_xq: null output or unaligned records");
     if (m == 0 || n == 0) return TB_OK;
+    if (m >= mfma_min_m()) {
+        MfmaParams q = mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size);
+        q.res = residual;
+        return mfma_ws(q, residual ? EPI_RESID : EPI_PLAIN, (hipStream_t)stream);
+    }
     W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
     p.res = residual;
     return w4_rows(p, residual ? EPI_RESID : EPI_PLAIN, m, const_cast<uint32_t *>(xq), false,
@@ -283,6 +342,11 @@ int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t *gate_w
     TB_REQUIRE(h && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: swiglu_w4a32_xq: null output or unaligned records");
     if (m == 0 || inter == 0) return TB_OK;
+    if (m >= mfma_min_m()) {
+        MfmaParams q = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+        q.w1 = up_w; q.s1 = up_s; q.b1 = up_b;
+        return mfma_ws(q, EPI_SWIGLU, (hipStream_t)stream);
+    }
     W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
     p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
     return w4_rows(p, EPI_SWIGLU, m, const_cast<uint32_t *>(xq), false, (hipStream_t)stream);

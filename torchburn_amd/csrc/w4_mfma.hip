@@ -1,0 +1,229 @@
+// Batched grouped-INT4 projection Y[M, N] = X[M, K] . deq(W)^T on FP32 MFMA
+// (v_mfma_f32_16x16x4_f32), for M >= 16 where the work is a dense contraction.
+//
+// Replaces the M > 1 path of the reference's w4a32_grouped_linear
+// (src/quantization/packed_v2.rs:557-624 -> gemm_w4a32_grouped,
+// src/quantization/gemv.rs:1690-1725), which runs one full GEMV per activation
+// row and so reads the weights M times; here every weight byte is read once per
+// 64 activation rows.  The batched SwiGLU of fused_swiglu_mlp_batched_w4a32
+// (src/quantization/fused_ops.rs:1267-1319: gate GEMM, up GEMM, silu * up,
+// down GEMM) maps onto the dual launch plus the SwiGLU reduce epilogue.
+//
+// Tiling.  A block (4 waves) owns 64 weight rows (16 per wave) x up to 64
+// activation rows (MT tiles of 16) x a K range of `klen` (split-K over blocks,
+// partial sums reduced by k_mfma_reduce in a fixed order, so results are
+// deterministic).  Per 128-wide K step:
+//   * X [16*MT, 128] is staged once per block in LDS (row pitch 132 floats,
+//     so the 16 rows of an MFMA operand read fall on distinct banks) and read
+//     by all four waves;
+//   * each lane loads one 16-byte chunk of its weight row (32 nibbles = one
+//     group at g32, half of one at g64) plus the group scale, and dequantizes
+//     it in registers straight into the MFMA B operand: (nib - 8) * s as
+//     fma(nib, s, -8 s).  Each weight element is used by exactly one wave, so
+//     staging W in LDS would only add traffic.
+//   * MFMA operand layout (16x16x4, one block): lane l supplies A[l % 16][l / 16]
+//     and B[l / 16][l % 16]; D[4 (l / 16) + r][l % 16] comes back in register r.
+//     The four lane groups q = l / 16 take K sub-ranges 32q..32q+31 of the step,
+//     so one MFMA consumes element e of each group's 32; the K order inside a
+//     contraction is free as long as A and B agree.
+//   * the next step's X tile, weight chunk and scale are loaded into registers
+//     before the current step's MFMAs are issued.
+#include <float.h>
+
+#include "gemv_common.hpp"
+#include "tb_common.hpp"
+#include "w4_gemv.hpp"
+#include "w4_mfma.hpp"
+
+namespace tb {
+
+using namespace gemv;
+
+namespace {
+
+constexpr int kBN = 64;        // weight rows per block
+constexpr int kBK = 128;       // K per step
+constexpr int kXP = kBK + 4;   // LDS row pitch of the X tile (floats)
+constexpr int kTargetBlocks = 512;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
+                                                 const uint8_t *__restrict__ w0,
+                                                 const float *__restrict__ s0,
+                                                 const uint8_t *__restrict__ w1,
+                                                 const float *__restrict__ s1,
+                                                 float *__restrict__ part, int m, int n, int k,
+                                                 int gshift, int klen, int nbx, int splits) {
+    constexpr int XV = MT * 2;   // float4 of the X tile per thread
+    __shared__ float xs[MT * 16 * kXP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int bx = blockIdx.x;
+    const int second = bx >= nbx ? 1 : 0;   // dual launch: blocks of the up projection
+    bx -= second * nbx;
+    const uint8_t *w = second ? w1 : w0;
+    const float *s = second ? s1 : s0;
+    const int m0 = blockIdx.z * MT * 16;
+    const int kb = blockIdx.y * klen;
+    const int ke = min(k, kb + klen);
+    const int row = bx * kBN + wave * 16 + (lane & 15);
+    const int q = lane >> 4;
+    const bool rok = row < n;
+    const uint8_t *wrow = w + (size_t)(rok ? row : 0) * (size_t)(k >> 1);
+    const float *srow = s + (size_t)(rok ? row : 0) * (size_t)(k >> gshift);
+
+    float4 xr[XV];
+    u32x4 wr;
+    float sr;
+    auto load_step = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int f = tid + 256 * i;
+            const int r = f >> 5, c = (f & 31) * 4;
+            const bool ok = (m0 + r < m) && (k0 + c < ke);
+            xr[i] = ok ? *reinterpret_cast<const float4 *>(x + (size_t)(m0 + r) * k + k0 + c)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const int kk = k0 + 32 * q;
+        const bool ok = rok && kk < ke;
+        wr = ok ? load_nt16(wrow + (kk >> 1)) : u32x4{0u, 0u, 0u, 0u};
+        sr = ok ? srow[kk >> gshift] : 0.f;
+    };
+
+    f32x4 acc[MT][2];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_step(kb);
+    for (int k0 = kb; k0 < ke; k0 += kBK) {
+        __syncthreads();   // the previous step's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int f = tid + 256 * i;
+            *reinterpret_cast<float4 *>(xs + (f >> 5) * kXP + (f & 31) * 4) = xr[i];
+        }
+        const u32x4 cw = wr;
+        const float sc = sr;
+        __syncthreads();
+        if (k0 + kBK < ke) load_step(k0 + kBK);
+        const float nsc = -8.0f * sc;
+        const uint32_t dws[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = dws[d] & 0x0F0F0F0Fu, hi = (dws[d] >> 4) & 0x0F0F0F0Fu;
+            float b[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                b[2 * i] = fmaf((float)((lo >> (8 * i)) & 0xFFu), sc, nsc);
+                b[2 * i + 1] = fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, nsc);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const float *xa = xs + (t * 16 + (lane & 15)) * kXP + 32 * q + 8 * d;
+                const float4 a0 = *reinterpret_cast<const float4 *>(xa);
+                const float4 a1 = *reinterpret_cast<const float4 *>(xa + 4);
+                const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    acc[t][e & 1] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc[t][e & 1], 0, 0, 0);
+            }
+        }
+    }
+
+    const int col = bx * kBN + wave * 16 + (lane & 15);
+    if (col >= n) return;
+    float *pb = part + (size_t)(second * splits + blockIdx.y) * (size_t)m * n;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const f32x4 v = acc[t][0] + acc[t][1];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mr = m0 + t * 16 + 4 * q + r;
+            if (mr < m) pb[(size_t)mr * n + col] = v[r];
+        }
+    }
+}
+
+// Sum of the split-K partials in split order, then the epilogue.
+__global__ __launch_bounds__(256) void k_mfma_reduce(const float *__restrict__ part, int splits,
+                                                     int m, int n, const float *__restrict__ b0,
+                                                     const float *__restrict__ b1,
+                                                     const float *__restrict__ res,
+                                                     float *__restrict__ y, int epi) {
+    const size_t total = (size_t)m * n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int col = (int)(i % (size_t)n);
+        float g = 0.f;
+        for (int s = 0; s < splits; ++s) g += part[(size_t)s * total + i];
+        if (b0) g += b0[col];
+        if (epi == EPI_SWIGLU) {
+            float u = 0.f;
+            for (int s = 0; s < splits; ++s) u += part[(size_t)(splits + s) * total + i];
+            if (b1) u += b1[col];
+            y[i] = silu(g) * u;
+        } else {
+            if (epi == EPI_RESID) g += res[i];
+            y[i] = g;
+        }
+    }
+}
+
+struct Plan {
+    int mt, mz, nbx, klen, splits;
+};
+
+Plan plan(int m, int n, int k, bool dual) {
+    Plan pl;
+    const int tiles = (m + 15) / 16;
+    pl.mt = tiles < 4 ? tiles : 4;
+    pl.mz = (tiles + pl.mt - 1) / pl.mt;
+    pl.nbx = (n + kBN - 1) / kBN;
+    const int blocks = pl.nbx * (dual ? 2 : 1) * pl.mz;
+    const int steps = (k + kBK - 1) / kBK;
+    int want = (kTargetBlocks + blocks - 1) / blocks;
+    if (want > steps) want = steps;
+    if (want < 1) want = 1;
+    const int per = (steps + want - 1) / want;
+    pl.klen = per * kBK;
+    pl.splits = (k + pl.klen - 1) / pl.klen;
+    return pl;
+}
+
+}  // namespace
+
+size_t w4_mfma_partials_bytes(int m, int n, int k, bool dual) {
+    const Plan pl = plan(m, n, k, dual);
+    return (size_t)(dual ? 2 : 1) * pl.splits * (size_t)m * n * sizeof(float);
+}
+
+int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
+    const bool dual = p.w1 != nullptr;
+    TB_REQUIRE(p.k % 32 == 0 && p.m >= 1 && p.n >= 1, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: MFMA projection needs K % 32 == 0");
+    const Plan pl = plan(p.m, p.n, p.k, dual);
+    dim3 grid(pl.nbx * (dual ? 2 : 1), pl.splits, pl.mz);
+#define TB_MFMA_LAUNCH(MT)                                                                   \
+    hipLaunchKernelGGL((k_w4_mfma<MT>), grid, dim3(256), 0, st, p.x, p.w0, p.s0, p.w1, p.s1, \
+                       part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx, pl.splits)
+    switch (pl.mt) {
+        case 1: TB_MFMA_LAUNCH(1); break;
+        case 2: TB_MFMA_LAUNCH(2); break;
+        case 3: TB_MFMA_LAUNCH(3); break;
+        default: TB_MFMA_LAUNCH(4); break;
+    }
+#undef TB_MFMA_LAUNCH
+    TB_LAUNCHED();
+    const size_t total = (size_t)p.m * p.n;
+    size_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_mfma_reduce, dim3((unsigned)blocks), dim3(256), 0, st, part, pl.splits,
+                       p.m, p.n, p.b0, dual ? p.b1 : nullptr, p.res, p.y,
+                       dual ? (int)EPI_SWIGLU : epi);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+}  // namespace tb
