@@ -98,6 +98,11 @@ def test_decoder_from_empty_cache(cuda):
           num_layers=1),                                  # Qwen head layout (G = 7)
     small(num_heads=8, num_kv_heads=2, head_dim=128, hidden=1024, intermediate=2048,
           num_layers=2, qkv_bias=False),                  # Llama head layout (G = 4)
+    small(num_heads=4, num_kv_heads=4, head_dim=64, num_layers=1),     # MHA (G = 1)
+    small(num_heads=2, num_kv_heads=2, head_dim=128, num_layers=1),    # MHA, head_dim 128
+    small(num_heads=6, num_kv_heads=2, head_dim=64, hidden=384, num_layers=1),  # G = 3
+    small(num_heads=16, num_kv_heads=2, head_dim=128, hidden=2048, num_layers=1),  # G = 8
+    small(num_heads=16, num_kv_heads=1, head_dim=64, hidden=1024, num_layers=1),   # G = 16
 ])
 def test_decoder_head_layouts(cuda, cfg):
     run_parity(cfg, 7, prefill=130, steps=6, max_seq=200)

@@ -223,6 +223,170 @@ __global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
     }
 }
 
+// Register-resident split-KV attention, used when G = hq / hkv <= 8 (GP = G
+// rounded up to a power of two).  Same grid, tile and partial layout as k_attn;
+// no LDS round trip for K and V:
+//   * wave w owns positions t0 + 16w .. t0 + 16w + 15; lane (c, rg) holds float4
+//     column c of K and V for its NI positions i * RPL + rg (every load in
+//     flight at once) and column c of the G query heads;
+//   * per lane 4-element partial dots for all (position, head) pairs, then one
+//     transpose reduction over the C4 lanes of a row leaves each (position,
+//     head) score in exactly one representative lane;
+//   * per wave and head: max m and l = sum e^(s - m) by butterflies over the
+//     lane bits that do not encode the head; the probabilities go through a
+//     2 KB LDS table to the lanes holding V, which accumulate o per head and
+//     fold their row groups with two shuffles;
+//   * the four waves' (o, m, l) combine through LDS into the block's partial.
+template <int HD, int GP>
+__global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ st,
+                                                  const float *__restrict__ qkv,
+                                                  const float *__restrict__ kc,
+                                                  const float *__restrict__ vc,
+                                                  float *__restrict__ part, int G, int max_seq,
+                                                  int nsplit, float scale) {
+    constexpr int T = kAttnTile;
+    constexpr int PW = T / 4;              // positions per wave
+    constexpr int C4 = HD / 4;             // lanes per position row
+    constexpr int B = Log2<C4>::value;
+    constexpr int RPL = 64 / C4;           // positions per wave-wide load
+    constexpr int NI = PW / RPL;           // positions per lane
+    constexpr int NV = NI * GP;            // (position, head) partials per lane
+    constexpr int CH = NV < C4 ? NV : C4;  // partials reduced per transpose pass
+    constexpr int NCH = NV / CH;
+    constexpr int LGP = Log2<GP>::value;
+    constexpr int RB = B - Log2<CH>::value;   // low lane bits that hold replicas
+    static_assert(T == 64 && PW % RPL == 0 && GP <= C4, "attention tile layout");
+    __shared__ float sp[4][PW][GP];
+    __shared__ float so[4][GP][HD];
+    __shared__ float sml[4][GP][2];
+
+    const int kvh = blockIdx.x, spl = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int seq = st->pos + 1;
+    const int t0 = spl * T;
+    if (t0 >= seq) return;   // tile past the sequence: the merge never reads it
+    const int c = lane & (C4 - 1), rg = lane >> B;
+    const int pbase = t0 + wave * PW;
+
+    const float4 *k4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * max_seq * C4 + c;
+    const float4 *v4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * max_seq * C4 + c;
+    const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
+    float4 kr[NI], vr[NI], qr[GP];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int p = pbase + i * RPL + rg;
+        const bool ok = p < seq;
+        kr[i] = ok ? k4[(size_t)p * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        vr[i] = ok ? v4[(size_t)p * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+        qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int g = 0; g < GP; ++g)
+            v[i * GP + g] = fmaf(qr[g].w, kr[i].w,
+                                 fmaf(qr[g].z, kr[i].z, fmaf(qr[g].y, kr[i].y, qr[g].x * kr[i].x)));
+
+    // Lane l now holds, per chunk ch, the score of flat index ch * CH + (c >> RB).
+    const int vi = c >> RB;
+    const int g = vi & (GP - 1);
+    const bool rep = (c & ((1 << RB) - 1)) == 0;
+    float sc[NCH];
+    bool ok[NCH];
+    int pw[NCH];
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        float t[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) t[j] = v[ch * CH + j];
+        transpose_reduce<CH>(t, lane, B);
+        const int i = (ch * CH + vi) >> LGP;
+        pw[ch] = i * RPL + rg;
+        ok[ch] = g < G && pbase + pw[ch] < seq;
+        sc[ch] = t[0] * scale;
+        if (ok[ch]) m = fmaxf(m, sc[ch]);
+    }
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        if (j < RB || j >= RB + LGP) m = fmaxf(m, __shfl_xor(m, 1 << j));
+    float l = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        const float p = ok[ch] ? expf(sc[ch] - m) : 0.f;
+        if (rep) sp[wave][pw[ch]][g] = p;
+        if (rep) l += p;
+    }
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        if (j < RB || j >= RB + LGP) l += __shfl_xor(l, 1 << j);
+    if (rg == 0 && rep && vi < GP) {
+        sml[wave][g][0] = m;
+        sml[wave][g][1] = l;
+    }
+    __syncthreads();
+
+    float4 acc[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const float *pr = sp[wave][i * RPL + rg];
+#pragma unroll
+        for (int h = 0; h < GP; ++h) {
+            const float p = pr[h];
+            acc[h].x = fmaf(p, vr[i].x, acc[h].x);
+            acc[h].y = fmaf(p, vr[i].y, acc[h].y);
+            acc[h].z = fmaf(p, vr[i].z, acc[h].z);
+            acc[h].w = fmaf(p, vr[i].w, acc[h].w);
+        }
+    }
+#pragma unroll
+    for (int j = B; j < 6; ++j)
+#pragma unroll
+        for (int h = 0; h < GP; ++h) {
+            acc[h].x += __shfl_xor(acc[h].x, 1 << j);
+            acc[h].y += __shfl_xor(acc[h].y, 1 << j);
+            acc[h].z += __shfl_xor(acc[h].z, 1 << j);
+            acc[h].w += __shfl_xor(acc[h].w, 1 << j);
+        }
+    if (rg == 0) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+            if (h < G) *reinterpret_cast<float4 *>(&so[wave][h][4 * c]) = acc[h];
+    }
+    __syncthreads();
+
+    for (int idx = tid; idx < G * C4; idx += 256) {
+        const int h = idx / C4, cc = idx - h * C4;
+        float M = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, sml[w][h][0]);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float e = expf(sml[w][h][0] - M);
+            const float4 ow = *reinterpret_cast<const float4 *>(&so[w][h][4 * cc]);
+            o.x = fmaf(e, ow.x, o.x);
+            o.y = fmaf(e, ow.y, o.y);
+            o.z = fmaf(e, ow.z, o.z);
+            o.w = fmaf(e, ow.w, o.w);
+            L = fmaf(e, sml[w][h][1], L);
+        }
+        float *dst = part + ((size_t)(kvh * G + h) * nsplit + spl) * (HD + 4);
+        *reinterpret_cast<float4 *>(dst + 4 * cc) = o;
+        if (cc == 0) {
+            dst[HD] = M;
+            dst[HD + 1] = L;
+        }
+    }
+}
+
 // Merge of one query head's tiles: M = max m_s, L = sum e^(m_s - M) l_s,
 // o = sum e^(m_s - M) o_s / L; then the head's x chunk records for the O
 // projection.  blockDim = 64: thread = (half of the tiles, float4 column).
@@ -407,7 +571,28 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
                                         G * kAttnTile + 2 * G);
     TB_REQUIRE(lds <= 160 * 1024, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: attention tile does not fit in LDS for this head layout");
-    if (hd == 128) {
+    const int gp = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 0;
+    if (gp && (hd == 128 || hd == 64)) {
+#define TB_ATTN_REG(HD, GP)                                                                    \
+    hipLaunchKernelGGL((k_attn_reg<HD, GP>), dim3(hkv, ns), dim3(256), 0, s, st, qkv, kc, vc, \
+                       part, G, max_seq, ns, scale)
+        if (hd == 128) {
+            if (gp == 1) TB_ATTN_REG(128, 1);
+            else if (gp == 2) TB_ATTN_REG(128, 2);
+            else if (gp == 4) TB_ATTN_REG(128, 4);
+            else TB_ATTN_REG(128, 8);
+            TB_LAUNCHED();
+            hipLaunchKernelGGL(k_attn_merge<128>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
+        } else {
+            if (gp == 1) TB_ATTN_REG(64, 1);
+            else if (gp == 2) TB_ATTN_REG(64, 2);
+            else if (gp == 4) TB_ATTN_REG(64, 4);
+            else TB_ATTN_REG(64, 8);
+            TB_LAUNCHED();
+            hipLaunchKernelGGL(k_attn_merge<64>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
+        }
+#undef TB_ATTN_REG
+    } else if (hd == 128) {
         hipLaunchKernelGGL(k_attn<128>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc, part,
                            hq, hkv, max_seq, ns, scale);
         TB_LAUNCHED();
