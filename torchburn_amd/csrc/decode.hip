@@ -87,6 +87,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const DecState *__restrict__ st
     if (xq) build_xrec8(o, sub, live, xq + (size_t)rec * kXRecDwords);
 }
 
+// First input of the fused-RMSNorm step: x = embed[token], x * w in f32 and as
+// chunk records (w = the first layer's input-norm weight; the consumer divides
+// by the RMS) and the sums of squares of x over 16-element pieces.  Eight lanes
+// per 32-element chunk.
+__global__ __launch_bounds__(256) void k_embed_rec(const DecState *__restrict__ st,
+                                                   const float *__restrict__ embed,
+                                                   float *__restrict__ x,
+                                                   const float *__restrict__ w,
+                                                   float *__restrict__ xw,
+                                                   uint32_t *__restrict__ xq,
+                                                   float *__restrict__ ssq, int H) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int rec = t >> 3, sub = t & 7;
+    const bool live = rec < H / 32;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f), ww = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (live) {
+        const int i4 = rec * 8 + sub;
+        v = reinterpret_cast<const float4 *>(embed + (size_t)st->token * H)[i4];
+        reinterpret_cast<float4 *>(x)[i4] = v;
+        ww = reinterpret_cast<const float4 *>(w)[i4];
+    }
+    const float4 p = make_float4(v.x * ww.x, v.y * ww.y, v.z * ww.z, v.w * ww.w);
+    if (live) reinterpret_cast<float4 *>(xw)[rec * 8 + sub] = p;
+    build_xrec8(p, sub, live, xq + (size_t)rec * kXRecDwords);
+    float sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
+    sq += __shfl_xor(sq, 1);
+    sq += __shfl_xor(sq, 2);
+    if (live && (sub & 3) == 0) ssq[rec * 2 + (sub >> 2)] = sq;
+}
+
 // Rotate-half RoPE on the q and k heads of qkv and the KV-cache append at the
 // current position (src/llm/decoder.rs:28-68, 1115-1146):
 //   x1' = x1*c1 - x2*s1,  x2' = x2*c2 + x1*s2   (products rounded separately)
@@ -545,6 +575,16 @@ int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float
                    std::to_string(kMaxHidden));
     const int blocks = (H / 32 + kNormChunks - 1) / kNormChunks;
     hipLaunchKernelGGL(k_rmsnorm, dim3(blocks), dim3(256), 0, s, st, embed, x, w, xn, xq, H, eps);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_embed_rec(const DecState *st, const float *embed, float *x, const float *w,
+                     float *xw, uint32_t *xq, float *ssq, int H, hipStream_t s) {
+    TB_REQUIRE(H % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: hidden size must be a multiple of 32");
+    const int threads = H / 4;
+    hipLaunchKernelGGL(k_embed_rec, dim3((threads + 255) / 256), dim3(256), 0, s, st, embed, x, w,
+                       xw, xq, ssq, H);
     TB_LAUNCHED();
     return TB_OK;
 }

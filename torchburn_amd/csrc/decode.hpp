@@ -23,6 +23,10 @@ constexpr int kMaxTiles = 1024;     // max_seq_len <= kMaxTiles * kAttnTile
 
 int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
                    uint32_t *xq, int H, float eps, hipStream_t s);
+// x = embed[token]; x * w in f32 (xw) and as records (xq); 16-element sums of
+// squares of x (the fused-RMSNorm step's first input).
+int launch_embed_rec(const DecState *st, const float *embed, float *x, const float *w,
+                     float *xw, uint32_t *xq, float *ssq, int H, hipStream_t s);
 int launch_rope_kv(const DecState *st, float *qkv, const float *cos_t, const float *sin_t,
                    float *kc, float *vc, int hq, int hkv, int hd, int max_seq, hipStream_t s);
 int attn_nsplit(int max_seq);

@@ -15,6 +15,8 @@
 // device state block, so the same graph replays for every step and a greedy
 // generation runs without host round trips.
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -49,6 +51,10 @@ struct Decoder {
     tb_decoder_config cfg{};
     int H = 0, I = 0, hq = 0, hkv = 0, hd = 0, V = 0, L = 0, max_seq = 0, tq = 0, nsplit = 0;
     int wbits = 4, lmbits = 4, gs = 32;
+    bool fused = true;   // INT4: RMSNorms fused into the GEMVs (TB_DECODER_UNFUSED=1: separate)
+    // Rows per GEMV block for QKV, O, gate/up, down, lm_head (0 = the GEMV's
+    // default; TB_DECODER_J="qkv,o,gu,down,lm" overrides, for tuning sweeps).
+    int rj[5] = {0, 0, 0, 0, 0};
     float eps = 1e-6f;
     int device = 0;
     hipStream_t st = nullptr;
@@ -63,6 +69,7 @@ struct Decoder {
     float *logits = nullptr, *part = nullptr, *am_v = nullptr;
     int *am_i = nullptr, *history = nullptr;
     uint32_t *xq_h = nullptr, *xq_a = nullptr, *xq_i = nullptr;
+    float *ssq = nullptr;   // 16-element sums of squares of x (fused RMSNorm)
     DecState *state = nullptr;    // device
     DecState *hstate = nullptr;   // pinned host staging
     int hist_cap = 0;
@@ -113,17 +120,39 @@ struct Decoder {
         return bits == 4 ? (size_t)n * (size_t)(k / gs) * 4 : (bits == 8 ? (size_t)n * 4 : 0);
     }
 
+    // Fused-RMSNorm wiring of an INT4 projection: the input side (records of
+    // x * xw, sums of squares) and the output side (records of y * rec_w).
+    struct Fuse {
+        const float *ssq_in = nullptr;
+        uint32_t *rec_out = nullptr;
+        const float *rec_w = nullptr;
+        float *xw_out = nullptr;
+        float *ssq_out = nullptr;
+    };
+
     // One projection y = W x [+ bias] [+ residual] or the gate/up pair.
     int proj(int bits, const float *xin, const uint32_t *xq, const void *w, const float *s,
              const float *b, const void *w2, const float *s2, const float *res, float *y,
-             int n, int k, int epi, const RopeArgs *rope = nullptr) {
+             int n, int k, int epi, const RopeArgs *rope = nullptr, const Fuse *fu = nullptr,
+             int rows_j = 0) {
         if (bits == 4) {
             W4Params p{};
+            p.rows_j = rows_j;
             p.x = xin; p.xq = xq;
             p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
             p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
             p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k; p.gshift = gshift(gs);
             if (rope) p.rope = *rope;
+            if (fu) {
+                p.ssq_in = fu->ssq_in;
+                p.ssq_n = H / 16;
+                p.norm_h = H;
+                p.eps = eps;
+                p.rec_out = fu->rec_out;
+                p.rec_w = fu->rec_w;
+                p.xw_out = fu->xw_out;
+                p.ssq_out = fu->ssq_out;
+            }
             return w4_gemv(p, epi, st);
         }
         DenseParams p{};
@@ -134,9 +163,71 @@ struct Decoder {
         return dense_gemv(p, bits == 8 ? W_I8 : W_F32, epi, st);
     }
 
+    // The INT4 step with every RMSNorm fused into the GEMVs around it: the
+    // producer of x (embedding, O and down projections) writes the records of
+    // x * w_norm (and that product in f32 to xn, read only on the NaN/Inf
+    // path) and the 16-element sums of squares of x; the consumer (QKV,
+    // gate/up, lm_head) scales its dots by 1 / rms.  h's records come from
+    // the gate/up epilogue.  Kernels per layer: QKV, attention (split +
+    // merge), O, gate/up, down.
+    int enqueue_step_fused() {
+        int rc = launch_embed_rec(state, embed, x, layers[0].in_norm, xn, xq_h, ssq, H, st);
+        if (rc) return rc;
+        for (int l = 0; l < L; ++l) {
+            const Layer &y = layers[l];
+            float *kcl = kc + (size_t)l * hkv * max_seq * hd;
+            float *vcl = vc + (size_t)l * hkv * max_seq * hd;
+            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq};
+            Fuse fq;
+            fq.ssq_in = ssq;
+            rc = proj(4, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv, tq, H,
+                      EPI_ROPE, &ra, &fq, rj[0]);
+            if (rc) return rc;
+            rc = launch_attention(state, qkv, kcl, vcl, part, attn, xq_a, hq, hkv, hd, max_seq,
+                                  st);
+            if (rc) return rc;
+            Fuse fo;
+            fo.rec_out = xq_h;
+            fo.rec_w = y.post_norm;
+            fo.xw_out = xn;
+            fo.ssq_out = ssq;
+            rc = proj(4, attn, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H, hq * hd,
+                      EPI_RESID, nullptr, &fo, rj[1]);
+            if (rc) return rc;
+            Fuse fg;
+            fg.ssq_in = ssq;
+            fg.rec_out = xq_i;
+            rc = proj(4, xn, xq_h, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, h, I, H,
+                      EPI_SWIGLU, nullptr, &fg, rj[2]);
+            if (rc) return rc;
+            Fuse fd;
+            fd.rec_out = xq_h;
+            fd.rec_w = l + 1 < L ? layers[l + 1].in_norm : final_norm;
+            fd.xw_out = xn;
+            fd.ssq_out = ssq;
+            rc = proj(4, h, xq_i, y.down_w, y.down_s, nullptr, nullptr, nullptr, x, x, H, I,
+                      EPI_RESID, nullptr, &fd, rj[3]);
+            if (rc) return rc;
+        }
+        if (lmbits == 4) {
+            Fuse fl;
+            fl.ssq_in = ssq;
+            rc = proj(4, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V, H,
+                      EPI_PLAIN, nullptr, &fl, rj[4]);
+        } else {
+            rc = launch_rmsnorm(state, nullptr, x, final_norm, xn, nullptr, H, eps, st);
+            if (rc) return rc;
+            rc = proj(lmbits, xn, nullptr, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits,
+                      V, H, EPI_PLAIN);
+        }
+        if (rc) return rc;
+        return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
+    }
+
     // Enqueues one decoder step (reference step_internal) on `st`.
     int enqueue_step() {
         const bool q4 = wbits == 4;
+        if (q4 && fused) return enqueue_step_fused();
         int rc;
         for (int l = 0; l < L; ++l) {
             const Layer &y = layers[l];
@@ -405,8 +496,15 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
         (rc = d->alloc(&d->state, sizeof(DecState))) ||
         (rc = d->alloc(&d->xq_h, (size_t)(d->H / 32) * kXRecDwords * 4)) ||
         (rc = d->alloc(&d->xq_a, (size_t)(d->hq * d->hd / 32) * kXRecDwords * 4)) ||
-        (rc = d->alloc(&d->xq_i, (size_t)(d->I / 32) * kXRecDwords * 4)))
+        (rc = d->alloc(&d->xq_i, (size_t)(d->I / 32) * kXRecDwords * 4)) ||
+        (rc = d->alloc(&d->ssq, (size_t)(d->H / 16) * 4)))
         return bail(rc);
+    {
+        const char *e = getenv("TB_DECODER_UNFUSED");
+        d->fused = !(e && e[0] == '1');
+        const char *j = getenv("TB_DECODER_J");
+        if (j) sscanf(j, "%d,%d,%d,%d,%d", &d->rj[0], &d->rj[1], &d->rj[2], &d->rj[3], &d->rj[4]);
+    }
     if (d->lmbits != 32) {
         TB_REQUIRE(lm_head_s, TB_ERR_VALUE, "lm_head scales are required for a quantized lm_head");
         if ((rc = d->upload(&d->lm_s, lm_head_s, d->sbytes(d->lmbits, d->V, d->H)))) return bail(rc);

@@ -87,31 +87,38 @@ __device__ __forceinline__ void transpose_reduce(float (&v)[V], int lane, int b)
 // (src/quantization/fused_ops.rs:404-405).
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Lane layout of one GEMV block: `nwaves` K-slices of `sw` chunk-lanes; a row
-// spans 2^b lanes and `rps` rows are processed side by side per step.
+// Lane layout of one GEMV block: `nks` K-slices of `sw` chunk-lanes (one wave
+// each); a row spans 2^b lanes and `rps` rows are processed side by side per
+// step; `ng` row groups of `jr` = J * rps rows each (ng * nks waves in all).
 struct Layout {
     int c, sw, b, rps, rpb;   // chunks per row, lanes per slice, log2 span, rows/step, rows/block
+    int nks, ng, jr;          // K-slice waves, row groups, rows per group
     int nwaves;
 };
 
 // Picks the split of a row of `c` chunks over waves and lanes for V partials
-// per lane.  Returns false when the row needs more than kMaxWaves slices.
-inline bool make_layout(int c, int logv, int j, Layout &L) {
+// per lane, with at least `min_rows` rows per block when the wave budget allows
+// (row groups).  Returns false when the row needs more than kMaxWaves slices.
+inline bool make_layout(int c, int logv, int j, Layout &L, int min_rows = 0) {
     int bnat;
     if (c <= 64) {
-        L.nwaves = 1;
+        L.nks = 1;
         bnat = ceil_log2(c);
         L.sw = c;
     } else {
-        L.nwaves = (c + 63) / 64;
+        L.nks = (c + 63) / 64;
         bnat = 6;
-        L.sw = (c + L.nwaves - 1) / L.nwaves;
+        L.sw = (c + L.nks - 1) / L.nks;
     }
-    if (L.nwaves > kMaxWaves) return false;
+    if (L.nks > kMaxWaves) return false;
     L.c = c;
     L.b = bnat > logv ? bnat : logv;
     L.rps = 64 >> L.b;
-    L.rpb = j * L.rps;
+    L.jr = j * L.rps;
+    L.ng = 1;
+    while (L.jr * L.ng < min_rows && L.nks * L.ng * 2 <= kMaxWaves) L.ng *= 2;
+    L.nwaves = L.nks * L.ng;
+    L.rpb = L.jr * L.ng;
     return true;
 }
 
@@ -125,6 +132,15 @@ __device__ __forceinline__ int rope_row(int l, int hd) {
 // Output side of a GEMV block.  Row scales (per-channel INT8) multiply the row
 // dot before bias: y = dot * s + b, as the reference's w8a32 rows do
 // (src/quantization/gemv.rs:777-785).
+//
+// Fused RMSNorm (decoder, M == 1).  A consumer whose records hold x * w_norm
+// (not yet divided by the RMS) gets `ssq_in`: sums of squares of x over
+// consecutive 16-element pieces.  Every block sums them in the same order and
+// scales its dots by inv = 1 / sqrt(sum / H + eps) (fast_rms_norm,
+// src/quantization/fused_ops.rs:1066-1089).  A producer whose rows form x (the
+// O and down projections with the residual add) or h (gate/up) writes, besides
+// y, the records of y * rec_w (rec_w = the next RMSNorm weight, or none) and,
+// with `ssq_out`, the 16-element sums of squares of y.
 struct Epi {
     const float *b0, *b1;     // bias of the (first, second) matrix or null
     const float *rs0, *rs1;   // per-row scales or null; *_len == 1 -> one scalar
@@ -133,19 +149,123 @@ struct Epi {
     float *y;                 // output [m, n]
     int n, m;
     RopeArgs rope;            // EPI_ROPE (m == 1)
+    const float *ssq_in;      // consumer: [ssq_n] sums of squares, or null
+    int ssq_n;
+    float inv_h, eps;         // 1 / H and the RMSNorm epsilon
+    uint32_t *rec_out;        // producer: records of y [* rec_w], or null
+    const float *rec_w;
+    float *xw_out;            // producer: y [* rec_w] in f32 (the consumer's NaN/Inf path)
+    float *ssq_out;           // producer: [n / 16] sums of squares of y, or null
 };
 
 __device__ __forceinline__ float row_scale(const float *rs, int len, int row) {
     return rs ? (len > 1 ? rs[row] : rs[0]) : 1.0f;
 }
 
+// Sums of squares a thread of the smallest (one-wave) block loads: H / 16 <= 512.
+constexpr int kMaxSsqPerThread = 8;
+
+// Epilogue operands of one output (row, activation row): loaded by the thread
+// that will write it right after the weight loads are issued, so they arrive
+// while the dot products run instead of costing a round trip after the
+// reduction.
+struct EpiIn {
+    float b0, b1, s0, s1;   // bias and row scale (1 when none) of the row (and its pair)
+    float res;              // residual (EPI_RESID)
+    float pb0, ps0;         // EPI_ROPE: bias and scale of the rotation partner row
+    float c, s;             // EPI_ROPE: cos / sin at the current position
+    float ssq;              // this thread's share of the fused-RMSNorm sum of squares
+    int pos;                // EPI_ROPE
+};
+
+// Output slot of thread t: row group g = t / (rps * J * M), then (r2, j, m)
+// inside the group; the row is row0 + g * jr + j * rps + r2.  False for idle
+// threads and rows past n / m.
+template <int J, int M>
+__device__ __forceinline__ bool epi_slot(const Layout &L, int row0, const Epi &e, int &row, int &m,
+                                         int &grp, int &j, int &r2) {
+    constexpr int OUT = J * M;
+    const int t = threadIdx.x;
+    const int per = L.rps * OUT;
+    grp = j = r2 = m = 0;
+    row = row0;
+    if (t >= L.ng * per) return false;
+    grp = t / per;
+    const int tt = t - grp * per;
+    r2 = tt / OUT;
+    const int jm = tt - r2 * OUT;
+    j = jm / M;
+    m = jm - j * M;
+    row = row0 + grp * L.jr + j * L.rps + r2;
+    return row < e.n && m < e.m;
+}
+
+// EPI_ROPE: the position, first of all loads (the cos / sin loads need it).
+template <int EPI>
+__device__ __forceinline__ int epi_pos(const Epi &e) {
+    return EPI == EPI_ROPE ? *e.rope.pos : 0;
+}
+
+template <int J, int M, bool DUAL, int EPI>
+__device__ __forceinline__ EpiIn epi_load(const Layout &L, int row0, const Epi &e, int pos) {
+    EpiIn in;
+    in.b0 = in.b1 = in.res = in.pb0 = in.c = in.s = in.ssq = 0.f;
+    in.s0 = in.s1 = in.ps0 = 1.f;
+    in.pos = pos;
+    if (e.ssq_in) {
+        // Straight-line (a loop here would make the compiler drain the load
+        // counter, i.e. wait for the weights, at its back-edge).
+        const int nt = L.nwaves * 64;
+#pragma unroll
+        for (int u = 0; u < kMaxSsqPerThread; ++u) {
+            const int i = threadIdx.x + u * nt;
+            if (i < e.ssq_n) in.ssq += e.ssq_in[i];
+        }
+    }
+    int row, m, grp, j, r2;
+    if (!epi_slot<J, M>(L, row0, e, row, m, grp, j, r2)) return in;
+    if (EPI == EPI_ROPE) {
+        const RopeArgs &R = e.rope;
+        const int prow = rope_row(row, R.hd), qrow = rope_row(row ^ 1, R.hd);
+        in.b0 = e.b0 ? e.b0[prow] : 0.f;
+        in.pb0 = e.b0 ? e.b0[qrow] : 0.f;
+        in.s0 = row_scale(e.rs0, e.rs0_len, prow);
+        in.ps0 = row_scale(e.rs0, e.rs0_len, qrow);
+        const int head = prow / R.hd, r = prow - head * R.hd;
+        if (head < R.hq + R.hkv) {
+            in.c = R.cos_t[(size_t)pos * R.hd + r];
+            in.s = R.sin_t[(size_t)pos * R.hd + r];
+        }
+    } else {
+        in.b0 = e.b0 ? e.b0[row] : 0.f;
+        in.s0 = row_scale(e.rs0, e.rs0_len, row);
+        if (DUAL) {
+            in.b1 = e.b1 ? e.b1[row] : 0.f;
+            in.s1 = row_scale(e.rs1, e.rs1_len, row);
+        }
+        if (EPI == EPI_RESID) in.res = e.res[(size_t)m * e.n + row];
+    }
+    return in;
+}
+
+__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *rec,
+                                                int half);
+
+// LDS a GEMV block needs besides the partials: wave sums of squares, and the
+// block's outputs while their records are built.
+constexpr int kMaxRecRows = 256;
+struct EpiShared {
+    float ssq[kMaxWaves];
+    float out[kMaxRecRows];
+};
+
 // Cross-lane + cross-wave reduction of the V = D*J*M per-lane partials and the
 // epilogue.  Value index of a partial: (d * J + j) * M + m.
 template <int V, int J, int M, bool DUAL, int EPI>
-__device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, const Layout &L,
-                                                 int lane, int wave, int row0, const Epi &e) {
+__device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiShared &sh,
+                                                 const Layout &L, int lane, int wave, int row0,
+                                                 const Epi &e, const EpiIn &in) {
     constexpr int LOGV = Log2<V>::value;
-    constexpr int OUT = J * M;
     const int rr = lane >> L.b;
     const int cl = lane & ((1 << L.b) - 1);
     transpose_reduce<V>(v, lane, L.b);
@@ -154,73 +274,113 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, cons
         const int idx = (cl >> low) & (V - 1);
         red[(wave * L.rps + rr) * V + idx] = v[0];
     }
+    if (e.ssq_in) {
+        float t = in.ssq;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+        if (lane == 0) sh.ssq[wave] = t;
+    }
     __syncthreads();
-    const int t = threadIdx.x;
-    if (t < L.rps * OUT) {
-        const int r2 = t / OUT, jm = t - r2 * OUT;
-        const int j = jm / M, m = jm - j * M;
-        const int row = row0 + j * L.rps + r2;
-        if (row < e.n && m < e.m) {
-            float a0 = 0.f, a1 = 0.f;
-            for (int w = 0; w < L.nwaves; ++w) {
-                const float *rw = red + (w * L.rps + r2) * V;
-                a0 += rw[j * M + m];
-                if (DUAL) a1 += rw[(J + j) * M + m];
+    float inv = 1.f;
+    if (e.ssq_in) {
+        float tot = 0.f;
+        for (int w = 0; w < L.nwaves; ++w) tot += sh.ssq[w];
+        inv = 1.0f / sqrtf(tot * e.inv_h + e.eps);
+    }
+    int row, m, grp, j, r2;
+    const bool live = epi_slot<J, M>(L, row0, e, row, m, grp, j, r2);
+    float outv = 0.f;
+    if (live) {
+        float a0 = 0.f, a1 = 0.f;
+        for (int ks = 0; ks < L.nks; ++ks) {
+            const float *rw = red + ((grp * L.nks + ks) * L.rps + r2) * V;
+            a0 += rw[j * M + m];
+            if (DUAL) a1 += rw[(J + j) * M + m];
+        }
+        a0 *= inv;
+        a1 *= inv;
+        const size_t o = (size_t)m * e.n + row;
+        if (EPI == EPI_ROPE) {
+            // Both rows of the rotation pair are in this block: logical rows lr
+            // and lr ^ 1 (RoPE: src/llm/decoder.rs:28-68, products rounded
+            // separately; KV append: decoder.rs:1137-1146).
+            const RopeArgs &R = e.rope;
+            const int loc = (row ^ 1) - row0;
+            const int pg = loc / L.jr, rem = loc - pg * L.jr;
+            const int pj = rem / L.rps, pr2 = rem - pj * L.rps;
+            float ap = 0.f;
+            for (int ks = 0; ks < L.nks; ++ks)
+                ap += red[((pg * L.nks + ks) * L.rps + pr2) * V + pj * M];
+            ap *= inv;
+            const int prow = rope_row(row, R.hd);
+            const float own = a0 * in.s0 + in.b0;
+            const float oth = ap * in.ps0 + in.pb0;
+            const int head = prow / R.hd, r = prow - head * R.hd, half = R.hd >> 1;
+            float val = own;
+            if (head < R.hq + R.hkv) {
+                // r < half: own = x1, oth = x2 -> x1*c - x2*s; else own = x2 -> x2*c + x1*s
+                val = r < half ? __fsub_rn(__fmul_rn(own, in.c), __fmul_rn(oth, in.s))
+                               : __fadd_rn(__fmul_rn(own, in.c), __fmul_rn(oth, in.s));
             }
-            const size_t o = (size_t)m * e.n + row;
-            if (EPI == EPI_ROPE) {
-                // Both rows of the rotation pair are in this block: logical rows
-                // lr and lr ^ 1 (RoPE: src/llm/decoder.rs:28-68, products
-                // rounded separately; KV append: decoder.rs:1137-1146).
-                const RopeArgs &R = e.rope;
-                const int lr = row, pl = lr ^ 1;
-                const int pj = (pl - row0) / L.rps, pr2 = (pl - row0) - pj * L.rps;
-                float ap = 0.f;
-                for (int w = 0; w < L.nwaves; ++w) ap += red[(w * L.rps + pr2) * V + pj * M];
-                const int prow = rope_row(lr, R.hd), qrow = rope_row(pl, R.hd);
-                const float own = a0 * row_scale(e.rs0, e.rs0_len, prow) + (e.b0 ? e.b0[prow] : 0.f);
-                const float oth = ap * row_scale(e.rs0, e.rs0_len, qrow) + (e.b0 ? e.b0[qrow] : 0.f);
-                const int head = prow / R.hd, r = prow - head * R.hd, half = R.hd >> 1;
-                const int pos = *R.pos;
-                float val = own;
-                if (head < R.hq + R.hkv) {
-                    const int i = r < half ? r : r - half;
-                    const float c = R.cos_t[(size_t)pos * R.hd + r];
-                    const float s = R.sin_t[(size_t)pos * R.hd + r];
-                    // r < half: own = x1, oth = x2 -> x1*c - x2*s; else own = x2 -> x2*c + x1*s
-                    val = r < half ? __fsub_rn(__fmul_rn(own, c), __fmul_rn(oth, s))
-                                   : __fadd_rn(__fmul_rn(own, c), __fmul_rn(oth, s));
-                    (void)i;
-                }
-                if (head < R.hq) {
-                    e.y[prow] = val;
-                } else if (head < R.hq + R.hkv) {
-                    R.kc[((size_t)(head - R.hq) * R.max_seq + pos) * R.hd + r] = val;
-                } else {
-                    R.vc[((size_t)(head - R.hq - R.hkv) * R.max_seq + pos) * R.hd + r] = val;
-                }
-            } else if (EPI == EPI_SWIGLU) {
-                const float g = a0 * row_scale(e.rs0, e.rs0_len, row) + (e.b0 ? e.b0[row] : 0.f);
-                const float u = a1 * row_scale(e.rs1, e.rs1_len, row) + (e.b1 ? e.b1[row] : 0.f);
-                e.y[o] = silu(g) * u;
+            if (head < R.hq) {
+                e.y[prow] = val;
+            } else if (head < R.hq + R.hkv) {
+                R.kc[((size_t)(head - R.hq) * R.max_seq + in.pos) * R.hd + r] = val;
             } else {
-                const float val =
-                    a0 * row_scale(e.rs0, e.rs0_len, row) + (e.b0 ? e.b0[row] : 0.f);
-                e.y[o] = (EPI == EPI_RESID) ? e.res[o] + val : val;
+                R.vc[((size_t)(head - R.hq - R.hkv) * R.max_seq + in.pos) * R.hd + r] = val;
+            }
+        } else if (EPI == EPI_SWIGLU) {
+            const float g = a0 * in.s0 + in.b0;
+            const float u = a1 * in.s1 + in.b1;
+            outv = silu(g) * u;
+            e.y[o] = outv;
+        } else {
+            const float val = a0 * in.s0 + in.b0;
+            outv = (EPI == EPI_RESID) ? in.res + val : val;
+            e.y[o] = outv;
+        }
+    }
+    if (EPI != EPI_ROPE && e.rec_out) {
+        // Records (and sums of squares) of this block's outputs, M == 1: quads
+        // of lanes build one 16-row half record each.
+        const int t = threadIdx.x;
+        // For M == 1 the slots of threads 0 .. rpb-1 are the rpb rows of the block.
+        if (t < L.rpb) sh.out[row - row0] = live ? outv : 0.f;
+        __syncthreads();
+        if (t < (L.rpb >> 2)) {
+            const int base = row0 + 16 * (t >> 2), q = t & 3;
+            const bool ok = base < e.n;
+            const float4 yv = *reinterpret_cast<const float4 *>(&sh.out[4 * t]);
+            float4 wv = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (ok && e.rec_w) wv = *reinterpret_cast<const float4 *>(e.rec_w + base + 4 * q);
+            const float4 xv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
+            build_half_rec4(xv, q, ok, e.rec_out + (size_t)(base >> 5) * kXRecDwords,
+                            (base >> 4) & 1);
+            if (ok && e.xw_out) *reinterpret_cast<float4 *>(e.xw_out + base + 4 * q) = xv;
+            if (e.ssq_out) {
+                float sq = fmaf(yv.x, yv.x, fmaf(yv.y, yv.y, fmaf(yv.z, yv.z, yv.w * yv.w)));
+                sq += __shfl_xor(sq, 1);
+                sq += __shfl_xor(sq, 2);
+                if (ok && q == 0) e.ssq_out[base >> 4] = sq;
             }
         }
     }
 }
 
-// Builds one x chunk record (kXRecDwords) cooperatively in a group of 8
-// consecutive lanes; lane `sub` (0..7) holds elements 4*sub .. 4*sub + 3 of the
-// 32-element chunk in v.  x_i ~= sx * X_i with sx = 2^(e - 23), amax < 2^e,
-// |X_i| < 2^23: the power-of-two step makes the scaling exact and rounds off
-// only bits below 2^(e - 23), the precision an f32 partial sum of this chunk
-// has.  Limb l of U_i = X_i + 2^23 (bits [4l, 4l + 4)) goes to nibble (i & 7) of
-// dword limb[l][i >> 3], the nibble order of the packed weights.  All 8 lanes
-// must call this; `out` is written when `live`.
-__device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32_t *out) {
+// Builds one half (16 elements) of an x chunk record in a quad of 4
+// consecutive lanes; lane q (0..3) holds elements 4q .. 4q + 3 of the half in v.
+// x_i ~= sx * X_i with sx = 2^(e - 23), amax < 2^e, |X_i| < 2^23: the
+// power-of-two step makes the scaling exact and rounds off only bits below
+// 2^(e - 23), the precision an f32 partial sum of these elements has.  Limb l
+// of U_i = X_i + 2^23 (bits [4l, 4l + 4)) goes to nibble (i & 7) of dword
+// limb[l][i >> 3] (i = element index in the 32-element chunk), the nibble
+// order of the packed weights.  Record layout (kXRecDwords): 24 limb dwords
+// (limb l at 4l .. 4l + 3; dwords 0-1 of a limb hold half 0, 2-3 half 1), then
+// {step of half 0, step of half 1, sum X of half 0, sum X of half 1}; a step is
+// NaN when its half holds NaN/Inf.  All 4 lanes must call this; `rec` is
+// written when `live`.
+__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *rec,
+                                                int half) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
     int fin = 1;
     float amax = 0.f;
@@ -230,7 +390,7 @@ __device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32
         amax = fmaxf(amax, fabsf(xv[i]));
     }
 #pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
+    for (int o = 1; o < 4; o <<= 1) {
         amax = fmaxf(amax, __shfl_xor(amax, o));
         fin &= __shfl_xor(fin, o);
     }
@@ -246,23 +406,29 @@ __device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32
         X = X > 8388607 ? 8388607 : (X < -8388607 ? -8388607 : X);
         ssum += X;
         const uint32_t U = (uint32_t)(X + 8388608);
-        const int nib = (sub & 1) * 4 + i;   // nibble of element 4*sub + i in its dword
+        const int nib = (q & 1) * 4 + i;   // nibble of element 4q + i in its dword
 #pragma unroll
         for (int l = 0; l < 6; ++l) lw[l] |= ((U >> (4 * l)) & 15u) << (4 * nib);
     }
 #pragma unroll
-    for (int o = 1; o < 8; o <<= 1) ssum += __shfl_xor(ssum, o);
+    for (int o = 1; o < 4; o <<= 1) ssum += __shfl_xor(ssum, o);
 #pragma unroll
     for (int l = 0; l < 6; ++l) lw[l] |= __shfl_xor(lw[l], 1);
     if (!live) return;
-    if ((sub & 1) == 0) {
+    if ((q & 1) == 0) {
 #pragma unroll
-        for (int l = 0; l < 6; ++l) out[l * 4 + (sub >> 1)] = lw[l];
+        for (int l = 0; l < 6; ++l) rec[l * 4 + half * 2 + (q >> 1)] = lw[l];
     }
-    if (sub == 0) {
-        out[24] = __float_as_uint(fin ? ldexpf(1.0f, e - 23) : __builtin_nanf(""));
-        out[25] = (uint32_t)ssum;
+    if (q == 0) {
+        rec[24 + half] = __float_as_uint(fin ? ldexpf(1.0f, e - 23) : __builtin_nanf(""));
+        rec[26 + half] = (uint32_t)ssum;
     }
+}
+
+// One whole chunk record from 8 consecutive lanes; lane `sub` (0..7) holds
+// elements 4*sub .. 4*sub + 3 of the 32-element chunk.
+__device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32_t *out) {
+    build_half_rec4(v, sub & 3, live, out, sub >> 2);
 }
 
 }  // namespace gemv

@@ -40,7 +40,7 @@ struct DenseGemv {
 
     const DenseParams &p;
     const Layout &L;
-    int lane, wave, rr, cl, chunk;
+    int lane, wave, grp, rr, cl, chunk;
     bool act;
     size_t bpr, boff;
     float xr[M][32];
@@ -49,9 +49,10 @@ struct DenseGemv {
     __device__ __forceinline__ DenseGemv(const DenseParams &pp, const Layout &ll) : p(pp), L(ll) {
         lane = threadIdx.x & 63;
         wave = threadIdx.x >> 6;
+        grp = wave / L.nks;
         rr = lane >> L.b;
         cl = lane & ((1 << L.b) - 1);
-        const int chunk_raw = wave * L.sw + cl;
+        const int chunk_raw = (wave - grp * L.nks) * L.sw + cl;
         act = (cl < L.sw) && (chunk_raw < L.c);
         chunk = act ? chunk_raw : 0;
         bpr = (size_t)p.k * BPE;
@@ -87,7 +88,7 @@ struct DenseGemv {
         bt.ok = 0u;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int row_raw = row0 + j * L.rps + rr;
+            const int row_raw = row0 + grp * L.jr + j * L.rps + rr;
             const bool ok = act && row_raw < p.n;
             bt.ok |= ok ? (1u << j) : 0u;
             const int row = !ok ? 0 : (EPI == EPI_ROPE ? rope_row(row_raw, p.rope.hd) : row_raw);
@@ -154,17 +155,22 @@ template <int WT, int M, int J, bool DUAL, int EPI>
 __global__ __launch_bounds__(512) void k_dense_gemv(DenseParams p, Layout L, Epi e) {
     using G = DenseGemv<WT, M, J, DUAL, EPI>;
     __shared__ float red[kMaxWaves * 64];
+    __shared__ EpiShared sh;
     G g(p, L);
     typename G::Batch a;
     float4 raw[M][8];
+    const int row0 = blockIdx.x * L.rpb;
+    const int pos = epi_pos<EPI>(e);
     g.issue_x(raw);
     __builtin_amdgcn_sched_barrier(0);
     g.issue(blockIdx.x, a);
     __builtin_amdgcn_sched_barrier(0);
+    const EpiIn in = epi_load<J, M, DUAL, EPI>(L, row0, e, pos);
+    __builtin_amdgcn_sched_barrier(0);
     g.unpack_x(raw);
     float v[G::V];
     g.dots(a, v);
-    reduce_and_store<G::V, J, M, DUAL, EPI>(v, red, L, g.lane, g.wave, blockIdx.x * L.rpb, e);
+    reduce_and_store<G::V, J, M, DUAL, EPI>(v, red, sh, L, g.lane, g.wave, row0, e, in);
 }
 
 template <int WT, int M, int J, bool DUAL, int EPI>

@@ -55,26 +55,27 @@ struct W4Gemv {
     // The lane's x chunk records (one per activation row).
     struct XRec {
         u32x4 limbs[M][6];
-        u32x2 tail[M];   // {step bits, sum of integers}; the 2 pad dwords are not read
+        u32x4 tail[M];   // {step 0-15, step 16-31, sum 0-15, sum 16-31}
     };
 
     const W4Params &p;
     const Layout &L;
-    int lane, wave, rr, cl, chunk;
+    int lane, wave, grp, rr, cl, chunk;
     bool act;
     size_t bpr, boff;
     int gcols, sg;
     uint32_t limb[M][6][NDW];   // limb[m][l][d] nibble e = bits [4l, 4l+4) of U_{8d+e}
-    int sxq[M];                 // sum_i X_i of the chunk
-    float sx[M];                // power-of-two step of the chunk
+    int sxq[M][2];              // sum_i X_i of each 16-element half
+    float sx[M][2];             // power-of-two step of each half
     bool finite;                // false -> the wave takes the f32 path
 
     __device__ __forceinline__ W4Gemv(const W4Params &pp, const Layout &ll) : p(pp), L(ll) {
         lane = threadIdx.x & 63;
         wave = threadIdx.x >> 6;
+        grp = wave / L.nks;
         rr = lane >> L.b;
         cl = lane & ((1 << L.b) - 1);
-        const int chunk_raw = wave * L.sw + cl;
+        const int chunk_raw = (wave - grp * L.nks) * L.sw + cl;
         act = (cl < L.sw) && (chunk_raw < L.c);
         // Idle lanes read a valid chunk and contribute zero (scale forced to 0).
         chunk = act ? chunk_raw : 0;
@@ -91,7 +92,7 @@ struct W4Gemv {
             const uint32_t *rp = p.xq + ((size_t)mm * L.c + chunk) * kXRecDwords;
 #pragma unroll
             for (int i = 0; i < 6; ++i) xr.limbs[m][i] = reinterpret_cast<const u32x4 *>(rp)[i];
-            xr.tail[m] = *reinterpret_cast<const u32x2 *>(rp + 24);
+            xr.tail[m] = reinterpret_cast<const u32x4 *>(rp)[6];
         }
     }
 
@@ -104,9 +105,11 @@ struct W4Gemv {
                 const u32x4 t = xr.limbs[m][l];
                 limb[m][l][0] = t.x; limb[m][l][1] = t.y; limb[m][l][2] = t.z; limb[m][l][3] = t.w;
             }
-            sx[m] = __uint_as_float(xr.tail[m].x);
-            sxq[m] = (int)xr.tail[m].y;
-            fin = fin && (m >= p.m || !__builtin_isnan(sx[m]));
+            sx[m][0] = __uint_as_float(xr.tail[m].x);
+            sx[m][1] = __uint_as_float(xr.tail[m].y);
+            sxq[m][0] = (int)xr.tail[m].z;
+            sxq[m][1] = (int)xr.tail[m].w;
+            fin = fin && (m >= p.m || !(__builtin_isnan(sx[m][0]) || __builtin_isnan(sx[m][1])));
         }
         // One vote per wave, so the integer path runs without per-lane branches.
         finite = __all(fin ? 1 : 0) != 0;
@@ -134,7 +137,7 @@ struct W4Gemv {
         bt.ok = 0u;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int row_raw = row0 + j * L.rps + rr;
+            const int row_raw = row0 + grp * L.jr + j * L.rps + rr;
             const bool ok = act && row_raw < p.n;
             bt.ok |= ok ? (1u << j) : 0u;
             // rows past N re-read row 0 with weight 0
@@ -150,10 +153,10 @@ struct W4Gemv {
         }
     }
 
-    // Dot products of the batch:
+    // Dot products of the batch, per 16-element half h of the chunk:
     //   sum_i (n_i - 8) X_i = 4096 * (hi - 2048 * sum n) + lo - 8 * sum X
     // with lo / hi the limb sums 0..2 / 3..5 (all exact in 32-bit integers);
-    // one f32 rounding, then * step * group scale.
+    // one f32 rounding per half, then * step, summed, * group scale.
     __device__ __forceinline__ void dots(const Batch &bt, float (&v)[V]) const {
         if (!finite) {
 #pragma unroll
@@ -173,26 +176,31 @@ struct W4Gemv {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const uint32_t(&q)[NDW] = bt.q[d][j];
-                uint32_t sn = 0u;
+                uint32_t sn[2];
 #pragma unroll
-                for (int dw = 0; dw < NDW; ++dw)
-                    sn = __builtin_amdgcn_udot8(q[dw], 0x11111111u, sn, false);
+                for (int h = 0; h < 2; ++h)
+                    sn[h] = __builtin_amdgcn_udot8(
+                        q[2 * h + 1], 0x11111111u,
+                        __builtin_amdgcn_udot8(q[2 * h], 0x11111111u, 0u, false), false);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    uint32_t a[6];
+                    float r[2];
 #pragma unroll
-                    for (int l = 0; l < 6; ++l) {
-                        a[l] = 0u;
+                    for (int h = 0; h < 2; ++h) {
+                        uint32_t a[6];
 #pragma unroll
-                        for (int dw = 0; dw < NDW; ++dw)
-                            a[l] = __builtin_amdgcn_udot8(q[dw], limb[m][l][dw], a[l], false);
+                        for (int l = 0; l < 6; ++l)
+                            a[l] = __builtin_amdgcn_udot8(
+                                q[2 * h + 1], limb[m][l][2 * h + 1],
+                                __builtin_amdgcn_udot8(q[2 * h], limb[m][l][2 * h], 0u, false),
+                                false);
+                        const int lo = (int)(a[0] + 16u * a[1] + 256u * a[2]);
+                        const int hi = (int)(a[3] + 16u * a[4] + 256u * a[5]);
+                        const int t = hi - 2048 * (int)sn[h];
+                        r[h] = 8.0f * (float)(512 * t - sxq[m][h]) + (float)lo;
                     }
-                    const int lo = (int)(a[0] + 16u * a[1] + 256u * a[2]);
-                    const int hi = (int)(a[3] + 16u * a[4] + 256u * a[5]);
-                    const int t = hi - 2048 * (int)sn;
-                    const float r = 8.0f * (float)(512 * t - sxq[m]) + (float)lo;
                     const float sc = ((bt.ok >> j) & 1u) ? bt.sc[d][j] : 0.f;
-                    v[(d * J + j) * M + m] = sc * (sx[m] * r);
+                    v[(d * J + j) * M + m] = sc * fmaf(sx[m][0], r[0], sx[m][1] * r[1]);
                 }
             }
         }
@@ -200,24 +208,30 @@ struct W4Gemv {
 };
 
 // One block = one batch of J rows.  Order matters: x record loads, then the
-// batch's weight and scale loads, then the dot products (which wait only for
-// what they read, since loads retire in issue order).  Straight-line code: a
+// batch's weight and scale loads, then the epilogue operands, then the dot
+// products (which wait only for what they read, since loads retire in issue
+// order).  Straight-line code: a
 // loop back-edge would make the compiler drain the load counter early.
 template <int M, int J, bool DUAL, int EPI>
 __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p, Layout L, Epi e) {
     using G = W4Gemv<M, J, DUAL, EPI>;
     __shared__ float red[kMaxWaves * 64];
+    __shared__ EpiShared sh;
     G g(p, L);
     typename G::Batch a;
     typename G::XRec xr;
+    const int row0 = blockIdx.x * L.rpb;
+    const int pos = epi_pos<EPI>(e);
     g.issue_x(xr);
     __builtin_amdgcn_sched_barrier(0);
     g.issue(blockIdx.x, a);
     __builtin_amdgcn_sched_barrier(0);
+    const EpiIn in = epi_load<J, M, DUAL, EPI>(L, row0, e, pos);
+    __builtin_amdgcn_sched_barrier(0);
     g.unpack_x(xr);
     float v[G::V];
     g.dots(a, v);
-    reduce_and_store<G::V, J, M, DUAL, EPI>(v, red, L, g.lane, g.wave, blockIdx.x * L.rpb, e);
+    reduce_and_store<G::V, J, M, DUAL, EPI>(v, red, sh, L, g.lane, g.wave, row0, e, in);
 }
 
 // Chunk records of x [m, k]: eight lanes per (row, 32-element chunk).
@@ -238,10 +252,18 @@ int launch(const W4Params &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
     Layout L;
-    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L), TB_ERR_UNSUPPORTED,
+    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, p.rec_out ? 16 : 0), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32 GEMV supports K <= " + std::to_string(kMaxWaves * 64 * 32));
     Epi e{};
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m; e.rope = p.rope;
+    e.ssq_in = p.ssq_in; e.ssq_n = p.ssq_n; e.eps = p.eps;
+    e.inv_h = p.norm_h > 0 ? 1.0f / (float)p.norm_h : 0.f;
+    e.rec_out = p.rec_out; e.rec_w = p.rec_w; e.xw_out = p.xw_out; e.ssq_out = p.ssq_out;
+    if (p.rec_out)
+        TB_REQUIRE(p.m == 1 && EPI != EPI_ROPE && L.rpb % 16 == 0 && L.rpb <= kMaxRecRows &&
+                       p.n % 32 == 0,
+                   TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: records of the output need M == 1, "
+                                       "N % 32 == 0 and 16-row blocks");
     if (EPI == EPI_ROPE)
         TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
@@ -259,9 +281,7 @@ int dispatch_m(const W4Params &p, hipStream_t st) {
     if (p.m <= 1) {
         const int j = p.rows_j ? p.rows_j : (DUAL ? 8 : 16);
         if (j == 4) return launch<1, 4, DUAL, EPI>(p, st);
-        if constexpr (!DUAL) {
-            if (j == 16) return launch<1, 16, DUAL, EPI>(p, st);
-        }
+        if (j == 16) return launch<1, 16, DUAL, EPI>(p, st);
         return launch<1, 8, DUAL, EPI>(p, st);
     }
     return launch<2, DUAL ? 4 : 8, DUAL, EPI>(p, st);
@@ -283,7 +303,11 @@ int w4_gemv(W4Params p, int epi, hipStream_t st) {
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4 GEMV needs K % 32 == 0");
     if (p.w1 != nullptr) return dispatch_m<true, EPI_SWIGLU>(p, st);
     if (epi == EPI_RESID) return dispatch_m<false, EPI_RESID>(p, st);
-    if (epi == EPI_ROPE) return launch<1, 16, false, EPI_ROPE>(p, st);
+    if (epi == EPI_ROPE) {
+        if (p.rows_j == 4) return launch<1, 4, false, EPI_ROPE>(p, st);
+        if (p.rows_j == 8) return launch<1, 8, false, EPI_ROPE>(p, st);
+        return launch<1, 16, false, EPI_ROPE>(p, st);
+    }
     return dispatch_m<false, EPI_PLAIN>(p, st);
 }
 

@@ -22,10 +22,11 @@ struct RopeArgs {
 // Activation rows per GEMV pass (x is held in VGPRs).
 constexpr int kMaxRowsPerPass = 2;
 
-// An x chunk record: 32 activations as a 24-bit fixed-point integer per element
-// in six 4-bit limb planes (24 dwords), then {step (f32 bits; NaN when the chunk
-// holds NaN/Inf), sum of the integers, 0, 0} (112 bytes, 16-byte aligned).  Built once per activation vector by xquant()
-// and read by every block of the GEMV.
+// An x chunk record: 32 activations as 24-bit fixed-point integers in six
+// 4-bit limb planes (24 dwords), then {step of elements 0-15, step of 16-31,
+// integer sum of 0-15, of 16-31} (steps as f32 bits, NaN when the half holds
+// NaN/Inf): 112 bytes, 16-byte aligned.  Built once per activation vector by
+// xquant() or by the producing kernel, read by every block of the GEMV.
 constexpr int kXRecDwords = 28;
 
 struct W4Params {
@@ -43,6 +44,19 @@ struct W4Params {
     int gshift;        // log2(group_size)
     int rows_j;        // rows per block (tuning: 4, 8 or 16; 0 = default)
     RopeArgs rope;     // EPI_ROPE only
+    // Fused RMSNorm (M == 1).  Consumer: xq holds records of x * w_norm (and
+    // p.x that product in f32, for the NaN/Inf path); ssq_in [ssq_n] the sums
+    // of squares of x over 16-element pieces; the dots are scaled by
+    // 1 / sqrt(sum / norm_h + eps).
+    const float *ssq_in;
+    int ssq_n, norm_h;
+    float eps;
+    // Producer: y * rec_w as records into rec_out and in f32 into xw_out, and
+    // the 16-row sums of squares of y into ssq_out (16-row blocks).
+    uint32_t *rec_out;
+    const float *rec_w;
+    float *xw_out;
+    float *ssq_out;
 };
 
 // One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
