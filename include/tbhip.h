@@ -62,8 +62,10 @@ TB_API const char *tb_version(void);
  * src/ffi/quantization_ffi.rs:56-85 -> src/quantization/packed_v2.rs:557-624
  * -> gemm_w4a32_grouped / gemv_w4a32_grouped (src/quantization/gemv.rs:1514-1725).
  * x f32 [M, K], w u8 [N, ceil(K/2)], scales f32 [N, ceil(K/gs)], bias f32 [N]
- * or NULL, out f32 [M, N].  group_size is 32 or 64 and must divide K.
- * M <= 15 runs the GEMV kernels; M >= 16 runs the dequantize + FP32-MFMA GEMM.
+ * or NULL, out f32 [M, N].  group_size is 32 or 64 and must divide K (the
+ * reference's quantizer requires the same, python/torchburn/quantization.py:75-79).
+ * M <= 4 runs the GEMV kernels (passes of 2 rows); M >= 5 the FP32-MFMA
+ * projection (weights dequantized in registers into the MFMA operand).
  */
 TB_API int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float *scales,
                             const float *bias, float *out, int64_t m, int64_t n, int64_t k,
@@ -112,8 +114,8 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
  * Activation chunk records, for callers that reuse one x across several INT4
  * projections (no reference counterpart: the reference converts x inside each
  * GEMV).  A record holds 32 activations as 24-bit fixed-point integers in six
- * 4-bit limb planes plus a power-of-two step: 112 bytes per 32 elements,
- * tb_x_records_bytes(m, k) in total.  tb_xquant builds them from x [M, K];
+ * 4-bit limb planes plus a power-of-two step and an integer sum per 16-element
+ * half: 112 bytes per 32 elements, tb_x_records_bytes(m, k) in total.  tb_xquant builds them from x [M, K];
  * the *_xq GEMVs read them instead of building their own (x itself is still
  * read when a chunk holds NaN/Inf).  residual may be NULL.
  */

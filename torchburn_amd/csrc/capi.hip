@@ -39,9 +39,10 @@ int rows_j_env() {
     return v;
 }
 // Activation rows from which INT4 projections run on FP32 MFMA instead of the
-// GEMV (TB_MFMA_MIN_M overrides; tuning sweeps only).
+// GEMV (measured crossover: passes of 2 rows re-read the weights, the MFMA
+// tile pads to 16 rows; TB_MFMA_MIN_M overrides, for tuning sweeps only).
 int64_t mfma_min_m() {
-    static int v = env_int("TB_MFMA_MIN_M", 16);
+    static int v = env_int("TB_MFMA_MIN_M", 5);
     return v < 1 ? 1 : v;
 }
 }  // namespace

@@ -36,6 +36,13 @@ __device__ __forceinline__ u32x4 load_nt16(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// Non-temporal 16-byte load of 4 floats (streamed-once data such as the KV cache).
+__device__ __forceinline__ float4 load_nt_f4(const float *p) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    const f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // q & mask, opaque to the optimiser.  With the mask visible, the compiler folds
 // "(float)((q & 0x0F0F0F0F) >> 8 & 0xFF)" into v_bfe_u32 + v_cvt_f32_ubyte0 (two
 // instructions per byte); behind this AND each byte converts with a single
@@ -174,7 +181,7 @@ struct EpiIn {
     float res;              // residual (EPI_RESID)
     float pb0, ps0;         // EPI_ROPE: bias and scale of the rotation partner row
     float c, s;             // EPI_ROPE: cos / sin at the current position
-    float ssq;              // this thread's share of the fused-RMSNorm sum of squares
+    float ssq[kMaxSsqPerThread];   // this thread's share of the fused-RMSNorm sums of squares
     int pos;                // EPI_ROPE
 };
 
@@ -209,17 +216,18 @@ __device__ __forceinline__ int epi_pos(const Epi &e) {
 template <int J, int M, bool DUAL, int EPI>
 __device__ __forceinline__ EpiIn epi_load(const Layout &L, int row0, const Epi &e, int pos) {
     EpiIn in;
-    in.b0 = in.b1 = in.res = in.pb0 = in.c = in.s = in.ssq = 0.f;
+    in.b0 = in.b1 = in.res = in.pb0 = in.c = in.s = 0.f;
     in.s0 = in.s1 = in.ps0 = 1.f;
     in.pos = pos;
     if (e.ssq_in) {
-        // Straight-line (a loop here would make the compiler drain the load
-        // counter, i.e. wait for the weights, at its back-edge).
+        // Unconditional loads of clamped indices, summed after the dots: a load
+        // consumed here (or under a per-lane branch) would make the compiler
+        // wait for every weight load issued before it.
         const int nt = L.nwaves * 64;
 #pragma unroll
         for (int u = 0; u < kMaxSsqPerThread; ++u) {
             const int i = threadIdx.x + u * nt;
-            if (i < e.ssq_n) in.ssq += e.ssq_in[i];
+            in.ssq[u] = e.ssq_in[i < e.ssq_n ? i : 0];
         }
     }
     int row, m, grp, j, r2;
@@ -275,7 +283,11 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
         red[(wave * L.rps + rr) * V + idx] = v[0];
     }
     if (e.ssq_in) {
-        float t = in.ssq;
+        float t = 0.f;
+        const int nt = L.nwaves * 64;
+#pragma unroll
+        for (int u = 0; u < kMaxSsqPerThread; ++u)
+            if ((int)threadIdx.x + u * nt < e.ssq_n) t += in.ssq[u];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
         if (lane == 0) sh.ssq[wave] = t;
