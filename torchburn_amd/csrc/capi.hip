@@ -290,6 +290,20 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
     hipStream_t st = (hipStream_t)stream;
     W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
     p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
+    if (m == 1) {
+        // One row: the gate/up epilogue writes h's chunk records as well, so the
+        // down projection needs no separate record pass.
+        rc = xquant(x, xq, 1, (int)k, st);
+        if (rc) return rc;
+        p.xq = xq;
+        p.rec_out = hq;
+        rc = w4_gemv(p, EPI_SWIGLU, st);
+        if (rc) return rc;
+        W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
+        d.xq = hq;
+        d.res = residual;
+        return w4_gemv(d, residual ? EPI_RESID : EPI_PLAIN, st);
+    }
     rc = w4_rows(p, EPI_SWIGLU, m, xq, true, st);
     if (rc) return rc;
     W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);

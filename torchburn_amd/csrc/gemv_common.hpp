@@ -169,8 +169,9 @@ __device__ __forceinline__ float row_scale(const float *rs, int len, int row) {
     return rs ? (len > 1 ? rs[row] : rs[0]) : 1.0f;
 }
 
-// Sums of squares a thread of the smallest (one-wave) block loads: H / 16 <= 512.
-constexpr int kMaxSsqPerThread = 8;
+// Sums of squares per thread of a fused-RMSNorm consumer: the consumer's K is H,
+// so its block has 64 * ceil(H / 2048) threads or more and H / 16 entries to sum.
+constexpr int kMaxSsqPerThread = 2;
 
 // Epilogue operands of one output (row, activation row): loaded by the thread
 // that will write it right after the weight loads are issued, so they arrive

@@ -155,7 +155,7 @@ template <int WT, int M, int J, bool DUAL, int EPI>
 __global__ __launch_bounds__(512) void k_dense_gemv(DenseParams p, Layout L, Epi e) {
     using G = DenseGemv<WT, M, J, DUAL, EPI>;
     __shared__ float red[kMaxWaves * 64];
-    __shared__ EpiShared sh;
+    __shared__ EpiShared sh;   // one batch per block: a single LDS set
     G g(p, L);
     typename G::Batch a;
     float4 raw[M][8];

@@ -259,6 +259,9 @@ int launch(const W4Params &p, hipStream_t st) {
     e.ssq_in = p.ssq_in; e.ssq_n = p.ssq_n; e.eps = p.eps;
     e.inv_h = p.norm_h > 0 ? 1.0f / (float)p.norm_h : 0.f;
     e.rec_out = p.rec_out; e.rec_w = p.rec_w; e.xw_out = p.xw_out; e.ssq_out = p.ssq_out;
+    if (p.ssq_in)
+        TB_REQUIRE(p.m == 1 && p.ssq_n <= kMaxSsqPerThread * L.nwaves * 64, TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: fused RMSNorm input needs M == 1 and K == H");
     if (p.rec_out)
         TB_REQUIRE(p.m == 1 && EPI != EPI_ROPE && L.rpb % 16 == 0 && L.rpb <= kMaxRecRows &&
                        p.n % 32 == 0,

@@ -1,5 +1,6 @@
 // Batched grouped-INT4 projection Y[M, N] = X[M, K] . deq(W)^T on FP32 MFMA
-// (v_mfma_f32_16x16x4_f32), for M >= 16 where the work is a dense contraction.
+// (v_mfma_f32_16x16x4_f32), for batches of M >= 5 rows (16-row tiles), where
+// the work is a dense contraction.
 //
 // Replaces the M > 1 path of the reference's w4a32_grouped_linear
 // (src/quantization/packed_v2.rs:557-624 -> gemm_w4a32_grouped,
@@ -27,8 +28,12 @@
 //     so one MFMA consumes element e of each group's 32; the K order inside a
 //     contraction is free as long as A and B agree.
 //   * the next step's X tile, weight chunk and scale are loaded into registers
-//     before the current step's MFMAs are issued.
+//     before the current step's MFMAs are issued; X tiles alternate between two
+//     LDS buffers, so each step needs one barrier;
+//   * up to four independent accumulators per 16-row tile keep dependent MFMAs
+//     apart (small M has few tiles to interleave).
 #include <float.h>
+#include <stdlib.h>
 
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
@@ -44,7 +49,7 @@ namespace {
 constexpr int kBN = 64;        // weight rows per block
 constexpr int kBK = 128;       // K per step
 constexpr int kXP = kBK + 4;   // LDS row pitch of the X tile (floats)
-constexpr int kTargetBlocks = 512;
+constexpr int kTargetBlocks = 512;   // split-K target (TB_MFMA_BLOCKS overrides, tuning only)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -56,8 +61,10 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
                                                  const float *__restrict__ s1,
                                                  float *__restrict__ part, int m, int n, int k,
                                                  int gshift, int klen, int nbx, int splits) {
-    constexpr int XV = MT * 2;   // float4 of the X tile per thread
-    __shared__ float xs[MT * 16 * kXP];
+    constexpr int XV = MT * 2;             // float4 of the X tile per thread
+    constexpr int NACC = MT <= 2 ? 4 : 2;  // independent accumulation chains per M tile
+    constexpr int NB = MT <= 2 ? 2 : 1;    // X tile buffers (two cost occupancy at MT >= 3)
+    __shared__ float xs[NB][MT * 16 * kXP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int bx = blockIdx.x;
     const int second = bx >= nbx ? 1 : 0;   // dual launch: blocks of the up projection
@@ -91,17 +98,23 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
         sr = ok ? srow[kk >> gshift] : 0.f;
     };
 
-    f32x4 acc[MT][2];
+    f32x4 acc[MT][NACC];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int c = 0; c < NACC; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     load_step(kb);
-    for (int k0 = kb; k0 < ke; k0 += kBK) {
-        __syncthreads();   // the previous step's LDS reads are done
+    int buf = 0;
+    for (int k0 = kb; k0 < ke; k0 += kBK, buf ^= (NB - 1)) {
+        float *xb = xs[buf];
+        // With two buffers, `buf` was last read two steps ago, before the
+        // previous step's barrier; with one, wait for this step's readers.
+        if (NB == 1) __syncthreads();
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
             const int f = tid + 256 * i;
-            *reinterpret_cast<float4 *>(xs + (f >> 5) * kXP + (f & 31) * 4) = xr[i];
+            *reinterpret_cast<float4 *>(xb + (f >> 5) * kXP + (f & 31) * 4) = xr[i];
         }
         const u32x4 cw = wr;
         const float sc = sr;
@@ -111,6 +124,15 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
         const uint32_t dws[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
+            float a[MT][8];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const float *xa = xb + (t * 16 + (lane & 15)) * kXP + 32 * q + 8 * d;
+                const float4 a0 = *reinterpret_cast<const float4 *>(xa);
+                const float4 a1 = *reinterpret_cast<const float4 *>(xa + 4);
+                a[t][0] = a0.x; a[t][1] = a0.y; a[t][2] = a0.z; a[t][3] = a0.w;
+                a[t][4] = a1.x; a[t][5] = a1.y; a[t][6] = a1.z; a[t][7] = a1.w;
+            }
             const uint32_t lo = dws[d] & 0x0F0F0F0Fu, hi = (dws[d] >> 4) & 0x0F0F0F0Fu;
             float b[8];
 #pragma unroll
@@ -119,16 +141,11 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
                 b[2 * i + 1] = fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, nsc);
             }
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const float *xa = xs + (t * 16 + (lane & 15)) * kXP + 32 * q + 8 * d;
-                const float4 a0 = *reinterpret_cast<const float4 *>(xa);
-                const float4 a1 = *reinterpret_cast<const float4 *>(xa + 4);
-                const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            for (int e = 0; e < 8; ++e)
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    acc[t][e & 1] =
-                        __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc[t][e & 1], 0, 0, 0);
-            }
+                for (int t = 0; t < MT; ++t)
+                    acc[t][e % NACC] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        a[t][e], b[e], acc[t][e % NACC], 0, 0, 0);
         }
     }
 
@@ -137,7 +154,9 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
     float *pb = part + (size_t)(second * splits + blockIdx.y) * (size_t)m * n;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-        const f32x4 v = acc[t][0] + acc[t][1];
+        f32x4 v = acc[t][0];
+#pragma unroll
+        for (int c = 1; c < NACC; ++c) v += acc[t][c];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int mr = m0 + t * 16 + 4 * q + r;
@@ -175,6 +194,15 @@ struct Plan {
     int mt, mz, nbx, klen, splits;
 };
 
+int target_blocks() {
+    static int v = [] {
+        const char *e = getenv("TB_MFMA_BLOCKS");
+        const int t = e ? atoi(e) : 0;
+        return t > 0 ? t : kTargetBlocks;
+    }();
+    return v;
+}
+
 Plan plan(int m, int n, int k, bool dual) {
     Plan pl;
     const int tiles = (m + 15) / 16;
@@ -183,7 +211,7 @@ Plan plan(int m, int n, int k, bool dual) {
     pl.nbx = (n + kBN - 1) / kBN;
     const int blocks = pl.nbx * (dual ? 2 : 1) * pl.mz;
     const int steps = (k + kBK - 1) / kBK;
-    int want = (kTargetBlocks + blocks - 1) / blocks;
+    int want = (target_blocks() + blocks - 1) / blocks;
     if (want > steps) want = steps;
     if (want < 1) want = 1;
     const int per = (steps + want - 1) / want;
