@@ -163,6 +163,7 @@ struct Epi {
     const float *rec_w;
     float *xw_out;            // producer: y [* rec_w] in f32 (the consumer's NaN/Inf path)
     float *ssq_out;           // producer: [n / 16] sums of squares of y, or null
+    const float *any;         // >= n readable floats: stand-in base for absent operands
 };
 
 __device__ __forceinline__ float row_scale(const float *rs, int len, int row) {
@@ -214,47 +215,70 @@ __device__ __forceinline__ int epi_pos(const Epi &e) {
     return EPI == EPI_ROPE ? *e.rope.pos : 0;
 }
 
+// Every load is unconditional (clamped indices, the `any` buffer standing in
+// for absent operands) and the raw values are fixed up only in the epilogue
+// (epi_fix): with per-lane branches or a value consumed here, the compiler
+// would wait for every weight load issued before these before the dot
+// products could start.
 template <int J, int M, bool DUAL, int EPI>
 __device__ __forceinline__ EpiIn epi_load(const Layout &L, int row0, const Epi &e, int pos) {
     EpiIn in;
     in.b0 = in.b1 = in.res = in.pb0 = in.c = in.s = 0.f;
     in.s0 = in.s1 = in.ps0 = 1.f;
     in.pos = pos;
-    if (e.ssq_in) {
-        // Unconditional loads of clamped indices, summed after the dots: a load
-        // consumed here (or under a per-lane branch) would make the compiler
-        // wait for every weight load issued before it.
+    {
+        const float *sq = e.ssq_in ? e.ssq_in : e.any;   // summed only with ssq_in
         const int nt = L.nwaves * 64;
 #pragma unroll
         for (int u = 0; u < kMaxSsqPerThread; ++u) {
             const int i = threadIdx.x + u * nt;
-            in.ssq[u] = e.ssq_in[i < e.ssq_n ? i : 0];
+            in.ssq[u] = sq[i < e.ssq_n ? i : 0];
         }
     }
     int row, m, grp, j, r2;
-    if (!epi_slot<J, M>(L, row0, e, row, m, grp, j, r2)) return in;
+    const bool live = epi_slot<J, M>(L, row0, e, row, m, grp, j, r2);
+    const int rw = live ? row : 0, mm = live ? m : 0;
+    const float *b0 = e.b0 ? e.b0 : e.any, *b1 = e.b1 ? e.b1 : e.any;
+    const float *rs0 = e.rs0 ? e.rs0 : e.any, *rs1 = e.rs1 ? e.rs1 : e.any;
     if (EPI == EPI_ROPE) {
         const RopeArgs &R = e.rope;
-        const int prow = rope_row(row, R.hd), qrow = rope_row(row ^ 1, R.hd);
-        in.b0 = e.b0 ? e.b0[prow] : 0.f;
-        in.pb0 = e.b0 ? e.b0[qrow] : 0.f;
-        in.s0 = row_scale(e.rs0, e.rs0_len, prow);
-        in.ps0 = row_scale(e.rs0, e.rs0_len, qrow);
-        const int head = prow / R.hd, r = prow - head * R.hd;
-        if (head < R.hq + R.hkv) {
-            in.c = R.cos_t[(size_t)pos * R.hd + r];
-            in.s = R.sin_t[(size_t)pos * R.hd + r];
-        }
+        const int prow = rope_row(rw, R.hd), qrow = rope_row(rw ^ 1, R.hd);
+        in.b0 = b0[prow];
+        in.pb0 = b0[qrow];
+        in.s0 = rs0[e.rs0_len > 1 ? prow : 0];
+        in.ps0 = rs0[e.rs0_len > 1 ? qrow : 0];
+        // cos / sin of the row's place in its head (unused for V rows)
+        const int r = prow % R.hd;
+        in.c = R.cos_t[(size_t)pos * R.hd + r];
+        in.s = R.sin_t[(size_t)pos * R.hd + r];
     } else {
-        in.b0 = e.b0 ? e.b0[row] : 0.f;
-        in.s0 = row_scale(e.rs0, e.rs0_len, row);
+        in.b0 = b0[rw];
+        in.s0 = rs0[e.rs0_len > 1 ? rw : 0];
         if (DUAL) {
-            in.b1 = e.b1 ? e.b1[row] : 0.f;
-            in.s1 = row_scale(e.rs1, e.rs1_len, row);
+            in.b1 = b1[rw];
+            in.s1 = rs1[e.rs1_len > 1 ? rw : 0];
         }
-        if (EPI == EPI_RESID) in.res = e.res[(size_t)m * e.n + row];
+        if (EPI == EPI_RESID) in.res = e.res[(size_t)mm * e.n + rw];
     }
     return in;
+}
+
+// The loaded operands with the absent ones replaced: bias 0, row scale 1.
+__device__ __forceinline__ EpiIn epi_fix(EpiIn in, const Epi &e) {
+    if (!e.b0) in.b0 = in.pb0 = 0.f;
+    if (!e.b1) in.b1 = 0.f;
+    if (!e.rs0) in.s0 = in.ps0 = 1.f;
+    if (!e.rs1) in.s1 = 1.f;
+    return in;
+}
+
+// Lane exchanges inside a quad of 4 lanes (DPP quad_perm; every lane of the
+// quad must be active): value of lane ^ 1, lane ^ 2.
+__device__ __forceinline__ int quad_xor1(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ int quad_xor2(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
 }
 
 __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *rec,
@@ -273,7 +297,7 @@ struct EpiShared {
 template <int V, int J, int M, bool DUAL, int EPI>
 __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiShared &sh,
                                                  const Layout &L, int lane, int wave, int row0,
-                                                 const Epi &e, const EpiIn &in) {
+                                                 const Epi &e, const EpiIn &in_raw) {
     constexpr int LOGV = Log2<V>::value;
     const int rr = lane >> L.b;
     const int cl = lane & ((1 << L.b) - 1);
@@ -288,7 +312,7 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
         const int nt = L.nwaves * 64;
 #pragma unroll
         for (int u = 0; u < kMaxSsqPerThread; ++u)
-            if ((int)threadIdx.x + u * nt < e.ssq_n) t += in.ssq[u];
+            if ((int)threadIdx.x + u * nt < e.ssq_n) t += in_raw.ssq[u];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
         if (lane == 0) sh.ssq[wave] = t;
@@ -302,6 +326,7 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
     }
     int row, m, grp, j, r2;
     const bool live = epi_slot<J, M>(L, row0, e, row, m, grp, j, r2);
+    const EpiIn in = epi_fix(in_raw, e);
     float outv = 0.f;
     if (live) {
         float a0 = 0.f, a1 = 0.f;
@@ -402,11 +427,10 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
         fin &= __builtin_isfinite(xv[i]) != 0;
         amax = fmaxf(amax, fabsf(xv[i]));
     }
-#pragma unroll
-    for (int o = 1; o < 4; o <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o));
-        fin &= __shfl_xor(fin, o);
-    }
+    amax = fmaxf(amax, __int_as_float(quad_xor1(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(quad_xor2(__float_as_int(amax))));
+    fin &= quad_xor1(fin);
+    fin &= quad_xor2(fin);
     int e = 0;
     (void)frexpf(amax, &e);
     e = e < -100 ? -100 : e;
@@ -423,10 +447,10 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
 #pragma unroll
         for (int l = 0; l < 6; ++l) lw[l] |= ((U >> (4 * l)) & 15u) << (4 * nib);
     }
+    ssum += quad_xor1(ssum);
+    ssum += quad_xor2(ssum);
 #pragma unroll
-    for (int o = 1; o < 4; o <<= 1) ssum += __shfl_xor(ssum, o);
-#pragma unroll
-    for (int l = 0; l < 6; ++l) lw[l] |= __shfl_xor(lw[l], 1);
+    for (int l = 0; l < 6; ++l) lw[l] |= (uint32_t)quad_xor1((int)lw[l]);
     if (!live) return;
     if ((q & 1) == 0) {
 #pragma unroll

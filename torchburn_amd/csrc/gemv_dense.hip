@@ -184,6 +184,7 @@ int launch(const DenseParams &p, hipStream_t st) {
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m;
     e.rs0 = p.rs0; e.rs1 = p.rs1; e.rs0_len = p.rs0_len; e.rs1_len = p.rs1_len;
     e.rope = p.rope;
+    e.any = static_cast<const float *>(p.w0);   // n * k / 4 >= n floats (k >= 32)
     if (EPI == EPI_ROPE)
         TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");

@@ -142,13 +142,16 @@ struct W4Gemv {
             bt.ok |= ok ? (1u << j) : 0u;
             // rows past N re-read row 0 with weight 0
             const int row = !ok ? 0 : (EPI == EPI_ROPE ? rope_row(row_raw, p.rope.hd) : row_raw);
+            // 32-bit offsets from the uniform bases (weights < 4 GiB, checked
+            // at launch): one VGPR per address, SGPR-based addressing.
+            const uint32_t wo = (uint32_t)row * (uint32_t)bpr + (uint32_t)boff;
+            const uint32_t so = ((uint32_t)row * (uint32_t)gcols + (uint32_t)sg) * 4u;
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                const uint8_t *w = d ? p.w1 : p.w0;
-                const float *s = d ? p.s1 : p.s0;
-                const u32x4 v = load_nt16(w + (size_t)row * bpr + boff);
+                const u32x4 v = load_nt16((d ? p.w1 : p.w0) + wo);
                 bt.q[d][j][0] = v.x; bt.q[d][j][1] = v.y; bt.q[d][j][2] = v.z; bt.q[d][j][3] = v.w;
-                bt.sc[d][j] = s[(size_t)row * gcols + sg];
+                bt.sc[d][j] = *reinterpret_cast<const float *>(
+                    reinterpret_cast<const char *>(d ? p.s1 : p.s0) + so);
             }
         }
     }
@@ -259,6 +262,7 @@ int launch(const W4Params &p, hipStream_t st) {
     e.ssq_in = p.ssq_in; e.ssq_n = p.ssq_n; e.eps = p.eps;
     e.inv_h = p.norm_h > 0 ? 1.0f / (float)p.norm_h : 0.f;
     e.rec_out = p.rec_out; e.rec_w = p.rec_w; e.xw_out = p.xw_out; e.ssq_out = p.ssq_out;
+    e.any = p.s0;   // n * k / group >= n floats
     if (p.ssq_in)
         TB_REQUIRE(p.m == 1 && p.ssq_n <= kMaxSsqPerThread * L.nwaves * 64, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: fused RMSNorm input needs M == 1 and K == H");
@@ -270,6 +274,8 @@ int launch(const W4Params &p, hipStream_t st) {
     if (EPI == EPI_ROPE)
         TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
+    TB_REQUIRE((size_t)p.n * (size_t)(p.k / 2) < (1ull << 32), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4 GEMV weights must be under 4 GiB");
     const int grid = (p.n + L.rpb - 1) / L.rpb;
     hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI>), dim3(grid), dim3(L.nwaves * 64), 0, st, p, L,
                        e);
