@@ -154,6 +154,57 @@ TB_API int tb_fused_swiglu_mlp_w8a32(const float *x, const int8_t *gate_w, const
 
 /* ------------------------------------------------------------------------ */
 /* Decoder (replaces RustQwenDecoder, reference src/llm/decoder.rs:176-1374)   */
+/*
+ * Per-layer decode steps on caller-owned device buffers (one token, M = 1).
+ *
+ * fused_attention_step_w4a32 (binding src/ffi/quantization_ffi.rs:345-406,
+ * kernel src/quantization/fused_ops.rs:891-1062):
+ *   qkv = W_qkv x + qkv_b; RoPE on q and k with the current position's row
+ *   cos / sin [head_dim] (q1' = q1 c[i] - q2 s[i], q2' = q2 c[i+d/2] + q1 s[i+d/2]);
+ *   k, v appended to k_cache / v_cache [num_kv_heads, max_seq, head_dim] at
+ *   `offset`; GQA attention over positions 0..offset; out = W_o attn + o_b.
+ * The caches are updated in place, as the reference's are.  TB_UNSUPPORTED when
+ * offset >= max_seq (the reference panics), when num_heads is not a multiple of
+ * num_kv_heads, or for head_dim outside {32, 64, ..., 256}.
+ */
+TB_API int tb_fused_attention_step_w4a32(const float *x, const uint8_t *qkv_w, const float *qkv_s,
+                                         const float *qkv_b, const uint8_t *o_w,
+                                         const float *o_s, const float *o_b, float *k_cache,
+                                         float *v_cache, const float *cos, const float *sin,
+                                         float *out, int64_t hidden, int64_t offset,
+                                         int64_t max_seq, int64_t num_heads,
+                                         int64_t num_kv_heads, int64_t head_dim,
+                                         int64_t group_size, void *stream);
+
+/* fused_attention_step_w8a32 (binding src/ffi/quantization_ffi.rs:284-343, kernel
+ * src/quantization/fused_ops.rs:718-888): as above with INT8 per-channel weights,
+ * scales of 1 or N elements. */
+TB_API int tb_fused_attention_step_w8a32(const float *x, const int8_t *qkv_w, const float *qkv_s,
+                                         int64_t qkv_s_len, const float *qkv_b,
+                                         const int8_t *o_w, const float *o_s, int64_t o_s_len,
+                                         const float *o_b, float *k_cache, float *v_cache,
+                                         const float *cos, const float *sin, float *out,
+                                         int64_t hidden, int64_t offset, int64_t max_seq,
+                                         int64_t num_heads, int64_t num_kv_heads,
+                                         int64_t head_dim, void *stream);
+
+/*
+ * fused_transformer_layer_step_w4a32 (binding src/ffi/quantization_ffi.rs:408-480,
+ * kernel src/quantization/fused_transformer.rs:16-376), x [hidden] updated in place:
+ *   xn = RMSNorm(x, input_norm_w, eps); x += attention step of xn (as above);
+ *   xn = RMSNorm(x, post_norm_w, eps);
+ *   x += W_down (silu(W_gate xn + gate_b) * (W_up xn + up_b)) + down_b.
+ */
+TB_API int tb_fused_transformer_layer_step_w4a32(
+    float *x, const float *input_norm_w, const uint8_t *qkv_w, const float *qkv_s,
+    const float *qkv_b, const uint8_t *o_w, const float *o_s, const float *o_b,
+    const float *post_norm_w, const uint8_t *gate_w, const float *gate_s, const float *gate_b,
+    const uint8_t *up_w, const float *up_s, const float *up_b, const uint8_t *down_w,
+    const float *down_s, const float *down_b, float *k_cache, float *v_cache, const float *cos,
+    const float *sin, int64_t hidden, int64_t intermediate, int64_t offset, int64_t max_seq,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t group_size, double eps,
+    void *stream);
+
 /* ------------------------------------------------------------------------ */
 
 typedef struct tb_decoder tb_decoder;

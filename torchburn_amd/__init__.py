@@ -9,6 +9,11 @@ from ._lib import UnsupportedOpError
 from .decoder import RustQwenDecoder, create_rust_qwen_decoder
 from .quantization import (
     QuantizedLinear,
+    fused_attention_step,
+    fused_attention_step_w4a32,
+    fused_attention_step_w8a32,
+    fused_transformer_layer_step,
+    fused_transformer_layer_step_w4a32,
     fused_swiglu_mlp,
     fused_swiglu_mlp_w4a32,
     fused_swiglu_mlp_w8a32,
@@ -27,6 +32,11 @@ __all__ = [
     "w8a32_linear",
     "UnsupportedOpError",
     "QuantizedLinear",
+    "fused_attention_step",
+    "fused_attention_step_w4a32",
+    "fused_attention_step_w8a32",
+    "fused_transformer_layer_step",
+    "fused_transformer_layer_step_w4a32",
     "fused_swiglu_mlp",
     "fused_swiglu_mlp_w4a32",
     "quantize_model",

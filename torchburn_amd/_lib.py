@@ -46,6 +46,10 @@ _SIGS = {
     "tb_xquant": [_p, _p, _i64, _i64, _p],
     "tb_w4a32_gemv_xq": [_p] * 7 + [_i64] * 4 + [_p],
     "tb_swiglu_w4a32_xq": [_p] * 9 + [_i64] * 4 + [_p],
+    "tb_fused_attention_step_w4a32": [_p] * 12 + [_i64] * 7 + [_p],
+    "tb_fused_attention_step_w8a32": [_p] * 3 + [_i64] + [_p] * 3 + [_i64] + [_p] * 6 +
+                                     [_i64] * 6 + [_p],
+    "tb_fused_transformer_layer_step_w4a32": [_p] * 22 + [_i64] * 8 + [C.c_double, _p],
 }
 
 

@@ -177,7 +177,7 @@ struct Decoder {
             const Layer &y = layers[l];
             float *kcl = kc + (size_t)l * hkv * max_seq * hd;
             float *vcl = vc + (size_t)l * hkv * max_seq * hd;
-            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq};
+            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, hd};
             Fuse fq;
             fq.ssq_in = ssq;
             rc = proj(4, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv, tq, H,
@@ -237,7 +237,7 @@ struct Decoder {
                                 q4 ? xq_h : nullptr, H, eps, st);
             if (rc) return rc;
             // QKV projection + bias + RoPE + KV-cache append in one kernel.
-            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq};
+            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, hd};
             rc = proj(wbits, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv,
                       tq, H, EPI_ROPE, &ra);
             if (rc) return rc;

@@ -249,8 +249,8 @@ __device__ __forceinline__ EpiIn epi_load(const Layout &L, int row0, const Epi &
         in.ps0 = rs0[e.rs0_len > 1 ? qrow : 0];
         // cos / sin of the row's place in its head (unused for V rows)
         const int r = prow % R.hd;
-        in.c = R.cos_t[(size_t)pos * R.hd + r];
-        in.s = R.sin_t[(size_t)pos * R.hd + r];
+        in.c = R.cos_t[(size_t)pos * R.tab_stride + r];
+        in.s = R.sin_t[(size_t)pos * R.tab_stride + r];
     } else {
         in.b0 = b0[rw];
         in.s0 = rs0[e.rs0_len > 1 ? rw : 0];

@@ -13,6 +13,9 @@ namespace tb {
 // Records the message of the last failing call on this thread and returns code.
 int fail(int code, const std::string &msg);
 
+// The library's device scratch (grow-only, one per device) of at least `bytes`.
+int workspace(size_t bytes, void **out);
+
 #define TB_HIP(expr)                                                                   \
     do {                                                                               \
         hipError_t _e = (expr);                                                        \

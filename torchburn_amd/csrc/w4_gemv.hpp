@@ -14,9 +14,10 @@ enum Epilogue { EPI_PLAIN = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ROPE = 3 };
 // holds both halves of every pair it rotates.
 struct RopeArgs {
     const int *pos;           // device: current position
-    const float *cos_t, *sin_t;   // [max_seq, hd] tables
+    const float *cos_t, *sin_t;   // cos / sin of position p at [p * tab_stride + i]
     float *kc, *vc;           // this layer's caches [hkv, max_seq, hd]
     int hq, hkv, hd, max_seq;
+    int tab_stride;           // hd for [max_seq, hd] tables, 0 for one position's row
 };
 
 // Activation rows per GEMV pass (x is held in VGPRs).

@@ -270,6 +270,163 @@ def fused_swiglu_mlp(x: torch.Tensor, gate: Any, up: Any, down: Any) -> torch.Te
 
 
 # --------------------------------------------------------------------------
+# Per-layer decode steps (reference quantization.py:408-572; native
+# fused_ops.rs:718-1062, fused_transformer.rs:16-376)
+# --------------------------------------------------------------------------
+
+def _cache_on_gpu(c: torch.Tensor, dev: torch.device, name: str) -> Tuple[torch.Tensor, int]:
+    """The KV cache as a contiguous f32 GPU tensor (the caller's own storage when
+    it already is one) and its max_seq (the length of dim -2: [.., Hkv, max, hd])."""
+    if c.ndim < 3:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {name} must be [..., num_kv_heads, max_seq, head_dim]")
+    g = c if (c.device == dev and c.dtype == torch.float32 and c.is_contiguous()) else \
+        c.detach().to(device=dev, dtype=torch.float32).contiguous()
+    return g, int(c.shape[-2])
+
+
+def _write_back(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """In-place semantics of the reference (its caches / x are mutated): copy the
+    GPU result into the caller's tensor when it is not that tensor."""
+    if src.data_ptr() != dst.data_ptr():
+        with torch.no_grad():
+            dst.copy_(src.reshape(dst.shape))
+
+
+def _attention_step(bits: int, x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v_cache, cos, sin,
+                    offset: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                    group_size: int) -> torch.Tensor:
+    name = f"fused_attention_step_w{bits}a32"
+    if x.ndim < 1:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name} requires x with at least 1 dim")
+    dev = _target(x)
+    h = x.shape[-1]
+    x1 = _on_gpu(x.reshape(-1, h)[0], torch.float32, dev)   # the reference reads the first row
+    wdt = torch.uint8 if bits == 4 else torch.int8
+    qw, ow = _on_gpu(qkv_w, wdt, dev), _on_gpu(o_w, wdt, dev)
+    qs, os_ = _on_gpu(qkv_s, torch.float32, dev), _on_gpu(o_s, torch.float32, dev)
+    qb, ob = _on_gpu(qkv_b, torch.float32, dev), _on_gpu(o_b, torch.float32, dev)
+    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache")
+    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache")
+    cs = _on_gpu(cos.reshape(-1), torch.float32, dev)
+    sn = _on_gpu(sin.reshape(-1), torch.float32, dev)
+    nq = (num_heads + 2 * num_kv_heads) * head_dim
+    if qw.shape[0] != nq or ow.shape[0] != h:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {name}: qkv rows {qw.shape[0]} (expected {nq}) / "
+            f"o rows {ow.shape[0]} (expected {h})")
+    if cs.numel() < head_dim or sn.numel() < head_dim:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: cos / sin need head_dim values")
+    out = torch.empty(h, dtype=torch.float32, device=dev)
+    if bits == 4:
+        _lib.call("tb_fused_attention_step_w4a32", _ptr(x1), _ptr(qw), _ptr(qs), _ptr(qb),
+                  _ptr(ow), _ptr(os_), _ptr(ob), _ptr(kc), _ptr(vc), _ptr(cs), _ptr(sn),
+                  _ptr(out), h, offset, max_seq, num_heads, num_kv_heads, head_dim, group_size,
+                  _stream(dev))
+    else:
+        qs, os_ = qs.reshape(-1), os_.reshape(-1)
+        _lib.call("tb_fused_attention_step_w8a32", _ptr(x1), _ptr(qw), _ptr(qs), qs.numel(),
+                  _ptr(qb), _ptr(ow), _ptr(os_), os_.numel(), _ptr(ob), _ptr(kc), _ptr(vc),
+                  _ptr(cs), _ptr(sn), _ptr(out), h, offset, max_seq, num_heads, num_kv_heads,
+                  head_dim, _stream(dev))
+    _write_back(k_cache, kc)
+    _write_back(v_cache, vc)
+    return out.reshape(1, h).to(x.device)
+
+
+def fused_attention_step_w4a32(x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v_cache, cos,
+                               sin, offset: int, num_heads: int, num_kv_heads: int,
+                               head_dim: int, group_size: int) -> torch.Tensor:
+    """One attention decode step on INT4 projections (reference
+    fused_ops.rs:891-1062): QKV + bias, RoPE with this position's cos / sin row,
+    k / v written into the caches at `offset` (in place), GQA attention over
+    0..offset, O projection + bias.  Returns [1, hidden]."""
+    return _attention_step(4, x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v_cache, cos, sin,
+                           offset, num_heads, num_kv_heads, head_dim, group_size)
+
+
+def fused_attention_step_w8a32(x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v_cache, cos,
+                               sin, offset: int, num_heads: int, num_kv_heads: int,
+                               head_dim: int) -> torch.Tensor:
+    """fused_attention_step_w4a32 with INT8 per-channel projections (reference
+    fused_ops.rs:718-888)."""
+    return _attention_step(8, x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v_cache, cos, sin,
+                           offset, num_heads, num_kv_heads, head_dim, 32)
+
+
+def fused_transformer_layer_step_w4a32(x, input_norm_w, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b,
+                                       post_norm_w, gate_w, gate_s, gate_b, up_w, up_s, up_b,
+                                       down_w, down_s, down_b, k_cache, v_cache, cos, sin,
+                                       offset: int, num_heads: int, num_kv_heads: int,
+                                       head_dim: int, group_size: int, eps: float = 1e-6) -> None:
+    """One decoder layer in place on x [.., hidden] (reference
+    fused_transformer.rs:16-376): x += attention(RMSNorm(x)); x += MLP(RMSNorm(x))."""
+    name = "fused_transformer_layer_step_w4a32"
+    if x.ndim < 1:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name} requires x with at least 1 dim")
+    dev = _target(x)
+    h = x.shape[-1]
+    xg = x if (x.device == dev and x.dtype == torch.float32 and x.is_contiguous()) else \
+        x.detach().to(device=dev, dtype=torch.float32).contiguous()
+    g = lambda t, dt=torch.float32: _on_gpu(t, dt, dev)
+    qw, ow, gw, uw, dw = (g(t, torch.uint8) for t in (qkv_w, o_w, gate_w, up_w, down_w))
+    qs, os_, gs, us, ds = (g(t) for t in (qkv_s, o_s, gate_s, up_s, down_s))
+    qb, ob, gb, ub, db = (g(t) for t in (qkv_b, o_b, gate_b, up_b, down_b))
+    inw, pnw = g(input_norm_w), g(post_norm_w)
+    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache")
+    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache")
+    cs, sn = g(cos.reshape(-1)), g(sin.reshape(-1))
+    inter = gw.shape[0]
+    if dw.shape[0] != h or dw.shape[1] != (inter + 1) // 2:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {name}: down weight {list(dw.shape)} does not match "
+            f"({h}, {(inter + 1) // 2})")
+    _lib.call("tb_fused_transformer_layer_step_w4a32", _ptr(xg), _ptr(inw), _ptr(qw), _ptr(qs),
+              _ptr(qb), _ptr(ow), _ptr(os_), _ptr(ob), _ptr(pnw), _ptr(gw), _ptr(gs), _ptr(gb),
+              _ptr(uw), _ptr(us), _ptr(ub), _ptr(dw), _ptr(ds), _ptr(db), _ptr(kc), _ptr(vc),
+              _ptr(cs), _ptr(sn), h, inter, offset, max_seq, num_heads, num_kv_heads, head_dim,
+              group_size, float(eps), _stream(dev))
+    _write_back(k_cache, kc)
+    _write_back(v_cache, vc)
+    _write_back(x, xg)
+
+
+def fused_attention_step(x: torch.Tensor, qkv: Any, o_proj: Any, k_cache: torch.Tensor,
+                         v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, offset: int,
+                         num_heads: int, num_kv_heads: int, head_dim: int) -> torch.Tensor:
+    """Attention decode step over QuantizedLinear modules (reference quantization.py:408-485);
+    returns x's shape."""
+    if qkv.bits == 8:
+        out = fused_attention_step_w8a32(x, qkv.qweight, qkv.scales, qkv.bias, o_proj.qweight,
+                                         o_proj.scales, o_proj.bias, k_cache, v_cache, cos, sin,
+                                         offset, num_heads, num_kv_heads, head_dim)
+    elif qkv.bits == 4:
+        out = fused_attention_step_w4a32(x, qkv.qweight, qkv.scales, qkv.bias, o_proj.qweight,
+                                         o_proj.scales, o_proj.bias, k_cache, v_cache, cos, sin,
+                                         offset, num_heads, num_kv_heads, head_dim,
+                                         qkv.group_size)
+    else:
+        raise ValueError(f"Unsupported bits={qkv.bits}")
+    return out.reshape(x.shape)
+
+
+def fused_transformer_layer_step(x: torch.Tensor, layer: Any, k_cache: torch.Tensor,
+                                 v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                                 offset: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                                 eps: float = 1e-6) -> torch.Tensor:
+    """One decoder block over a layer of QuantizedLinear modules (reference
+    quantization.py:488-572): x is updated in place and returned."""
+    at, mlp = layer.self_attn, layer.mlp
+    qkv, o, gt, up, dn = at.qkv_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj
+    fused_transformer_layer_step_w4a32(
+        x, layer.input_layernorm.weight, qkv.qweight, qkv.scales, qkv.bias, o.qweight, o.scales,
+        o.bias, layer.post_attention_layernorm.weight, gt.qweight, gt.scales, gt.bias, up.qweight,
+        up.scales, up.bias, dn.qweight, dn.scales, dn.bias, k_cache, v_cache, cos, sin, offset,
+        num_heads, num_kv_heads, head_dim, qkv.group_size, eps)
+    return x
+
+
+# --------------------------------------------------------------------------
 # QuantizedLinear (reference quantization.py:756-869)
 # --------------------------------------------------------------------------
 
