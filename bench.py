@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--decode", default="llama4,llama8,qwen",
                     help="decode runs: comma list of llama4, llama8, qwen, or 'none'")
     ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="batched prefill timed on the llama4 decoder (0: skip)")
     ap.add_argument("--batched", default="16x4096,16x14336,64x4096,64x14336",
                     help="config 3 MxN projections (K=4096) on FP32 MFMA, or 'none'")
     ap.add_argument("--mlp-batches", default="4,8",
@@ -281,7 +283,7 @@ def mlp_batch_section(torch, args, dev):
     return out
 
 
-def decode_run(torch, name, steps):
+def decode_run(torch, name, steps, prefill_tokens=0):
     from torchburn_amd import synth
     from torchburn_amd.decoder import decoder_from_weights
     cfg, wk, lk, kvlen, seed = {
@@ -306,14 +308,39 @@ def decode_run(torch, name, steps):
     first = seed % cfg["vocab"]
     dec.time_greedy(first, kvlen, min(8, steps))          # warm-up (same positions)
     ms = dec.time_greedy(first, kvlen, steps)
+    pre = prefill_run(dec, cfg, prefill_tokens) if prefill_tokens and wk == 4 else None
     dec.close()
     torch.cuda.empty_cache()
     byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk) for i in range(steps)) / steps
     sec = ms / 1e3 / steps
-    return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(ms / steps, 4),
-            "bytes_per_token": int(byts), "kv_len": kvlen,
-            "roofline_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4),
-            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / byts, 1)}
+    out = {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(ms / steps, 4),
+           "bytes_per_token": int(byts), "kv_len": kvlen,
+           "roofline_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / byts, 1)}
+    if pre:
+        out["prefill"] = pre
+    return out
+
+
+def prefill_run(dec, cfg, n):
+    """Batched prompt prefill of n tokens from an empty cache (wall clock of the
+    whole call: token upload, every layer's kernels, lm_head, logits download)."""
+    from torchburn_amd import synth
+    g = np.random.default_rng(7)
+    prompt = [int(t) for t in g.integers(0, cfg["vocab"], n)]
+    dec.reset_kv_cache()
+    dec.prefill_tokens(prompt, 0)                      # warm-up, allocates the batch buffers
+    times = []
+    for _ in range(3):
+        dec.reset_kv_cache()
+        t0 = time.perf_counter()
+        dec.prefill_tokens(prompt, 0)
+        times.append(time.perf_counter() - t0)
+    sec = min(times)
+    fl = synth.prefill_flops(cfg, n)
+    return {"tokens": n, "ms": round(sec * 1e3, 3), "tok_s": round(n / sec, 1),
+            "tflops": round(fl / sec / 1e12, 2), "flops": fl,
+            "mfma_fp32_frac": round(fl / sec / 1e12 / MFMA_F32_PEAK, 4)}
 
 
 def main():
@@ -346,7 +373,8 @@ def main():
     decode = {}
     if args.decode != "none":
         for name in args.decode.split(","):
-            decode[name] = decode_run(torch, name.strip(), args.decode_steps)
+            decode[name] = decode_run(torch, name.strip(), args.decode_steps,
+                                      args.prefill_tokens if name.strip() == "llama4" else 0)
     line = {
         "metric": "INT4 GEMV HBM GB/s (% of 8 TB/s); decode tokens/sec at 8B shape, 1 GPU",
         "value": round(gbs, 1),

@@ -98,6 +98,30 @@ def test_mfma_swiglu_mlp_matches_oracle(cuda, m, k, inter, gs):
     assert err < TOL
 
 
+@pytest.mark.parametrize("shape", [(2, 40), (1, 1), (3, 1)])
+def test_swiglu_mlp_batched_name_matches_oracle(cuda, shape):
+    """fused_swiglu_mlp_batched_w4a32 on (batch, T, K): rows flattened, output
+    (batch, T, N_down); no residual.  (1, 1) is the reference's per-token branch."""
+    b, t = shape
+    k, inter, gs = 896, 4864, 64
+    print(f"case fused_swiglu_mlp_batched_w4a32 batch={b} T={t}", flush=True)
+    g = synth.rng(34, b, t)
+    x = synth.activations(g, b * t, k)
+    gw, gsc = synth.int4_weight(g, inter, k, gs)
+    uw, usc = synth.int4_weight(g, inter, k, gs)
+    dw, dsc = synth.int4_weight(g, k, inter, gs)
+    db = g.normal(0, 0.1, k).astype(np.float32)
+    ref = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, db=db, group_size=gs)
+    out = tb.fused_swiglu_mlp_batched_w4a32(T(x.reshape(b, t, k), cuda), T(gw, cuda),
+                                            T(gsc, cuda), None, T(uw, cuda), T(usc, cuda), None,
+                                            T(dw, cuda), T(dsc, cuda), T(db, cuda))
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (b, t, k)
+    err = rel(out.cpu().numpy().reshape(b * t, k), ref)
+    print(f"max rel err {err:.3g}", flush=True)
+    assert err < TOL
+
+
 def test_mfma_special_cases(cuda):
     """x == 0 -> bias exactly; one-hot rows -> columns of the dequantized matrix;
     constant q with unit scales -> c * sum(x)."""

@@ -16,6 +16,7 @@ from .quantization import (
     fused_transformer_layer_step_w4a32,
     fused_swiglu_mlp,
     fused_swiglu_mlp_w4a32,
+    fused_swiglu_mlp_batched_w4a32,
     fused_swiglu_mlp_w8a32,
     quantize_model,
     quantize_weight_int4_grouped,
@@ -39,6 +40,7 @@ __all__ = [
     "fused_transformer_layer_step_w4a32",
     "fused_swiglu_mlp",
     "fused_swiglu_mlp_w4a32",
+    "fused_swiglu_mlp_batched_w4a32",
     "quantize_model",
     "quantize_weight_int4_grouped",
     "quantize_weight_int8",

@@ -660,6 +660,206 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ 
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Batched prefill (M consecutive prompt positions per launch)
+// ---------------------------------------------------------------------------
+
+// X[m] = embed[tok[m]] (tokens validated on the host).
+__global__ __launch_bounds__(256) void k_embed_rows(const int *__restrict__ tok,
+                                                    const float *__restrict__ embed,
+                                                    float *__restrict__ X, int H) {
+    const float4 *src = reinterpret_cast<const float4 *>(embed + (size_t)tok[blockIdx.x] * H);
+    float4 *dst = reinterpret_cast<float4 *>(X + (size_t)blockIdx.x * H);
+    for (int i = threadIdx.x; i < H / 4; i += blockDim.x) dst[i] = src[i];
+}
+
+// RMSNorm of one row per block, with k_rmsnorm's arithmetic (the same
+// per-thread sum order and two roundings of (x * inv) * w).
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ X,
+                                                      const float *__restrict__ w,
+                                                      float *__restrict__ Xn, int H, float eps) {
+    __shared__ float scratch[16];
+    const int tid = threadIdx.x;
+    const float4 *s4 = reinterpret_cast<const float4 *>(X + (size_t)blockIdx.x * H);
+    float ss = 0.f;
+    for (int i = tid; i < H / 4; i += blockDim.x) {
+        const float4 v = s4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    const float tot = block_sum(ss, scratch);
+    const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+    float4 *d4 = reinterpret_cast<float4 *>(Xn + (size_t)blockIdx.x * H);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    for (int i = tid; i < H / 4; i += blockDim.x) {
+        const float4 v = s4[i], ww = w4[i];
+        d4[i] = make_float4(__fmul_rn(__fmul_rn(v.x, inv), ww.x), __fmul_rn(__fmul_rn(v.y, inv), ww.y),
+                            __fmul_rn(__fmul_rn(v.z, inv), ww.z), __fmul_rn(__fmul_rn(v.w, inv), ww.w));
+    }
+}
+
+// RoPE of the q and k heads of row m (position start + m) and the KV-cache
+// append, as the decode epilogue does it (decoder.rs:28-68, 1137-1146):
+// q1' = q1 c[i] - q2 s[i], q2' = q2 c[i + d/2] + q1 s[i + d/2], products
+// rounded separately.  Grid (M, hq + 2 hkv), hd / 2 threads.
+__global__ void k_rope_rows(const float *__restrict__ qkv, int nq, float *__restrict__ q,
+                            float *__restrict__ kc, float *__restrict__ vc,
+                            const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                            int start, int hq, int hkv, int hd, int max_seq) {
+    const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x, half = hd >> 1;
+    const int pos = start + m;
+    const float *src = qkv + (size_t)m * nq + (size_t)head * hd;
+    const float x1 = src[i], x2 = src[i + half];
+    if (head < hq + hkv) {
+        const float *cr = cos_t + (size_t)pos * hd, *sr = sin_t + (size_t)pos * hd;
+        const float y1 = __fsub_rn(__fmul_rn(x1, cr[i]), __fmul_rn(x2, sr[i]));
+        const float y2 = __fadd_rn(__fmul_rn(x2, cr[i + half]), __fmul_rn(x1, sr[i + half]));
+        float *dst = head < hq ? q + ((size_t)m * hq + head) * hd
+                               : kc + ((size_t)(head - hq) * max_seq + pos) * hd;
+        dst[i] = y1;
+        dst[i + half] = y2;
+    } else {
+        float *dst = vc + ((size_t)(head - hq - hkv) * max_seq + pos) * hd;
+        dst[i] = x1;
+        dst[i + half] = x2;
+    }
+}
+
+// Causal GQA attention of M consecutive query positions start .. start+M-1
+// over the cache (query at position p sees keys 0..p; decoder.rs:1148-1213):
+// one query head and 64 query positions per block; K and V tiles of 64
+// positions staged in LDS (zero past the last position the block needs);
+// 4 x 4 score micro-tiles per thread; online softmax with a running max and
+// sum per row, then 1 / max(sum, 1e-30).  out [M][hq * HD].
+template <int HD>
+__global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ q,
+                                                      const float *__restrict__ kc,
+                                                      const float *__restrict__ vc,
+                                                      float *__restrict__ out, int start, int M,
+                                                      int hq, int hkv, int max_seq, float scale) {
+    constexpr int QT = 64, KT = 64, HP = HD + 4, OC = HD / 16;
+    __shared__ __attribute__((aligned(16))) float sq[QT][HP];
+    __shared__ __attribute__((aligned(16))) float sk[KT][HP];
+    __shared__ __attribute__((aligned(16))) float sv[KT][HP];
+    __shared__ float sp[QT][KT + 1];
+    const int h = blockIdx.y, kvh = h / (hq / hkv);
+    const int m0 = blockIdx.x * QT;
+    const int t = threadIdx.x, rg = t >> 4, kg = t & 15;   // rows 4rg.., keys 4kg.., cols kg*OC..
+    for (int i = t; i < QT * (HD / 4); i += 256) {
+        const int r = i / (HD / 4), c4 = i - r * (HD / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m0 + r < M) v = reinterpret_cast<const float4 *>(q + ((size_t)(m0 + r) * hq + h) * HD)[c4];
+        *reinterpret_cast<float4 *>(&sq[r][4 * c4]) = v;
+    }
+    float mrun[4], lrun[4], o[4][OC];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        mrun[r] = -INFINITY;
+        lrun[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < OC; ++c) o[r][c] = 0.f;
+    }
+    const int last = start + min(m0 + QT, M) - 1;   // last position any row of the block sees
+    const int ntiles = last / KT + 1;
+    const float *kb = kc + (size_t)kvh * max_seq * HD, *vb = vc + (size_t)kvh * max_seq * HD;
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();
+        for (int i = t; i < KT * (HD / 4); i += 256) {
+            const int j = i / (HD / 4), c4 = i - j * (HD / 4);
+            const int p = kt * KT + j;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (p <= last) {
+                kv = reinterpret_cast<const float4 *>(kb + (size_t)p * HD)[c4];
+                vv = reinterpret_cast<const float4 *>(vb + (size_t)p * HD)[c4];
+            }
+            *reinterpret_cast<float4 *>(&sk[j][4 * c4]) = kv;
+            *reinterpret_cast<float4 *>(&sv[j][4 * c4]) = vv;
+        }
+        __syncthreads();
+        float s[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s[r][j] = 0.f;
+        for (int d = 0; d < HD; d += 4) {
+            float4 qa[4], kk[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) qa[r] = *reinterpret_cast<const float4 *>(&sq[4 * rg + r][d]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kk[j] = *reinterpret_cast<const float4 *>(&sk[4 * kg + j][d]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    s[r][j] = fmaf(qa[r].x, kk[j].x, s[r][j]);
+                    s[r][j] = fmaf(qa[r].y, kk[j].y, s[r][j]);
+                    s[r][j] = fmaf(qa[r].z, kk[j].z, s[r][j]);
+                    s[r][j] = fmaf(qa[r].w, kk[j].w, s[r][j]);
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int pq = start + m0 + 4 * rg + r;
+            float mt = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pk = kt * KT + 4 * kg + j;
+                s[r][j] = pk <= pq ? s[r][j] * scale : -INFINITY;
+                mt = fmaxf(mt, s[r][j]);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
+            const float mn = fmaxf(mrun[r], mt);
+            // all-masked so far: nothing to rescale, every p is 0
+            const float alpha = mn == -INFINITY ? 1.f : expf(mrun[r] - mn);
+            float ls = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float pj = mn == -INFINITY ? 0.f : expf(s[r][j] - mn);
+                sp[4 * rg + r][4 * kg + j] = pj;
+                ls += pj;
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) ls += __shfl_xor(ls, off);
+            lrun[r] = lrun[r] * alpha + ls;
+            mrun[r] = mn;
+#pragma unroll
+            for (int c = 0; c < OC; ++c) o[r][c] *= alpha;
+        }
+        __syncthreads();
+        for (int j = 0; j < KT; ++j) {
+            float pv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pv[r] = sp[4 * rg + r][j];
+#pragma unroll
+            for (int c = 0; c < OC; c += 4) {
+                const float4 vv = *reinterpret_cast<const float4 *>(&sv[j][kg * OC + c]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    o[r][c] = fmaf(pv[r], vv.x, o[r][c]);
+                    o[r][c + 1] = fmaf(pv[r], vv.y, o[r][c + 1]);
+                    o[r][c + 2] = fmaf(pv[r], vv.z, o[r][c + 2]);
+                    o[r][c + 3] = fmaf(pv[r], vv.w, o[r][c + 3]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 4 * rg + r;
+        if (m >= M) continue;
+        const float inv = 1.0f / fmaxf(lrun[r], 1e-30f);
+        float *dst = out + ((size_t)m * hq + h) * HD + kg * OC;
+#pragma unroll
+        for (int c = 0; c < OC; c += 4)
+            *reinterpret_cast<float4 *>(dst + c) =
+                make_float4(o[r][c] * inv, o[r][c + 1] * inv, o[r][c + 2] * inv, o[r][c + 3] * inv);
+    }
+}
+
 }  // namespace
 
 int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
@@ -751,6 +951,48 @@ int launch_argmax(const float *logits, int n, float *pv, int *pi, DecState *st, 
     TB_LAUNCHED();
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, pv, pi, kArgmaxBlocks, n, st,
                        history, hist_cap);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_embed_rows(const int *tok, const float *embed, float *X, int M, int H, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_rows, dim3(M), dim3(256), 0, s, tok, embed, X, H);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_rmsnorm_rows(const float *X, const float *w, float *Xn, int M, int H, float eps,
+                        hipStream_t s) {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(M), dim3(256), 0, s, X, w, Xn, H, eps);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const float *cos_t,
+                     const float *sin_t, int start, int M, int hq, int hkv, int hd, int max_seq,
+                     hipStream_t s) {
+    const int nq = (hq + 2 * hkv) * hd;
+    hipLaunchKernelGGL(k_rope_rows, dim3(M, hq + 2 * hkv), dim3(hd / 2), 0, s, qkv, nq, q, kc, vc,
+                       cos_t, sin_t, start, hq, hkv, hd, max_seq);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int launch_prefill_attention(const float *q, const float *kc, const float *vc, float *out,
+                             int start, int M, int hq, int hkv, int hd, int max_seq,
+                             hipStream_t s) {
+    TB_REQUIRE(hq % hkv == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: num_heads must be a multiple of num_kv_heads");
+    const dim3 grid((M + 63) / 64, hq);
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_prefill_attn<128>, grid, dim3(256), 0, s, q, kc, vc, out, start, M,
+                           hq, hkv, max_seq, scale);
+    else if (hd == 64)
+        hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, q, kc, vc, out, start, M, hq,
+                           hkv, max_seq, scale);
+    else
+        return fail(TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: head_dim must be 64 or 128");
     TB_LAUNCHED();
     return TB_OK;
 }

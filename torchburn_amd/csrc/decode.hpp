@@ -34,6 +34,18 @@ int attn_nsplit(int max_seq);
 int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
                      float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
                      hipStream_t s);
+// Batched prefill: M consecutive positions start .. start+M-1.
+int launch_embed_rows(const int *tok, const float *embed, float *X, int M, int H, hipStream_t s);
+int launch_rmsnorm_rows(const float *X, const float *w, float *Xn, int M, int H, float eps,
+                        hipStream_t s);
+// qkv [M][(hq + 2 hkv) hd] -> q [M][hq][hd] rotated; k (rotated) and v into the caches.
+int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const float *cos_t,
+                     const float *sin_t, int start, int M, int hq, int hkv, int hd, int max_seq,
+                     hipStream_t s);
+// Causal attention of the M rows of q over cache positions 0 .. start + m; out [M][hq hd].
+int launch_prefill_attention(const float *q, const float *kc, const float *vc, float *out,
+                             int start, int M, int hq, int hkv, int hd, int max_seq,
+                             hipStream_t s);
 int launch_argmax(const float *logits, int n, float *pv, int *pi, DecState *st, int *history,
                   int hist_cap, hipStream_t s);
 

@@ -28,6 +28,7 @@
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
+#include "w4_mfma.hpp"
 
 struct tb_decoder;
 
@@ -295,6 +296,102 @@ struct Decoder {
         hstate->step = 0;
         hstate->argmax = 0;
         TB_HIP(hipMemcpyAsync(state, hstate, sizeof(DecState), hipMemcpyHostToDevice, st));
+        return TB_OK;
+    }
+
+    // ---- Batched prefill (INT4 projections on the FP32-MFMA GEMM) ----------
+    // Chunks of up to kPrefillRows prompt positions go through each layer as
+    // one batch: row RMSNorms, QKV GEMM (+bias), RoPE + KV append for every
+    // row, causal prefill attention, O GEMM + residual, gate/up GEMM with
+    // SwiGLU, down GEMM + residual; the last row then takes the final norm
+    // and lm_head as a step would.  Buffers are allocated on first use.
+    static constexpr int kPrefillRows = 256;
+    float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
+          *pf_a = nullptr, *pf_h = nullptr, *pf_part = nullptr;
+    int *pf_tok = nullptr;
+
+    int prefill_alloc() {
+        if (pf_x) return TB_OK;
+        const int R = kPrefillRows;
+        const size_t nq = (size_t)(hq + 2 * hkv) * hd;
+        size_t part = w4_mfma_partials_bytes(R, (int)nq, H, false);
+        part = std::max(part, w4_mfma_partials_bytes(R, H, hq * hd, false));
+        part = std::max(part, w4_mfma_partials_bytes(R, I, H, true));
+        part = std::max(part, w4_mfma_partials_bytes(R, H, I, false));
+        int rc;
+        if ((rc = alloc(&pf_x, (size_t)R * H * 4)) || (rc = alloc(&pf_xn, (size_t)R * H * 4)) ||
+            (rc = alloc(&pf_qkv, (size_t)R * nq * 4)) ||
+            (rc = alloc(&pf_q, (size_t)R * hq * hd * 4)) ||
+            (rc = alloc(&pf_a, (size_t)R * hq * hd * 4)) || (rc = alloc(&pf_h, (size_t)R * I * 4)) ||
+            (rc = alloc(&pf_part, part)) || (rc = alloc(&pf_tok, (size_t)R * 4)))
+            return rc;
+        return TB_OK;
+    }
+
+    int gemm(const float *xin, const void *w, const float *s, const float *b, const void *w2,
+             const float *s2, const float *res, float *y, int m, int n, int k, int epi) {
+        MfmaParams p{};
+        p.x = xin;
+        p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
+        p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
+        p.res = res; p.y = y; p.m = m; p.n = n; p.k = k; p.gshift = gshift(gs);
+        return w4_mfma(p, epi, pf_part, st);
+    }
+
+    bool prefill_batchable(const int64_t *tokens, int64_t n) const {
+        static const bool loop_only = getenv("TB_PREFILL_LOOP") != nullptr;
+        if (loop_only || wbits != 4 || n < 16) return false;
+        for (int64_t i = 0; i < n; ++i)
+            if (tokens[i] < 0 || tokens[i] >= V) return false;   // the step's zero-logit rule
+        return true;
+    }
+
+    int prefill_batched(const int64_t *tokens, int64_t n, int64_t start) {
+        int rc = prefill_alloc();
+        if (rc) return rc;
+        const int nq = (hq + 2 * hkv) * hd;
+        // Host copy of the whole prompt, alive until the closing synchronize.
+        std::vector<int> tok32(tokens, tokens + n);
+        for (int64_t c0 = 0; c0 < n; c0 += kPrefillRows) {
+            const int M = (int)std::min<int64_t>(kPrefillRows, n - c0);
+            const int pos0 = (int)(start + c0);
+            TB_HIP(hipMemcpyAsync(pf_tok, tok32.data() + c0, (size_t)M * 4, hipMemcpyHostToDevice,
+                                  st));
+            if ((rc = launch_embed_rows(pf_tok, embed, pf_x, M, H, st))) return rc;
+            for (int l = 0; l < L; ++l) {
+                const Layer &y = layers[l];
+                float *kcl = kc + (size_t)l * hkv * max_seq * hd;
+                float *vcl = vc + (size_t)l * hkv * max_seq * hd;
+                if ((rc = launch_rmsnorm_rows(pf_x, y.in_norm, pf_xn, M, H, eps, st)) ||
+                    (rc = gemm(pf_xn, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, pf_qkv,
+                               M, nq, H, EPI_PLAIN)) ||
+                    (rc = launch_rope_rows(pf_qkv, pf_q, kcl, vcl, cos_t, sin_t, pos0, M, hq, hkv,
+                                           hd, max_seq, st)) ||
+                    (rc = launch_prefill_attention(pf_q, kcl, vcl, pf_a, pos0, M, hq, hkv, hd,
+                                                   max_seq, st)) ||
+                    (rc = gemm(pf_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H,
+                               hq * hd, EPI_RESID)) ||
+                    (rc = launch_rmsnorm_rows(pf_x, y.post_norm, pf_xn, M, H, eps, st)) ||
+                    (rc = gemm(pf_xn, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, pf_h,
+                               M, I, H, EPI_SWIGLU)) ||
+                    (rc = gemm(pf_h, y.down_w, y.down_s, nullptr, nullptr, nullptr, pf_x, pf_x, M,
+                               H, I, EPI_RESID)))
+                    return rc;
+            }
+            if (c0 + M == n) {
+                // The last position's hidden state -> final norm -> lm_head.
+                TB_HIP(hipMemcpyAsync(x, pf_x + (size_t)(M - 1) * H, (size_t)H * 4,
+                                      hipMemcpyDeviceToDevice, st));
+                if ((rc = launch_rmsnorm(state, nullptr, x, final_norm, xn,
+                                         lmbits == 4 ? xq_h : nullptr, H, eps, st)) ||
+                    (rc = proj(lmbits, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr,
+                               logits, V, H, EPI_PLAIN)))
+                    return rc;
+            }
+        }
+        kv_used = std::max<int64_t>(kv_used, start + n);
+        TB_HIP(hipMemcpyAsync(host_logits.data(), logits, (size_t)V * 4, hipMemcpyDeviceToHost, st));
+        TB_HIP(hipStreamSynchronize(st));
         return TB_OK;
     }
 
@@ -638,9 +735,14 @@ int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n, int64_t 
     TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
                "prefill " + std::to_string(n) + " tokens at offset " + std::to_string(start_offset) +
                    " exceeds max_seq_len " + std::to_string(d->max_seq));
-    for (int64_t i = 0; i < n; ++i) {
-        int rc = d->step(tokens[i], start_offset + i, i + 1 == n, nullptr);
+    if (d->prefill_batchable(tokens, n)) {
+        int rc = d->prefill_batched(tokens, n, start_offset);
         if (rc) return rc;
+    } else {
+        for (int64_t i = 0; i < n; ++i) {
+            int rc = d->step(tokens[i], start_offset + i, i + 1 == n, nullptr);
+            if (rc) return rc;
+        }
     }
     *offset_out = start_offset + n;
     return TB_OK;

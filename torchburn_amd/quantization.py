@@ -207,6 +207,25 @@ def fused_swiglu_mlp_w4a32(
     return out.reshape(*x.shape[:-1], n_out).to(x.device)
 
 
+def fused_swiglu_mlp_batched_w4a32(
+    x: torch.Tensor,
+    gate_w: torch.Tensor, gate_s: torch.Tensor, gate_b: Optional[torch.Tensor],
+    up_w: torch.Tensor, up_s: torch.Tensor, up_b: Optional[torch.Tensor],
+    down_w: torch.Tensor, down_s: torch.Tensor, down_b: Optional[torch.Tensor],
+    group_size: int = 64,
+) -> torch.Tensor:
+    """Prefill SwiGLU MLP over x (batch, T, K) -> (batch, T, N_down)
+    (reference quantization_ffi.rs:511-570 -> fused_ops.rs:1267-1319: gate GEMM,
+    up GEMM, silu(g) * u, down GEMM; one row delegates to the per-token path).
+    Both cases go through tb_fused_swiglu_mlp_w4a32, which runs rows >= 5 as the
+    FP32-MFMA GEMM pair and fewer as GEMV passes."""
+    if x.dim() < 1:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} fused_swiglu_mlp_batched_w4a32: x needs >= 1 dim")
+    return fused_swiglu_mlp_w4a32(x, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s,
+                                  down_b, group_size)
+
+
 def w8a32_linear(
     x: torch.Tensor,
     w: torch.Tensor,

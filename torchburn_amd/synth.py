@@ -142,6 +142,19 @@ def decoder_weights_torch(cfg: dict, seed: int, wkind: int = 4, lmkind: int = 4,
                 lm_head_w=lm_w, lm_head_s=lm_s, layers=layers)
 
 
+def prefill_flops(cfg: dict, n: int, start: int = 0) -> int:
+    """Algorithmic FLOPs of prefilling n prompt tokens after `start` cached ones:
+    2 per multiply-add of the four projections for every token, QK^T and PV over
+    positions 0..p for the token at p, and the lm_head for the last token only."""
+    H, I = cfg["hidden"], cfg["intermediate"]
+    hq, hkv, hd = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    tq = (hq + 2 * hkv) * hd
+    lin = 2 * (tq * H + H * hq * hd + 3 * I * H)
+    keys = sum(start + i + 1 for i in range(n))
+    attn = 2 * 2 * hq * hd * keys
+    return cfg["num_layers"] * (lin * n + attn) + 2 * cfg["vocab"] * H
+
+
 def decode_bytes_per_token(cfg: dict, pos: int, wkind: int, lmkind: int,
                            group_size: int = 32) -> int:
     """Algorithmic HBM bytes of one decoder step at position `pos`: every weight
