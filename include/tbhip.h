@@ -72,6 +72,49 @@ TB_API int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, cons
                             int64_t group_size, void *stream);
 
 /*
+ * The v2 layout (src/quantization/packed_v2.rs:26-143): each 64-element group
+ * of a row is one 34-byte block, 32 bytes of v1 nibbles then the group scale as
+ * little-endian IEEE binary16.
+ *
+ * out[m, n] = sum_g f16(block[n, g]) * sum_{i in g} (nib - 8) * x[m, i] + bias[n]:
+ * the reference's w4a32_grouped_linear_v2 (binding
+ * src/ffi/quantization_ffi.rs:87-108 -> src/quantization/packed_v2.rs:489-553
+ * -> gemv_w4a32_grouped_v2, packed_v2.rs:326-485).  w_blocked u8 [N, (K/64)*34]
+ * (4-byte aligned); group_size must be 64 and K a multiple of 64 (the
+ * reference's quantizer requires both, python/torchburn/quantization.py:121-152).
+ */
+TB_API int tb_w4a32_grouped_linear_v2(const float *x, const uint8_t *w_blocked, const float *bias,
+                                      float *out, int64_t m, int64_t n, int64_t k,
+                                      int64_t group_size, void *stream);
+
+/*
+ * v1 nibbles [N, K/2] + f32 scales [N, K/64] -> v2 blocks [N, (K/64)*34], the
+ * scales rounded to binary16 to nearest even: pack_rows_w4a32_group64_v1_to_v2
+ * (src/quantization/packed_v2.rs:114-143, f32_to_f16 66-105), run on the device.
+ */
+TB_API int tb_pack_rows_w4a32_group64_v1_to_v2(const uint8_t *w_packed, const float *scales,
+                                               uint8_t *out, int64_t n, int64_t k, void *stream);
+
+/*
+ * v2 blocks [N, (K/64)*34] -> f32 weights [N, K], (nib - 8) * f16 scale:
+ * dequantize_int4_grouped_v2 (python/torchburn/quantization.py:155-169).
+ */
+TB_API int tb_dequantize_int4_grouped_v2(const uint8_t *w_blocked, float *out, int64_t n,
+                                         int64_t k, void *stream);
+
+/*
+ * Selects the reference's AVX-512 VNNI-tier semantics for group-64 INT4
+ * projections (tb_w4a32_grouped_linear[_residual] at group 64 and
+ * tb_w4a32_grouped_linear_v2): each activation row is quantized to bytes,
+ * s_x = max(max|x|, 1e-10) / 127, q = round-half-even(x * (1 / s_x))
+ * (src/quantization/gemv.rs:1353-1389), and contracted with the nibbles
+ * (gemv.rs:1422-1473, packed_v2.rs:204-323).  The reference picks this by CPU
+ * feature (gemv.rs:1541-1563); 0 (the default) is its exact W4A32 result.
+ * Returns the previous setting.  Process-wide.
+ */
+TB_API int tb_set_vnni_semantics(int enabled);
+
+/*
  * out = residual + w4a32_grouped_linear(x, ...).  The reference performs the
  * residual add as a separate pass after the projection
  * (src/llm/decoder.rs:1235-1238 and 1344-1347, fast_vector_add at

@@ -74,6 +74,19 @@ def lib():
         L.orc_decoder_copy_kv.argtypes = [_vp, _i64, _vp, _vp, _i64, _i64]
         L.orc_decoder_copy_kv.restype = C.c_int
         L.orc_num_threads.restype = C.c_int
+        _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16_n.argtypes = [_f32p, _u16p, _i64]
+        L.orc_f16_to_f32_n.argtypes = [_u16p, _f32p, _i64]
+        L.orc_pack_v1_to_v2.argtypes = [_u8p, _f32p, _u8p, _i64, _i64]
+        L.orc_gemv_w4_v2.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64]
+        L.orc_gemm_w4_v2.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64]
+        L.orc_quantize_act_u8.argtypes = [_f32p, _i64, _u8p]
+        L.orc_quantize_act_u8.restype = C.c_float
+        L.orc_gemv_w4a8_g64.argtypes = [_vp, _vp, _vp, C.c_int, _vp, _vp, _i64, _i64]
         _lib = L
     return _lib
 
@@ -133,6 +146,71 @@ def gemv_w4_f64(x, w, s, bias=None, group_size=32) -> np.ndarray:
     n = w.shape[0]
     y = np.empty(n, np.float64)
     lib().orc_gemv_w4_f64(_p(x), _p(w), _p(s), _p(bias), _p(y), n, x.size, group_size)
+    return y
+
+
+def f32_to_f16_bits(v) -> np.ndarray:
+    """IEEE binary16 bits of each f32, round to nearest even (packed_v2.rs:66-105)."""
+    v = _c(v, np.float32).reshape(-1)
+    out = np.empty(v.size, np.uint16)
+    lib().orc_f32_to_f16_n(v, out, v.size)
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    """binary16 bits -> f32 (packed_v2.rs:32-56)."""
+    h = _c(h, np.uint16).reshape(-1)
+    out = np.empty(h.size, np.float32)
+    lib().orc_f16_to_f32_n(h, out, h.size)
+    return out
+
+
+def pack_v1_to_v2(w: np.ndarray, s: np.ndarray, k: int) -> np.ndarray:
+    """v1 nibbles [n, k/2] + f32 scales [n, k/64] -> v2 blocks [n, (k/64) * 34]."""
+    w, s = _c(w, np.uint8), _c(s, np.float32)
+    n = w.shape[0]
+    out = np.empty((n, (k // 64) * 34), np.uint8)
+    lib().orc_pack_v1_to_v2(w, s, out, n, k)
+    return out
+
+
+def gemm_w4_v2(x, blocked, bias=None) -> np.ndarray:
+    """w4a32_grouped_linear_v2 (packed_v2.rs:489-553), exact (non-VNNI) tiers."""
+    x = _c(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    m, k = x2.shape
+    blocked = _c(blocked, np.uint8)
+    n = blocked.shape[0]
+    y = np.empty((m, n), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().orc_gemm_w4_v2(_p(x2), _p(blocked), _p(b), _p(y), m, n, k)
+    return y
+
+
+def quantize_act_u8(x):
+    """(bytes, s_x) of quantize_activation_to_u8 (gemv.rs:1353-1389)."""
+    x = _c(x, np.float32).reshape(-1)
+    out = np.empty(x.size, np.uint8)
+    sx = lib().orc_quantize_act_u8(x, x.size, out)
+    return out, float(np.float32(sx))
+
+
+def gemm_w4a8_g64(x, w, s=None, bias=None, blocked=False) -> np.ndarray:
+    """The AVX-512 VNNI tier's W4A8 GEMV at group 64 (gemv.rs:1422-1473; v2 blocks
+    packed_v2.rs:204-323), one activation row at a time."""
+    x = _c(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    m, k = x2.shape
+    w = _c(w, np.uint8)
+    n = w.shape[0]
+    sv = None if s is None else _c(s, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    y = np.empty((m, n), np.float32)
+    for i in range(m):
+        xi = np.ascontiguousarray(x2[i])
+        yi = np.empty(n, np.float32)
+        lib().orc_gemv_w4a8_g64(_p(xi), _p(w), _p(sv), int(blocked), _p(b), _p(yi), n, k)
+        y[i] = yi
     return y
 
 

@@ -212,6 +212,184 @@ ORC_API void orc_gemv_w4_f64(const float *x, const uint8_t *w, const float *s,
 }
 
 /* ------------------------------------------------------------------------ */
+/* f2: the v2 layout, packed_v2.rs:26-143.  One 34-byte block per 64-element  */
+/* group: 32 bytes of v1 nibbles, then the group scale as IEEE binary16,       */
+/* little-endian.                                                             */
+/* ------------------------------------------------------------------------ */
+
+/* binary16 -> binary32 (packed_v2.rs:32-56): exact for every finite value;   */
+/* +-inf kept; any NaN becomes the default quiet NaN.                          */
+ORC_API float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u;
+    float v;
+    if (e == 0)
+        v = ldexpf((float)m, -24); /* zero or subnormal: m * 2^-24 */
+    else if (e == 31)
+        v = m ? NAN : INFINITY;
+    else {
+        uint32_t b = ((e + 112u) << 23) | (m << 13);
+        memcpy(&v, &b, 4);
+    }
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    if (!(e == 31 && m)) bits |= sign;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+
+/* binary32 -> binary16, round to nearest even (packed_v2.rs:66-105):        */
+/* overflow to +-inf, NaN to sign | 0x7E00, underflow to signed zero, with   */
+/* RNE on the bits shifted out in the subnormal range.                        */
+ORC_API uint16_t orc_f32_to_f16(float v) {
+    uint32_t x;
+    memcpy(&x, &v, 4);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    int32_t e = (int32_t)((x >> 23) & 0xFFu);
+    uint32_t m = x & 0x7FFFFFu;
+    if (e == 0xFF) return sign | (m ? 0x7E00u : 0x7C00u);
+    int32_t ub = e - 127;                  /* unbiased exponent */
+    if (ub > 15) return sign | 0x7C00u;
+    uint32_t sig, drop;                    /* significand and bits to drop */
+    uint32_t base;
+    if (ub >= -14) {                       /* normal half: keep 10 mantissa bits */
+        sig = m;
+        drop = 13;
+        base = (uint32_t)(ub + 15) << 10;
+    } else {
+        if (ub < -25) return sign;          /* below half the smallest subnormal */
+        sig = m | 0x800000u;                /* subnormal half: value = sig * 2^(ub-23) */
+        drop = (uint32_t)(-ub - 1);         /* 14..24 bits */
+        base = 0;
+    }
+    uint32_t keep = sig >> drop, rem = sig & ((1u << drop) - 1u), half = 1u << (drop - 1);
+    uint32_t r = base + keep;             /* a carry may reach the exponent: still RNE */
+    if (rem > half || (rem == half && (keep & 1u))) r += 1u;
+    return sign | (uint16_t)r;
+}
+
+ORC_API void orc_f32_to_f16_n(const float *v, uint16_t *h, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) h[i] = orc_f32_to_f16(v[i]);
+}
+
+ORC_API void orc_f16_to_f32_n(const uint16_t *h, float *v, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) v[i] = orc_f16_to_f32(h[i]);
+}
+
+/* pack_rows_w4a32_group64_v1_to_v2, packed_v2.rs:114-143 (k % 64 == 0). */
+ORC_API void orc_pack_v1_to_v2(const uint8_t *w, const float *s, uint8_t *out, int64_t n,
+                               int64_t k) {
+    int64_t ng = k / 64, bpr = k / 2;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t g = 0; g < ng; ++g) {
+            uint8_t *blk = out + (r * ng + g) * 34;
+            memcpy(blk, w + r * bpr + g * 32, 32);
+            uint16_t h = orc_f32_to_f16(s[r * ng + g]);
+            blk[32] = (uint8_t)(h & 0xFF);
+            blk[33] = (uint8_t)(h >> 8);
+        }
+}
+
+static inline float v2_scale(const uint8_t *blk) {
+    return orc_f16_to_f32((uint16_t)(blk[32] | (blk[33] << 8)));
+}
+
+/* v2 GEMV, exact tiers (packed_v2.rs:145-200, 326-485 without VNNI): per     */
+/* group the two 32-element halves (unpack_fma32 on bytes 0..15 and 16..31),  */
+/* added lane by lane, then acc = fma(sum, f16 scale, acc); tree16 at the end. */
+HOT static void w4_v2_rows(const float *x, const uint8_t *w, const float *bias, float *y,
+                           int64_t r0, int64_t r1, int64_t k) {
+    int64_t ng = k / 64;
+    for (int64_t r = r0; r < r1; ++r) {
+        const uint8_t *wr = w + r * ng * 34;
+        float acc[L16] = {0}, p0[L16], p1[L16];
+        for (int64_t g = 0; g < ng; ++g) {
+            const uint8_t *blk = wr + g * 34;
+            float sc = v2_scale(blk);
+            unpack_fma32(x + g * 64, blk, p0);
+            unpack_fma32(x + g * 64 + 32, blk + 16, p1);
+            for (int i = 0; i < L16; ++i) acc[i] = fmaf(p0[i] + p1[i], sc, acc[i]);
+        }
+        y[r] = tree16(acc) + (bias ? bias[r] : 0.f);
+    }
+}
+
+ORC_API void orc_gemv_w4_v2(const float *x, const uint8_t *w, const float *bias, float *y,
+                            int64_t n, int64_t k) {
+    int64_t ch = rayon_chunk(n);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (n + ch - 1) / ch; ++c)
+        w4_v2_rows(x, w, bias, y, c * ch, (c + 1) * ch < n ? (c + 1) * ch : n, k);
+}
+
+/* w4a32_grouped_linear_v2 for M rows (packed_v2.rs:541-550): M GEMVs. */
+ORC_API void orc_gemm_w4_v2(const float *x, const uint8_t *w, const float *bias, float *y,
+                            int64_t m, int64_t n, int64_t k) {
+    for (int64_t i = 0; i < m; ++i) orc_gemv_w4_v2(x + i * k, w, bias, y + i * n, n, k);
+}
+
+/* ------------------------------------------------------------------------ */
+/* f2: the W4A8 semantics of the AVX-512 VNNI tier at group 64.              */
+/* quantize_activation_to_u8_avx512, gemv.rs:1353-1389: s_x = max(max|x|,   */
+/* 1e-10) / 127; q = round-to-nearest-even(x * (1 / s_x)) (cvtps_epi32 under  */
+/* the default MXCSR); byte = q + 128.  The scalar tail (k % 16) rounds half  */
+/* away from zero and divides; it is unused for k % 64 == 0.                  */
+/* ------------------------------------------------------------------------ */
+ORC_API float orc_quantize_act_u8(const float *x, int64_t k, uint8_t *out) {
+    float mx = 0.f;
+    for (int64_t i = 0; i < k; ++i) {
+        float a = fabsf(x[i]);
+        mx = a > mx ? a : mx;
+    }
+    if (mx < 1e-10f) mx = 1e-10f;
+    float sx = mx / 127.0f, inv = 1.0f / sx;
+    for (int64_t i = 0; i < k; ++i) {
+        float q = nearbyintf(x[i] * inv);
+        out[i] = (uint8_t)((int32_t)q + 128);
+    }
+    return sx;
+}
+
+/* gemv_row_w4a8_group64_vnni_avx512 (gemv.rs:1422-1473; v2 block form       */
+/* packed_v2.rs:204-241 and the 8-row form 288-323, same arithmetic per row): */
+/* lane j of the 16 dpbusd lanes holds the exact integer sum over elements   */
+/* 4j..4j+3 of (byte - 128) * (nib - 8); acc_j = fma((float)lane, s_x * s_w,  */
+/* acc_j) per group; tree16 at the end.  blocked != 0: w holds v2 blocks.     */
+HOT static void w4a8_rows(const uint8_t *xu, float sx, const uint8_t *w, const float *s,
+                          int blocked, const float *bias, float *y, int64_t r0, int64_t r1,
+                          int64_t k) {
+    int64_t ng = k / 64;
+    for (int64_t r = r0; r < r1; ++r) {
+        float acc[L16] = {0};
+        for (int64_t g = 0; g < ng; ++g) {
+            const uint8_t *nib = blocked ? w + (r * ng + g) * 34 : w + r * (k / 2) + g * 32;
+            float sw = blocked ? v2_scale(nib) : s[r * ng + g];
+            float sc = sx * sw;
+            for (int j = 0; j < L16; ++j) {
+                int32_t t = 0;
+                for (int e = 4 * j; e < 4 * j + 4; ++e) {
+                    uint8_t b = nib[e / 2];
+                    int32_t q = (int32_t)((e & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+                    t += ((int32_t)xu[g * 64 + e] - 128) * q;
+                }
+                acc[j] = fmaf((float)t, sc, acc[j]);
+            }
+        }
+        y[r] = tree16(acc) + (bias ? bias[r] : 0.f);
+    }
+}
+
+ORC_API void orc_gemv_w4a8_g64(const float *x, const uint8_t *w, const float *s, int blocked,
+                               const float *bias, float *y, int64_t n, int64_t k) {
+    uint8_t *xu = (uint8_t *)malloc((size_t)k);
+    float sx = orc_quantize_act_u8(x, k, xu);
+    int64_t ch = rayon_chunk(n);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (n + ch - 1) / ch; ++c)
+        w4a8_rows(xu, sx, w, s, blocked, bias, y, c * ch, (c + 1) * ch < n ? (c + 1) * ch : n, k);
+    free(xu);
+}
+
+/* ------------------------------------------------------------------------ */
 /* a7/a8: SwiGLU.  Neuron pair swiglu.rs:205-255 (g32) / 85-163 (g64) is the   */
 /* a4 row kernel applied to the gate and the up row with shared x;           */
 /* h = silu(g + gb) * (u + ub), silu(g) = g / (1 + exp(-g))                  */

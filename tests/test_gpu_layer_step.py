@@ -201,3 +201,12 @@ def test_layer_step_errors(cuda):
         tb.fused_attention_step_w4a32(*args(max_seq, hq, hkv))
     with pytest.raises(tb.UnsupportedOpError):
         tb.fused_attention_step_w4a32(*args(10, hq, 3))
+    # head_dim outside {64, 128} is rejected before any kernel writes the caches
+    # (16 heads of 32 and 4 KV heads: the same QKV rows and O width as 8 x 64 / 2 x 64)
+    kc32 = T(np.zeros((1, 2 * hkv, max_seq, 32), np.float32), cuda)
+    with pytest.raises(tb.UnsupportedOpError, match="head_dim"):
+        tb.fused_attention_step_w4a32(T(x, cuda), *(T(a, cuda) for a in qkv),
+                                      *(T(a, cuda) for a in o), kc32, kc32.clone(),
+                                      T(cr[:32], cuda), T(sr[:32], cuda), 10, 2 * hq, 2 * hkv,
+                                      32, 32)
+    assert not kc32.any()

@@ -1,0 +1,153 @@
+"""Parity of the v2 layout (34-byte group-64 blocks, f16 scales) and of the W4A8
+(AVX-512 VNNI tier) semantics with the CPU oracle.
+
+  pack / quantize_v2 / dequantize_v2   bit-exact against the oracle's
+      pack_rows_w4a32_group64_v1_to_v2 (packed_v2.rs:114-143) and its f32 -> f16
+      round-to-nearest-even (66-105), including subnormal, overflowing and NaN scales
+  w4a32_grouped_linear_v2   max|d| / max|ref| < 1e-4 against the oracle's
+      gemv_w4a32_grouped_v2 restatement (packed_v2.rs:145-200, 326-485), GEMV
+      (M <= 4) and MFMA (M >= 5) paths, odd group counts (rows only 2-byte aligned)
+  set_vnni_semantics   group-64 projections against the oracle's W4A8 GEMV
+      (gemv.rs:1353-1473, packed_v2.rs:204-323), < 1e-4; group 32 unaffected
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from torchburn_amd import synth
+import torchburn_amd as tb
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def T(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def weights(g, n, k):
+    w, s = synth.int4_weight(g, n, k, 64)
+    return w, s
+
+
+@pytest.mark.parametrize("n,k", [(7, 64), (33, 896), (256, 4096), (5, 192)])
+def test_pack_v1_to_v2_bit_exact(cuda, n, k):
+    print(f"case pack_rows_w4a32_group64_v1_to_v2 n={n} k={k}", flush=True)
+    g = synth.rng(91, n, k)
+    w, s = weights(g, n, k)
+    s = s.copy()
+    flat = s.reshape(-1)
+    specials = np.float32([65504.0, 65520.0, 1e6, 6.0e-5, 3e-6, 2.0 ** -25, 1e-9, np.nan])
+    flat[: min(flat.size, specials.size)] = specials[: flat.size]
+    ref = O.pack_v1_to_v2(w, s, k)
+    got = tb.pack_rows_w4a32_group64_v1_to_v2(T(w, cuda), T(s, cuda), k)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_quantize_and_dequantize_v2(cuda):
+    print("case quantize_weight_int4_grouped_v2 / dequantize_int4_grouped_v2", flush=True)
+    g = np.random.default_rng(92)
+    w = g.standard_normal((48, 512)).astype(np.float32)
+    blocked = tb.quantize_weight_int4_grouped_v2(T(w, cuda))
+    wq, sc = O.quantize_int4_grouped(w, 64)
+    assert np.array_equal(blocked.cpu().numpy(), O.pack_v1_to_v2(wq, sc, 512))
+    deq = tb.dequantize_int4_grouped_v2(blocked).cpu().numpy()
+    q = O.unpack_int4(wq, 512).astype(np.float32)
+    s16 = sc.astype(np.float16).astype(np.float32)
+    assert np.array_equal(deq, q * np.repeat(s16, 64, axis=1))
+    with pytest.raises(ValueError):
+        tb.quantize_weight_int4_grouped_v2(T(w, cuda), group_size=32)
+
+
+SHAPES = [
+    # m, n, k
+    (1, 64, 896),       # Qwen hidden, 14 groups
+    (1, 4096, 4096),
+    (2, 517, 192),      # 3 groups: rows 102 bytes (2-byte aligned)
+    (3, 1000, 2048),
+    (4, 96, 64),        # one group per row
+    (5, 300, 896),      # MFMA from M = 5
+    (16, 4096, 4096),
+    (64, 1031, 576),    # 9 groups, ragged N
+]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_v2_matches_oracle(cuda, m, n, k):
+    print(f"case w4a32_grouped_linear_v2 m={m} n={n} k={k}", flush=True)
+    g = synth.rng(93, m, n, k)
+    w, s = weights(g, n, k)
+    blocked = O.pack_v1_to_v2(w, s, k)
+    x = synth.activations(g, m, k)
+    bias = g.normal(0, 0.1, n).astype(np.float32)
+    ref = O.gemm_w4_v2(x, blocked, bias)
+    y = tb.w4a32_grouped_linear_v2(T(x, cuda), T(blocked, cuda), T(bias, cuda))
+    torch.cuda.synchronize()
+    err = rel(y.cpu().numpy(), ref)
+    print(f"max rel err {err:.3g}", flush=True)
+    assert err < TOL
+
+
+def test_linear_v2_shapes_and_errors(cuda):
+    g = synth.rng(94)
+    w, s = weights(g, 32, 256)
+    blocked = T(O.pack_v1_to_v2(w, s, 256), cuda)
+    x = T(synth.activations(g, 6, 256), cuda)
+    y = tb.w4a32_grouped_linear_v2(x.reshape(2, 3, 256), blocked)
+    assert tuple(y.shape) == (2, 3, 32)
+    with pytest.raises(tb.UnsupportedOpError, match="dimension mismatch"):
+        tb.w4a32_grouped_linear_v2(x[:, :192], blocked)
+    fake32 = torch.zeros((32, 272), dtype=torch.uint8, device=cuda)   # 8 "groups" of 32
+    with pytest.raises(tb.UnsupportedOpError, match="64-element groups"):
+        tb.w4a32_grouped_linear_v2(x, fake32, group_size=32)
+    # a stream that is not 4-byte aligned is refused, not read
+    raw = torch.zeros(32 * 136 + 2, dtype=torch.uint8, device=cuda)
+    view = raw[2:].view(32, 136)
+    with pytest.raises(tb.UnsupportedOpError, match="aligned"):
+        tb.w4a32_grouped_linear_v2(x, view)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 896), (2, 64, 4096), (8, 300, 1024)])
+def test_vnni_semantics_g64(cuda, m, n, k):
+    print(f"case vnni semantics m={m} n={n} k={k}", flush=True)
+    g = synth.rng(95, m, n, k)
+    w, s = weights(g, n, k)
+    blocked = O.pack_v1_to_v2(w, s, k)
+    x = synth.activations(g, m, k)
+    bias = g.normal(0, 0.1, n).astype(np.float32)
+    prev = tb.set_vnni_semantics(True)
+    try:
+        y1 = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), T(bias, cuda),
+                                     group_size=64).cpu().numpy()
+        y2 = tb.w4a32_grouped_linear_v2(T(x, cuda), T(blocked, cuda), T(bias, cuda)).cpu().numpy()
+    finally:
+        tb.set_vnni_semantics(prev)
+    ref1 = O.gemm_w4a8_g64(x, w, s, bias)
+    ref2 = O.gemm_w4a8_g64(x, blocked, None, bias, blocked=True)
+    e1, e2 = rel(y1, ref1), rel(y2, ref2)
+    print(f"max rel err v1 {e1:.3g} v2 {e2:.3g}", flush=True)
+    assert e1 < TOL and e2 < TOL
+    # the W4A8 result differs from the exact one by the activation rounding
+    assert rel(y1, O.gemm_w4(x, w, s, bias, group_size=64)) > 10 * TOL
+
+
+def test_vnni_semantics_leaves_g32_and_default(cuda):
+    g = synth.rng(96)
+    w, s = synth.int4_weight(g, 128, 512, 32)
+    x = synth.activations(g, 1, 512)
+    prev = tb.set_vnni_semantics(True)
+    try:
+        y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), group_size=32)
+        y = y.cpu().numpy()
+    finally:
+        assert tb.set_vnni_semantics(prev) is True
+    assert rel(y, O.gemm_w4(x, w, s, None, group_size=32)) < TOL

@@ -18,11 +18,16 @@ from .quantization import (
     fused_swiglu_mlp_w4a32,
     fused_swiglu_mlp_batched_w4a32,
     fused_swiglu_mlp_w8a32,
+    dequantize_int4_grouped_v2,
+    pack_rows_w4a32_group64_v1_to_v2,
     quantize_model,
     quantize_weight_int4_grouped,
+    quantize_weight_int4_grouped_v2,
     quantize_weight_int8,
+    set_vnni_semantics,
     w4a32_grouped_linear,
     w4a32_grouped_linear_residual,
+    w4a32_grouped_linear_v2,
     w8a32_linear,
 )
 
@@ -46,4 +51,9 @@ __all__ = [
     "quantize_weight_int8",
     "w4a32_grouped_linear",
     "w4a32_grouped_linear_residual",
+    "w4a32_grouped_linear_v2",
+    "quantize_weight_int4_grouped_v2",
+    "dequantize_int4_grouped_v2",
+    "pack_rows_w4a32_group64_v1_to_v2",
+    "set_vnni_semantics",
 ]

@@ -6,6 +6,8 @@
 // UnsupportedOpError.
 #include <stdlib.h>
 
+#include <atomic>
+
 #include <mutex>
 #include <string>
 #include <vector>
@@ -14,6 +16,7 @@
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
 #include "w4_mfma.hpp"
+#include "v2_layout.hpp"
 
 namespace tb {
 
@@ -144,6 +147,69 @@ static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
     return TB_OK;
 }
 
+// W4A8 semantics of the reference's AVX-512 VNNI tier for group-64 INT4
+// projections (gemv.rs:1392-1473, packed_v2.rs:366-370): off by default, the
+// exact W4A32 contraction of its scalar / AVX2 / AVX-512 tiers.
+std::atomic<int> g_vnni{0};
+
+static size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// One INT4 projection y = x . deq(W)^T (+ bias) (+ residual) over m rows, with
+// the weights as v1 nibbles + f32 scales or as v2 blocks.  Under W4A8
+// semantics (group 64) each row of x is first replaced by its byte
+// quantization q * s_x.  Workspace: [x' | records or split-K partials].
+static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
+                     const float *bias, const float *res, float *out, int64_t m, int64_t n,
+                     int64_t k, int64_t gs, hipStream_t st) {
+    const bool a8 = gs == 64 && g_vnni.load(std::memory_order_relaxed) != 0;
+    const size_t xb = a8 ? up256((size_t)m * (size_t)k * sizeof(float)) : 0;
+    const int epi = res ? EPI_RESID : EPI_PLAIN;
+    const bool mf = m >= mfma_min_m();
+    const size_t rest = mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
+                           : xq_bytes(m, k);
+    void *ws = nullptr;
+    int rc = workspace(xb + rest, &ws);
+    if (rc) return rc;
+    const float *xin = x;
+    if (a8) {
+        if ((rc = act_u8(x, static_cast<float *>(ws), m, k, st))) return rc;
+        xin = static_cast<const float *>(ws);
+    }
+    void *tail = static_cast<char *>(ws) + xb;
+    if (mf) {
+        MfmaParams q = mfma_params(xin, w, s, bias, out, m, n, k, gs);
+        q.res = res;
+        q.v2 = v2 ? 1 : 0;
+        return w4_mfma(q, epi, static_cast<float *>(tail), st);
+    }
+    W4Params p = w4_params(xin, w, s, bias, out, m, n, k, gs);
+    p.res = res;
+    p.v2 = v2 ? 1 : 0;
+    return w4_rows(p, epi, m, static_cast<uint32_t *>(tail), true, st);
+}
+
+// Validates a v2 projection: group 64, K % 64 == 0, 4-byte aligned blocks.
+static int check_v2(const float *x, const uint8_t *w, int64_t m, int64_t n, int64_t k,
+                    int64_t gs, const char *what) {
+    const std::string op(what);
+    TB_REQUIRE(x && w, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": null pointer");
+    TB_REQUIRE(m >= 0 && n >= 0 && k > 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": negative or empty dimension");
+    TB_REQUIRE(gs == 64, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": the v2 layout is defined for 64-element groups, got " +
+                   std::to_string(gs));
+    TB_REQUIRE(k % 64 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": K=" + std::to_string(k) +
+                   " must be a multiple of 64 for the v2 layout");
+    TB_REQUIRE(k <= (1 << 20) && n < (1ll << 31) && m < (1ll << 31) &&
+                   (size_t)n * (size_t)(k / 64) * 34 < (1ull << 32),
+               TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": dimension too large");
+    TB_REQUIRE(aligned(x, 16) && aligned(w, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op +
+                   ": x must be 16-byte and the blocks 4-byte aligned device pointers");
+    return TB_OK;
+}
+
 static int check_w8(const float *x, const int8_t *w, const float *s, int64_t s_len, int64_t m,
                     int64_t n, int64_t k, const char *what) {
     const std::string op(what);
@@ -189,14 +255,49 @@ int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float
     if (rc) return rc;
     TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_grouped_linear: null output");
     if (m == 0 || n == 0) return TB_OK;
-    if (m >= mfma_min_m())
-        return mfma_ws(mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size),
-                       EPI_PLAIN, (hipStream_t)stream);
-    void *ws = nullptr;
-    rc = workspace(xq_bytes(m, k), &ws);
+    return linear_w4(x, w_packed, scales, false, bias, nullptr, out, m, n, k, group_size,
+                     (hipStream_t)stream);
+}
+
+int tb_w4a32_grouped_linear_v2(const float *x, const uint8_t *w_blocked, const float *bias,
+                               float *out, int64_t m, int64_t n, int64_t k, int64_t group_size,
+                               void *stream) {
+    int rc = check_v2(x, w_blocked, m, n, k, group_size, "w4a32_grouped_linear_v2");
     if (rc) return rc;
-    W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
-    return w4_rows(p, EPI_PLAIN, m, (uint32_t *)ws, true, (hipStream_t)stream);
+    TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_grouped_linear_v2: null output");
+    if (m == 0 || n == 0) return TB_OK;
+    return linear_w4(x, w_blocked, nullptr, true, bias, nullptr, out, m, n, k, 64,
+                     (hipStream_t)stream);
+}
+
+int tb_pack_rows_w4a32_group64_v1_to_v2(const uint8_t *w_packed, const float *scales,
+                                        uint8_t *out, int64_t n, int64_t k, void *stream) {
+    TB_REQUIRE(w_packed && scales && out, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: pack_rows_w4a32_group64_v1_to_v2: null pointer");
+    TB_REQUIRE(n >= 0 && k > 0 && k % 64 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: pack_rows_w4a32_group64_v1_to_v2: K=" + std::to_string(k) +
+                   " must be a positive multiple of 64");
+    TB_REQUIRE(aligned(w_packed, 16) && aligned(scales, 4) && aligned(out, 2), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: pack_rows_w4a32_group64_v1_to_v2: misaligned device pointer");
+    return pack_v1_to_v2(w_packed, scales, out, n, k, (hipStream_t)stream);
+}
+
+int tb_dequantize_int4_grouped_v2(const uint8_t *w_blocked, float *out, int64_t n, int64_t k,
+                                  void *stream) {
+    TB_REQUIRE(w_blocked && out, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: dequantize_int4_grouped_v2: null pointer");
+    TB_REQUIRE(n >= 0 && k > 0 && k % 64 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: dequantize_int4_grouped_v2: K=" + std::to_string(k) +
+                   " must be a positive multiple of 64");
+    TB_REQUIRE(aligned(w_blocked, 4) && aligned(out, 16), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: dequantize_int4_grouped_v2: misaligned device pointer");
+    TB_REQUIRE((size_t)n * (size_t)(k / 64) * 34 < (1ull << 32), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: dequantize_int4_grouped_v2: blocks must be under 4 GiB");
+    return dequant_v2(w_blocked, out, n, k, (hipStream_t)stream);
+}
+
+int tb_set_vnni_semantics(int enabled) {
+    return g_vnni.exchange(enabled ? 1 : 0);
 }
 
 int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
@@ -208,17 +309,8 @@ int tb_w4a32_grouped_linear_residual(const float *x, const uint8_t *w_packed,
     TB_REQUIRE(out && residual, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32_grouped_linear_residual: null output or residual");
     if (m == 0 || n == 0) return TB_OK;
-    if (m >= mfma_min_m()) {
-        MfmaParams q = mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size);
-        q.res = residual;
-        return mfma_ws(q, EPI_RESID, (hipStream_t)stream);
-    }
-    void *ws = nullptr;
-    rc = workspace(xq_bytes(m, k), &ws);
-    if (rc) return rc;
-    W4Params p = w4_params(x, w_packed, scales, bias, out, m, n, k, group_size);
-    p.res = residual;
-    return w4_rows(p, EPI_RESID, m, (uint32_t *)ws, true, (hipStream_t)stream);
+    return linear_w4(x, w_packed, scales, false, bias, residual, out, m, n, k, group_size,
+                     (hipStream_t)stream);
 }
 
 int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,

@@ -36,6 +36,45 @@ __device__ __forceinline__ u32x4 load_nt16(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// ---- v2 weight stream (34-byte group-64 blocks: 32 bytes of nibbles, then
+// the group scale as little-endian IEEE binary16; packed_v2.rs:26-143) ----
+constexpr int kV2Block = 34;
+
+// The 16 nibble bytes at byte offset o (o even) of a v2 stream whose base is
+// 4-byte aligned.  Five dword-aligned loads cover [o & ~3, (o & ~3) + 20), and
+// a funnel shift drops the 0 or 2 leading bytes.  Every dword read holds a
+// byte of the chunk or of its block's scale, so no read leaves the buffer.
+__device__ __forceinline__ u32x4 load_v2_chunk(const uint8_t *w, uint32_t o) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(w + (o & ~3u));
+    uint32_t d[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) d[i] = __builtin_nontemporal_load(p + i);
+    const uint32_t sh = (o & 2u) * 8u;   // 0 or 16 bits
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbit(d[1], d[0], sh);
+    r.y = __builtin_amdgcn_alignbit(d[2], d[1], sh);
+    r.z = __builtin_amdgcn_alignbit(d[3], d[2], sh);
+    r.w = __builtin_amdgcn_alignbit(d[4], d[3], sh);
+    return r;
+}
+
+// binary16 bits -> f32 (packed_v2.rs:32-56) in integer arithmetic, so f16
+// subnormal scales decode exactly whatever the denormal mode: exponent 0 is
+// m * 2^-24, 31 is inf / NaN, otherwise the exponent is rebiased.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    const float sub = (float)m * 5.9604644775390625e-8f;   // m * 2^-24, exact
+    const uint32_t nrm = ((e + 112u) << 23) | (m << 13);
+    const uint32_t special = m ? 0x7FC00000u : 0x7F800000u;
+    const uint32_t bits = e == 0 ? __float_as_uint(sub) : (e == 31 ? special : nrm);
+    return __uint_as_float(e == 31 && m ? bits : (bits | sign));
+}
+
+// The f32 scale of the v2 block that starts at byte offset b.
+__device__ __forceinline__ float load_v2_scale(const uint8_t *w, uint32_t b) {
+    return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(w + b + 32u));
+}
+
 // Non-temporal 16-byte load of 4 floats (streamed-once data such as the KV cache).
 __device__ __forceinline__ float4 load_nt_f4(const float *p) {
     typedef float f32x4_t __attribute__((ext_vector_type(4)));

@@ -83,8 +83,8 @@ int check_attn(const char *what, int64_t H, int64_t offset, int64_t max_seq, int
                "TB_UNSUPPORTED: " + op + ": null cache or RoPE row");
     TB_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0 && hq / hkv <= 64, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: " + op + ": num_heads must be a multiple of num_kv_heads");
-    TB_REQUIRE(hd >= 32 && hd <= 256 && hd % 32 == 0, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": head_dim must be a multiple of 32 in [32, 256]");
+    TB_REQUIRE(hd == 64 || hd == 128, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": head_dim must be 64 or 128");
     TB_REQUIRE(H > 0 && H % 32 == 0 && H <= kMaxHidden, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: " + op + ": hidden size must be a multiple of 32 and <= " +
                    std::to_string(kMaxHidden));

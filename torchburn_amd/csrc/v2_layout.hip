@@ -1,0 +1,149 @@
+// The v2 INT4 layout and the W4A8 activation semantics, on gfx950.
+//
+// v2 (packed_v2.rs:26-143): each 64-element group of a row is one 34-byte
+// block, 32 bytes of v1 nibbles then the group scale as little-endian IEEE
+// binary16.  k_pack_v2 replaces pack_rows_w4a32_group64_v1_to_v2
+// (packed_v2.rs:114-143) with f32_to_f16's round-to-nearest-even
+// (packed_v2.rs:66-105); k_dequant_v2 replaces dequantize_int4_grouped_v2
+// (python/torchburn/quantization.py:155-169).  The GEMV over the blocks is the
+// V2 form of k_w4_gemv / k_w4_mfma.
+//
+// W4A8 (gemv.rs:1353-1389): on hosts with AVX-512 VNNI the reference's group-64
+// GEMVs first quantize each activation row to bytes, s_x = max(max|x|, 1e-10) /
+// 127, q = round-to-nearest-even(x * (1 / s_x)), and contract q exactly with the
+// nibbles.  k_act_u8 writes x' = q * s_x per row; a GEMV over x' reproduces
+// that result to f32 rounding.
+#include <math.h>
+
+#include "gemv_common.hpp"
+#include "tb_common.hpp"
+#include "v2_layout.hpp"
+
+namespace tb {
+
+using namespace gemv;
+
+namespace {
+
+// binary32 -> binary16 bits, round to nearest even, in integer arithmetic:
+// NaN -> sign | 0x7E00, overflow -> +-inf, below half the smallest subnormal
+// -> +-0 (packed_v2.rs:66-105).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+    const uint32_t x = __float_as_uint(v);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e = (int)((x >> 23) & 0xFFu);
+    const uint32_t m = x & 0x7FFFFFu;
+    if (e == 0xFF) return sign | (m ? 0x7E00u : 0x7C00u);
+    const int ub = e - 127;
+    if (ub > 15) return sign | 0x7C00u;
+    if (ub < -25) return sign;
+    const bool normal = ub >= -14;
+    const uint32_t sig = normal ? m : (m | 0x800000u);
+    const uint32_t drop = normal ? 13u : (uint32_t)(-ub - 1);   // 13 .. 24
+    const uint32_t base = normal ? (uint32_t)(ub + 15) << 10 : 0u;
+    const uint32_t keep = sig >> drop, rem = sig & ((1u << drop) - 1u), half = 1u << (drop - 1u);
+    uint32_t r = base + keep;   // a carry into the exponent is still RNE
+    if (rem > half || (rem == half && (keep & 1u))) r += 1u;
+    return sign | r;
+}
+
+// One thread per (row, group): 32 nibble bytes and the f16 scale into a
+// 34-byte block (2-byte aligned: 17 half-word stores).
+__global__ __launch_bounds__(256) void k_pack_v2(const uint8_t *__restrict__ w,
+                                                 const float *__restrict__ s,
+                                                 uint8_t *__restrict__ out, int64_t n, int ng) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * ng) return;
+    const int64_t row = t / ng;
+    const int g = (int)(t - row * ng);
+    const uint4 *src = reinterpret_cast<const uint4 *>(w + row * (int64_t)ng * 32 + g * 32);
+    const uint4 a = src[0], b = src[1];
+    const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint16_t *dst = reinterpret_cast<uint16_t *>(out + t * kV2Block);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dst[2 * i] = (uint16_t)(d[i] & 0xFFFFu);
+        dst[2 * i + 1] = (uint16_t)(d[i] >> 16);
+    }
+    dst[16] = (uint16_t)f32_to_f16_bits(s[t]);
+}
+
+// One thread per (row, 32-element half block): (nib - 8) * f16 scale.
+__global__ __launch_bounds__(256) void k_dequant_v2(const uint8_t *__restrict__ blocked,
+                                                    float *__restrict__ out, int64_t n, int ng) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * ng * 2) return;
+    const int64_t blk = t >> 1;
+    const int h = (int)(t & 1);
+    const uint32_t o = (uint32_t)(blk * kV2Block);
+    const u32x4 q = load_v2_chunk(blocked, o + 16u * (uint32_t)h);
+    const float sc = load_v2_scale(blocked, o);
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float4 *dst = reinterpret_cast<float4 *>(out + t * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)((int)((d[i] >> (4 * e)) & 15u) - 8) * sc;
+        dst[2 * i] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[2 * i + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// One block per activation row: s_x = max(max|x|, 1e-10) / 127, then
+// x' = q * s_x with q = rint(x * (1 / s_x)).  A NaN element gives q = 0 (the
+// reference's int conversion of NaN lands on byte 128, i.e. q = 0); fmaxf skips
+// NaN in the maximum.
+__global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
+                                                float *__restrict__ xo, int k) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * k;
+    float *yr = xo + (size_t)blockIdx.x * k;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(xr[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (mx < 1e-10f) mx = 1e-10f;
+    const float sx = __fdiv_rn(mx, 127.0f);
+    const float inv = __fdiv_rn(1.0f, sx);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) {
+        const float t = __fmul_rn(xr[i], inv);
+        const float q = __builtin_isnan(t) ? 0.f : __builtin_rintf(t);
+        yr[i] = __fmul_rn(q, sx);
+    }
+}
+
+}  // namespace
+
+int pack_v1_to_v2(const uint8_t *w, const float *s, uint8_t *out, int64_t n, int64_t k,
+                  hipStream_t st) {
+    const int ng = (int)(k / 64);
+    const int64_t total = n * ng;
+    if (total == 0) return TB_OK;
+    hipLaunchKernelGGL(k_pack_v2, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, w, s,
+                       out, n, ng);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int dequant_v2(const uint8_t *blocked, float *out, int64_t n, int64_t k, hipStream_t st) {
+    const int ng = (int)(k / 64);
+    const int64_t total = n * ng * 2;
+    if (total == 0) return TB_OK;
+    hipLaunchKernelGGL(k_dequant_v2, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       blocked, out, n, ng);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int act_u8(const float *x, float *xo, int64_t m, int64_t k, hipStream_t st) {
+    if (m == 0) return TB_OK;
+    hipLaunchKernelGGL(k_act_u8, dim3((unsigned)m), dim3(256), 0, st, x, xo, (int)k);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+}  // namespace tb

@@ -1,0 +1,20 @@
+// Internal launchers of the v2-layout and W4A8 kernels (v2_layout.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tb {
+
+// v1 nibbles [n, k/2] (16-byte aligned) + f32 scales [n, k/64] -> v2 blocks
+// [n, (k/64) * 34] with f16 scales (k % 64 == 0).
+int pack_v1_to_v2(const uint8_t *w, const float *s, uint8_t *out, int64_t n, int64_t k,
+                  hipStream_t st);
+
+// v2 blocks [n, (k/64) * 34] (4-byte aligned) -> f32 weights [n, k] (16-byte aligned).
+int dequant_v2(const uint8_t *blocked, float *out, int64_t n, int64_t k, hipStream_t st);
+
+// Per row of x [m, k]: x' = q * s_x, the activations the W4A8 tier contracts.
+int act_u8(const float *x, float *xo, int64_t m, int64_t k, hipStream_t st);
+
+}  // namespace tb

@@ -28,6 +28,11 @@
 //     silu(g)*u of a gate/up pair) writes the outputs.
 //   * A wave whose x chunk holds NaN/Inf takes an f32 path instead (the
 //     reference's unpack-and-fma), so non-finite values propagate.
+//   * V2: the weights are the v2 stream (34-byte group-64 blocks with f16
+//     scales, packed_v2.rs:26-143; gemv_w4a32_grouped_v2, packed_v2.rs:326-485).
+//     A chunk is one half of a block: its 16 nibble bytes come from five
+//     dword-aligned loads and a funnel shift, its scale from the block's two
+//     trailing bytes; the arithmetic is unchanged.
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
 
@@ -37,7 +42,7 @@ using namespace gemv;
 
 namespace {
 
-template <int M, int J, bool DUAL, int EPI>
+template <int M, int J, bool DUAL, int EPI, bool V2>
 struct W4Gemv {
     static constexpr int D = DUAL ? 2 : 1;
     static constexpr int V = D * J * M;
@@ -62,7 +67,7 @@ struct W4Gemv {
     const Layout &L;
     int lane, wave, grp, rr, cl, chunk;
     bool act;
-    size_t bpr, boff;
+    size_t bpr, boff, soff;
     int gcols, sg;
     uint32_t limb[M][6][NDW];   // limb[m][l][d] nibble e = bits [4l, 4l+4) of U_{8d+e}
     int sxq[M][2];              // sum_i X_i of each 16-element half
@@ -81,8 +86,15 @@ struct W4Gemv {
         chunk = act ? chunk_raw : 0;
         gcols = p.k >> p.gshift;
         sg = (chunk * 32) >> p.gshift;
-        bpr = (size_t)(p.k >> 1);
-        boff = (size_t)chunk * 16;
+        if (V2) {
+            bpr = (size_t)(p.k >> 6) * kV2Block;
+            soff = (size_t)(chunk >> 1) * kV2Block;   // the chunk's block
+            boff = soff + (size_t)(chunk & 1) * 16;
+        } else {
+            bpr = (size_t)(p.k >> 1);
+            soff = 0;
+            boff = (size_t)chunk * 16;
+        }
     }
 
     __device__ __forceinline__ void issue_x(XRec &xr) const {
@@ -148,10 +160,17 @@ struct W4Gemv {
             const uint32_t so = ((uint32_t)row * (uint32_t)gcols + (uint32_t)sg) * 4u;
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                const u32x4 v = load_nt16((d ? p.w1 : p.w0) + wo);
+                const uint8_t *wb = d ? p.w1 : p.w0;
+                u32x4 v;
+                if (V2) {
+                    v = load_v2_chunk(wb, wo);
+                    bt.sc[d][j] = load_v2_scale(wb, (uint32_t)row * (uint32_t)bpr + (uint32_t)soff);
+                } else {
+                    v = load_nt16(wb + wo);
+                    bt.sc[d][j] = *reinterpret_cast<const float *>(
+                        reinterpret_cast<const char *>(d ? p.s1 : p.s0) + so);
+                }
                 bt.q[d][j][0] = v.x; bt.q[d][j][1] = v.y; bt.q[d][j][2] = v.z; bt.q[d][j][3] = v.w;
-                bt.sc[d][j] = *reinterpret_cast<const float *>(
-                    reinterpret_cast<const char *>(d ? p.s1 : p.s0) + so);
             }
         }
     }
@@ -215,9 +234,9 @@ struct W4Gemv {
 // products (which wait only for what they read, since loads retire in issue
 // order).  Straight-line code: a
 // loop back-edge would make the compiler drain the load counter early.
-template <int M, int J, bool DUAL, int EPI>
+template <int M, int J, bool DUAL, int EPI, bool V2>
 __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p, Layout L, Epi e) {
-    using G = W4Gemv<M, J, DUAL, EPI>;
+    using G = W4Gemv<M, J, DUAL, EPI, V2>;
     __shared__ float red[kMaxWaves * 64];
     __shared__ EpiShared sh;
     G g(p, L);
@@ -250,7 +269,7 @@ __global__ __launch_bounds__(256) void k_xquant(const float *__restrict__ x,
     build_xrec8(v, sub, live, xq + (size_t)rec * kXRecDwords);
 }
 
-template <int M, int J, bool DUAL, int EPI>
+template <int M, int J, bool DUAL, int EPI, bool V2 = false>
 int launch(const W4Params &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
@@ -262,7 +281,8 @@ int launch(const W4Params &p, hipStream_t st) {
     e.ssq_in = p.ssq_in; e.ssq_n = p.ssq_n; e.eps = p.eps;
     e.inv_h = p.norm_h > 0 ? 1.0f / (float)p.norm_h : 0.f;
     e.rec_out = p.rec_out; e.rec_w = p.rec_w; e.xw_out = p.xw_out; e.ssq_out = p.ssq_out;
-    e.any = p.s0;   // n * k / group >= n floats
+    // n floats of any valid buffer: the scales (n * k / group), or the v2 stream
+    e.any = V2 ? reinterpret_cast<const float *>(p.w0) : p.s0;
     if (p.ssq_in)
         TB_REQUIRE(p.m == 1 && p.ssq_n <= kMaxSsqPerThread * L.nwaves * 64, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: fused RMSNorm input needs M == 1 and K == H");
@@ -274,26 +294,30 @@ int launch(const W4Params &p, hipStream_t st) {
     if (EPI == EPI_ROPE)
         TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
-    TB_REQUIRE((size_t)p.n * (size_t)(p.k / 2) < (1ull << 32), TB_ERR_UNSUPPORTED,
+    const size_t wbytes = V2 ? (size_t)(p.k / 64) * kV2Block : (size_t)(p.k / 2);
+    TB_REQUIRE((size_t)p.n * wbytes < (1ull << 32), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4 GEMV weights must be under 4 GiB");
+    if (V2)
+        TB_REQUIRE(p.k % 64 == 0 && !DUAL && ((uintptr_t)p.w0 & 3u) == 0, TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: v2 blocks need K % 64 == 0 and a 4-byte aligned stream");
     const int grid = (p.n + L.rpb - 1) / L.rpb;
-    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI>), dim3(grid), dim3(L.nwaves * 64), 0, st, p, L,
-                       e);
+    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI, V2>), dim3(grid), dim3(L.nwaves * 64), 0, st,
+                       p, L, e);
     TB_LAUNCHED();
     return TB_OK;
 }
 
-template <bool DUAL, int EPI>
+template <bool DUAL, int EPI, bool V2 = false>
 int dispatch_m(const W4Params &p, hipStream_t st) {
     // x stays in VGPRs, so one pass takes <= 2 rows.  Rows per block: 8 for a
     // gate/up pair (16 weight loads in flight per lane), 16 for one matrix.
     if (p.m <= 1) {
         const int j = p.rows_j ? p.rows_j : (DUAL ? 8 : 16);
-        if (j == 4) return launch<1, 4, DUAL, EPI>(p, st);
-        if (j == 16) return launch<1, 16, DUAL, EPI>(p, st);
-        return launch<1, 8, DUAL, EPI>(p, st);
+        if (j == 4) return launch<1, 4, DUAL, EPI, V2>(p, st);
+        if (j == 16) return launch<1, 16, DUAL, EPI, V2>(p, st);
+        return launch<1, 8, DUAL, EPI, V2>(p, st);
     }
-    return launch<2, DUAL ? 4 : 8, DUAL, EPI>(p, st);
+    return launch<2, DUAL ? 4 : 8, DUAL, EPI, V2>(p, st);
 }
 
 }  // namespace
@@ -310,6 +334,17 @@ int w4_gemv(W4Params p, int epi, hipStream_t st) {
     TB_REQUIRE(p.m >= 1 && p.m <= kMaxRowsPerPass, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4 GEMV pass takes 1..2 rows");
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4 GEMV needs K % 32 == 0");
+    if (p.v2) {
+        TB_REQUIRE(p.w1 == nullptr, TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: v2 blocks take single projections");
+        if (epi == EPI_RESID) return dispatch_m<false, EPI_RESID, true>(p, st);
+        if (epi == EPI_ROPE) {
+            if (p.rows_j == 4) return launch<1, 4, false, EPI_ROPE, true>(p, st);
+            if (p.rows_j == 8) return launch<1, 8, false, EPI_ROPE, true>(p, st);
+            return launch<1, 16, false, EPI_ROPE, true>(p, st);
+        }
+        return dispatch_m<false, EPI_PLAIN, true>(p, st);
+    }
     if (p.w1 != nullptr) return dispatch_m<true, EPI_SWIGLU>(p, st);
     if (epi == EPI_RESID) return dispatch_m<false, EPI_RESID>(p, st);
     if (epi == EPI_ROPE) {

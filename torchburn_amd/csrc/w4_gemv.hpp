@@ -43,6 +43,8 @@ struct W4Params {
     float *y;          // [m, n] output
     int m, n, k;
     int gshift;        // log2(group_size)
+    int v2;            // 1: w0 is the v2 stream of 34-byte group-64 blocks (f16
+                       // scales inside, s0 unused; K % 64 == 0, 4-byte aligned)
     int rows_j;        // rows per block (tuning: 4, 8 or 16; 0 = default)
     RopeArgs rope;     // EPI_ROPE only
     // Fused RMSNorm (M == 1).  Consumer: xq holds records of x * w_norm (and

@@ -32,6 +32,9 @@
 //     LDS buffers, so each step needs one barrier;
 //   * up to four independent accumulators per 16-row tile keep dependent MFMAs
 //     apart (small M has few tiles to interleave).
+//   * V2: weights in the v2 stream (34-byte group-64 blocks with f16 scales,
+//     packed_v2.rs:26-143): a lane's 16-byte chunk is one half of a block,
+//     read with dword-aligned loads and a funnel shift (load_v2_chunk).
 #include <float.h>
 #include <stdlib.h>
 
@@ -53,7 +56,7 @@ constexpr int kTargetBlocks = 512;   // split-K target (TB_MFMA_BLOCKS overrides
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int MT>
+template <int MT, bool V2>
 __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
                                                  const uint8_t *__restrict__ w0,
                                                  const float *__restrict__ s0,
@@ -78,7 +81,8 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
     const int q = lane >> 4;
     const bool rok = row < n;
     const uint8_t *wrow = w + (size_t)(rok ? row : 0) * (size_t)(k >> 1);
-    const float *srow = s + (size_t)(rok ? row : 0) * (size_t)(k >> gshift);
+    const float *srow = V2 ? nullptr : s + (size_t)(rok ? row : 0) * (size_t)(k >> gshift);
+    const uint32_t vrow = (uint32_t)(rok ? row : 0) * (uint32_t)((k >> 6) * kV2Block);
 
     float4 xr[XV];
     u32x4 wr;
@@ -94,8 +98,16 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
         }
         const int kk = k0 + 32 * q;
         const bool ok = rok && kk < ke;
-        wr = ok ? load_nt16(wrow + (kk >> 1)) : u32x4{0u, 0u, 0u, 0u};
-        sr = ok ? srow[kk >> gshift] : 0.f;
+        if (V2) {
+            const int kc = ok ? kk : 0;   // addresses stay inside the stream
+            const uint32_t blk = vrow + (uint32_t)(kc >> 6) * kV2Block;
+            wr = ok ? load_v2_chunk(w, blk + (uint32_t)((kc >> 5) & 1) * 16u)
+                    : u32x4{0u, 0u, 0u, 0u};
+            sr = ok ? load_v2_scale(w, blk) : 0.f;
+        } else {
+            wr = ok ? load_nt16(wrow + (kk >> 1)) : u32x4{0u, 0u, 0u, 0u};
+            sr = ok ? srow[kk >> gshift] : 0.f;
+        }
     };
 
     f32x4 acc[MT][NACC];
@@ -231,11 +243,24 @@ int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
     const bool dual = p.w1 != nullptr;
     TB_REQUIRE(p.k % 32 == 0 && p.m >= 1 && p.n >= 1, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: MFMA projection needs K % 32 == 0");
+    if (p.v2)
+        TB_REQUIRE(p.k % 64 == 0 && ((uintptr_t)p.w0 & 3u) == 0 &&
+                       (!dual || ((uintptr_t)p.w1 & 3u) == 0) &&
+                       (size_t)p.n * (size_t)(p.k / 64) * kV2Block < (1ull << 32),
+                   TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: v2 blocks need K % 64 == 0, a 4-byte aligned stream "
+                   "under 4 GiB");
     const Plan pl = plan(p.m, p.n, p.k, dual);
     dim3 grid(pl.nbx * (dual ? 2 : 1), pl.splits, pl.mz);
 #define TB_MFMA_LAUNCH(MT)                                                                   \
-    hipLaunchKernelGGL((k_w4_mfma<MT>), grid, dim3(256), 0, st, p.x, p.w0, p.s0, p.w1, p.s1, \
-                       part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx, pl.splits)
+    if (p.v2)                                                                                \
+        hipLaunchKernelGGL((k_w4_mfma<MT, true>), grid, dim3(256), 0, st, p.x, p.w0, p.s0,   \
+                           p.w1, p.s1, part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx,        \
+                           pl.splits);                                                       \
+    else                                                                                     \
+        hipLaunchKernelGGL((k_w4_mfma<MT, false>), grid, dim3(256), 0, st, p.x, p.w0, p.s0,  \
+                           p.w1, p.s1, part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx,        \
+                           pl.splits)
     switch (pl.mt) {
         case 1: TB_MFMA_LAUNCH(1); break;
         case 2: TB_MFMA_LAUNCH(2); break;

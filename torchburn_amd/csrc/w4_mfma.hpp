@@ -19,6 +19,8 @@ struct MfmaParams {
     float *y;            // [m, n]
     int m, n, k;
     int gshift;          // log2(group_size)
+    int v2;              // 1: w0 / w1 are v2 streams of 34-byte group-64 blocks
+                         // (f16 scales inside, s0 / s1 unused)
 };
 
 // Bytes of split-K partials w4_mfma needs for this shape (dual = SwiGLU pair).

@@ -96,6 +96,73 @@ def quantize_weight_int4_grouped(
     return packed, scales
 
 
+def pack_rows_w4a32_group64_v1_to_v2(w_packed: torch.Tensor, scales: torch.Tensor,
+                                     k: int) -> torch.Tensor:
+    """v1 nibbles (N, K/2) + f32 scales (N, K/64) -> v2 blocks (N, (K/64) * 34) uint8:
+    per group 32 nibble bytes then the scale as little-endian binary16, rounded to
+    nearest even (reference src/quantization/packed_v2.rs:114-143, 66-105)."""
+    if k % 64 != 0:
+        raise ValueError(f"K={k} must be divisible by 64 for the v2 layout")
+    dev = _target(w_packed)
+    w = _on_gpu(w_packed, torch.uint8, dev)
+    s = _on_gpu(scales, torch.float32, dev)
+    n = w.shape[0]
+    if tuple(w.shape) != (n, k // 2) or s.numel() != n * (k // 64):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} pack_rows_w4a32_group64_v1_to_v2: expected packed "
+            f"({n}, {k // 2}) and {n * (k // 64)} scales, got {list(w.shape)} / {s.numel()}")
+    out = torch.empty((n, (k // 64) * 34), dtype=torch.uint8, device=dev)
+    _lib.call("tb_pack_rows_w4a32_group64_v1_to_v2", _ptr(w), _ptr(s), _ptr(out), n, k,
+              _stream(dev))
+    return out.to(w_packed.device)
+
+
+def quantize_weight_int4_grouped_v2(
+    weight: torch.Tensor,
+    group_size: int = 64,
+    chunk_size: int = 1024,
+) -> torch.Tensor:
+    """(N, K) float -> v2 blocks (N, (K/64) * 34) uint8 (reference
+    python/torchburn/quantization.py:121-152): the v1 quantizer, then each group's
+    nibbles and binary16 scale packed into one 34-byte block."""
+    if weight.ndim != 2:
+        raise ValueError(
+            f"Expected 2D weight matrix for quantize_weight_int4_grouped_v2, got {weight.ndim}D")
+    n, k = weight.shape
+    if k % group_size != 0:
+        raise ValueError(f"K={k} must be divisible by group_size={group_size}")
+    if group_size != 64:
+        raise ValueError(f"the v2 layout is defined for group_size=64, got {group_size}")
+    packed, scales = quantize_weight_int4_grouped(weight, group_size, chunk_size)
+    return pack_rows_w4a32_group64_v1_to_v2(packed, scales, k).to(weight.device)
+
+
+def dequantize_int4_grouped_v2(blocked: torch.Tensor, group_size: int = 64) -> torch.Tensor:
+    """Inverse of quantize_weight_int4_grouped_v2: f32 (N, K) with (nib - 8) * f16 scale
+    (reference python/torchburn/quantization.py:155-169)."""
+    if group_size != 64:
+        raise ValueError(f"the v2 layout is defined for group_size=64, got {group_size}")
+    dev = _target(blocked)
+    b = _on_gpu(blocked, torch.uint8, dev)
+    n, cols = b.shape
+    if cols % 34 != 0:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} v2 rows must be whole 34-byte blocks, got {cols} bytes")
+    k = (cols // 34) * 64
+    out = torch.empty((n, k), dtype=torch.float32, device=dev)
+    _lib.call("tb_dequantize_int4_grouped_v2", _ptr(b), _ptr(out), n, k, _stream(dev))
+    return out.to(blocked.device)
+
+
+def set_vnni_semantics(enabled: bool) -> bool:
+    """Selects the reference's AVX-512 VNNI-tier arithmetic for group-64 INT4
+    projections: activations quantized per row to bytes (s_x = max|x| / 127,
+    round-half-even) before the contraction (src/quantization/gemv.rs:1353-1473).
+    Off by default (the exact W4A32 result of the other tiers).  Returns the
+    previous setting."""
+    return bool(_lib.lib().tb_set_vnni_semantics(1 if enabled else 0))
+
+
 def quantize_weight_int8(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """(N, K) float -> (int8 (N, K), float32 scales (N,)).
 
@@ -149,6 +216,40 @@ def w4a32_grouped_linear(
     out = torch.empty((m, n), dtype=torch.float32, device=dev)
     _lib.call("tb_w4a32_grouped_linear", _ptr(x2), _ptr(w), _ptr(s), _ptr(b), _ptr(out),
               m, n, k, group_size, _stream(dev))
+    return out.reshape(*x.shape[:-1], n).to(x.device)
+
+
+def w4a32_grouped_linear_v2(
+    x: torch.Tensor,
+    blocked: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    group_size: int = 64,
+) -> torch.Tensor:
+    """out[..., N] = x[..., K] @ dequant(blocked)^T + bias over v2 blocks
+    (reference quantization.py:172-190 -> packed_v2.rs:489-553)."""
+    if x.dim() < 1:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_grouped_linear_v2 requires x with at least 1 dimension")
+    dev = _target(x)
+    k = x.shape[-1]
+    x2 = _on_gpu(x.reshape(-1, k), torch.float32, dev)
+    m = x2.shape[0]
+    w = _on_gpu(blocked, torch.uint8, dev)
+    b = _on_gpu(bias, torch.float32, dev)
+    if w.ndim != 2:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_grouped_linear_v2 requires 2D blocked weight matrix")
+    n = w.shape[0]
+    expected = (k // group_size) * 34
+    if w.shape[1] != expected:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_grouped_linear_v2 dimension mismatch: K={k} "
+            f"group={group_size} needs {expected} blocked bytes per row, got {w.shape[1]}")
+    if b is not None and b.numel() != n:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} bias must have {n} elements")
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _lib.call("tb_w4a32_grouped_linear_v2", _ptr(x2), _ptr(w), _ptr(b), _ptr(out), m, n, k,
+              group_size, _stream(dev))
     return out.reshape(*x.shape[:-1], n).to(x.device)
 
 
