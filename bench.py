@@ -45,8 +45,8 @@ def parse():
     ap.add_argument("--copies", type=int, default=4, help="weight copies rotated (> 256 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--decode", default="llama4,llama8,qwen",
-                    help="decode runs: comma list of llama4, llama8, qwen, or 'none'")
+    ap.add_argument("--decode", default="llama4,llama8,qwen,qwen64",
+                    help="decode runs: comma list of llama4, llama8, qwen, qwen64, or 'none'")
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="batched prefill timed on the llama4 decoder (0: skip)")
@@ -290,10 +290,14 @@ def decode_run(torch, name, steps, prefill_tokens=0):
         "llama4": (synth.LLAMA3_8B, 4, 4, 4096, 0x7B + 5),
         "llama8": (synth.LLAMA3_8B, 8, 8, 4096, 0x7B + 5),
         "qwen": (synth.QWEN_0_5B, 4, 32, 2048, 0x7B + 4),
+        # the reference's own Qwen decode setting: INT4 g64 with an INT4 lm_head,
+        # QKV / O / down / lm_head on v2 blocks (decoder.rs:361-390)
+        "qwen64": (synth.QWEN_0_5B, 4, 4, 2048, 0x7B + 4),
     }[name]
+    gs = 64 if name == "qwen64" else 32
     max_seq = kvlen + steps
-    w = synth.decoder_weights_torch(cfg, seed, wk, lk, 32)
-    dec = decoder_from_weights(w, cfg, group_size=32, max_seq_len=max_seq)
+    w = synth.decoder_weights_torch(cfg, seed, wk, lk, gs)
+    dec = decoder_from_weights(w, cfg, group_size=gs, max_seq_len=max_seq)
     del w
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 1)
@@ -311,7 +315,8 @@ def decode_run(torch, name, steps, prefill_tokens=0):
     pre = prefill_run(dec, cfg, prefill_tokens) if prefill_tokens and wk == 4 else None
     dec.close()
     torch.cuda.empty_cache()
-    byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk) for i in range(steps)) / steps
+    byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk, gs, v2=name == "qwen64")
+               for i in range(steps)) / steps
     sec = ms / 1e3 / steps
     out = {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(ms / steps, 4),
            "bytes_per_token": int(byts), "kv_len": kvlen,

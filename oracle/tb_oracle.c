@@ -672,11 +672,14 @@ typedef struct {
     const void *qkv_w, *o_w, *gate_w, *up_w, *down_w;
     const float *qkv_s, *o_s, *gate_s, *up_s, *down_s;
     const float *qkv_b; /* may be NULL */
+    uint8_t *qkv_w2, *o_w2, *down_w2; /* owned v2 blocks (use_v2) */
 } orc_layer;
 
 typedef struct {
     int64_t L, H, I, hq, hkv, hd, V, gs, max_seq;
     int wkind, lmkind;
+    int use_v2; /* decoder.rs:361-390 */
+    uint8_t *lm_w2;
     float eps;
     const float *embed, *final_norm;
     const void *lm_w;
@@ -705,6 +708,18 @@ ORC_API orc_decoder *orc_decoder_create(int64_t L, int64_t H, int64_t I, int64_t
     d->sin_t = (float *)malloc((size_t)(max_seq * hd) * sizeof(float));
     orc_rope_tables(d->cos_t, d->sin_t, max_seq, hd, theta);
     int64_t tq = (hq + 2 * hkv) * hd;
+    /* decoder.rs:361-390: group 64 with hidden, QKV rows, num_heads * head_dim,
+     * intermediate and vocab all multiples of 64 -> QKV, O, down and lm_head run
+     * the v2 GEMV on blocks repacked at load (f16 scales); gate / up stay v1.
+     * (The reference passes the output width as the pack's row length for QKV and
+     * lm_head; the pack copies 32-byte chunks and scales in one running order, so
+     * the bytes are the same as with the true row length.) */
+    d->use_v2 = wkind == 4 && gs == 64 && H % 64 == 0 && tq % 64 == 0 && (hq * hd) % 64 == 0 &&
+                I % 64 == 0 && V % 64 == 0;
+    if (d->use_v2 && lmkind == 4) {
+        d->lm_w2 = (uint8_t *)malloc((size_t)V * (size_t)(H / 64) * 34);
+        orc_pack_v1_to_v2((const uint8_t *)lm_w, lm_s, d->lm_w2, V, H);
+    }
     d->x = (float *)calloc((size_t)H, 4);
     d->xn = (float *)calloc((size_t)H, 4);
     d->qkv = (float *)calloc((size_t)tq, 4);
@@ -726,10 +741,24 @@ ORC_API void orc_decoder_set_layer(orc_decoder *d, int64_t l, const float *in_no
     y->in_norm = in_norm; y->qkv_w = qkv_w; y->qkv_s = qkv_s; y->o_w = o_w; y->o_s = o_s;
     y->post_norm = post_norm; y->gate_w = gate_w; y->gate_s = gate_s; y->up_w = up_w;
     y->up_s = up_s; y->down_w = down_w; y->down_s = down_s; y->qkv_b = qkv_b;
+    if (d->use_v2) {
+        int64_t H = d->H, I = d->I, qd = d->hq * d->hd, tq = qd + 2 * d->hkv * d->hd;
+        free(y->qkv_w2); free(y->o_w2); free(y->down_w2);
+        y->qkv_w2 = (uint8_t *)malloc((size_t)tq * (size_t)(H / 64) * 34);
+        y->o_w2 = (uint8_t *)malloc((size_t)H * (size_t)(qd / 64) * 34);
+        y->down_w2 = (uint8_t *)malloc((size_t)H * (size_t)(I / 64) * 34);
+        orc_pack_v1_to_v2((const uint8_t *)qkv_w, qkv_s, y->qkv_w2, tq, H);
+        orc_pack_v1_to_v2((const uint8_t *)o_w, o_s, y->o_w2, H, qd);
+        orc_pack_v1_to_v2((const uint8_t *)down_w, down_s, y->down_w2, H, I);
+    }
 }
 
 ORC_API void orc_decoder_destroy(orc_decoder *d) {
     if (!d) return;
+    for (int64_t l = 0; l < d->L; ++l) {
+        free(d->layers[l].qkv_w2); free(d->layers[l].o_w2); free(d->layers[l].down_w2);
+    }
+    free(d->lm_w2);
     free(d->layers); free(d->kc); free(d->vc); free(d->cos_t); free(d->sin_t);
     free(d->x); free(d->xn); free(d->qkv); free(d->att); free(d->o); free(d->h);
     free(d->dn); free(d->logits); free(d);
@@ -776,7 +805,10 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
     for (int64_t l = 0; l < d->L; ++l) {
         const orc_layer *y = &d->layers[l];
         orc_rms_norm(d->x, y->in_norm, d->xn, H, d->eps);
-        proj(d, d->wkind, d->xn, y->qkv_w, y->qkv_s, y->qkv_b, d->qkv, tq, H);
+        if (d->use_v2)
+            orc_gemv_w4_v2(d->xn, y->qkv_w2, y->qkv_b, d->qkv, tq, H);
+        else
+            proj(d, d->wkind, d->xn, y->qkv_w, y->qkv_s, y->qkv_b, d->qkv, tq, H);
         float *q = d->qkv, *k = d->qkv + qd, *v = d->qkv + qd + kvd;
         for (int64_t h = 0; h < hq; ++h) orc_rope_apply(q + h * hd, cp, sp, half);
         for (int64_t h = 0; h < hkv; ++h) orc_rope_apply(k + h * hd, cp, sp, half);
@@ -786,7 +818,10 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
             memcpy(vc + (h * d->max_seq + offset) * hd, v + h * hd, (size_t)hd * 4);
         }
         orc_attention(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1);
-        proj(d, d->wkind, d->att, y->o_w, y->o_s, NULL, d->o, H, qd);
+        if (d->use_v2)
+            orc_gemv_w4_v2(d->att, y->o_w2, NULL, d->o, H, qd);
+        else
+            proj(d, d->wkind, d->att, y->o_w, y->o_s, NULL, d->o, H, qd);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->o[i];
         orc_rms_norm(d->x, y->post_norm, d->xn, H, d->eps);
         if (d->wkind == 4)
@@ -795,11 +830,17 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
         else
             orc_swiglu_h_w8(d->xn, (const int8_t *)y->gate_w, y->gate_s,
                             (const int8_t *)y->up_w, y->up_s, d->h, d->I, H);
-        proj(d, d->wkind, d->h, y->down_w, y->down_s, NULL, d->dn, H, d->I);
+        if (d->use_v2)
+            orc_gemv_w4_v2(d->h, y->down_w2, NULL, d->dn, H, d->I);
+        else
+            proj(d, d->wkind, d->h, y->down_w, y->down_s, NULL, d->dn, H, d->I);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->dn[i];
     }
     orc_rms_norm(d->x, d->final_norm, d->xn, H, d->eps);
-    proj(d, d->lmkind, d->xn, d->lm_w, d->lm_s, NULL, d->logits, d->V, H);
+    if (d->lm_w2)
+        orc_gemv_w4_v2(d->xn, d->lm_w2, NULL, d->logits, d->V, H);
+    else
+        proj(d, d->lmkind, d->xn, d->lm_w, d->lm_s, NULL, d->logits, d->V, H);
 }
 
 /* Copy a prefilled KV prefix, decoder.rs:479-523: src is [hkv, src_max, hd]. */

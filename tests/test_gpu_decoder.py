@@ -88,6 +88,13 @@ def test_small_decoder_variants(cuda, variant):
     run_parity(small(), 5, prefill=37, steps=12, **variant)
 
 
+@pytest.mark.parametrize("lmkind", [4, 32, 8])
+def test_decoder_group64_v2_blocks(cuda, lmkind):
+    """Group 64 with every dimension a multiple of 64 (vocab 1024): QKV, O, down
+    and an INT4 lm_head run on v2 blocks with f16 scales (decoder.rs:361-390)."""
+    run_parity(small(vocab=1024), 15, lmkind=lmkind, gs=64, prefill=37, steps=10)
+
+
 def test_decoder_from_empty_cache(cuda):
     """seq_len == 1 at the first step: attention returns v (decoder.rs:1169-1177)."""
     run_parity(small(), 6, prefill=0, steps=10)

@@ -1,6 +1,6 @@
 """Parity of the batched prompt prefill with the CPU oracle's step-by-step prefill.
 
-The reference's prefill_tokens (src/llm/decoder.rs:609-660) runs one decoder
+The reference's prefill_tokens (src/llm/decoder.rs:431-447) runs one decoder
 step per prompt token and keeps the last step's logits.  The gfx950 decoder
 runs prompts of 16 or more in-vocabulary tokens (INT4 projections) as batches:
 row RMSNorms, the QKV / O / gate-up / down projections on the FP32-MFMA GEMM,
@@ -91,6 +91,12 @@ def test_prefill_llama_head_layout_fp32_lm_head(cuda):
 
 def test_prefill_threshold_g64_int8_lm_head(cuda):
     run_prefill(small(), 24, 16, gs=64, lmkind=8)
+
+
+def test_prefill_group64_v2_blocks(cuda):
+    """Group 64, vocab 1024: the batched projections read v2 blocks for QKV, O
+    and down and the lm_head (MFMA V2 path)."""
+    run_prefill(small(vocab=1024), 28, 100, start=7, gs=64)
 
 
 def test_prefill_qwen_layer_shape(cuda):

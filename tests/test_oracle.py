@@ -22,7 +22,10 @@ budgets are reproduced here):
                      seq_len 1 returns v; identical keys give mean(V)
   argmax             decoder.rs:32-40 KAT, ties -> lowest index
   decoder step       an independent float64 torch model built from library ops
-                     (rms_norm, complex RoPE, SDPA, silu) on a small config
+                     (rms_norm, complex RoPE, SDPA, silu) on a small config; at
+                     group 64 with every dimension a multiple of 64 the model uses
+                     binary16-rounded QKV / O / down / lm_head scales (the
+                     reference's v2 repack) and the f32-scale model is shown to differ
 """
 import math
 
@@ -277,10 +280,13 @@ def test_argmax_kat_and_ties():
 
 # ------------------------------------------------------------ decoder step ---
 
-def torch_step(w, cfg, kv, tok, pos, gs):
+def torch_step(w, cfg, kv, tok, pos, gs, f16=False):
     """One decoder step in float64 from torch library ops (independent of the
-    oracle's C code): rms_norm, complex RoPE, SDPA with GQA, silu."""
+    oracle's C code): rms_norm, complex RoPE, SDPA with GQA, silu.  f16: QKV, O,
+    down and lm_head use binary16-rounded scales (numpy's float16), the effect
+    of the reference's v2 repack at group 64 (decoder.rs:361-390)."""
     D = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    r16 = (lambda s: s.astype(np.float16).astype(np.float32)) if f16 else (lambda s: s)
     H, hq, hkv, hd = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     half = hd // 2
     freq = D(cfg["rope_theta"] ** (-(2.0 * np.arange(half)) / hd))
@@ -293,7 +299,7 @@ def torch_step(w, cfg, kv, tok, pos, gs):
     x = D(w["embed"][tok])
     for li, lw in enumerate(w["layers"]):
         xn = F.rms_norm(x, (H,), D(lw["in_norm"]), eps=cfg["eps"])
-        qkv = D(dequant(lw["qkv_w"], lw["qkv_s"], H, gs)) @ xn
+        qkv = D(dequant(lw["qkv_w"], r16(lw["qkv_s"]), H, gs)) @ xn
         if lw.get("qkv_b") is not None:
             qkv = qkv + D(lw["qkv_b"])
         q = rope(qkv[:hq * hd].reshape(hq, hd))
@@ -304,22 +310,26 @@ def torch_step(w, cfg, kv, tok, pos, gs):
         vc[:, pos] = v
         att = F.scaled_dot_product_attention(q[None, :, None], kc[None, :, :pos + 1],
                                              vc[None, :, :pos + 1], enable_gqa=True)[0, :, 0]
-        x = x + D(dequant(lw["o_w"], lw["o_s"], hq * hd, gs)) @ att.reshape(-1)
+        x = x + D(dequant(lw["o_w"], r16(lw["o_s"]), hq * hd, gs)) @ att.reshape(-1)
         xn = F.rms_norm(x, (H,), D(lw["post_norm"]), eps=cfg["eps"])
         h = F.silu(D(dequant(lw["gate_w"], lw["gate_s"], H, gs)) @ xn) * \
             (D(dequant(lw["up_w"], lw["up_s"], H, gs)) @ xn)
-        x = x + D(dequant(lw["down_w"], lw["down_s"], cfg["intermediate"], gs)) @ h
+        x = x + D(dequant(lw["down_w"], r16(lw["down_s"]), cfg["intermediate"], gs)) @ h
     xn = F.rms_norm(x, (H,), D(w["final_norm"]), eps=cfg["eps"])
-    return (D(dequant(w["lm_head_w"], w["lm_head_s"], H, gs)) @ xn).numpy()
+    return (D(dequant(w["lm_head_w"], r16(w["lm_head_s"]), H, gs)) @ xn).numpy()
 
 
-def test_decoder_step_vs_torch_float64():
+@pytest.mark.parametrize("gs,vocab,v2", [(32, 300, False), (64, 300, False), (64, 320, True)])
+def test_decoder_step_vs_torch_float64(gs, vocab, v2):
+    """v2: group 64 with every dimension a multiple of 64 (vocab 320) -> the
+    reference's v2 repack (f16 scales on QKV / O / down / lm_head); vocab 300
+    keeps the v1 f32 scales."""
     cfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
-               head_dim=32 * 2, vocab=300, eps=1e-6, rope_theta=1e6, qkv_bias=True)
-    gs, max_seq, pre = 32, 24, 9
+               head_dim=32 * 2, vocab=vocab, eps=1e-6, rope_theta=1e6, qkv_bias=True)
+    max_seq, pre = 24, 9
     w = synth.decoder_weights(cfg, 21, 4, 4, gs)
     ocfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
-                head_dim=64, vocab=300, group_size=gs, max_seq=max_seq, rope_theta=1e6,
+                head_dim=64, vocab=vocab, group_size=gs, max_seq=max_seq, rope_theta=1e6,
                 eps=1e-6, wkind=4, lmkind=4)
     dec = O.Decoder(w, ocfg)
     kvp = synth.kv_prefill(cfg, 21, pre, max_seq)
@@ -331,11 +341,14 @@ def test_decoder_step_vs_torch_float64():
     for step in range(4):
         pos = pre + step
         lo = dec.step(tok, pos)
-        lt = torch_step(w, cfg, tkv, tok, pos, gs)
+        kv_other = [(k.clone(), v.clone()) for k, v in tkv]
+        lt = torch_step(w, cfg, tkv, tok, pos, gs, f16=v2)
         assert rel(lo, lt) < 1e-5, f"step {step}"
+        if gs == 64:   # the scale precision is visible: the other model is off by > 1e-4
+            assert rel(lo, torch_step(w, cfg, kv_other, tok, pos, gs, f16=not v2)) > 1e-4
         assert O.argmax(lo) == int(np.argmax(lt))
         tok = O.argmax(lo)
     assert dec.kv_len() == pre + 4
     # out-of-range token / position -> zeroed logits (decoder.rs:1066-1089)
-    assert not dec.step(300, 3).any() and not dec.step(1, max_seq).any()
+    assert not dec.step(vocab, 3).any() and not dec.step(1, max_seq).any()
     dec.close()

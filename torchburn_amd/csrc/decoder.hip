@@ -29,6 +29,7 @@
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
 #include "w4_mfma.hpp"
+#include "v2_layout.hpp"
 
 struct tb_decoder;
 
@@ -52,6 +53,12 @@ struct Decoder {
     tb_decoder_config cfg{};
     int H = 0, I = 0, hq = 0, hkv = 0, hd = 0, V = 0, L = 0, max_seq = 0, tq = 0, nsplit = 0;
     int wbits = 4, lmbits = 4, gs = 32;
+    // Group 64 with every dimension a multiple of 64: the reference repacks QKV,
+    // O, down and the lm_head into v2 blocks, so their scales are binary16
+    // (decoder.rs:361-390); gate / up keep f32 scales.  Here those projections
+    // keep v1 nibbles with scales rounded to binary16 at load: the same numbers
+    // through the v1 GEMV, which streams faster than the 34-byte blocks.
+    bool v2 = false;
     bool fused = true;   // INT4: RMSNorms fused into the GEMVs (TB_DECODER_UNFUSED=1: separate)
     // Rows per GEMV block for QKV, O, gate/up, down, lm_head (0 = the GEMV's
     // default; TB_DECODER_J="qkv,o,gu,down,lm" overrides, for tuning sweeps).
@@ -110,6 +117,19 @@ struct Decoder {
         int rc = alloc(dst, bytes);
         if (rc) return rc;
         TB_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyDefault));
+        return TB_OK;
+    }
+
+    // An INT4 projection [n, k] whose scales the reference holds in binary16
+    // (v2 repack, group 64): v1 nibbles as given, scales rounded to binary16
+    // on the device (f32_to_f16, packed_v2.rs:66-105).
+    int upload_f16_scaled(void **w_dst, float **s_dst, const void *w, const float *s, int64_t n,
+                          int64_t k) {
+        int rc;
+        if ((rc = upload(w_dst, w, wbytes(4, n, k))) || (rc = upload(s_dst, s, sbytes(4, n, k))))
+            return rc;
+        if ((rc = round_scales_f16(*s_dst, n * (k / gs), st))) return rc;
+        TB_HIP(hipStreamSynchronize(st));
         return TB_OK;
     }
 
@@ -564,6 +584,8 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
     d->L = (int)c.num_layers; d->max_seq = (int)c.max_seq_len; d->gs = (int)c.group_size;
     d->wbits = c.weight_bits; d->lmbits = c.lm_head_bits; d->eps = (float)c.rms_norm_eps;
     d->tq = (d->hq + 2 * d->hkv) * d->hd;
+    d->v2 = d->wbits == 4 && d->gs == 64 && d->H % 64 == 0 && d->tq % 64 == 0 &&
+            (d->hq * d->hd) % 64 == 0 && d->I % 64 == 0 && d->V % 64 == 0;
     d->nsplit = attn_nsplit(d->max_seq);
     d->hist_cap = d->max_seq;
     d->layers.resize(d->L);
@@ -582,7 +604,6 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
     const size_t kv = (size_t)d->L * d->hkv * d->max_seq * d->hd * sizeof(float);
     if ((rc = d->upload(&d->embed, embed, (size_t)d->V * d->H * 4)) ||
         (rc = d->upload(&d->final_norm, final_norm, (size_t)d->H * 4)) ||
-        (rc = d->upload(&d->lm_w, lm_head_w, d->wbytes(d->lmbits, d->V, d->H))) ||
         (rc = d->alloc(&d->kc, kv)) || (rc = d->alloc(&d->vc, kv)) ||
         (rc = d->alloc(&d->x, d->H * 4)) || (rc = d->alloc(&d->xn, d->H * 4)) ||
         (rc = d->alloc(&d->qkv, d->tq * 4)) || (rc = d->alloc(&d->attn, d->hq * d->hd * 4)) ||
@@ -602,9 +623,16 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
         const char *j = getenv("TB_DECODER_J");
         if (j) sscanf(j, "%d,%d,%d,%d,%d", &d->rj[0], &d->rj[1], &d->rj[2], &d->rj[3], &d->rj[4]);
     }
-    if (d->lmbits != 32) {
+    if (d->lmbits != 32)
         TB_REQUIRE(lm_head_s, TB_ERR_VALUE, "lm_head scales are required for a quantized lm_head");
-        if ((rc = d->upload(&d->lm_s, lm_head_s, d->sbytes(d->lmbits, d->V, d->H)))) return bail(rc);
+    if (d->v2 && d->lmbits == 4) {
+        if ((rc = d->upload_f16_scaled(&d->lm_w, &d->lm_s, lm_head_w, lm_head_s, d->V, d->H)))
+            return bail(rc);
+    } else {
+        if ((rc = d->upload(&d->lm_w, lm_head_w, d->wbytes(d->lmbits, d->V, d->H)))) return bail(rc);
+        if (d->lmbits != 32 &&
+            (rc = d->upload(&d->lm_s, lm_head_s, d->sbytes(d->lmbits, d->V, d->H))))
+            return bail(rc);
     }
     std::vector<float> ct, stb;
     rope_tables(ct, stb, d->max_seq, d->hd, c.rope_theta);
@@ -636,17 +664,24 @@ int tb_decoder_set_layer(tb_decoder *d, int64_t layer, const float *in_norm, con
     int rc;
     if ((rc = d->upload(&y.in_norm, in_norm, H * 4)) ||
         (rc = d->upload(&y.post_norm, post_norm, H * 4)) ||
-        (rc = d->upload(&y.qkv_w, qkv_w, d->wbytes(b, d->tq, H))) ||
-        (rc = d->upload(&y.qkv_s, qkv_s, d->sbytes(b, d->tq, H))) ||
-        (rc = d->upload(&y.o_w, o_w, d->wbytes(b, H, qd))) ||
-        (rc = d->upload(&y.o_s, o_s, d->sbytes(b, H, qd))) ||
         (rc = d->upload(&y.gate_w, gate_w, d->wbytes(b, I, H))) ||
         (rc = d->upload(&y.gate_s, gate_s, d->sbytes(b, I, H))) ||
         (rc = d->upload(&y.up_w, up_w, d->wbytes(b, I, H))) ||
-        (rc = d->upload(&y.up_s, up_s, d->sbytes(b, I, H))) ||
-        (rc = d->upload(&y.down_w, down_w, d->wbytes(b, H, I))) ||
-        (rc = d->upload(&y.down_s, down_s, d->sbytes(b, H, I))))
+        (rc = d->upload(&y.up_s, up_s, d->sbytes(b, I, H))))
         return rc;
+    if (d->v2) {
+        if ((rc = d->upload_f16_scaled(&y.qkv_w, &y.qkv_s, qkv_w, qkv_s, d->tq, H)) ||
+            (rc = d->upload_f16_scaled(&y.o_w, &y.o_s, o_w, o_s, H, qd)) ||
+            (rc = d->upload_f16_scaled(&y.down_w, &y.down_s, down_w, down_s, H, I)))
+            return rc;
+    } else if ((rc = d->upload(&y.qkv_w, qkv_w, d->wbytes(b, d->tq, H))) ||
+               (rc = d->upload(&y.qkv_s, qkv_s, d->sbytes(b, d->tq, H))) ||
+               (rc = d->upload(&y.o_w, o_w, d->wbytes(b, H, qd))) ||
+               (rc = d->upload(&y.o_s, o_s, d->sbytes(b, H, qd))) ||
+               (rc = d->upload(&y.down_w, down_w, d->wbytes(b, H, I))) ||
+               (rc = d->upload(&y.down_s, down_s, d->sbytes(b, H, I)))) {
+        return rc;
+    }
     if (qkv_b && (rc = d->upload(&y.qkv_b, qkv_b, (size_t)d->tq * 4))) return rc;
     y.set = true;
     return TB_OK;

@@ -68,6 +68,12 @@ __global__ __launch_bounds__(256) void k_pack_v2(const uint8_t *__restrict__ w,
     dst[16] = (uint16_t)f32_to_f16_bits(s[t]);
 }
 
+// s[i] = f16_to_f32(f32_to_f16(s[i])): scales as the v2 blocks carry them.
+__global__ __launch_bounds__(256) void k_round_f16(float *__restrict__ s, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) s[i] = f16_bits_to_f32(f32_to_f16_bits(s[i]));
+}
+
 // One thread per (row, 32-element half block): (nib - 8) * f16 scale.
 __global__ __launch_bounds__(256) void k_dequant_v2(const uint8_t *__restrict__ blocked,
                                                     float *__restrict__ out, int64_t n, int ng) {
@@ -135,6 +141,13 @@ int dequant_v2(const uint8_t *blocked, float *out, int64_t n, int64_t k, hipStre
     if (total == 0) return TB_OK;
     hipLaunchKernelGGL(k_dequant_v2, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                        blocked, out, n, ng);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int round_scales_f16(float *s, int64_t n, hipStream_t st) {
+    if (n == 0) return TB_OK;
+    hipLaunchKernelGGL(k_round_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, n);
     TB_LAUNCHED();
     return TB_OK;
 }

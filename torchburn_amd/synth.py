@@ -156,22 +156,25 @@ def prefill_flops(cfg: dict, n: int, start: int = 0) -> int:
 
 
 def decode_bytes_per_token(cfg: dict, pos: int, wkind: int, lmkind: int,
-                           group_size: int = 32) -> int:
+                           group_size: int = 32, v2: bool = False) -> int:
     """Algorithmic HBM bytes of one decoder step at position `pos`: every weight
     byte once (projections, norms, lm_head, one embedding row) plus the KV rows
-    0..pos read and the new K/V row written."""
+    0..pos read and the new K/V row written.  v2: QKV, O, down and an INT4
+    lm_head are 34-byte blocks per 64 weights (group 64)."""
     H, I = cfg["hidden"], cfg["intermediate"]
     hq, hkv, hd = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     tq = (hq + 2 * hkv) * hd
 
-    def proj(n, k, bits):
+    def proj(n, k, bits, blocks=False):
+        if bits == 4 and blocks:
+            return n * (k // 64) * 34
         if bits == 4:
             return n * ((k + 1) // 2) + 4 * n * (k // group_size)
         if bits == 8:
             return n * k + 4 * n
         return 4 * n * k
 
-    layer = (proj(tq, H, wkind) + proj(H, hq * hd, wkind) + 2 * proj(I, H, wkind) +
-             proj(H, I, wkind) + 2 * 4 * H + (4 * tq if cfg.get("qkv_bias") else 0))
+    layer = (proj(tq, H, wkind, v2) + proj(H, hq * hd, wkind, v2) + 2 * proj(I, H, wkind) +
+             proj(H, I, wkind, v2) + 2 * 4 * H + (4 * tq if cfg.get("qkv_bias") else 0))
     kv = 2 * hkv * (pos + 1) * hd * 4 + 2 * hkv * hd * 4
-    return (cfg["num_layers"] * (layer + kv) + proj(cfg["vocab"], H, lmkind) + 4 * H + 4 * H)
+    return (cfg["num_layers"] * (layer + kv) + proj(cfg["vocab"], H, lmkind, v2) + 4 * H + 4 * H)
