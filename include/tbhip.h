@@ -103,6 +103,35 @@ TB_API int tb_dequantize_int4_grouped_v2(const uint8_t *w_blocked, float *out, i
                                          int64_t k, void *stream);
 
 /*
+ * f32 weights [N, K] -> v1 nibbles [N, K/2] + f32 scales [N, K/gs] on the device:
+ * quantize_weight_int4_grouped (python/torchburn/quantization.py:53-118),
+ * s = max(max|w| / 7, 1e-8) per group, q = clamp(round_half_even(w / s), -8, 7).
+ * group_size 32 or 64; K % group_size != 0 is TB_ERR_VALUE with the
+ * reference's message.
+ */
+TB_API int tb_quantize_weight_int4_grouped(const float *w, uint8_t *packed, float *scales,
+                                           int64_t n, int64_t k, int64_t group_size,
+                                           void *stream);
+
+/*
+ * f32 weights [N, K] -> int8 [N, K] + per-row f32 scales [N] on the device:
+ * quantize_linear_weights_int8 (binding src/ffi/quantization_ffi.rs:258-269 ->
+ * src/quantization/fused_ops.rs:554-589), s = max|w| / 127 (1 when max|w| <= 1e-8),
+ * q = clamp(round_half_away(w * (1 / s)), -127, 127).
+ */
+TB_API int tb_quantize_weight_int8(const float *w, int8_t *q, float *scales, int64_t n,
+                                   int64_t k, void *stream);
+
+/*
+ * v2 blocks [N, (K/64)*34] -> v1 nibbles [N, K/2] + f32 scales [N, K/64]: the
+ * quantized-cache migration of the reference's loader
+ * (python/torchburn/llm/loader.py:540-561), on the device.
+ */
+TB_API int tb_unpack_rows_w4a32_group64_v2_to_v1(const uint8_t *w_blocked, uint8_t *w_packed,
+                                                 float *scales, int64_t n, int64_t k,
+                                                 void *stream);
+
+/*
  * Selects the reference's AVX-512 VNNI-tier semantics for group-64 INT4
  * projections (tb_w4a32_grouped_linear[_residual] at group 64 and
  * tb_w4a32_grouped_linear_v2): each activation row is quantized to bytes,

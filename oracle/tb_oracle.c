@@ -474,7 +474,7 @@ ORC_API void orc_gemv_w8(const float *x, const int8_t *w, const float *s, int64_
 }
 
 /* Per-channel INT8 quantizer, fused_ops.rs:554-589: s = amax/127 (1 when    */
-/* amax == 0), q = clamp(round_half_away(w * (1/s)), -127, 127).             */
+/* amax <= 1e-8), q = clamp(round_half_away(w * (1/s)), -127, 127).          */
 ORC_API void orc_quantize_int8(const float *w, int8_t *q, float *s, int64_t n, int64_t k) {
     for (int64_t r = 0; r < n; ++r) {
         float amax = 0.f;
@@ -482,7 +482,7 @@ ORC_API void orc_quantize_int8(const float *w, int8_t *q, float *s, int64_t n, i
             float a = fabsf(w[r * k + i]);
             amax = a > amax ? a : amax;
         }
-        float sc = amax > 0.f ? amax / 127.0f : 1.0f;
+        float sc = amax > 1e-8f ? amax / 127.0f : 1.0f; /* fused_ops.rs:575 */
         float inv = 1.0f / sc;
         s[r] = sc;
         for (int64_t i = 0; i < k; ++i) {

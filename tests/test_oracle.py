@@ -14,6 +14,8 @@ budgets are reproduced here):
   swiglu             float64 closed form via torch.nn.functional.silu
   gemv_w8            the dot_f32_i8 KAT (tests/parity/int8.rs:24-37), float64,
                      quality budget (int8.rs:41-67)
+  quantize_int8      numpy closed form with ties away from zero and the 1e-8
+                     zero-row threshold (fused_ops.rs:554-589)
   rms_norm           the reference's KAT (tests/parity/decoder.rs:14-29) and
                      torch.nn.functional.rms_norm in float64
   rope               RoPE as a complex rotation in float64 (a different formula),
@@ -209,6 +211,26 @@ def test_gemv_w8_vs_float64_and_quality():
     qq, ss = O.quantize_int8(ww.reshape(n, k))
     y = O.gemv_w8(xx[None], qq, ss)[0]
     assert rel(y, ww.reshape(n, k).astype(np.float64) @ xx) < 0.05
+
+
+def test_quantize_int8_closed_form():
+    """fused_ops.rs:554-589: s = amax / 127 (1 when amax <= 1e-8); q = round half
+    away from zero of w * (1 / s), clamped to +-127."""
+    g = np.random.default_rng(8)
+    w = g.standard_normal((6, 96)).astype(np.float32)
+    w[1] = 0.0                                  # amax 0 -> scale 1
+    w[2] = np.float32(5e-9) * np.sign(w[2])     # amax <= 1e-8 -> scale 1, q 0
+    w[3, :4] = [127.0, 2.5, -2.5, 0.5]          # scale 1: ties away from zero
+    w[3, 4:] = 0.0
+    q, s = O.quantize_int8(w)
+    amax = np.abs(w).max(1)
+    s_want = np.where(amax > np.float32(1e-8), amax / np.float32(127.0), np.float32(1.0))
+    assert np.array_equal(s, s_want.astype(np.float32))
+    t = (w * (np.float32(1.0) / s_want.astype(np.float32))[:, None]).astype(np.float32)
+    t = t.astype(np.float64)
+    r = np.where(t >= 0, np.floor(t + 0.5), np.ceil(t - 0.5))
+    assert np.array_equal(q, np.clip(r, -127, 127).astype(np.int8))
+    assert list(q[3, :4]) == [127, 3, -3, 1] and not q[2].any()
 
 
 # -------------------------------------------------------- norm, rope, attn ---

@@ -25,6 +25,7 @@ from .quantization import (
     quantize_weight_int4_grouped_v2,
     quantize_weight_int8,
     set_vnni_semantics,
+    unpack_rows_w4a32_group64_v2_to_v1,
     w4a32_grouped_linear,
     w4a32_grouped_linear_residual,
     w4a32_grouped_linear_v2,
@@ -56,4 +57,5 @@ __all__ = [
     "dequantize_int4_grouped_v2",
     "pack_rows_w4a32_group64_v1_to_v2",
     "set_vnni_semantics",
+    "unpack_rows_w4a32_group64_v2_to_v1",
 ]

@@ -43,6 +43,9 @@ _SIGS = {
     "tb_pack_rows_w4a32_group64_v1_to_v2": [_p, _p, _p, _i64, _i64, _p],
     "tb_dequantize_int4_grouped_v2": [_p, _p, _i64, _i64, _p],
     "tb_set_vnni_semantics": [C.c_int],
+    "tb_quantize_weight_int4_grouped": [_p, _p, _p, _i64, _i64, _i64, _p],
+    "tb_quantize_weight_int8": [_p, _p, _p, _i64, _i64, _p],
+    "tb_unpack_rows_w4a32_group64_v2_to_v1": [_p, _p, _p, _i64, _i64, _p],
     "tb_swiglu_w4a32": [_p] * 8 + [_i64] * 4 + [_p],
     "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
     "tb_w8a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],

@@ -17,6 +17,7 @@
 #include "w4_gemv.hpp"
 #include "w4_mfma.hpp"
 #include "v2_layout.hpp"
+#include "quantize.hpp"
 
 namespace tb {
 
@@ -294,6 +295,49 @@ int tb_dequantize_int4_grouped_v2(const uint8_t *w_blocked, float *out, int64_t 
     TB_REQUIRE((size_t)n * (size_t)(k / 64) * 34 < (1ull << 32), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: dequantize_int4_grouped_v2: blocks must be under 4 GiB");
     return dequant_v2(w_blocked, out, n, k, (hipStream_t)stream);
+}
+
+int tb_quantize_weight_int4_grouped(const float *w, uint8_t *packed, float *scales, int64_t n,
+                                    int64_t k, int64_t group_size, void *stream) {
+    TB_REQUIRE(w && packed && scales, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4_grouped: null pointer");
+    TB_REQUIRE(group_size == 32 || group_size == 64, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4_grouped: group_size must be 32 or 64, got " +
+                   std::to_string(group_size));
+    TB_REQUIRE(n >= 0 && k > 0 && k <= (1 << 30), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4_grouped: bad shape");
+    TB_REQUIRE(k % group_size == 0, TB_ERR_VALUE,
+               "Weight dimension K=" + std::to_string(k) + " must be divisible by group_size=" +
+                   std::to_string(group_size) + ". Consider padding the weight tensor along dim 1 "
+                   "to a multiple of " + std::to_string(group_size) + ".");
+    TB_REQUIRE(aligned(w, 4) && aligned(scales, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4_grouped: misaligned device pointer");
+    return quantize_int4_grouped(w, packed, scales, n, k, (int)group_size, (hipStream_t)stream);
+}
+
+int tb_quantize_weight_int8(const float *w, int8_t *q, float *scales, int64_t n, int64_t k,
+                            void *stream) {
+    TB_REQUIRE(w && q && scales, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int8: null pointer");
+    TB_REQUIRE(n >= 0 && k > 0 && k <= (1 << 30) && n < (1ll << 31), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int8: bad shape");
+    TB_REQUIRE(aligned(w, 4) && aligned(scales, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int8: misaligned device pointer");
+    return quantize_int8(w, q, scales, n, k, (hipStream_t)stream);
+}
+
+int tb_unpack_rows_w4a32_group64_v2_to_v1(const uint8_t *w_blocked, uint8_t *w_packed,
+                                          float *scales, int64_t n, int64_t k, void *stream) {
+    TB_REQUIRE(w_blocked && w_packed && scales, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: unpack_rows_w4a32_group64_v2_to_v1: null pointer");
+    TB_REQUIRE(n >= 0 && k > 0 && k % 64 == 0 && (size_t)n * (size_t)(k / 64) * 34 < (1ull << 32),
+               TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: unpack_rows_w4a32_group64_v2_to_v1: K must be a multiple of 64 "
+               "and the blocks under 4 GiB");
+    TB_REQUIRE(aligned(w_blocked, 4) && aligned(w_packed, 16) && aligned(scales, 4),
+               TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: unpack_rows_w4a32_group64_v2_to_v1: misaligned device pointer");
+    return unpack_v2_to_v1(w_blocked, w_packed, scales, n, k, (hipStream_t)stream);
 }
 
 int tb_set_vnni_semantics(int enabled) {

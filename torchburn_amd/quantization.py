@@ -70,7 +70,9 @@ def quantize_weight_int4_grouped(
 
     Per group: s = max(amax / 7, 1e-8); q = clamp(round_half_even(w / s), -8, 7);
     byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4  (reference quantization.py:53-118).
-    Rows are processed in chunks of ``chunk_size`` to bound peak memory.
+    Runs on the GPU (tb_quantize_weight_int4_grouped), ``chunk_size`` rows of a
+    host tensor at a time; the result is on the weight's device.  Group sizes 32
+    and 64 (the ones the GEMVs read).
     """
     if weight.ndim != 2:
         raise ValueError(
@@ -81,19 +83,20 @@ def quantize_weight_int4_grouped(
         raise ValueError(
             f"Weight dimension K={k} must be divisible by group_size={group_size}. "
             f"Consider padding the weight tensor along dim 1 to a multiple of {group_size}.")
-    ng = k // group_size
-    dev = weight.device
+    if group_size not in (32, 64):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} quantize_weight_int4_grouped: group_size must be 32 or 64, "
+            f"got {group_size}")
+    dev = _target(weight)
     packed = torch.empty((n, (k + 1) // 2), dtype=torch.uint8, device=dev)
-    scales = torch.empty((n, ng), dtype=torch.float32, device=dev)
-    for r0 in range(0, n, chunk_size):
-        r1 = min(r0 + chunk_size, n)
-        wg = weight[r0:r1].detach().to(torch.float32).view(r1 - r0, ng, group_size)
-        s = torch.clamp(wg.abs().amax(dim=-1, keepdim=True) / 7.0, min=1e-8)
-        q = torch.clamp(torch.round(wg / s), -8, 7).to(torch.int8).view(r1 - r0, k)
-        u = (q + 8).to(torch.uint8)
-        packed[r0:r1] = (u[:, 0::2] & 0x0F) | ((u[:, 1::2] & 0x0F) << 4)
-        scales[r0:r1] = s.view(r1 - r0, ng)
-    return packed, scales
+    scales = torch.empty((n, k // group_size), dtype=torch.float32, device=dev)
+    step = n if weight.is_cuda else max(int(chunk_size), 1)
+    for r0 in range(0, n, step):
+        r1 = min(r0 + step, n)
+        wc = _on_gpu(weight[r0:r1].detach(), torch.float32, dev)
+        _lib.call("tb_quantize_weight_int4_grouped", _ptr(wc), _ptr(packed[r0:r1]),
+                  _ptr(scales[r0:r1]), r1 - r0, k, group_size, _stream(dev))
+    return packed.to(weight.device), scales.to(weight.device)
 
 
 def pack_rows_w4a32_group64_v1_to_v2(w_packed: torch.Tensor, scales: torch.Tensor,
@@ -164,19 +167,37 @@ def set_vnni_semantics(enabled: bool) -> bool:
 
 
 def quantize_weight_int8(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(N, K) float -> (int8 (N, K), float32 scales (N,)).
-
-    s = amax / 127 (1 when amax == 0); q = clamp(round_half_away(w * (1/s)), -127, 127)
-    (reference src/quantization/fused_ops.rs:554-589).
-    """
+    """(N, K) float -> (int8 (N, K), float32 scales (N,)) on the GPU
+    (tb_quantize_weight_int8): s = amax / 127 (1 when amax <= 1e-8);
+    q = clamp(round_half_away(w * (1/s)), -127, 127) (reference
+    src/quantization/fused_ops.rs:554-589).  The result is on w's device."""
     if w.ndim != 2:
         raise ValueError(f"Expected 2D weight, got {w.shape}")
-    wf = w.detach().to(torch.float32)
-    amax = wf.abs().amax(dim=1)
-    s = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
-    v = wf * (1.0 / s)[:, None]
-    q = torch.clamp(torch.sign(v) * torch.floor(v.abs() + 0.5), -127, 127).to(torch.int8)
-    return q, s
+    n, k = w.shape
+    dev = _target(w)
+    wc = _on_gpu(w.detach(), torch.float32, dev)
+    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+    s = torch.empty(n, dtype=torch.float32, device=dev)
+    _lib.call("tb_quantize_weight_int8", _ptr(wc), _ptr(q), _ptr(s), n, k, _stream(dev))
+    return q.to(w.device), s.to(w.device)
+
+
+def unpack_rows_w4a32_group64_v2_to_v1(blocked: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """v2 blocks (N, (K/64) * 34) -> (v1 nibbles (N, K/2), f32 scales (N, K/64)): the
+    reference loader's cache migration (python/torchburn/llm/loader.py:540-561),
+    on the device.  The result is on the blocks' device."""
+    dev = _target(blocked)
+    b = _on_gpu(blocked, torch.uint8, dev)
+    n, cols = b.shape
+    if cols % 34 != 0:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} v2 rows must be whole 34-byte blocks, got {cols} bytes")
+    k = (cols // 34) * 64
+    w = torch.empty((n, k // 2), dtype=torch.uint8, device=dev)
+    s = torch.empty((n, k // 64), dtype=torch.float32, device=dev)
+    _lib.call("tb_unpack_rows_w4a32_group64_v2_to_v1", _ptr(b), _ptr(w), _ptr(s), n, k,
+              _stream(dev))
+    return w.to(blocked.device), s.to(blocked.device)
 
 
 # --------------------------------------------------------------------------
