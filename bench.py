@@ -313,6 +313,7 @@ def decode_run(torch, name, steps, prefill_tokens=0):
     dec.time_greedy(first, kvlen, min(8, steps))          # warm-up (same positions)
     ms = dec.time_greedy(first, kvlen, steps)
     pre = prefill_run(dec, cfg, prefill_tokens) if prefill_tokens and wk == 4 else None
+    sampled = sampled_run(dec, first, kvlen, steps) if name in ("llama4", "qwen64") else None
     dec.close()
     torch.cuda.empty_cache()
     byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk, gs, v2=name == "qwen64")
@@ -324,7 +325,27 @@ def decode_run(torch, name, steps, prefill_tokens=0):
            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / byts, 1)}
     if pre:
         out["prefill"] = pre
+    if sampled:
+        out["sampled"] = sampled
     return out
+
+
+def sampled_run(dec, first, kvlen, steps):
+    """generate_loop with temperature 0.7, top_k 40, top_p 0.9 and repetition
+    penalty 1.1 over the same positions (device sampler in the step graph), wall
+    clock of the whole call."""
+    args = dict(temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.1)
+    dec.set_seed(1)
+    dec.generate_loop(first, kvlen, min(8, steps), **args)          # warm-up, captures
+    times = []
+    for _ in range(2):
+        dec.set_seed(1)
+        t0 = time.perf_counter()
+        toks, _ = dec.generate_loop(first, kvlen, steps, **args)
+        times.append(time.perf_counter() - t0)
+    sec = min(times) / steps
+    return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(sec * 1e3, 4),
+            "params": args, "tokens": steps}
 
 
 def prefill_run(dec, cfg, n):

@@ -132,6 +132,26 @@ TB_API int tb_unpack_rows_w4a32_group64_v2_to_v1(const uint8_t *w_blocked, uint8
                                                  void *stream);
 
 /*
+ * Token sampling on the device over device logits [vocab]: apply_repetition_penalty
+ * (src/llm/decoder.rs:878-899; logits modified in place, recent: device int64
+ * [n_recent], each distinct in-vocabulary token once) then sample_logits
+ * (decoder.rs:908-1020): greedy when temperature is not finite or <= 0 or
+ * top_k == 1, else the top-k (ties: lower index first; non-finite logits as
+ * -inf), softmax at the temperature, nucleus cut at top_p, one draw.  The
+ * reference draws from an unseeded generator; here draw number `counter` of
+ * `seed` is u = tb_sample_uniform(seed, counter).  top_k <= 128 and vocab <=
+ * 262144.  Synchronizes the stream; *token_out and *u_out (or -1 when nothing
+ * was drawn) are host values.
+ */
+TB_API int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t top_k,
+                            float top_p, float repetition_penalty, const int64_t *recent,
+                            int64_t n_recent, uint64_t seed, uint64_t counter, int64_t *token_out,
+                            float *u_out, void *stream);
+
+/* The uniform in [0, 1) (24 bits) of draw `counter` under `seed`: splitmix64. */
+TB_API float tb_sample_uniform(uint64_t seed, uint64_t counter);
+
+/*
  * Selects the reference's AVX-512 VNNI-tier semantics for group-64 INT4
  * projections (tb_w4a32_grouped_linear[_residual] at group 64 and
  * tb_w4a32_grouped_linear_v2): each activation row is quantized to bytes,
@@ -318,7 +338,10 @@ TB_API int tb_decoder_step(tb_decoder *d, int64_t token, int64_t offset, float *
 
 /* decode_and_sample (decoder.rs:752-777, 878-1020): repetition penalty over
  * `recent`, then greedy (temperature <= 0 or not finite, or top_k == 1) or
- * top-k / top-p sampling from the decoder's seeded generator. */
+ * top-k / top-p sampling from the decoder's seeded generator.  top_k <= 128
+ * samples on the device (tb_sample_logits, draws numbered from the last
+ * tb_decoder_set_seed); larger top_k reads the logits back and samples on the
+ * host. */
 TB_API int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t offset,
                                         float temperature, int64_t top_k,
                                         float repetition_penalty, const int64_t *recent,
@@ -331,6 +354,20 @@ TB_API int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t of
 TB_API int tb_decoder_generate(tb_decoder *d, int64_t first_token, int64_t seq_len,
                                int64_t max_new_tokens, int64_t eos_token_id,
                                int64_t *tokens_out, int64_t *n_out, int64_t *seq_len_out);
+
+/* generate_loop with sampling (decoder.rs:788-832, window 859-876): the window
+ * starts as the last 64 of recent_seed (n_seed ids, may be NULL when 0), each
+ * step pushes its input token, applies the penalty over the window and samples
+ * the next token.  With top_k <= 128 the steps inside the cache run as replays
+ * of a graph whose tail samples on the device (no logits read back; with an
+ * EOS token one 4-byte read per step).  Greedy without a penalty is
+ * tb_decoder_generate. */
+TB_API int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_len,
+                                       int64_t max_new_tokens, float temperature, int64_t top_k,
+                                       float repetition_penalty, float top_p,
+                                       int64_t eos_token_id, const int64_t *recent_seed,
+                                       int64_t n_seed, int64_t *tokens_out, int64_t *n_out,
+                                       int64_t *seq_len_out);
 
 /* prefill_tokens (decoder.rs:431-447): TB_ERR_VALUE when start_offset + n >
  * max_seq_len. */

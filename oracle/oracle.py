@@ -87,6 +87,10 @@ def lib():
         L.orc_quantize_act_u8.argtypes = [_f32p, _i64, _u8p]
         L.orc_quantize_act_u8.restype = C.c_float
         L.orc_gemv_w4a8_g64.argtypes = [_vp, _vp, _vp, C.c_int, _vp, _vp, _i64, _i64]
+        L.orc_repetition_penalty.argtypes = [_f32p, _i64, _vp, _i64, C.c_float]
+        L.orc_sample_logits.argtypes = [_f32p, _i64, C.c_float, _i64, C.c_float, C.c_float,
+                                        C.POINTER(_i64)]
+        L.orc_sample_logits.restype = _i64
         _lib = L
     return _lib
 
@@ -212,6 +216,24 @@ def gemm_w4a8_g64(x, w, s=None, bias=None, blocked=False) -> np.ndarray:
         lib().orc_gemv_w4a8_g64(_p(xi), _p(w), _p(sv), int(blocked), _p(b), _p(yi), n, k)
         y[i] = yi
     return y
+
+
+def repetition_penalty(logits, recent, penalty) -> np.ndarray:
+    """apply_repetition_penalty (decoder.rs:878-899) on a copy."""
+    lg = np.array(logits, dtype=np.float32, copy=True).reshape(-1)
+    rec = np.ascontiguousarray(np.asarray(list(recent), dtype=np.int64))
+    lib().orc_repetition_penalty(lg, lg.size, rec.ctypes.data if rec.size else None, rec.size,
+                                 float(penalty))
+    return lg
+
+
+def sample_logits(logits, temperature, top_k, top_p, u):
+    """(token, candidates) of sample_logits (decoder.rs:908-1020) with the draw u."""
+    lg = _c(logits, np.float32).reshape(-1)
+    kept = _i64()
+    tok = lib().orc_sample_logits(lg, lg.size, float(temperature), int(top_k), float(top_p),
+                                  float(u), C.byref(kept))
+    return int(tok), int(kept.value)
 
 
 def swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None, group_size=32):

@@ -657,6 +657,90 @@ ORC_API int64_t orc_argmax(const float *v, int64_t n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* f4: sampling.  apply_repetition_penalty, decoder.rs:878-899: each distinct */
+/* in-vocabulary recent token's logit / penalty when > 0, else * penalty.     */
+/* ------------------------------------------------------------------------ */
+ORC_API void orc_repetition_penalty(float *logits, int64_t V, const int64_t *recent, int64_t n,
+                                    float penalty) {
+    if (!(penalty > 1.0f) || n <= 0) return;
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t t = recent[i], dup = 0;
+        if (t < 0 || t >= V) continue;
+        for (int64_t j = 0; j < i && !dup; ++j) dup = recent[j] == t;
+        if (dup) continue;
+        float l = logits[t];
+        logits[t] = l > 0.f ? l / penalty : l * penalty;
+    }
+}
+
+/* sample_logits, decoder.rs:908-1020, with the uniform u supplied:          */
+/*  greedy (temperature not finite or <= 0, or top_k == 1): first index of   */
+/*  the largest raw logit (NaN never chosen);                                */
+/*  else k = clamp(top_k, 1, V) candidates, non-finite logits as -inf, taken */
+/*  by (value descending, index ascending) and visited in that order;         */
+/*  p_i = exp((v_i - v_0) * (1/T)); nucleus: keep while the normalised mass  */
+/*  before the item is <= top_p (0 < top_p < 1); r = u * kept mass; first    */
+/*  item whose running mass >= r.  *kept_out = candidates after top-k.       */
+typedef struct { float v; int64_t i; } orc_item;
+static int item_cmp(const void *a, const void *b) {
+    const orc_item *x = (const orc_item *)a, *y = (const orc_item *)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->i < y->i ? -1 : (x->i > y->i);
+}
+
+ORC_API int64_t orc_sample_logits(const float *logits, int64_t V, float temperature,
+                                  int64_t top_k, float top_p, float u, int64_t *kept_out) {
+    if (V <= 0) return 0;
+    if (!isfinite(temperature) || temperature <= 0.f || top_k == 1) {
+        int64_t bi = -1;
+        for (int64_t i = 0; i < V; ++i)
+            if (!isnan(logits[i]) && (bi < 0 || logits[i] > logits[bi])) bi = i;
+        if (kept_out) *kept_out = 1;
+        return bi < 0 ? 0 : bi;
+    }
+    int64_t k = top_k < 1 ? 1 : (top_k > V ? V : top_k);
+    orc_item *it = (orc_item *)malloc((size_t)V * sizeof(orc_item));
+    for (int64_t i = 0; i < V; ++i) {
+        it[i].v = isfinite(logits[i]) ? logits[i] : -INFINITY;
+        it[i].i = i;
+    }
+    qsort(it, (size_t)V, sizeof(orc_item), item_cmp);
+    float *p = (float *)malloc((size_t)k * sizeof(float));
+    float mx = it[0].v, inv_t = 1.0f / temperature, pre = 0.f;
+    for (int64_t i = 0; i < k; ++i) {
+        p[i] = expf((it[i].v - mx) * inv_t);
+        pre += p[i];
+    }
+    int64_t kept = k;
+    if (top_p > 0.f && top_p < 1.f && k > 1 && pre > 0.f) {
+        float inv = 1.0f / pre, cum = 0.f;
+        for (int64_t i = 0; i < k; ++i) {
+            if (cum > top_p) {
+                kept = i;
+                break;
+            }
+            cum += p[i] * inv;
+        }
+    }
+    float ks = 0.f;
+    for (int64_t i = 0; i < kept; ++i) ks += p[i];
+    float r = u * ks, acc = 0.f;
+    int64_t tok = it[0].i;
+    for (int64_t i = 0; i < kept; ++i) {
+        acc += p[i];
+        if (acc >= r) {
+            tok = it[i].i;
+            break;
+        }
+    }
+    if (kept_out) *kept_out = k;
+    free(p);
+    free(it);
+    return tok;
+}
+
+/* ------------------------------------------------------------------------ */
 /* a16: RustQwenDecoder::step_internal, decoder.rs:1051-1374.                 */
 /* The oracle borrows every weight pointer (the caller keeps them alive) and */
 /* owns its KV cache [L][hkv, max_seq, hd], RoPE tables and scratch, as the  */

@@ -1,0 +1,78 @@
+"""The device sampler (tb_sample_logits) against the oracle's restatement of
+apply_repetition_penalty + sample_logits (decoder.rs:878-1020), pinned in
+tests/test_oracle_sample.py.  The draw u of (seed, counter) comes from the
+library's generator (tb_sample_uniform); given u the token must be identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+import torchburn_amd as tb
+
+pytestmark = pytest.mark.gpu
+
+
+CASES = [
+    # V, T, top_k, top_p, penalty
+    (1000, 0.7, 40, 1.0, 1.0),
+    (151936, 0.7, 40, 0.9, 1.1),
+    (128256, 1.3, 128, 0.5, 1.0),
+    (2048 * 3 + 5, 0.5, 2, 1.0, 1.2),
+    (151936, 0.0, 40, 1.0, 1.0),       # greedy
+    (151936, 0.9, 1, 1.0, 1.3),        # top_k 1 -> greedy after the penalty
+    (5000, 1.0, 0, 1.0, 1.0),          # top_k 0 -> one candidate
+    (300, 2.0, 128, 0.95, 1.5),
+]
+
+
+@pytest.mark.parametrize("V,T,k,top_p,pen", CASES)
+def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
+    print(f"case sample_logits V={V} T={T} top_k={k} top_p={top_p} penalty={pen}", flush=True)
+    g = np.random.default_rng(V + k)
+    for trial in range(6):
+        lg = (g.standard_normal(V) * 3).astype(np.float32)
+        if trial == 1:
+            lg[g.integers(0, V, 20)] = np.nan
+            lg[g.integers(0, V, 5)] = -np.inf
+        if trial == 2:
+            lg[:] = np.round(lg)                  # many ties
+        if trial == 3:
+            lg[:] = 0.0                           # all equal
+        recent = list(g.integers(0, V, 30)) + [V + 5, -1]
+        seed, counter = int(g.integers(0, 2 ** 63)), int(g.integers(0, 1000))
+        tok, u = tb.sample_logits(torch.from_numpy(lg).to(cuda), T, k, top_p, pen, recent,
+                                  seed=seed, counter=counter, return_u=True)
+        greedy = not np.isfinite(T) or T <= 0 or k == 1
+        uu = tb.sample_uniform(seed, counter)
+        if not greedy and max(1, min(k, V)) > 1:
+            assert u == uu
+        else:
+            assert u == -1.0
+        ref, _ = O.sample_logits(O.repetition_penalty(lg, recent, pen), T, k, top_p, uu)
+        assert tok == ref, (trial, tok, ref)
+
+
+def test_sampler_leaves_logits_and_limits(cuda):
+    lg = torch.randn(1000, device=cuda)
+    before = lg.clone()
+    tb.sample_logits(lg, 0.7, 40, 1.0, 1.5, [1, 2, 3])
+    assert torch.equal(lg, before)
+    with pytest.raises(tb.UnsupportedOpError, match="top_k"):
+        tb.sample_logits(lg, 0.7, 129)
+
+
+def test_sampler_seed_reproducible_and_distribution(cuda):
+    V = 64
+    g = np.random.default_rng(5)
+    lg = (g.standard_normal(V) * 1.5).astype(np.float32)
+    t = torch.from_numpy(lg).to(cuda)
+    a = [tb.sample_logits(t, 1.0, 16, 1.0, seed=7, counter=i) for i in range(400)]
+    b = [tb.sample_logits(t, 1.0, 16, 1.0, seed=7, counter=i) for i in range(400)]
+    assert a == b
+    order = sorted(range(V), key=lambda i: (-lg[i], i))[:16]
+    p = np.exp(lg[order].astype(np.float64) - lg[order[0]])
+    p /= p.sum()
+    freq = np.array([a.count(o) for o in order]) / len(a)
+    assert set(a) <= set(order)
+    assert np.abs(freq - p).max() < 0.08

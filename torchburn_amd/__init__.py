@@ -7,6 +7,7 @@ meaning and error behaviour.
 """
 from ._lib import UnsupportedOpError
 from .decoder import RustQwenDecoder, create_rust_qwen_decoder
+from .sampling import sample_logits, sample_uniform
 from .quantization import (
     QuantizedLinear,
     fused_attention_step,
@@ -58,4 +59,6 @@ __all__ = [
     "pack_rows_w4a32_group64_v1_to_v2",
     "set_vnni_semantics",
     "unpack_rows_w4a32_group64_v2_to_v1",
+    "sample_logits",
+    "sample_uniform",
 ]

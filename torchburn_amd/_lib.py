@@ -46,6 +46,8 @@ _SIGS = {
     "tb_quantize_weight_int4_grouped": [_p, _p, _p, _i64, _i64, _i64, _p],
     "tb_quantize_weight_int8": [_p, _p, _p, _i64, _i64, _p],
     "tb_unpack_rows_w4a32_group64_v2_to_v1": [_p, _p, _p, _i64, _i64, _p],
+    "tb_sample_logits": [_p, _i64, C.c_float, _i64, C.c_float, C.c_float, _p, _i64,
+                         C.c_uint64, C.c_uint64, _p, _p, _p],
     "tb_swiglu_w4a32": [_p] * 8 + [_i64] * 4 + [_p],
     "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
     "tb_w8a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
@@ -62,7 +64,8 @@ _SIGS = {
 
 def declared_symbols() -> list:
     """Every entry point the Python layer binds (all are declared in include/tbhip.h)."""
-    return ["tb_last_error", "tb_version", "tb_x_records_bytes", *_SIGS.keys()]
+    return ["tb_last_error", "tb_version", "tb_x_records_bytes", "tb_sample_uniform",
+            *_SIGS.keys()]
 
 
 def lib():
@@ -80,6 +83,8 @@ def lib():
             L.tb_version.restype = C.c_char_p
             L.tb_x_records_bytes.restype = C.c_int64
             L.tb_x_records_bytes.argtypes = [C.c_int64, C.c_int64]
+            L.tb_sample_uniform.restype = C.c_float
+            L.tb_sample_uniform.argtypes = [C.c_uint64, C.c_uint64]
             for name, args in _SIGS.items():
                 fn = getattr(L, name)
                 fn.argtypes = args

@@ -4,8 +4,10 @@
 // (src/quantization/packed_v2.rs:565-596) and returns TB_ERR_UNSUPPORTED with
 // the reference's "TB_UNSUPPORTED:" marker, which the Python layer maps to
 // UnsupportedOpError.
+#include <math.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include <mutex>
@@ -18,6 +20,7 @@
 #include "w4_mfma.hpp"
 #include "v2_layout.hpp"
 #include "quantize.hpp"
+#include "sample.hpp"
 
 namespace tb {
 
@@ -338,6 +341,60 @@ int tb_unpack_rows_w4a32_group64_v2_to_v1(const uint8_t *w_blocked, uint8_t *w_p
                TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: unpack_rows_w4a32_group64_v2_to_v1: misaligned device pointer");
     return unpack_v2_to_v1(w_blocked, w_packed, scales, n, k, (hipStream_t)stream);
+}
+
+float tb_sample_uniform(uint64_t seed, uint64_t counter) { return sample_uniform(seed, counter); }
+
+int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t top_k, float top_p,
+                     float repetition_penalty, const int64_t *recent, int64_t n_recent,
+                     uint64_t seed, uint64_t counter, int64_t *token_out, float *u_out,
+                     void *stream) {
+    TB_REQUIRE(logits && token_out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: sample_logits: null pointer");
+    TB_REQUIRE(vocab > 0 && vocab <= (int64_t)kSampleMaxBlocks * kSampleSlice, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: sample_logits: vocabulary of " + std::to_string(vocab) +
+                   " outside 1.." + std::to_string(kSampleMaxBlocks * kSampleSlice));
+    TB_REQUIRE(n_recent <= 0 || recent, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: sample_logits: null recent tokens");
+    // decoder.rs:919-931: greedy when the temperature is not usable or top_k == 1
+    const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
+    const int64_t k = greedy ? 1 : std::max<int64_t>(1, std::min<int64_t>(top_k, vocab));
+    TB_REQUIRE(k <= kSampleMaxK, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: device sampling takes top_k <= " + std::to_string(kSampleMaxK));
+    SampleParams prm{};
+    prm.temperature = temperature;
+    prm.top_p = top_p;
+    prm.penalty = repetition_penalty;
+    prm.k = (int)k;
+    prm.greedy = greedy ? 1 : 0;
+    prm.seed = seed;
+    prm.counter = counter;
+    const size_t cand = (size_t)kSampleCand;
+    const size_t bytes = up256(sizeof(SampleParams)) + up256(sizeof(SampleOut)) +
+                         up256(cand * 4) + up256(cand * 4) + up256(kSampleMaxBlocks * 4);
+    void *ws = nullptr;
+    int rc = workspace(bytes, &ws);
+    if (rc) return rc;
+    char *w = static_cast<char *>(ws);
+    SampleParams *dprm = reinterpret_cast<SampleParams *>(w);
+    w += up256(sizeof(SampleParams));
+    SampleOut *dout = reinterpret_cast<SampleOut *>(w);
+    w += up256(sizeof(SampleOut));
+    SampleScratch sc;
+    sc.key = reinterpret_cast<uint32_t *>(w);
+    w += up256(cand * 4);
+    sc.idx = reinterpret_cast<int *>(w);
+    w += up256(cand * 4);
+    sc.cnt = reinterpret_cast<int *>(w);
+    hipStream_t st = (hipStream_t)stream;
+    TB_HIP(hipMemcpyAsync(dprm, &prm, sizeof(prm), hipMemcpyHostToDevice, st));
+    rc = launch_sample(logits, (int)vocab, recent, (int)n_recent, dprm, sc, dout, st);
+    if (rc) return rc;
+    SampleOut ho{};
+    TB_HIP(hipMemcpyAsync(&ho, dout, sizeof(ho), hipMemcpyDeviceToHost, st));
+    TB_HIP(hipStreamSynchronize(st));
+    *token_out = ho.token;
+    if (u_out) *u_out = ho.u;
+    return TB_OK;
 }
 
 int tb_set_vnni_semantics(int enabled) {

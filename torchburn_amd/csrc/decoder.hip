@@ -30,6 +30,7 @@
 #include "w4_gemv.hpp"
 #include "w4_mfma.hpp"
 #include "v2_layout.hpp"
+#include "sample.hpp"
 
 struct tb_decoder;
 
@@ -85,11 +86,26 @@ struct Decoder {
     hipGraphExec_t exec = nullptr;
     int64_t kv_used = 0;
     std::vector<float> host_logits;
-    std::mt19937_64 rng{0x7B};
+    std::mt19937_64 rng{0x7B};   // host sampler (top_k beyond the device sampler's range)
+
+    // Device sampler: parameters, result, candidates, the generation loop's
+    // recent-token window, the decode_and_sample recent list, and the step
+    // graph whose tail samples instead of taking the argmax.
+    SampleParams *sprm = nullptr;
+    SampleOut *sout = nullptr;
+    SampleWindow *swin = nullptr;
+    SampleScratch sws{};
+    int64_t *srec = nullptr;
+    int64_t srec_cap = 0;
+    uint64_t seed = 0x7B, draws = 0;
+    hipGraph_t graph_s = nullptr;
+    hipGraphExec_t exec_s = nullptr;
 
     ~Decoder() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
+        if (exec_s) (void)hipGraphExecDestroy(exec_s);
+        if (graph_s) (void)hipGraphDestroy(graph_s);
         if (st) (void)hipStreamSynchronize(st);
         for (void *p : allocs) (void)hipFree(p);
         if (hstate) (void)hipHostFree(hstate);
@@ -98,15 +114,43 @@ struct Decoder {
         if (st) (void)hipStreamDestroy(st);
     }
 
-    template <class T>
-    int alloc(T **p, size_t bytes) {
-        void *q = nullptr;
-        hipError_t e = hipMalloc(&q, bytes < 256 ? 256 : bytes);
+    // Device memory.  Buffers under kArena / 4 are carved (256-byte aligned)
+    // from arenas of kArena bytes, larger ones get their own allocation: the
+    // decoder's hundreds of per-layer tensors then sit in a few large mappings
+    // instead of one allocation each, whatever the process allocated before.
+    static constexpr size_t kArena = (size_t)256 << 20;
+    char *arena = nullptr;
+    size_t arena_left = 0;
+
+    int raw_alloc(void **q, size_t bytes) {
+        hipError_t e = hipMalloc(q, bytes);
         if (e != hipSuccess)
             return fail(e == hipErrorOutOfMemory ? TB_ERR_MEMORY : TB_ERR_HIP,
                         "Out of memory allocating " + std::to_string(bytes >> 20) +
                             " MB for the decoder on the GPU: " + hipGetErrorString(e));
-        allocs.push_back(q);
+        allocs.push_back(*q);
+        return TB_OK;
+    }
+
+    template <class T>
+    int alloc(T **p, size_t bytes) {
+        bytes = (bytes + 255) & ~(size_t)255;
+        if (bytes == 0) bytes = 256;
+        void *q = nullptr;
+        int rc;
+        if (bytes >= kArena / 4) {
+            if ((rc = raw_alloc(&q, bytes))) return rc;
+        } else {
+            if (bytes > arena_left) {
+                void *a = nullptr;
+                if ((rc = raw_alloc(&a, kArena))) return rc;
+                arena = static_cast<char *>(a);
+                arena_left = kArena;
+            }
+            q = arena;
+            arena += bytes;
+            arena_left -= bytes;
+        }
         *p = static_cast<T *>(q);
         return TB_OK;
     }
@@ -191,7 +235,14 @@ struct Decoder {
     // gate/up, lm_head) scales its dots by 1 / rms.  h's records come from
     // the gate/up epilogue.  Kernels per layer: QKV, attention (split +
     // merge), O, gate/up, down.
-    int enqueue_step_fused() {
+    // The step's tail: greedy argmax, or the device sampler over the window.
+    int enqueue_tail(bool sampled) {
+        if (!sampled) return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
+        return launch_sample(logits, V, nullptr, 0, sprm, sws, sout, st, swin, state, history,
+                             hist_cap);
+    }
+
+    int enqueue_step_fused(bool sampled) {
         int rc = launch_embed_rec(state, embed, x, layers[0].in_norm, xn, xq_h, ssq, H, st);
         if (rc) return rc;
         for (int l = 0; l < L; ++l) {
@@ -242,13 +293,13 @@ struct Decoder {
                       V, H, EPI_PLAIN);
         }
         if (rc) return rc;
-        return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
+        return enqueue_tail(sampled);
     }
 
     // Enqueues one decoder step (reference step_internal) on `st`.
-    int enqueue_step() {
+    int enqueue_step(bool sampled = false) {
         const bool q4 = wbits == 4;
-        if (q4 && fused) return enqueue_step_fused();
+        if (q4 && fused) return enqueue_step_fused(sampled);
         int rc;
         for (int l = 0; l < L; ++l) {
             const Layer &y = layers[l];
@@ -288,16 +339,15 @@ struct Decoder {
         rc = proj(lmbits, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V, H,
                   EPI_PLAIN);
         if (rc) return rc;
-        return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
+        return enqueue_tail(sampled);
     }
 
-    int ensure_graph() {
-        if (exec) return TB_OK;
+    int capture(bool sampled, hipGraph_t *gr, hipGraphExec_t *ex) {
         for (int l = 0; l < L; ++l)
             TB_REQUIRE(layers[l].set, TB_ERR_VALUE,
                        "decoder layer " + std::to_string(l) + " was never set");
         TB_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        int rc = enqueue_step();
+        int rc = enqueue_step(sampled);
         hipGraph_t g = nullptr;
         hipError_t e = hipStreamEndCapture(st, &g);
         if (rc) {
@@ -305,9 +355,85 @@ struct Decoder {
             return rc;
         }
         if (e != hipSuccess) return fail(TB_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(e));
-        graph = g;
-        TB_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        *gr = g;
+        TB_HIP(hipGraphInstantiate(ex, g, nullptr, nullptr, 0));
         return TB_OK;
+    }
+
+    int ensure_graph() { return exec ? TB_OK : capture(false, &graph, &exec); }
+
+    // ---- Device sampling -----------------------------------------------------
+    int sampler_alloc() {
+        if (sprm) return TB_OK;
+        int rc;
+        if ((rc = alloc(&sprm, sizeof(SampleParams))) || (rc = alloc(&sout, sizeof(SampleOut))) ||
+            (rc = alloc(&swin, sizeof(SampleWindow))) ||
+            (rc = alloc(&sws.key, (size_t)kSampleCand * 4)) ||
+            (rc = alloc(&sws.idx, (size_t)kSampleCand * 4)) ||
+            (rc = alloc(&sws.cnt, (size_t)kSampleMaxBlocks * 4)))
+            return rc;
+        return TB_OK;
+    }
+
+    int ensure_graph_s() {
+        int rc = sampler_alloc();
+        if (rc) return rc;
+        return exec_s ? TB_OK : capture(true, &graph_s, &exec_s);
+    }
+
+    // Upload of the sampling parameters (the draw counter continues the stream).
+    int set_sampler(float temperature, int64_t top_k, float top_p, float penalty) {
+        int rc = sampler_alloc();
+        if (rc) return rc;
+        const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
+        SampleParams p{};
+        p.temperature = temperature;
+        p.top_p = top_p;
+        p.penalty = penalty;
+        p.k = greedy ? 1 : (int)std::max<int64_t>(1, std::min<int64_t>(top_k, V));
+        p.greedy = greedy ? 1 : 0;
+        p.seed = seed;
+        p.counter = draws;
+        TB_HIP(hipMemcpyAsync(sprm, &p, sizeof(p), hipMemcpyHostToDevice, st));
+        return TB_OK;
+    }
+
+    // The draw counter after device draws, and the drawn token.
+    int sampler_result(int64_t *token) {
+        SampleParams p{};
+        SampleOut o{};
+        TB_HIP(hipMemcpyAsync(&p, sprm, sizeof(p), hipMemcpyDeviceToHost, st));
+        TB_HIP(hipMemcpyAsync(&o, sout, sizeof(o), hipMemcpyDeviceToHost, st));
+        TB_HIP(hipStreamSynchronize(st));
+        draws = p.counter;
+        if (token) *token = o.token;
+        return TB_OK;
+    }
+
+    bool device_samplable(float temperature, int64_t top_k) const {
+        const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
+        const int64_t k = greedy ? 1 : std::max<int64_t>(1, std::min<int64_t>(top_k, V));
+        return k <= kSampleMaxK && V <= kSampleMaxBlocks * kSampleSlice;
+    }
+
+    // decode_and_sample on the device: one step, then the sampler over the
+    // logits with the caller's recent tokens.
+    int step_and_sample(int64_t token, int64_t pos, float temperature, int64_t top_k, float top_p,
+                        float penalty, const int64_t *recent, int64_t n_recent, int64_t *out) {
+        int rc = step(token, pos, false, nullptr);
+        if (rc) return rc;
+        if ((rc = set_sampler(temperature, top_k, top_p, penalty))) return rc;
+        if (penalty > 1.0f && n_recent > 0) {
+            if (n_recent > srec_cap) {
+                if ((rc = alloc(&srec, (size_t)n_recent * 8))) return rc;
+                srec_cap = n_recent;
+            }
+            TB_HIP(hipMemcpyAsync(srec, recent, (size_t)n_recent * 8, hipMemcpyHostToDevice, st));
+        }
+        if ((rc = launch_sample(logits, V, srec, penalty > 1.0f ? (int)n_recent : 0, sprm, sws,
+                                sout, st)))
+            return rc;
+        return sampler_result(out);
     }
 
     int set_state(int token, int pos) {
@@ -703,10 +829,100 @@ int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t offset, f
     const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
     if (greedy && (repetition_penalty <= 1.0f || n_recent <= 0))
         return d->step(token, offset, false, token_out);
+    if (d->device_samplable(temperature, top_k))
+        return d->step_and_sample(token, offset, temperature, top_k, top_p, repetition_penalty,
+                                  recent, n_recent, token_out);
     int rc = d->step(token, offset, true, nullptr);
     if (rc) return rc;
     tb::repetition_penalty(d->host_logits, recent, n_recent, repetition_penalty);
     *token_out = tb::sample(d->host_logits, temperature, top_k, top_p, d->rng);
+    return TB_OK;
+}
+
+int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_len,
+                                int64_t max_new_tokens, float temperature, int64_t top_k,
+                                float repetition_penalty, float top_p, int64_t eos_token_id,
+                                const int64_t *recent_seed, int64_t n_seed, int64_t *tokens_out,
+                                int64_t *n_out, int64_t *seq_len_out) {
+    TB_REQUIRE(d && tokens_out && n_out && seq_len_out, TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(seq_len >= 0 && max_new_tokens >= 0, TB_ERR_VALUE, "negative length");
+    TB_REQUIRE(n_seed <= 0 || recent_seed, TB_ERR_VALUE, "null recent_seed");
+    const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
+    if (greedy && repetition_penalty <= 1.0f)
+        return tb_decoder_generate(d, first_token, seq_len, max_new_tokens, eos_token_id,
+                                   tokens_out, n_out, seq_len_out);
+    // generate_loop (decoder.rs:788-832) with its 64-token window (859-876):
+    // push the token, decode it at seq_len + generated - 1, sample the next.
+    std::vector<int64_t> win(recent_seed, recent_seed + std::max<int64_t>(n_seed, 0));
+    auto push = [&](int64_t t) {
+        win.push_back(t);
+        if ((int64_t)win.size() > kSampleWindow) win.erase(win.begin(), win.end() - kSampleWindow);
+    };
+    int64_t n = 0, next = first_token;
+    int rc;
+    if (!d->device_samplable(temperature, top_k)) {
+        while (n < max_new_tokens) {   // host sampler
+            if (eos_token_id >= 0 && next == eos_token_id) break;
+            tokens_out[n++] = next;
+            push(next);
+            if ((rc = d->step(next, seq_len + n - 1, true, nullptr))) return rc;
+            tb::repetition_penalty(d->host_logits, win.data(), (int64_t)win.size(),
+                                   repetition_penalty);
+            next = tb::sample(d->host_logits, temperature, top_k, top_p, d->rng);
+        }
+    } else {
+        if ((rc = d->ensure_graph_s()) || (rc = d->set_sampler(temperature, top_k, top_p,
+                                                               repetition_penalty)))
+            return rc;
+        SampleWindow hw{};
+        const int64_t w0 = std::min<int64_t>((int64_t)win.size(), kSampleWindow);
+        hw.n = (int)w0;
+        for (int64_t i = 0; i < w0; ++i) hw.tok[i] = win[win.size() - w0 + i];
+        TB_HIP(hipMemcpyAsync(d->swin, &hw, sizeof(hw), hipMemcpyHostToDevice, d->st));
+        // Steps inside the cache replay the sampling graph (window push,
+        // penalty, draw and the next token all on the device); with an EOS
+        // token each step's token is read back before the next.
+        const int64_t valid = d->in_range(first_token, seq_len)
+                                  ? std::min<int64_t>(max_new_tokens, d->max_seq - seq_len)
+                                  : 0;
+        if (valid > 0) {
+            if ((rc = d->set_state((int)first_token, (int)seq_len))) return rc;
+            if (eos_token_id < 0) {
+                for (int64_t i = 0; i < valid; ++i) TB_HIP(hipGraphLaunch(d->exec_s, d->st));
+                std::vector<int> hist((size_t)valid);
+                TB_HIP(hipMemcpyAsync(hist.data(), d->history, (size_t)valid * 4,
+                                      hipMemcpyDeviceToHost, d->st));
+                if ((rc = d->sampler_result(nullptr))) return rc;
+                for (int64_t i = 0; i < valid; ++i) {
+                    tokens_out[n++] = next;
+                    next = hist[(size_t)i];
+                }
+            } else {
+                while (n < valid && next != eos_token_id) {
+                    tokens_out[n++] = next;
+                    TB_HIP(hipGraphLaunch(d->exec_s, d->st));
+                    if ((rc = d->sampler_result(&next))) return rc;
+                }
+            }
+            d->kv_used = std::max<int64_t>(d->kv_used, seq_len + n);
+            // the device window now ends with the last decoded token
+            const int64_t used = n;
+            for (int64_t i = 0; i < used; ++i) push(tokens_out[i]);
+        }
+        // Positions past the cache: zeroed logits (decoder.rs:1066-1089), then
+        // the penalty and the draw as for any step.
+        while (n < max_new_tokens) {
+            if (eos_token_id >= 0 && next == eos_token_id) break;
+            tokens_out[n++] = next;
+            push(next);
+            if ((rc = d->step_and_sample(next, seq_len + n - 1, temperature, top_k, top_p,
+                                         repetition_penalty, win.data(), (int64_t)win.size(),
+                                         &next)))
+                return rc;
+        }
+    }
+    *n_out = n;
+    *seq_len_out = seq_len + n;
     return TB_OK;
 }
 
@@ -829,6 +1045,8 @@ int tb_decoder_get_logits(tb_decoder *d, float *out) {
 int tb_decoder_set_seed(tb_decoder *d, uint64_t seed) {
     TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
     d->rng.seed(seed);
+    d->seed = seed;
+    d->draws = 0;
     return TB_OK;
 }
 

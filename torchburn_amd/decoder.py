@@ -40,6 +40,8 @@ def _bind():
         "tb_decoder_decode_and_sample": [p, i64, i64, C.c_float, i64, C.c_float, p, i64,
                                          C.c_float, C.POINTER(i64)],
         "tb_decoder_generate": [p, i64, i64, i64, i64, p, C.POINTER(i64), C.POINTER(i64)],
+        "tb_decoder_generate_sampled": [p, i64, i64, i64, C.c_float, i64, C.c_float, C.c_float,
+                                        i64, p, i64, p, C.POINTER(i64), C.POINTER(i64)],
         "tb_decoder_prefill": [p, p, i64, i64, C.POINTER(i64)],
         "tb_decoder_reset_kv": [p],
         "tb_decoder_copy_kv": [p, i64, p, p, i64, i64],
@@ -170,30 +172,24 @@ class RustQwenDecoder:
                       repetition_penalty: float = 1.0, top_p: float = 1.0,
                       eos_token_id: Optional[int] = None,
                       recent_seed: Optional[Sequence[int]] = None) -> Tuple[List[int], int]:
-        """Whole decode loop in one call (decoder.rs:788-832)."""
+        """Whole decode loop in one call (decoder.rs:788-832).  Sampling with
+        top_k <= 128 runs on the device (see tb_decoder_generate_sampled)."""
+        toks = np.empty(max(int(max_new_tokens), 1), np.int64)
+        n, sl = C.c_int64(), C.c_int64()
+        eos = -1 if eos_token_id is None else int(eos_token_id)
         greedy = not np.isfinite(temperature) or temperature <= 0 or top_k == 1
         if greedy and repetition_penalty <= 1.0:
-            toks = np.empty(max(int(max_new_tokens), 1), np.int64)
-            n, sl = C.c_int64(), C.c_int64()
             _lib.check(_bind().tb_decoder_generate(
-                self._h, int(first_token), int(seq_len), int(max_new_tokens),
-                -1 if eos_token_id is None else int(eos_token_id), toks.ctypes.data,
-                C.byref(n), C.byref(sl)))
-            return toks[:n.value].tolist(), int(sl.value)
-        tokens: List[int] = []
-        recent = list(recent_seed or [])
-        nxt, generated = int(first_token), 0
-        while generated < max_new_tokens:
-            if eos_token_id is not None and nxt == eos_token_id:
-                break
-            tokens.append(nxt)
-            generated += 1
-            recent.append(nxt)
-            if len(recent) > RECENT_WINDOW:
-                del recent[:len(recent) - RECENT_WINDOW]
-            nxt = self.decode_and_sample(nxt, seq_len + generated - 1, temperature, top_k,
-                                         repetition_penalty, recent, top_p)
-        return tokens, seq_len + generated
+                self._h, int(first_token), int(seq_len), int(max_new_tokens), eos,
+                toks.ctypes.data, C.byref(n), C.byref(sl)))
+        else:
+            seed_ids = np.asarray(list(recent_seed or []), dtype=np.int64)
+            _lib.check(_bind().tb_decoder_generate_sampled(
+                self._h, int(first_token), int(seq_len), int(max_new_tokens), float(temperature),
+                int(top_k), float(repetition_penalty), float(top_p), eos,
+                seed_ids.ctypes.data if seed_ids.size else None, seed_ids.size,
+                toks.ctypes.data, C.byref(n), C.byref(sl)))
+        return toks[:n.value].tolist(), int(sl.value)
 
     def prefill_tokens(self, tokens: Sequence[int], start_offset: int) -> int:
         arr = np.asarray(list(tokens), dtype=np.int64)
