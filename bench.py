@@ -314,6 +314,7 @@ def decode_run(torch, name, steps, prefill_tokens=0):
     ms = dec.time_greedy(first, kvlen, steps)
     pre = prefill_run(dec, cfg, prefill_tokens) if prefill_tokens and wk == 4 else None
     sampled = sampled_run(dec, first, kvlen, steps) if name in ("llama4", "qwen64") else None
+    verify = verify_run(dec, cfg, kvlen) if name == "llama4" else None
     dec.close()
     torch.cuda.empty_cache()
     byts = sum(synth.decode_bytes_per_token(cfg, kvlen + i, wk, lk, gs, v2=name == "qwen64")
@@ -327,7 +328,27 @@ def decode_run(torch, name, steps, prefill_tokens=0):
         out["prefill"] = pre
     if sampled:
         out["sampled"] = sampled
+    if verify:
+        out["verify"] = verify
     return out
+
+
+def verify_run(dec, cfg, kvlen, k=5):
+    """verify_tokens of k draft positions as one batched forward against k
+    single steps with logits (the reference's loop), wall clock of the C calls
+    incl. the logits read back into host arrays (Python list conversion, which
+    the reference's API also pays, excluded from both)."""
+    toks = [int(t) for t in np.random.default_rng(3).integers(0, cfg["vocab"], k)]
+    dec._verify(kvlen, toks)                             # warm-up
+    t0 = time.perf_counter()
+    dec._verify(kvlen, toks)
+    batched = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for i, t in enumerate(toks):
+        dec._step(t, kvlen + i, True)
+    stepped = time.perf_counter() - t0
+    return {"positions": k, "batched_ms": round(batched * 1e3, 3),
+            "stepped_ms": round(stepped * 1e3, 3)}
 
 
 def sampled_run(dec, first, kvlen, steps):

@@ -369,6 +369,33 @@ TB_API int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64
                                        int64_t n_seed, int64_t *tokens_out, int64_t *n_out,
                                        int64_t *seq_len_out);
 
+/* verify_tokens (decoder.rs:565-581): logits_out (host [n, vocab]) receives the
+ * logits of every position start_offset + i, the KV cache gains the n rows.  An
+ * INT4 decoder runs the n positions as one batched forward (the prefill path,
+ * lm_head on every row); TB_ERR_VALUE when start_offset + n > max_seq_len. */
+TB_API int tb_decoder_verify(tb_decoder *d, int64_t start_offset, const int64_t *tokens,
+                             int64_t n, float *logits_out);
+
+/* speculative_accept (decoder.rs:588-727): verify the k draft tokens at
+ * `offset` (tb_decoder_verify), then Leviathan acceptance against draft_probs
+ * (host [k, vocab] row-major) with the uniforms of the decoder's seeded stream
+ * (tb_spec_uniform(seed, draw), draws continuing after tb_decoder_set_seed;
+ * the reference seeds from the clock).  k == 0 gives (0, vocab - 1). */
+TB_API int tb_decoder_speculative_accept(tb_decoder *d, int64_t offset,
+                                         const int64_t *draft_tokens, int64_t k,
+                                         const float *draft_probs, float temperature, float top_p,
+                                         int64_t *accepted, int64_t *bonus);
+
+/* The acceptance of speculative_accept over given target logits rows (host
+ * [k, vocab]) and uniforms u[0..n_u) (at most k + 1 are used, in order). */
+TB_API int tb_speculative_accept_rows(const float *target_rows, const int64_t *draft_tokens,
+                                      const float *draft_probs, int64_t k, int64_t vocab,
+                                      float temperature, float top_p, const double *u,
+                                      int64_t n_u, int64_t *accepted, int64_t *bonus);
+
+/* The f64 uniform in [0, 1) (53 bits) of draw `counter` under `seed`. */
+TB_API double tb_spec_uniform(uint64_t seed, uint64_t counter);
+
 /* prefill_tokens (decoder.rs:431-447): TB_ERR_VALUE when start_offset + n >
  * max_seq_len. */
 TB_API int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n,

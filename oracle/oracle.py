@@ -91,6 +91,8 @@ def lib():
         L.orc_sample_logits.argtypes = [_f32p, _i64, C.c_float, _i64, C.c_float, C.c_float,
                                         C.POINTER(_i64)]
         L.orc_sample_logits.restype = _i64
+        L.orc_speculative_accept.argtypes = [_vp, _vp, _vp, _i64, _i64, C.c_float, C.c_float,
+                                             _vp, _i64, C.POINTER(_i64), C.POINTER(_i64)]
         _lib = L
     return _lib
 
@@ -234,6 +236,19 @@ def sample_logits(logits, temperature, top_k, top_p, u):
     tok = lib().orc_sample_logits(lg, lg.size, float(temperature), int(top_k), float(top_p),
                                   float(u), C.byref(kept))
     return int(tok), int(kept.value)
+
+
+def speculative_accept(rows, draft, draft_probs, u, temperature=1.0, top_p=1.0):
+    """(accepted, bonus) of speculative_accept's acceptance (decoder.rs:608-726)."""
+    rows = _c(rows, np.float32)
+    k, v = rows.shape
+    d = np.ascontiguousarray(np.asarray(list(draft), dtype=np.int64))
+    dp = _c(draft_probs, np.float32).reshape(-1)
+    uu = np.ascontiguousarray(np.asarray(list(u), dtype=np.float64))
+    a, b = _i64(), _i64()
+    lib().orc_speculative_accept(_p(rows), _p(d), _p(dp), k, v, float(temperature), float(top_p),
+                                 _p(uu) if uu.size else None, uu.size, C.byref(a), C.byref(b))
+    return int(a.value), int(b.value)
 
 
 def swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None, group_size=32):

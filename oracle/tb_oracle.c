@@ -740,6 +740,113 @@ ORC_API int64_t orc_sample_logits(const float *logits, int64_t V, float temperat
     return tok;
 }
 
+/* speculative_accept's acceptance, decoder.rs:608-726, over target rows     */
+/* [K, V] and draft_probs [K, V] with the uniforms u[] consumed in order:     */
+/* per position the temperature softmax (non-finite -> -inf, sum clamped at  */
+/* 1e-30), accept while u <= min(p_t[d] / (p_d[d] + 1e-12), 1); on reject    */
+/* the bonus is drawn from max(0, p_t - p_d) in index order (argmax of p_t   */
+/* when its mass is <= 1e-12); all accepted: the bonus from the last row's   */
+/* distribution by probability (ties: lower index), nucleus-cut at top_p.    */
+static void orc_softmax_t(const float *lg, int64_t V, float temp, float *p) {
+    float t = (isfinite(temp) && temp > 0.f) ? temp : 1.0f, m = -INFINITY, s = 0.f;
+    for (int64_t j = 0; j < V; ++j) {
+        float v = isfinite(lg[j]) ? lg[j] : -INFINITY;
+        m = v > m ? v : m;
+    }
+    for (int64_t j = 0; j < V; ++j) {
+        p[j] = expf(((isfinite(lg[j]) ? lg[j] : -INFINITY) - m) / t);
+        s += p[j];
+    }
+    float inv = 1.0f / (s > 1e-30f ? s : 1e-30f);
+    for (int64_t j = 0; j < V; ++j) p[j] *= inv;
+}
+
+static const float *g_sort_p;
+static int prob_desc(const void *a, const void *b) {
+    int64_t x = *(const int64_t *)a, y = *(const int64_t *)b;
+    if (g_sort_p[x] > g_sort_p[y]) return -1;
+    if (g_sort_p[x] < g_sort_p[y]) return 1;
+    return x < y ? -1 : (x > y);
+}
+
+ORC_API void orc_speculative_accept(const float *rows, const int64_t *draft, const float *dp,
+                                    int64_t K, int64_t V, float temperature, float top_p,
+                                    const double *u, int64_t n_u, int64_t *accepted,
+                                    int64_t *bonus) {
+    int64_t ui = 0;
+#define NEXT_U() (ui < n_u ? u[ui++] : 0.0)
+    *accepted = 0;
+    *bonus = V - 1;
+    if (K == 0) return;
+    float *tp = (float *)malloc((size_t)V * sizeof(float));
+    for (int64_t i = 0; i < K; ++i) {
+        orc_softmax_t(rows + i * V, V, temperature, tp);
+        int64_t d = draft[i] < 0 ? 0 : (draft[i] > V - 1 ? V - 1 : draft[i]);
+        float pt = tp[d], pd = dp[i * V + d] > 0.f ? dp[i * V + d] : 0.f;
+        float acc = pt / (pd + 1e-12f);
+        if (acc > 1.f) acc = 1.f;
+        if (NEXT_U() <= (double)acc) {
+            *accepted += 1;
+            continue;
+        }
+        float sc = 0.f;
+        for (int64_t j = 0; j < V; ++j) {
+            float c = tp[j] - dp[i * V + j];
+            sc += c > 0.f ? c : 0.f;
+        }
+        if (sc > 1e-12f) {
+            float r = (float)NEXT_U() * sc, a = 0.f;
+            *bonus = V - 1;
+            for (int64_t j = 0; j < V; ++j) {
+                float c = tp[j] - dp[i * V + j];
+                a += c > 0.f ? c : 0.f;
+                if (a >= r) {
+                    *bonus = j;
+                    break;
+                }
+            }
+        } else {
+            int64_t bj = 0;
+            for (int64_t j = 1; j < V; ++j)
+                if (tp[j] > tp[bj]) bj = j;
+            *bonus = bj;
+        }
+        free(tp);
+        return;
+    }
+    orc_softmax_t(rows + (K - 1) * V, V, temperature, tp);
+    int64_t *idx = (int64_t *)malloc((size_t)V * sizeof(int64_t));
+    for (int64_t j = 0; j < V; ++j) idx[j] = j;
+    g_sort_p = tp;
+    qsort(idx, (size_t)V, sizeof(int64_t), prob_desc);
+    int64_t kept = V;
+    if (top_p > 0.f && top_p < 1.f) {
+        float cum = 0.f;
+        for (int64_t i = 0; i < V; ++i) {
+            if (cum > top_p) {
+                kept = i;
+                break;
+            }
+            cum += tp[idx[i]];
+        }
+        if (kept < 1) kept = 1;
+    }
+    float mass = 0.f;
+    for (int64_t i = 0; i < kept; ++i) mass += tp[idx[i]];
+    float r = (float)NEXT_U() * (mass > 1e-30f ? mass : 1e-30f), a = 0.f;
+    *bonus = idx[kept - 1];
+    for (int64_t i = 0; i < kept; ++i) {
+        a += tp[idx[i]];
+        if (a >= r) {
+            *bonus = idx[i];
+            break;
+        }
+    }
+#undef NEXT_U
+    free(idx);
+    free(tp);
+}
+
 /* ------------------------------------------------------------------------ */
 /* a16: RustQwenDecoder::step_internal, decoder.rs:1051-1374.                 */
 /* The oracle borrows every weight pointer (the caller keeps them alive) and */

@@ -87,3 +87,59 @@ def test_repetition_penalty_closed_form():
     out = O.repetition_penalty(lg, [0, 1, 0, 9, -1, 4, 1], 2.0)
     assert list(out) == [1.0, -2.0, 0.0, 4.0, -6.0]
     assert np.array_equal(O.repetition_penalty(lg, [0, 1], 1.0), lg)
+
+
+# ---------------------------------------------------------- speculative ---
+
+def softmax64(row, T=1.0):
+    r = np.where(np.isfinite(row), row, -np.inf).astype(np.float64) / T
+    e = np.exp(r - r.max())
+    return e / e.sum()
+
+
+def test_speculative_accept_rules():
+    """Closed forms of decoder.rs:608-726: a draft token the target rates at
+    least as likely is always accepted; a rejection draws from the normalised
+    max(0, p_t - p_d); all accepted draws the bonus from the last row."""
+    g = np.random.default_rng(11)
+    V, K = 50, 3
+    rows = (g.standard_normal((K, V)) * 2).astype(np.float32)
+    pt = [softmax64(r) for r in rows]
+    draft = [int(np.argmax(p)) for p in pt]
+    dp = np.zeros((K, V), np.float32)
+    for i in range(K):
+        dp[i, draft[i]] = np.float32(pt[i][draft[i]] * 0.5)   # p_t >= p_d: always accepted
+    acc, _ = O.speculative_accept(rows, draft, dp, [0.999999] * (K + 1))
+    assert acc == K
+    # all accepted: the bonus distribution over u is the last row's softmax
+    grid = (np.arange(4000) + 0.5) / 4000
+    cnt = np.zeros(V)
+    for uu in grid:
+        cnt[O.speculative_accept(rows, draft, dp, [0.0] * K + [uu])[1]] += 1
+    assert np.abs(cnt / grid.size - pt[-1]).max() < 1e-3
+    # rejection at position 1: the bonus distribution is max(0, p_t - p_d)
+    dp2 = np.full((K, V), 1.0 / V, np.float32)
+    dp2[1, draft[1]] = 1.0                  # draft far more confident than the target
+    c = np.maximum(pt[1] - dp2[1].astype(np.float64), 0)
+    c /= c.sum()
+    cnt = np.zeros(V)
+    for uu in grid:
+        a, b = O.speculative_accept(rows, draft, dp2, [0.0, 0.999999, uu])
+        assert a == 1
+        cnt[b] += 1
+    assert np.abs(cnt / grid.size - c).max() < 1e-3
+    # acceptance threshold p_t / p_d: u just above rejects, just below accepts
+    ratio = pt[1][draft[1]] / (1.0 + 1e-12)
+    assert O.speculative_accept(rows, draft, dp2, [0.0, ratio * 0.999, 0.5])[0] >= 2
+    assert O.speculative_accept(rows, draft, dp2, [0.0, ratio * 1.001, 0.5])[0] == 1
+
+
+def test_speculative_accept_nucleus_and_empty():
+    probs = np.array([0.5, 0.3, 0.2])
+    rows = np.log(probs).astype(np.float32)[None]
+    dp = np.zeros((1, 3), np.float32)
+    bon = {O.speculative_accept(rows, [0], dp, [0.0, uu], top_p=0.6)[1]
+           for uu in np.linspace(0, 0.999, 100)}
+    assert bon == {0, 1}
+    assert O.speculative_accept(np.zeros((0, 7), np.float32), [], np.zeros(0, np.float32),
+                                []) == (0, 6)

@@ -7,6 +7,8 @@
 // writes the next token and advances the position on the device.
 #include <float.h>
 
+#include <algorithm>
+
 #include "decode.hpp"
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
@@ -734,12 +736,19 @@ __global__ void k_rope_rows(const float *__restrict__ qkv, int nq, float *__rest
 // positions staged in LDS (zero past the last position the block needs);
 // 4 x 4 score micro-tiles per thread; online softmax with a running max and
 // sum per row, then 1 / max(sum, 1e-30).  out [M][hq * HD].
+//
+// Key-range split (blockIdx.z of nsplit, tps tiles each): with nsplit > 1 the
+// block writes its unnormalised o, running max and sum to part / pml and
+// k_prefill_merge combines the splits, so few query rows over a long cache
+// (verify_tokens, short chunks after a long prefix) still fill the chip.
 template <int HD>
 __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ q,
                                                       const float *__restrict__ kc,
                                                       const float *__restrict__ vc,
                                                       float *__restrict__ out, int start, int M,
-                                                      int hq, int hkv, int max_seq, float scale) {
+                                                      int hq, int hkv, int max_seq, float scale,
+                                                      int tps, float *__restrict__ part,
+                                                      float *__restrict__ pml) {
     constexpr int QT = 64, KT = 64, HP = HD + 4, OC = HD / 16;
     __shared__ __attribute__((aligned(16))) float sq[QT][HP];
     __shared__ __attribute__((aligned(16))) float sk[KT][HP];
@@ -764,8 +773,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
     }
     const int last = start + min(m0 + QT, M) - 1;   // last position any row of the block sees
     const int ntiles = last / KT + 1;
+    const int kt0 = blockIdx.z * tps, kt1 = min(ntiles, kt0 + tps);
     const float *kb = kc + (size_t)kvh * max_seq * HD, *vb = vc + (size_t)kvh * max_seq * HD;
-    for (int kt = 0; kt < ntiles; ++kt) {
+    for (int kt = kt0; kt < kt1; ++kt) {
         __syncthreads();
         for (int i = t; i < KT * (HD / 4); i += 256) {
             const int j = i / (HD / 4), c4 = i - j * (HD / 4);
@@ -847,6 +857,24 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             }
         }
     }
+    if (part) {   // one split of several: unnormalised o, max and sum
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 4 * rg + r;
+            if (m >= M) continue;
+            const size_t row = ((size_t)blockIdx.z * M + m) * hq + h;
+            float *dst = part + row * HD + kg * OC;
+#pragma unroll
+            for (int c = 0; c < OC; c += 4)
+                *reinterpret_cast<float4 *>(dst + c) =
+                    make_float4(o[r][c], o[r][c + 1], o[r][c + 2], o[r][c + 3]);
+            if (kg == 0) {
+                pml[row * 2] = mrun[r];
+                pml[row * 2 + 1] = lrun[r];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int m = m0 + 4 * rg + r;
@@ -858,6 +886,28 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             *reinterpret_cast<float4 *>(dst + c) =
                 make_float4(o[r][c] * inv, o[r][c + 1] * inv, o[r][c + 2] * inv, o[r][c + 3] * inv);
     }
+}
+
+// Combines the key-range splits of one (row, head): M = max m_s,
+// l = sum l_s e^(m_s - M), o = sum o_s e^(m_s - M) / max(l, 1e-30).  Splits
+// past a row's last tile hold m = -inf and contribute nothing.
+template <int HD>
+__global__ __launch_bounds__(HD) void k_prefill_merge(const float *__restrict__ part,
+                                                     const float *__restrict__ pml,
+                                                     float *__restrict__ out, int M, int hq,
+                                                     int nsplit) {
+    const int m = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, pml[(((size_t)sp * M + m) * hq + h) * 2]);
+    float l = 0.f, acc = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+        const size_t row = ((size_t)sp * M + m) * hq + h;
+        const float ms = pml[row * 2];
+        const float w = ms == -INFINITY ? 0.f : expf(ms - mx);
+        l = fmaf(pml[row * 2 + 1], w, l);
+        acc = fmaf(part[row * HD + c], w, acc);
+    }
+    out[((size_t)m * hq + h) * HD + c] = acc / fmaxf(l, 1e-30f);
 }
 
 }  // namespace
@@ -978,22 +1028,47 @@ int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const flo
     return TB_OK;
 }
 
+int prefill_attention_splits(int start, int M, int hq) {
+    const int qtiles = (M + 63) / 64;
+    const int tiles = (start + M - 1) / 64 + 1;          // tiles of the last query tile
+    const int want = (2048 + qtiles * hq - 1) / (qtiles * hq);   // ~8 blocks per CU
+    return std::max(1, std::min(want, tiles));
+}
+
+size_t prefill_attention_scratch(int M, int hq, int hd, int nsplit) {
+    return nsplit > 1 ? (size_t)nsplit * M * hq * (hd + 2) * sizeof(float) : 0;
+}
+
 int launch_prefill_attention(const float *q, const float *kc, const float *vc, float *out,
                              int start, int M, int hq, int hkv, int hd, int max_seq,
-                             hipStream_t s) {
+                             float *scratch, hipStream_t s) {
     TB_REQUIRE(hq % hkv == 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: num_heads must be a multiple of num_kv_heads");
-    const dim3 grid((M + 63) / 64, hq);
+    TB_REQUIRE(hd == 64 || hd == 128, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: head_dim must be 64 or 128");
+    const int nsplit = scratch ? prefill_attention_splits(start, M, hq) : 1;
+    const int tiles = (start + M - 1) / 64 + 1;
+    const int tps = (tiles + nsplit - 1) / nsplit;
+    float *part = nsplit > 1 ? scratch : nullptr;
+    float *pml = nsplit > 1 ? scratch + (size_t)nsplit * M * hq * hd : nullptr;
+    const dim3 grid((M + 63) / 64, hq, nsplit);
     const float scale = 1.0f / sqrtf((float)hd);
     if (hd == 128)
         hipLaunchKernelGGL(k_prefill_attn<128>, grid, dim3(256), 0, s, q, kc, vc, out, start, M,
-                           hq, hkv, max_seq, scale);
-    else if (hd == 64)
-        hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, q, kc, vc, out, start, M, hq,
-                           hkv, max_seq, scale);
+                           hq, hkv, max_seq, scale, tps, part, pml);
     else
-        return fail(TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: head_dim must be 64 or 128");
+        hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, q, kc, vc, out, start, M, hq,
+                           hkv, max_seq, scale, tps, part, pml);
     TB_LAUNCHED();
+    if (nsplit > 1) {
+        if (hd == 128)
+            hipLaunchKernelGGL(k_prefill_merge<128>, dim3(M, hq), dim3(128), 0, s, part, pml, out,
+                               M, hq, nsplit);
+        else
+            hipLaunchKernelGGL(k_prefill_merge<64>, dim3(M, hq), dim3(64), 0, s, part, pml, out,
+                               M, hq, nsplit);
+        TB_LAUNCHED();
+    }
     return TB_OK;
 }
 

@@ -492,7 +492,43 @@ struct Decoder {
         return true;
     }
 
-    int prefill_batched(const int64_t *tokens, int64_t n, int64_t start) {
+    // The lm_head over M rows of normalised hidden states xr [M, H] into
+    // y [M, V]: the MFMA GEMM for INT4 (64 rows per launch, its split-K
+    // partials in pf_lmpart), GEMV passes of 2 rows for INT8 / fp32.
+    float *pf_lmpart = nullptr;
+    float *pf_attn = nullptr;    // key-range split partials of the prefill attention
+    size_t pf_attn_bytes = 0;
+    float *pf_rows = nullptr;    // verify_tokens: logits of every position
+    int64_t pf_rows_n = 0;
+    int lm_rows(const float *xr, float *y, int M) {
+        int rc;
+        if (lmbits == 4) {
+            if (!pf_lmpart &&
+                (rc = alloc(&pf_lmpart, w4_mfma_partials_bytes(64, V, H, false))))
+                return rc;
+            for (int r0 = 0; r0 < M; r0 += 64) {
+                MfmaParams p{};
+                p.x = xr + (size_t)r0 * H;
+                p.w0 = static_cast<const uint8_t *>(lm_w); p.s0 = lm_s;
+                p.y = y + (size_t)r0 * V; p.m = std::min(64, M - r0); p.n = V; p.k = H;
+                p.gshift = gshift(gs);
+                if ((rc = w4_mfma(p, EPI_PLAIN, pf_lmpart, st))) return rc;
+            }
+            return TB_OK;
+        }
+        for (int r0 = 0; r0 < M; r0 += 2) {
+            DenseParams p{};
+            p.x = xr + (size_t)r0 * H; p.w0 = lm_w; p.rs0 = lm_s; p.rs0_len = lm_s ? V : 0;
+            p.y = y + (size_t)r0 * V; p.m = std::min(2, M - r0); p.n = V; p.k = H;
+            if ((rc = dense_gemv(p, lmbits == 8 ? W_I8 : W_F32, EPI_PLAIN, st))) return rc;
+        }
+        return TB_OK;
+    }
+
+    // rows_out (device [n, V]): every position's logits, as verify_tokens
+    // returns them (decoder.rs:565-581); otherwise only the last position's.
+    int prefill_batched(const int64_t *tokens, int64_t n, int64_t start,
+                        float *rows_out = nullptr) {
         int rc = prefill_alloc();
         if (rc) return rc;
         const int nq = (hq + 2 * hkv) * hd;
@@ -503,6 +539,12 @@ struct Decoder {
             const int pos0 = (int)(start + c0);
             TB_HIP(hipMemcpyAsync(pf_tok, tok32.data() + c0, (size_t)M * 4, hipMemcpyHostToDevice,
                                   st));
+            const size_t ab = prefill_attention_scratch(
+                M, hq, hd, prefill_attention_splits(pos0, M, hq));
+            if (ab > pf_attn_bytes) {
+                if ((rc = alloc(&pf_attn, ab))) return rc;
+                pf_attn_bytes = ab;
+            }
             if ((rc = launch_embed_rows(pf_tok, embed, pf_x, M, H, st))) return rc;
             for (int l = 0; l < L; ++l) {
                 const Layer &y = layers[l];
@@ -514,7 +556,7 @@ struct Decoder {
                     (rc = launch_rope_rows(pf_qkv, pf_q, kcl, vcl, cos_t, sin_t, pos0, M, hq, hkv,
                                            hd, max_seq, st)) ||
                     (rc = launch_prefill_attention(pf_q, kcl, vcl, pf_a, pos0, M, hq, hkv, hd,
-                                                   max_seq, st)) ||
+                                                   max_seq, pf_attn, st)) ||
                     (rc = gemm(pf_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H,
                                hq * hd, EPI_RESID)) ||
                     (rc = launch_rmsnorm_rows(pf_x, y.post_norm, pf_xn, M, H, eps, st)) ||
@@ -524,7 +566,14 @@ struct Decoder {
                                H, I, EPI_RESID)))
                     return rc;
             }
-            if (c0 + M == n) {
+            if (rows_out) {
+                if ((rc = launch_rmsnorm_rows(pf_x, final_norm, pf_xn, M, H, eps, st)) ||
+                    (rc = lm_rows(pf_xn, rows_out + (size_t)c0 * V, M)))
+                    return rc;
+                if (c0 + M == n)
+                    TB_HIP(hipMemcpyAsync(logits, rows_out + (size_t)(n - 1) * V, (size_t)V * 4,
+                                          hipMemcpyDeviceToDevice, st));
+            } else if (c0 + M == n) {
                 // The last position's hidden state -> final norm -> lm_head.
                 TB_HIP(hipMemcpyAsync(x, pf_x + (size_t)(M - 1) * H, (size_t)H * 4,
                                       hipMemcpyDeviceToDevice, st));
@@ -973,6 +1022,171 @@ int tb_decoder_generate(tb_decoder *d, int64_t first_token, int64_t seq_len,
     *n_out = n;
     *seq_len_out = seq_len + n;
     return TB_OK;
+}
+
+// Leviathan acceptance of speculative_accept (decoder.rs:588-727) over the
+// target rows [K, V] with the uniforms u[0..n_u) in order.
+static int spec_accept(const float *rows, const int64_t *draft, const float *dprobs, int64_t K,
+                       int64_t V, float temperature, float top_p, const double *u, int64_t n_u,
+                       int64_t *accepted, int64_t *bonus) {
+    int64_t ui = 0;
+    auto next_u = [&]() { return ui < n_u ? u[ui++] : 0.0; };
+    const float t = std::isfinite(temperature) && temperature > 0.f ? temperature : 1.0f;
+    std::vector<float> tp((size_t)V);
+    auto softmax = [&](const float *lg) {   // decoder.rs:624-641
+        float m = -INFINITY;
+        for (int64_t j = 0; j < V; ++j) m = std::max(m, std::isfinite(lg[j]) ? lg[j] : -INFINITY);
+        float sum = 0.f;
+        for (int64_t j = 0; j < V; ++j) {
+            tp[j] = expf(((std::isfinite(lg[j]) ? lg[j] : -INFINITY) - m) / t);
+            sum += tp[j];
+        }
+        const float inv = 1.0f / std::max(sum, 1e-30f);
+        for (int64_t j = 0; j < V; ++j) tp[j] *= inv;
+    };
+    *accepted = 0;
+    for (int64_t i = 0; i < K; ++i) {
+        softmax(rows + (size_t)i * V);
+        const int64_t d = std::min<int64_t>(std::max<int64_t>(draft[i], 0), V - 1);
+        const float pt = tp[d], pd = std::max(dprobs[(size_t)i * V + d], 0.f);
+        const float acc = std::min(pt / (pd + 1e-12f), 1.0f);
+        if (next_u() <= (double)acc) {
+            *accepted += 1;
+            continue;
+        }
+        // rejected: resample from max(0, p_target - p_draft) (decoder.rs:677-702)
+        std::vector<float> c((size_t)V);
+        float sc = 0.f;
+        for (int64_t j = 0; j < V; ++j) {
+            c[j] = std::max(tp[j] - dprobs[(size_t)i * V + j], 0.f);
+            sc += c[j];
+        }
+        if (sc > 1e-12f) {
+            const float r = (float)next_u() * sc;
+            float a = 0.f;
+            *bonus = V - 1;
+            for (int64_t j = 0; j < V; ++j) {
+                a += c[j];
+                if (a >= r) {
+                    *bonus = j;
+                    break;
+                }
+            }
+        } else {
+            int64_t bj = 0;
+            for (int64_t j = 1; j < V; ++j)
+                if (tp[j] > tp[bj]) bj = j;
+            *bonus = bj;
+        }
+        return TB_OK;
+    }
+    // all accepted: the bonus from the last row with the nucleus
+    // (decoder.rs:705-726), candidates by probability (ties: lower index)
+    softmax(rows + (size_t)(K - 1) * V);
+    std::vector<int64_t> idx((size_t)V);
+    for (int64_t j = 0; j < V; ++j) idx[j] = j;
+    std::stable_sort(idx.begin(), idx.end(), [&](int64_t a, int64_t b) { return tp[a] > tp[b]; });
+    int64_t kept = V;
+    if (top_p > 0.f && top_p < 1.f) {
+        float cum = 0.f;
+        for (int64_t i = 0; i < V; ++i) {
+            if (cum > top_p) {
+                kept = i;
+                break;
+            }
+            cum += tp[idx[i]];
+        }
+        kept = std::max<int64_t>(kept, 1);
+    }
+    float mass = 0.f;
+    for (int64_t i = 0; i < kept; ++i) mass += tp[idx[i]];
+    const float r = (float)next_u() * std::max(mass, 1e-30f);
+    float a = 0.f;
+    *bonus = idx[kept - 1];
+    for (int64_t i = 0; i < kept; ++i) {
+        a += tp[idx[i]];
+        if (a >= r) {
+            *bonus = idx[i];
+            break;
+        }
+    }
+    return TB_OK;
+}
+
+// The decoder's f64 uniforms for speculative acceptance: 53 bits of the same
+// splitmix64 stream as the sampler's draws.
+static double spec_uniform(uint64_t seed, uint64_t counter) {
+    uint64_t x = seed + (counter + 1ull) * 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    x ^= x >> 31;
+    return (double)(x >> 11) / 9007199254740992.0;
+}
+
+double tb_spec_uniform(uint64_t seed, uint64_t counter) { return spec_uniform(seed, counter); }
+
+int tb_speculative_accept_rows(const float *target_rows, const int64_t *draft_tokens,
+                               const float *draft_probs, int64_t k, int64_t vocab,
+                               float temperature, float top_p, const double *u, int64_t n_u,
+                               int64_t *accepted, int64_t *bonus) {
+    TB_REQUIRE(accepted && bonus, TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(vocab > 0 && k >= 0, TB_ERR_VALUE, "bad shape");
+    if (k == 0) {
+        *accepted = 0;
+        *bonus = vocab - 1;
+        return TB_OK;
+    }
+    TB_REQUIRE(target_rows && draft_tokens && draft_probs && (n_u == 0 || u), TB_ERR_VALUE,
+               "null argument");
+    return spec_accept(target_rows, draft_tokens, draft_probs, k, vocab, temperature, top_p, u,
+                       n_u, accepted, bonus);
+}
+
+int tb_decoder_verify(tb_decoder *d, int64_t start_offset, const int64_t *tokens, int64_t n,
+                      float *logits_out) {
+    TB_REQUIRE(d && (n == 0 || (tokens && logits_out)), TB_ERR_VALUE, "null argument");
+    TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
+               "verify exceeds max_seq_len");
+    if (n == 0) return TB_OK;
+    bool batch = d->wbits == 4 && n >= 2;
+    for (int64_t i = 0; i < n && batch; ++i) batch = tokens[i] >= 0 && tokens[i] < d->V;
+    if (!batch) {
+        for (int64_t i = 0; i < n; ++i) {
+            int rc = d->step(tokens[i], start_offset + i, true, nullptr);
+            if (rc) return rc;
+            memcpy(logits_out + (size_t)i * d->V, d->host_logits.data(), (size_t)d->V * 4);
+        }
+        return TB_OK;
+    }
+    // verify_tokens (decoder.rs:565-581) as one batched forward over the n
+    // positions: the weights are read once, not n times.
+    int rc;
+    if (n > d->pf_rows_n) {
+        if ((rc = d->alloc(&d->pf_rows, (size_t)n * d->V * 4))) return rc;
+        d->pf_rows_n = n;
+    }
+    if ((rc = d->prefill_batched(tokens, n, start_offset, d->pf_rows))) return rc;
+    TB_HIP(hipMemcpy(logits_out, d->pf_rows, (size_t)n * d->V * 4, hipMemcpyDeviceToHost));
+    return TB_OK;
+}
+
+int tb_decoder_speculative_accept(tb_decoder *d, int64_t offset, const int64_t *draft_tokens,
+                                  int64_t k, const float *draft_probs, float temperature,
+                                  float top_p, int64_t *accepted, int64_t *bonus) {
+    TB_REQUIRE(d && accepted && bonus, TB_ERR_VALUE, "null argument");
+    if (k == 0) {
+        *accepted = 0;
+        *bonus = d->V - 1;
+        return TB_OK;
+    }
+    TB_REQUIRE(draft_tokens && draft_probs, TB_ERR_VALUE, "draft_probs must be K×V row-major");
+    std::vector<float> rows((size_t)k * d->V);
+    int rc = tb_decoder_verify(d, offset, draft_tokens, k, rows.data());
+    if (rc) return rc;
+    std::vector<double> u((size_t)k + 1);
+    for (auto &v : u) v = spec_uniform(d->seed, d->draws++);
+    return spec_accept(rows.data(), draft_tokens, draft_probs, k, d->V, temperature, top_p,
+                       u.data(), (int64_t)u.size(), accepted, bonus);
 }
 
 int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n, int64_t start_offset,

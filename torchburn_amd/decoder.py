@@ -43,6 +43,11 @@ def _bind():
         "tb_decoder_generate_sampled": [p, i64, i64, i64, C.c_float, i64, C.c_float, C.c_float,
                                         i64, p, i64, p, C.POINTER(i64), C.POINTER(i64)],
         "tb_decoder_prefill": [p, p, i64, i64, C.POINTER(i64)],
+        "tb_decoder_verify": [p, i64, p, i64, p],
+        "tb_decoder_speculative_accept": [p, i64, p, i64, p, C.c_float, C.c_float,
+                                          C.POINTER(i64), C.POINTER(i64)],
+        "tb_speculative_accept_rows": [p, p, p, i64, i64, C.c_float, C.c_float, p, i64,
+                                       C.POINTER(i64), C.POINTER(i64)],
         "tb_decoder_reset_kv": [p],
         "tb_decoder_copy_kv": [p, i64, p, p, i64, i64],
         "tb_decoder_kv_len": [p, C.POINTER(i64)],
@@ -55,8 +60,31 @@ def _bind():
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = C.c_int
+    L.tb_spec_uniform.restype = C.c_double
+    L.tb_spec_uniform.argtypes = [C.c_uint64, C.c_uint64]
     L._tb_decoder_bound = True
     return L
+
+
+def speculative_accept_rows(target_rows, draft_tokens, draft_probs, u, temperature: float = 1.0,
+                            top_p: float = 1.0) -> Tuple[int, int]:
+    """The acceptance of speculative_accept over given target logits rows [K, V]
+    with the uniforms u (decoder.rs:608-726)."""
+    rows = np.ascontiguousarray(np.asarray(target_rows, dtype=np.float32))
+    k, v = (rows.shape if rows.ndim == 2 else (0, rows.size))
+    arr = np.asarray(list(draft_tokens), dtype=np.int64)
+    probs = np.ascontiguousarray(np.asarray(draft_probs, dtype=np.float32).reshape(-1))
+    uu = np.ascontiguousarray(np.asarray(list(u), dtype=np.float64))
+    a, b = C.c_int64(), C.c_int64()
+    _lib.check(_bind().tb_speculative_accept_rows(
+        rows.ctypes.data, arr.ctypes.data, probs.ctypes.data, k, v, float(temperature),
+        float(top_p), uu.ctypes.data if uu.size else None, uu.size, C.byref(a), C.byref(b)))
+    return int(a.value), int(b.value)
+
+
+def spec_uniform(seed: int, counter: int) -> float:
+    """The decoder's f64 uniform of draw ``counter`` under ``seed``."""
+    return float(_bind().tb_spec_uniform(int(seed) & (2 ** 64 - 1), int(counter) & (2 ** 64 - 1)))
 
 
 def decoder_symbols() -> list:
@@ -64,7 +92,8 @@ def decoder_symbols() -> list:
             "tb_decoder_decode_and_sample", "tb_decoder_generate", "tb_decoder_prefill",
             "tb_decoder_reset_kv", "tb_decoder_copy_kv", "tb_decoder_kv_len",
             "tb_decoder_get_logits", "tb_decoder_set_seed", "tb_decoder_time_greedy",
-            "tb_decoder_destroy"]
+            "tb_decoder_destroy", "tb_decoder_generate_sampled", "tb_decoder_verify",
+            "tb_decoder_speculative_accept", "tb_speculative_accept_rows", "tb_spec_uniform"]
 
 
 def _as_buffer(t: Any, dtype=None):
@@ -207,9 +236,34 @@ class RustQwenDecoder:
         return self.get_logits()
 
     def verify_tokens(self, start_offset: int, tokens: Sequence[int]) -> List[List[float]]:
+        """Logits of every position (decoder.rs:565-581); INT4 decoders run the
+        positions as one batched forward."""
+        return self._verify(start_offset, tokens).tolist()
+
+    def _verify(self, start_offset: int, tokens: Sequence[int]) -> np.ndarray:
         if start_offset + len(tokens) > self.max_seq_len:
             raise ValueError("verify exceeds max_seq_len")
-        return [self.step(t, start_offset + i) for i, t in enumerate(tokens)]
+        arr = np.asarray(list(tokens), dtype=np.int64)
+        out = np.empty((arr.size, self.vocab_size), np.float32)
+        _lib.check(_bind().tb_decoder_verify(self._h, int(start_offset),
+                                             arr.ctypes.data if arr.size else None, arr.size,
+                                             out.ctypes.data if arr.size else None))
+        return out
+
+    def speculative_accept(self, offset: int, draft_tokens: Sequence[int],
+                           draft_probs: Sequence[float], temperature: float = 1.0,
+                           top_p: float = 1.0) -> Tuple[int, int]:
+        """(accepted, bonus) of the reference's speculative step (decoder.rs:588-727)."""
+        arr = np.asarray(list(draft_tokens), dtype=np.int64)
+        probs = np.ascontiguousarray(np.asarray(draft_probs, dtype=np.float32).reshape(-1))
+        if arr.size and probs.size != arr.size * self.vocab_size:
+            raise ValueError("draft_probs must be K×V row-major")
+        a, b = C.c_int64(), C.c_int64()
+        _lib.check(_bind().tb_decoder_speculative_accept(
+            self._h, int(offset), arr.ctypes.data if arr.size else None, arr.size,
+            probs.ctypes.data if probs.size else None, float(temperature), float(top_p),
+            C.byref(a), C.byref(b)))
+        return int(a.value), int(b.value)
 
     # -- KV cache -------------------------------------------------------------
 
