@@ -93,3 +93,29 @@ def test_speculative_accept_matches_oracle(cuda, T, top_p):
         ref.close()
         dec.close()
     print(f"accepted counts seen: {sorted(outcomes)}", flush=True)
+
+
+@pytest.mark.parametrize("n,start", [(3, 40), (6, 2400)])
+def test_verify_llama_heads_long_prefix(cuda, n, start):
+    """head_dim 128, 4 query heads per KV head: 12 and 24 query rows per KV
+    head (the 16- and 32-row attention tiles); the 2400-position prefix splits
+    the key range 76 ways, more than one pass of the merge."""
+    print(f"case verify llama heads n={n} start={start}", flush=True)
+    cfg = small(num_layers=1, num_heads=8, num_kv_heads=2, head_dim=128, hidden=1024,
+                intermediate=2048, qkv_bias=False)
+    max_seq = start + 64
+    ref, dec = make(cfg, 4, 4, max_seq=max_seq, seed=43)
+    kv = synth.kv_prefill(cfg, 43, start, max_seq)
+    for li, (k, v) in enumerate(kv):
+        ref.copy_kv(li, k, v, start)
+    dec.copy_kv_cache_from_tensors([k for k, _ in kv], [v for _, v in kv], start)
+    g = np.random.default_rng(start + n)
+    toks = [int(t) for t in g.integers(0, 1000, n)]
+    rows = dec.verify_tokens(start, toks)
+    want = [ref.step(t, start + i) for i, t in enumerate(toks)]
+    err = max(rel(a, b) for a, b in zip(rows, want))
+    print(f"verify rows rel err {err:.3g}", flush=True)
+    assert len(rows) == n and err < 2e-4
+    assert dec.kv_len() == start + n
+    ref.close()
+    dec.close()

@@ -731,17 +731,25 @@ __global__ void k_rope_rows(const float *__restrict__ qkv, int nq, float *__rest
 }
 
 // Causal GQA attention of M consecutive query positions start .. start+M-1
-// over the cache (query at position p sees keys 0..p; decoder.rs:1148-1213):
-// one query head and 64 query positions per block; K and V tiles of 64
-// positions staged in LDS (zero past the last position the block needs);
-// 4 x 4 score micro-tiles per thread; online softmax with a running max and
-// sum per row, then 1 / max(sum, 1e-30).  out [M][hq * HD].
+// over the cache (query at position p sees keys 0..p; decoder.rs:1148-1213).
+//
+// A block owns one KV head and a tile of QT = 16 * RPT query rows, where the
+// rows of a KV head are its (position m, head g of the group) pairs, i = m * G
+// + g: every query head that shares the KV head reads each K / V tile from
+// the same LDS copy, and a short verify chunk (M * G rows) fills one small
+// tile instead of padding a position tile per head.  K and V tiles of KT = 16
+// * KPT positions are staged in LDS (zero past the last position the tile
+// needs); thread (rg, kg) scores rows RPT * rg + r against keys kg + 16 j and
+// owns output columns 64 c + 4 kg .. + 3 of its rows (consecutive lanes read
+// LDS rows HD + 4 floats apart, or consecutive float4s: no bank conflicts);
+// online softmax with a running max and sum per row, then 1 / max(sum,
+// 1e-30).  out [M][hq * HD].
 //
 // Key-range split (blockIdx.z of nsplit, tps tiles each): with nsplit > 1 the
 // block writes its unnormalised o, running max and sum to part / pml and
 // k_prefill_merge combines the splits, so few query rows over a long cache
 // (verify_tokens, short chunks after a long prefix) still fill the chip.
-template <int HD>
+template <int HD, int RPT, int KPT>
 __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ q,
                                                       const float *__restrict__ kc,
                                                       const float *__restrict__ vc,
@@ -749,36 +757,44 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
                                                       int hq, int hkv, int max_seq, float scale,
                                                       int tps, float *__restrict__ part,
                                                       float *__restrict__ pml) {
-    constexpr int QT = 64, KT = 64, HP = HD + 4, OC = HD / 16;
+    constexpr int QT = 16 * RPT, KT = 16 * KPT, HP = HD + 4, OC = HD / 16, C4 = HD / 4;
+    // unroll of the score and PV loops: none for the 64 x 64 tile (122 VGPRs;
+    // unrolled it grows past 150 or spills), by 4 for the small ones
+    constexpr int DU = RPT == 4 ? 1 : 4, JU = RPT == 4 ? 1 : 4;
     __shared__ __attribute__((aligned(16))) float sq[QT][HP];
     __shared__ __attribute__((aligned(16))) float sk[KT][HP];
-    __shared__ __attribute__((aligned(16))) float sv[KT][HP];
+    __shared__ __attribute__((aligned(16))) float sv[KT][HD];
     __shared__ float sp[QT][KT + 1];
-    const int h = blockIdx.y, kvh = h / (hq / hkv);
-    const int m0 = blockIdx.x * QT;
-    const int t = threadIdx.x, rg = t >> 4, kg = t & 15;   // rows 4rg.., keys 4kg.., cols kg*OC..
-    for (int i = t; i < QT * (HD / 4); i += 256) {
-        const int r = i / (HD / 4), c4 = i - r * (HD / 4);
+    const int G = hq / hkv, NR = M * G;
+    const int kvh = blockIdx.y, i0 = blockIdx.x * QT;
+    const int t = threadIdx.x, rg = t >> 4, kg = t & 15;   // rows RPT*rg.., keys KPT*kg..
+    for (int i = t; i < QT * C4; i += 256) {
+        const int r = i / C4, c4 = i - r * C4, ii = i0 + r;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m0 + r < M) v = reinterpret_cast<const float4 *>(q + ((size_t)(m0 + r) * hq + h) * HD)[c4];
+        if (ii < NR) {
+            const int m = ii / G, h = kvh * G + (ii - m * G);
+            v = reinterpret_cast<const float4 *>(q + ((size_t)m * hq + h) * HD)[c4];
+        }
         *reinterpret_cast<float4 *>(&sq[r][4 * c4]) = v;
     }
-    float mrun[4], lrun[4], o[4][OC];
+    float mrun[RPT], lrun[RPT], o[RPT][OC];
+    int pq[RPT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < RPT; ++r) {
         mrun[r] = -INFINITY;
         lrun[r] = 0.f;
+        pq[r] = start + (i0 + RPT * rg + r) / G;   // past `last` for padding rows: finite scores
 #pragma unroll
         for (int c = 0; c < OC; ++c) o[r][c] = 0.f;
     }
-    const int last = start + min(m0 + QT, M) - 1;   // last position any row of the block sees
+    const int last = start + (min(i0 + QT, NR) - 1) / G;   // last position any row sees
     const int ntiles = last / KT + 1;
     const int kt0 = blockIdx.z * tps, kt1 = min(ntiles, kt0 + tps);
     const float *kb = kc + (size_t)kvh * max_seq * HD, *vb = vc + (size_t)kvh * max_seq * HD;
     for (int kt = kt0; kt < kt1; ++kt) {
         __syncthreads();
-        for (int i = t; i < KT * (HD / 4); i += 256) {
-            const int j = i / (HD / 4), c4 = i - j * (HD / 4);
+        for (int i = t; i < KT * C4; i += 256) {
+            const int j = i / C4, c4 = i - j * C4;
             const int p = kt * KT + j;
             float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
             if (p <= last) {
@@ -789,21 +805,24 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             *reinterpret_cast<float4 *>(&sv[j][4 * c4]) = vv;
         }
         __syncthreads();
-        float s[4][4];
+        float s[RPT][KPT];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < RPT; ++r)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s[r][j] = 0.f;
+            for (int j = 0; j < KPT; ++j) s[r][j] = 0.f;
+#pragma unroll DU
         for (int d = 0; d < HD; d += 4) {
-            float4 qa[4], kk[4];
+            float4 qa[RPT], kk[KPT];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) qa[r] = *reinterpret_cast<const float4 *>(&sq[4 * rg + r][d]);
+            for (int r = 0; r < RPT; ++r)
+                qa[r] = *reinterpret_cast<const float4 *>(&sq[RPT * rg + r][d]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) kk[j] = *reinterpret_cast<const float4 *>(&sk[4 * kg + j][d]);
+            for (int j = 0; j < KPT; ++j)
+                kk[j] = *reinterpret_cast<const float4 *>(&sk[kg + 16 * j][d]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < RPT; ++r)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < KPT; ++j) {
                     s[r][j] = fmaf(qa[r].x, kk[j].x, s[r][j]);
                     s[r][j] = fmaf(qa[r].y, kk[j].y, s[r][j]);
                     s[r][j] = fmaf(qa[r].z, kk[j].z, s[r][j]);
@@ -811,13 +830,12 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
                 }
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int pq = start + m0 + 4 * rg + r;
+        for (int r = 0; r < RPT; ++r) {
             float mt = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int pk = kt * KT + 4 * kg + j;
-                s[r][j] = pk <= pq ? s[r][j] * scale : -INFINITY;
+            for (int j = 0; j < KPT; ++j) {
+                const int pk = kt * KT + kg + 16 * j;
+                s[r][j] = pk <= pq[r] ? s[r][j] * scale : -INFINITY;
                 mt = fmaxf(mt, s[r][j]);
             }
 #pragma unroll
@@ -827,9 +845,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             const float alpha = mn == -INFINITY ? 1.f : expf(mrun[r] - mn);
             float ls = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < KPT; ++j) {
                 const float pj = mn == -INFINITY ? 0.f : expf(s[r][j] - mn);
-                sp[4 * rg + r][4 * kg + j] = pj;
+                sp[RPT * rg + r][kg + 16 * j] = pj;
                 ls += pj;
             }
 #pragma unroll
@@ -840,15 +858,16 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             for (int c = 0; c < OC; ++c) o[r][c] *= alpha;
         }
         __syncthreads();
+#pragma unroll JU
         for (int j = 0; j < KT; ++j) {
-            float pv[4];
+            float pv[RPT];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pv[r] = sp[4 * rg + r][j];
+            for (int r = 0; r < RPT; ++r) pv[r] = sp[RPT * rg + r][j];
 #pragma unroll
             for (int c = 0; c < OC; c += 4) {
-                const float4 vv = *reinterpret_cast<const float4 *>(&sv[j][kg * OC + c]);
+                const float4 vv = *reinterpret_cast<const float4 *>(&sv[j][16 * c + 4 * kg]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
+                for (int r = 0; r < RPT; ++r) {
                     o[r][c] = fmaf(pv[r], vv.x, o[r][c]);
                     o[r][c + 1] = fmaf(pv[r], vv.y, o[r][c + 1]);
                     o[r][c + 2] = fmaf(pv[r], vv.z, o[r][c + 2]);
@@ -857,57 +876,107 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
             }
         }
     }
-    if (part) {   // one split of several: unnormalised o, max and sum
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 4 * rg + r;
-            if (m >= M) continue;
+    for (int r = 0; r < RPT; ++r) {
+        const int ii = i0 + RPT * rg + r;
+        if (ii >= NR) continue;
+        const int m = ii / G, h = kvh * G + (ii - m * G);
+        if (part) {   // one split of several: unnormalised o, max and sum
             const size_t row = ((size_t)blockIdx.z * M + m) * hq + h;
-            float *dst = part + row * HD + kg * OC;
+            float *dst = part + row * HD + 4 * kg;
 #pragma unroll
             for (int c = 0; c < OC; c += 4)
-                *reinterpret_cast<float4 *>(dst + c) =
+                *reinterpret_cast<float4 *>(dst + 16 * c) =
                     make_float4(o[r][c], o[r][c + 1], o[r][c + 2], o[r][c + 3]);
             if (kg == 0) {
                 pml[row * 2] = mrun[r];
                 pml[row * 2 + 1] = lrun[r];
             }
+        } else {
+            const float inv = 1.0f / fmaxf(lrun[r], 1e-30f);
+            float *dst = out + ((size_t)m * hq + h) * HD + 4 * kg;
+#pragma unroll
+            for (int c = 0; c < OC; c += 4)
+                *reinterpret_cast<float4 *>(dst + 16 * c) = make_float4(
+                    o[r][c] * inv, o[r][c + 1] * inv, o[r][c + 2] * inv, o[r][c + 3] * inv);
         }
-        return;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 4 * rg + r;
-        if (m >= M) continue;
-        const float inv = 1.0f / fmaxf(lrun[r], 1e-30f);
-        float *dst = out + ((size_t)m * hq + h) * HD + kg * OC;
-#pragma unroll
-        for (int c = 0; c < OC; c += 4)
-            *reinterpret_cast<float4 *>(dst + c) =
-                make_float4(o[r][c] * inv, o[r][c + 1] * inv, o[r][c + 2] * inv, o[r][c + 3] * inv);
     }
 }
 
 // Combines the key-range splits of one (row, head): M = max m_s,
 // l = sum l_s e^(m_s - M), o = sum o_s e^(m_s - M) / max(l, 1e-30).  Splits
-// past a row's last tile hold m = -inf and contribute nothing.
+// past a row's last tile hold m = -inf and contribute nothing.  256 threads =
+// SG split groups x HD / 4 float4 columns; each thread folds splits sg, sg +
+// SG, ... NB at a time (all NB loads in flight) with its own running max, and
+// the split groups combine through LDS.
 template <int HD>
-__global__ __launch_bounds__(HD) void k_prefill_merge(const float *__restrict__ part,
-                                                     const float *__restrict__ pml,
-                                                     float *__restrict__ out, int M, int hq,
-                                                     int nsplit) {
-    const int m = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, pml[(((size_t)sp * M + m) * hq + h) * 2]);
-    float l = 0.f, acc = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-        const size_t row = ((size_t)sp * M + m) * hq + h;
-        const float ms = pml[row * 2];
-        const float w = ms == -INFINITY ? 0.f : expf(ms - mx);
-        l = fmaf(pml[row * 2 + 1], w, l);
-        acc = fmaf(part[row * HD + c], w, acc);
+__global__ __launch_bounds__(256) void k_prefill_merge(const float *__restrict__ part,
+                                                      const float *__restrict__ pml,
+                                                      float *__restrict__ out, int M, int hq,
+                                                      int nsplit) {
+    constexpr int C4 = HD / 4, SG = 256 / C4, NB = 8;
+    __shared__ float4 so[SG][C4];
+    __shared__ float smx[SG], sl[SG];
+    const int m = blockIdx.x, h = blockIdx.y, c = threadIdx.x % C4, sg = threadIdx.x / C4;
+    float mx = -INFINITY, l = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = sg; s0 < nsplit; s0 += SG * NB) {
+        float ms[NB], ls[NB];
+        float4 ov[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int sp = s0 + u * SG;
+            const bool ok = sp < nsplit;
+            const size_t row = ((size_t)(ok ? sp : 0) * M + m) * hq + h;
+            ms[u] = ok ? pml[row * 2] : -INFINITY;
+            ls[u] = ok ? pml[row * 2 + 1] : 0.f;
+            ov[u] = ok ? reinterpret_cast<const float4 *>(part + row * HD)[c]
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float mn = mx;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) mn = fmaxf(mn, ms[u]);
+        if (mn == -INFINITY) continue;   // nothing seen yet
+        const float a = mx == -INFINITY ? 0.f : expf(mx - mn);
+        acc = make_float4(acc.x * a, acc.y * a, acc.z * a, acc.w * a);
+        l *= a;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const float w = ms[u] == -INFINITY ? 0.f : expf(ms[u] - mn);
+            l = fmaf(ls[u], w, l);
+            acc.x = fmaf(ov[u].x, w, acc.x);
+            acc.y = fmaf(ov[u].y, w, acc.y);
+            acc.z = fmaf(ov[u].z, w, acc.z);
+            acc.w = fmaf(ov[u].w, w, acc.w);
+        }
+        mx = mn;
     }
-    out[((size_t)m * hq + h) * HD + c] = acc / fmaxf(l, 1e-30f);
+    so[sg][c] = acc;
+    if (c == 0) {
+        smx[sg] = mx;
+        sl[sg] = l;
+    }
+    __syncthreads();
+    if (sg == 0) {
+        float mg = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < SG; ++g) mg = fmaxf(mg, smx[g]);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float lt = 0.f;
+#pragma unroll
+        for (int g = 0; g < SG; ++g) {
+            const float w = smx[g] == -INFINITY ? 0.f : expf(smx[g] - mg);
+            const float4 v = so[g][c];
+            o.x = fmaf(v.x, w, o.x);
+            o.y = fmaf(v.y, w, o.y);
+            o.z = fmaf(v.z, w, o.z);
+            o.w = fmaf(v.w, w, o.w);
+            lt = fmaf(sl[g], w, lt);
+        }
+        const float inv = 1.0f / fmaxf(lt, 1e-30f);
+        reinterpret_cast<float4 *>(out + ((size_t)m * hq + h) * HD)[c] =
+            make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    }
 }
 
 }  // namespace
@@ -1028,10 +1097,44 @@ int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const flo
     return TB_OK;
 }
 
-int prefill_attention_splits(int start, int M, int hq) {
-    const int qtiles = (M + 63) / 64;
-    const int tiles = (start + M - 1) / 64 + 1;          // tiles of the last query tile
-    const int want = (2048 + qtiles * hq - 1) / (qtiles * hq);   // ~8 blocks per CU
+namespace {
+
+// Query rows per tile (RPT) and key positions per tile (KPT), in sixteens, for
+// M positions x G heads per KV head: the smallest row tile that holds a short
+// chunk, with 32-key tiles for the small ones (44 / 54 KB of LDS, several
+// blocks per CU) and 64 x 64 tiles for long prompts.
+struct AttnShape {
+    int rpt, kpt;
+};
+AttnShape attn_shape(int M, int G) {
+    const int nr = M * G;
+    if (nr <= 16) return {1, 2};
+    if (nr <= 32) return {2, 2};
+    return {4, 4};
+}
+
+template <int HD>
+void launch_attn_tiles(AttnShape sh, dim3 grid, hipStream_t s, const float *q, const float *kc,
+                       const float *vc, float *out, int start, int M, int hq, int hkv,
+                       int max_seq, float scale, int tps, float *part, float *pml) {
+    if (sh.rpt == 1)
+        hipLaunchKernelGGL((k_prefill_attn<HD, 1, 2>), grid, dim3(256), 0, s, q, kc, vc, out,
+                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
+    else if (sh.rpt == 2)
+        hipLaunchKernelGGL((k_prefill_attn<HD, 2, 2>), grid, dim3(256), 0, s, q, kc, vc, out,
+                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
+    else
+        hipLaunchKernelGGL((k_prefill_attn<HD, 4, 4>), grid, dim3(256), 0, s, q, kc, vc, out,
+                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
+}
+
+}  // namespace
+
+int prefill_attention_splits(int start, int M, int hq, int hkv) {
+    const AttnShape sh = attn_shape(M, hq / hkv);
+    const int rtiles = (M * (hq / hkv) + 16 * sh.rpt - 1) / (16 * sh.rpt);
+    const int tiles = (start + M - 1) / (16 * sh.kpt) + 1;   // key tiles of the last row
+    const int want = (2048 + rtiles * hkv - 1) / (rtiles * hkv);   // ~8 blocks per CU
     return std::max(1, std::min(want, tiles));
 }
 
@@ -1042,30 +1145,32 @@ size_t prefill_attention_scratch(int M, int hq, int hd, int nsplit) {
 int launch_prefill_attention(const float *q, const float *kc, const float *vc, float *out,
                              int start, int M, int hq, int hkv, int hd, int max_seq,
                              float *scratch, hipStream_t s) {
-    TB_REQUIRE(hq % hkv == 0, TB_ERR_UNSUPPORTED,
+    TB_REQUIRE(hkv > 0 && hq % hkv == 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: num_heads must be a multiple of num_kv_heads");
     TB_REQUIRE(hd == 64 || hd == 128, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: head_dim must be 64 or 128");
-    const int nsplit = scratch ? prefill_attention_splits(start, M, hq) : 1;
-    const int tiles = (start + M - 1) / 64 + 1;
+    const AttnShape sh = attn_shape(M, hq / hkv);
+    const int nsplit = scratch ? prefill_attention_splits(start, M, hq, hkv) : 1;
+    const int tiles = (start + M - 1) / (16 * sh.kpt) + 1;
     const int tps = (tiles + nsplit - 1) / nsplit;
     float *part = nsplit > 1 ? scratch : nullptr;
     float *pml = nsplit > 1 ? scratch + (size_t)nsplit * M * hq * hd : nullptr;
-    const dim3 grid((M + 63) / 64, hq, nsplit);
+    const int rtiles = (M * (hq / hkv) + 16 * sh.rpt - 1) / (16 * sh.rpt);
+    const dim3 grid(rtiles, hkv, nsplit);
     const float scale = 1.0f / sqrtf((float)hd);
     if (hd == 128)
-        hipLaunchKernelGGL(k_prefill_attn<128>, grid, dim3(256), 0, s, q, kc, vc, out, start, M,
-                           hq, hkv, max_seq, scale, tps, part, pml);
+        launch_attn_tiles<128>(sh, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale, tps,
+                               part, pml);
     else
-        hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, q, kc, vc, out, start, M, hq,
-                           hkv, max_seq, scale, tps, part, pml);
+        launch_attn_tiles<64>(sh, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale, tps,
+                              part, pml);
     TB_LAUNCHED();
     if (nsplit > 1) {
         if (hd == 128)
-            hipLaunchKernelGGL(k_prefill_merge<128>, dim3(M, hq), dim3(128), 0, s, part, pml, out,
+            hipLaunchKernelGGL(k_prefill_merge<128>, dim3(M, hq), dim3(256), 0, s, part, pml, out,
                                M, hq, nsplit);
         else
-            hipLaunchKernelGGL(k_prefill_merge<64>, dim3(M, hq), dim3(64), 0, s, part, pml, out,
+            hipLaunchKernelGGL(k_prefill_merge<64>, dim3(M, hq), dim3(256), 0, s, part, pml, out,
                                M, hq, nsplit);
         TB_LAUNCHED();
     }

@@ -45,8 +45,8 @@ int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const flo
 // Causal attention of the M rows of q over cache positions 0 .. start + m; out [M][hq hd].
 // With scratch (prefill_attention_scratch bytes) the key range is split over
 // blocks when few query tiles meet a long cache; without, one block per tile
-// and head walks the whole range.
-int prefill_attention_splits(int start, int M, int hq);
+// and KV head walks the whole range.
+int prefill_attention_splits(int start, int M, int hq, int hkv);
 size_t prefill_attention_scratch(int M, int hq, int hd, int nsplit);
 int launch_prefill_attention(const float *q, const float *kc, const float *vc, float *out,
                              int start, int M, int hq, int hkv, int hd, int max_seq,

@@ -540,7 +540,7 @@ struct Decoder {
             TB_HIP(hipMemcpyAsync(pf_tok, tok32.data() + c0, (size_t)M * 4, hipMemcpyHostToDevice,
                                   st));
             const size_t ab = prefill_attention_scratch(
-                M, hq, hd, prefill_attention_splits(pos0, M, hq));
+                M, hq, hd, prefill_attention_splits(pos0, M, hq, hkv));
             if (ab > pf_attn_bytes) {
                 if ((rc = alloc(&pf_attn, ab))) return rc;
                 pf_attn_bytes = ab;
