@@ -1,4 +1,4 @@
-"""Parity of the batched INT4 projection on FP32 MFMA (M >= 16) with the CPU oracle.
+"""Parity of the batched INT4 projection (FP32 MFMA from M = 5) with the CPU oracle.
 
 The oracle's gemm_w4 restates the reference's gemm_w4a32_grouped
 (src/quantization/gemv.rs:1690-1725: one full GEMV per activation row), and
@@ -43,6 +43,12 @@ SHAPES = [
     (16, 7, 32, 32),          # one group per row, N below a wave's 16 rows
     (20, 64, 96, 32),         # K not a multiple of the 128-wide step
     (48, 200, 192, 64),       # K = 1.5 steps, group 64
+    (5, 4096, 4096, 32),      # verify-sized batches
+    (8, 14336, 4096, 32),
+    (7, 1000, 2048, 64),      # group 64
+    (9, 517, 1024, 32),       # four-row tiles 3 of 4 used, ragged N
+    (12, 96, 14336, 32),      # K split over many blocks
+    (6, 33, 96, 32),          # 3 chunks, N below a wave's 16 rows
 ]
 
 
@@ -149,13 +155,15 @@ def test_mfma_special_cases(cuda):
         np.testing.assert_allclose(y, np.broadcast_to(want, (m, n)), rtol=1e-5, atol=1e-4)
 
 
-def test_mfma_non_finite_propagate(cuda):
-    g = synth.rng(34)
-    m, n, k = 16, 128, 1024
+@pytest.mark.parametrize("m", [16, 6])
+def test_mfma_non_finite_propagate(cuda, m):
+    g = synth.rng(34, m)
+    n, k = 128, 1024
     w, s = synth.int4_weight(g, n, k, 32)
     x = synth.activations(g, m, k)
     x[3, 77] = np.nan
-    x[9, 500] = np.inf
+    x[m - 2, 500] = np.inf
+    x[m - 2, 900] = -np.inf
     ref = O.gemm_w4(x, w, s, None, group_size=32)
     y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), None, 32).cpu().numpy()
     assert np.array_equal(np.isnan(y), np.isnan(ref))

@@ -76,6 +76,7 @@ SHAPES = [
     (3, 1000, 2048),
     (4, 96, 64),        # one group per row
     (5, 300, 896),      # MFMA from M = 5
+    (9, 517, 192),      # MFMA path, ragged N over 2-byte aligned v2 rows
     (16, 4096, 4096),
     (64, 1031, 576),    # 9 groups, ragged N
 ]
