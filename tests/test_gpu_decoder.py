@@ -88,6 +88,17 @@ def test_small_decoder_variants(cuda, variant):
     run_parity(small(), 5, prefill=37, steps=12, **variant)
 
 
+@pytest.mark.parametrize("variant", [
+    dict(wkind=4, lmkind=32, gs=32),
+    dict(wkind=8, lmkind=8, gs=32),
+])
+def test_small_decoder_unfused_norms(cuda, variant, monkeypatch):
+    """TB_DECODER_UNFUSED=1: separate RMSNorm kernels instead of the fused
+    producer/consumer GEMV epilogues (read when the decoder is created)."""
+    monkeypatch.setenv("TB_DECODER_UNFUSED", "1")
+    run_parity(small(), 9, prefill=21, steps=8, **variant)
+
+
 @pytest.mark.parametrize("lmkind", [4, 32, 8])
 def test_decoder_group64_v2_blocks(cuda, lmkind):
     """Group 64 with every dimension a multiple of 64 (vocab 1024): QKV, O, down

@@ -60,7 +60,7 @@ struct Decoder {
     // keep v1 nibbles with scales rounded to binary16 at load: the same numbers
     // through the v1 GEMV, which streams faster than the 34-byte blocks.
     bool v2 = false;
-    bool fused = true;   // INT4: RMSNorms fused into the GEMVs (TB_DECODER_UNFUSED=1: separate)
+    bool fused = true;   // RMSNorms fused into the GEMVs (TB_DECODER_UNFUSED=1: separate)
     // Rows per GEMV block for QKV, O, gate/up, down, lm_head (0 = the GEMV's
     // default; TB_DECODER_J="qkv,o,gu,down,lm" overrides, for tuning sweeps).
     int rj[5] = {0, 0, 0, 0, 0};
@@ -225,16 +225,25 @@ struct Decoder {
         p.w1 = w2; p.rs1 = s2; p.rs1_len = s2 ? n : 0;
         p.res = res; p.y = y; p.m = 1; p.n = n; p.k = k;
         if (rope) p.rope = *rope;
+        if (fu) {
+            p.ssq_in = fu->ssq_in;
+            p.ssq_n = H / 16;
+            p.norm_h = H;
+            p.eps = eps;
+            p.rec_w = fu->rec_w;
+            p.xw_out = fu->xw_out;
+            p.ssq_out = fu->ssq_out;
+        }
         return dense_gemv(p, bits == 8 ? W_I8 : W_F32, epi, st);
     }
 
-    // The INT4 step with every RMSNorm fused into the GEMVs around it: the
-    // producer of x (embedding, O and down projections) writes the records of
-    // x * w_norm (and that product in f32 to xn, read only on the NaN/Inf
-    // path) and the 16-element sums of squares of x; the consumer (QKV,
-    // gate/up, lm_head) scales its dots by 1 / rms.  h's records come from
-    // the gate/up epilogue.  Kernels per layer: QKV, attention (split +
-    // merge), O, gate/up, down.
+    // The step with every RMSNorm fused into the GEMVs around it: the
+    // producer of x (embedding, O and down projections) writes x * w_norm in
+    // f32 to xn (INT4: also its records; the f32 copy is then read only on the
+    // NaN/Inf path) and the 16-element sums of squares of x; the consumer
+    // (QKV, gate/up, lm_head) scales its dots by 1 / rms.  INT4: h's records
+    // come from the gate/up epilogue.  Kernels per layer: QKV, attention
+    // (split + merge), O, gate/up, down.
     // The step's tail: greedy argmax, or the device sampler over the window.
     int enqueue_tail(bool sampled) {
         if (!sampled) return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
@@ -243,6 +252,8 @@ struct Decoder {
     }
 
     int enqueue_step_fused(bool sampled) {
+        const int wb = wbits;
+        const bool q4 = wb == 4;
         int rc = launch_embed_rec(state, embed, x, layers[0].in_norm, xn, xq_h, ssq, H, st);
         if (rc) return rc;
         for (int l = 0; l < L; ++l) {
@@ -252,46 +263,40 @@ struct Decoder {
             RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, hd};
             Fuse fq;
             fq.ssq_in = ssq;
-            rc = proj(4, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv, tq, H,
-                      EPI_ROPE, &ra, &fq, rj[0]);
+            rc = proj(wb, xn, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv, tq,
+                      H, EPI_ROPE, &ra, &fq, rj[0]);
             if (rc) return rc;
-            rc = launch_attention(state, qkv, kcl, vcl, part, attn, xq_a, hq, hkv, hd, max_seq,
-                                  st);
+            rc = launch_attention(state, qkv, kcl, vcl, part, attn, q4 ? xq_a : nullptr, hq, hkv,
+                                  hd, max_seq, st);
             if (rc) return rc;
             Fuse fo;
-            fo.rec_out = xq_h;
+            fo.rec_out = q4 ? xq_h : nullptr;
             fo.rec_w = y.post_norm;
             fo.xw_out = xn;
             fo.ssq_out = ssq;
-            rc = proj(4, attn, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H, hq * hd,
+            rc = proj(wb, attn, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H, hq * hd,
                       EPI_RESID, nullptr, &fo, rj[1]);
             if (rc) return rc;
             Fuse fg;
             fg.ssq_in = ssq;
-            fg.rec_out = xq_i;
-            rc = proj(4, xn, xq_h, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, h, I, H,
+            fg.rec_out = q4 ? xq_i : nullptr;
+            rc = proj(wb, xn, xq_h, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, h, I, H,
                       EPI_SWIGLU, nullptr, &fg, rj[2]);
             if (rc) return rc;
             Fuse fd;
-            fd.rec_out = xq_h;
+            fd.rec_out = q4 ? xq_h : nullptr;
             fd.rec_w = l + 1 < L ? layers[l + 1].in_norm : final_norm;
             fd.xw_out = xn;
             fd.ssq_out = ssq;
-            rc = proj(4, h, xq_i, y.down_w, y.down_s, nullptr, nullptr, nullptr, x, x, H, I,
+            rc = proj(wb, h, xq_i, y.down_w, y.down_s, nullptr, nullptr, nullptr, x, x, H, I,
                       EPI_RESID, nullptr, &fd, rj[3]);
             if (rc) return rc;
         }
-        if (lmbits == 4) {
-            Fuse fl;
-            fl.ssq_in = ssq;
-            rc = proj(4, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V, H,
-                      EPI_PLAIN, nullptr, &fl, rj[4]);
-        } else {
-            rc = launch_rmsnorm(state, nullptr, x, final_norm, xn, nullptr, H, eps, st);
-            if (rc) return rc;
-            rc = proj(lmbits, xn, nullptr, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits,
-                      V, H, EPI_PLAIN);
-        }
+        // lm_head: INT4, INT8 or fp32, always a fused-RMSNorm consumer of xn.
+        Fuse fl;
+        fl.ssq_in = ssq;
+        rc = proj(lmbits, xn, xq_h, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V, H,
+                  EPI_PLAIN, nullptr, &fl, rj[4]);
         if (rc) return rc;
         return enqueue_tail(sampled);
     }
@@ -299,7 +304,7 @@ struct Decoder {
     // Enqueues one decoder step (reference step_internal) on `st`.
     int enqueue_step(bool sampled = false) {
         const bool q4 = wbits == 4;
-        if (q4 && fused) return enqueue_step_fused(sampled);
+        if (fused) return enqueue_step_fused(sampled);
         int rc;
         for (int l = 0; l < L; ++l) {
             const Layer &y = layers[l];

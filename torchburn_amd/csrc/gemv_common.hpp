@@ -417,9 +417,9 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
             e.y[o] = outv;
         }
     }
-    if (EPI != EPI_ROPE && e.rec_out) {
-        // Records (and sums of squares) of this block's outputs, M == 1: quads
-        // of lanes build one 16-row half record each.
+    if (EPI != EPI_ROPE && (e.rec_out || e.xw_out || e.ssq_out)) {
+        // Records, y * rec_w in f32 and sums of squares of this block's
+        // outputs, M == 1: quads of lanes take one 16-row half each.
         const int t = threadIdx.x;
         // For M == 1 the slots of threads 0 .. rpb-1 are the rpb rows of the block.
         if (t < L.rpb) sh.out[row - row0] = live ? outv : 0.f;
@@ -431,8 +431,9 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
             float4 wv = make_float4(1.f, 1.f, 1.f, 1.f);
             if (ok && e.rec_w) wv = *reinterpret_cast<const float4 *>(e.rec_w + base + 4 * q);
             const float4 xv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
-            build_half_rec4(xv, q, ok, e.rec_out + (size_t)(base >> 5) * kXRecDwords,
-                            (base >> 4) & 1);
+            if (e.rec_out)
+                build_half_rec4(xv, q, ok, e.rec_out + (size_t)(base >> 5) * kXRecDwords,
+                                (base >> 4) & 1);
             if (ok && e.xw_out) *reinterpret_cast<float4 *>(e.xw_out + base + 4 * q) = xv;
             if (e.ssq_out) {
                 float sq = fmaf(yv.x, yv.x, fmaf(yv.y, yv.y, fmaf(yv.z, yv.z, yv.w * yv.w)));

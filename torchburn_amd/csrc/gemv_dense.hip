@@ -178,13 +178,25 @@ int launch(const DenseParams &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
     Layout L;
-    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L), TB_ERR_UNSUPPORTED,
+    const bool prod = p.xw_out || p.ssq_out;
+    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, prod ? 16 : 0), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: dense GEMV supports K <= " + std::to_string(kMaxWaves * 64 * 32));
     Epi e{};
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m;
     e.rs0 = p.rs0; e.rs1 = p.rs1; e.rs0_len = p.rs0_len; e.rs1_len = p.rs1_len;
     e.rope = p.rope;
+    e.ssq_in = p.ssq_in; e.ssq_n = p.ssq_n; e.eps = p.eps;
+    e.inv_h = p.norm_h > 0 ? 1.0f / (float)p.norm_h : 0.f;
+    e.rec_w = p.rec_w; e.xw_out = p.xw_out; e.ssq_out = p.ssq_out;
     e.any = static_cast<const float *>(p.w0);   // n * k / 4 >= n floats (k >= 32)
+    if (p.ssq_in)
+        TB_REQUIRE(p.m == 1 && p.ssq_n <= kMaxSsqPerThread * L.nwaves * 64, TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: fused RMSNorm input needs M == 1 and K == H");
+    if (prod)
+        TB_REQUIRE(p.m == 1 && EPI != EPI_ROPE && L.rpb % 16 == 0 && L.rpb <= kMaxRecRows &&
+                       p.n % 32 == 0,
+                   TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RMSNorm output needs M == 1, "
+                                       "N % 32 == 0 and 16-row blocks");
     if (EPI == EPI_ROPE)
         TB_REQUIRE(p.m == 1 && p.rope.hd % L.rpb == 0 && L.rpb % 2 == 0 && p.n % p.rope.hd == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: fused RoPE needs whole rotation pairs per block");
@@ -199,6 +211,9 @@ template <int WT, bool DUAL, int EPI>
 int dispatch_m(const DenseParams &p, hipStream_t st) {
     // Rows per block sized for ~16 loads of 16 bytes in flight per lane.
     if constexpr (WT == W_I8) {
+        // A fused-RMSNorm producer writes whole 16-row pieces: 16 rows per
+        // row group, so the K split over up to 8 waves stays available.
+        if (!DUAL && (p.xw_out || p.ssq_out)) return launch<WT, 1, 16, DUAL, EPI>(p, st);
         if (p.m <= 1) return launch<WT, 1, DUAL ? 4 : 8, DUAL, EPI>(p, st);
         return launch<WT, 2, DUAL ? 4 : 8, DUAL, EPI>(p, st);
     } else {
@@ -220,6 +235,8 @@ int dispatch_epi(const DenseParams &p, int epi, hipStream_t st) {
 int dense_gemv(const DenseParams &p, int wt, int epi, hipStream_t st) {
     TB_REQUIRE(p.m >= 1 && p.m <= kMaxRowsPerPass, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: dense GEMV pass takes 1..2 rows");
+    TB_REQUIRE(!(p.xw_out || p.ssq_out) || (wt == W_I8 && epi == EPI_RESID), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused RMSNorm outputs come from INT8 residual projections");
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: INT8/FP32 GEMV needs K % 32 == 0, got K=" + std::to_string(p.k));
     if (wt == W_I8) return dispatch_epi<W_I8>(p, epi, st);

@@ -24,6 +24,17 @@ struct DenseParams {
     float *y;           // [m, n]
     int m, n, k;
     RopeArgs rope;      // EPI_ROPE only
+    // Fused RMSNorm (M == 1), as W4Params.  Consumer: x holds x * w_norm and
+    // ssq_in [ssq_n] the sums of squares of x over 16-element pieces; the row
+    // dots are scaled by 1 / sqrt(sum / norm_h + eps) before the row scale.
+    // Producer (INT8 only; 16-row blocks): y * rec_w in f32 into xw_out and the
+    // 16-row sums of squares of y into ssq_out.
+    const float *ssq_in;
+    int ssq_n, norm_h;
+    float eps;
+    const float *rec_w;
+    float *xw_out;
+    float *ssq_out;
 };
 
 // One pass over m <= kMaxRowsPerPass activation rows; shapes validated by the

@@ -274,7 +274,8 @@ int launch(const W4Params &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
     Layout L;
-    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, p.rec_out ? 16 : 0), TB_ERR_UNSUPPORTED,
+    const bool prod = p.rec_out || p.xw_out || p.ssq_out;
+    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, prod ? 16 : 0), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32 GEMV supports K <= " + std::to_string(kMaxWaves * 64 * 32));
     Epi e{};
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m; e.rope = p.rope;
@@ -286,7 +287,7 @@ int launch(const W4Params &p, hipStream_t st) {
     if (p.ssq_in)
         TB_REQUIRE(p.m == 1 && p.ssq_n <= kMaxSsqPerThread * L.nwaves * 64, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: fused RMSNorm input needs M == 1 and K == H");
-    if (p.rec_out)
+    if (prod)
         TB_REQUIRE(p.m == 1 && EPI != EPI_ROPE && L.rpb % 16 == 0 && L.rpb <= kMaxRecRows &&
                        p.n % 32 == 0,
                    TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: records of the output need M == 1, "
