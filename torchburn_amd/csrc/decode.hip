@@ -304,18 +304,23 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
     const float4 *v4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * max_seq * C4 + c;
     const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
     float4 kr[NI], vr[NI], qr[GP];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int p = pbase + i * RPL + rg;
-        const bool ok = p < seq;
-        kr[i] = ok ? load_nt_f4(reinterpret_cast<const float *>(k4 + (size_t)p * C4))
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[i] = ok ? load_nt_f4(reinterpret_cast<const float *>(v4 + (size_t)p * C4))
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    // q, then every K row, then every V row: the scores and the softmax wait
+    // only for K, and run while V is still arriving.
 #pragma unroll
     for (int g = 0; g < GP; ++g)
         qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int p = pbase + i * RPL + rg;
+        kr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(k4 + (size_t)p * C4))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int p = pbase + i * RPL + rg;
+        vr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(v4 + (size_t)p * C4))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 
     float v[NV];
 #pragma unroll
@@ -491,30 +496,28 @@ __global__ __launch_bounds__(64) void k_attn_merge(const DecState *__restrict__ 
     }
 }
 
-// Merge of one query head's tiles with every partial load in one round trip:
-// 256 threads = NSG split groups x C4 float4 columns; each thread loads the
-// (o, m, l) of its splits s = sg, sg + NSG, ... (NB per pass, all in flight),
-// folds them with its own running max, then the split groups combine through
-// LDS: M = max m_s, L = sum e^(m_s - M) l_s, o = sum e^(m_s - M) o_s / max(L,
-// 1e-30) (src/llm/decoder.rs:1148-1213).  Writes o and the head's x chunk
-// records for the O projection.
+// Merge of one 32-column chunk of one query head's tiles: grid (hq, HD / 32),
+// 64 threads = 8 split groups x 8 float4 columns.  Thread (sg, c) folds the
+// (o, m, l) of splits sg, sg + 8, ... with all of a pass's loads in flight;
+// the groups combine through LDS: M = max m_s, L = sum e^(m_s - M) l_s,
+// o = sum e^(m_s - M) o_s / max(L, 1e-30) (src/llm/decoder.rs:1148-1213).
+// Lanes 0..7 then hold the chunk and write o and its x chunk record.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_merge_wide(const DecState *__restrict__ st,
+__global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restrict__ st,
                                                          const float *__restrict__ part,
                                                          float *__restrict__ out,
                                                          uint32_t *__restrict__ xq, int nsplit) {
-    constexpr int C4 = HD / 4, NSG = 256 / C4, NB = 12;
+    constexpr int NSG = 8, NB = 12;
     constexpr size_t rec = HD + 4;
-    __shared__ float4 so4[NSG][C4];
+    __shared__ float4 so4[NSG][8];
     __shared__ float smx[NSG], sl[NSG];
-    __shared__ float so[HD];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int c = tid % C4, sg = tid / C4;
+    const int h = blockIdx.x, ck = blockIdx.y, tid = threadIdx.x;
+    const int c = tid & 7, sg = tid >> 3;
     const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;
     const float *ph = part + (size_t)h * nsplit * rec;
     float M = -FLT_MAX, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < used; s0 += NSG * NB) {   // one pass up to NSG * NB tiles
+    for (int s0 = 0; s0 < used; s0 += NSG * NB) {
         float4 ov[NB];
         float mv[NB], lv[NB];
 #pragma unroll
@@ -522,7 +525,8 @@ __global__ __launch_bounds__(256) void k_attn_merge_wide(const DecState *__restr
             const int sp = s0 + sg + u * NSG;
             const bool ok = sp < used;
             const float *pp = ph + (size_t)(ok ? sp : 0) * rec;
-            ov[u] = ok ? *reinterpret_cast<const float4 *>(pp + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            ov[u] = ok ? *reinterpret_cast<const float4 *>(pp + 32 * ck + 4 * c)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
             mv[u] = ok ? pp[HD] : -FLT_MAX;
             lv[u] = ok ? pp[HD + 1] : 0.f;
         }
@@ -549,11 +553,11 @@ __global__ __launch_bounds__(256) void k_attn_merge_wide(const DecState *__restr
         sl[sg] = L;
     }
     __syncthreads();
-    if (tid < C4) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < 8) {
         float mg = -FLT_MAX;
 #pragma unroll
         for (int g = 0; g < NSG; ++g) mg = fmaxf(mg, smx[g]);
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
         float lt = 0.f;
 #pragma unroll
         for (int g = 0; g < NSG; ++g) {
@@ -567,20 +571,10 @@ __global__ __launch_bounds__(256) void k_attn_merge_wide(const DecState *__restr
         }
         const float inv = 1.0f / fmaxf(lt, 1e-30f);
         o = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-        reinterpret_cast<float4 *>(out + (size_t)h * HD)[tid] = o;
-        reinterpret_cast<float4 *>(so)[tid] = o;
+        reinterpret_cast<float4 *>(out + (size_t)h * HD + 32 * ck)[tid] = o;
     }
-    __syncthreads();
-    if (xq) {
-        constexpr int NREC = HD / 32;   // records of this head: 8 lanes each
-        const int rc = tid >> 3, sub = tid & 7;
-        if (rc < 8) {   // whole 8-lane groups of the first wave
-            const bool live = rc < NREC;
-            const float4 vv = live ? reinterpret_cast<const float4 *>(so + rc * 32)[sub]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            build_xrec8(vv, sub, live, xq + ((size_t)h * NREC + rc) * kXRecDwords);
-        }
-    }
+    // the whole wave takes part (8-lane groups); lanes 0..7 hold the chunk
+    if (xq) build_xrec8(o, tid & 7, tid < 8, xq + ((size_t)h * (HD / 32) + ck) * kXRecDwords);
 }
 
 // Greedy argmax, stage 1: per block the largest logit, lowest index on ties
@@ -1035,16 +1029,16 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
             else if (gp == 4) TB_ATTN_REG(128, 4);
             else TB_ATTN_REG(128, 8);
             TB_LAUNCHED();
-            hipLaunchKernelGGL(k_attn_merge_wide<128>, dim3(hq), dim3(256), 0, s, st, part, out, xq,
-                               ns);
+            hipLaunchKernelGGL(k_attn_merge_chunk<128>, dim3(hq, 4), dim3(64), 0, s, st, part, out,
+                               xq, ns);
         } else {
             if (gp == 1) TB_ATTN_REG(64, 1);
             else if (gp == 2) TB_ATTN_REG(64, 2);
             else if (gp == 4) TB_ATTN_REG(64, 4);
             else TB_ATTN_REG(64, 8);
             TB_LAUNCHED();
-            hipLaunchKernelGGL(k_attn_merge_wide<64>, dim3(hq), dim3(256), 0, s, st, part, out, xq,
-                               ns);
+            hipLaunchKernelGGL(k_attn_merge_chunk<64>, dim3(hq, 2), dim3(64), 0, s, st, part, out,
+                               xq, ns);
         }
 #undef TB_ATTN_REG
     } else if (hd == 128) {
