@@ -310,10 +310,13 @@ int launch(const W4Params &p, hipStream_t st) {
 
 template <bool DUAL, int EPI, bool V2 = false>
 int dispatch_m(const W4Params &p, hipStream_t st) {
-    // x stays in VGPRs, so one pass takes <= 2 rows.  Rows per block: 8 for a
-    // gate/up pair (16 weight loads in flight per lane), 16 for one matrix.
+    // x stays in VGPRs, so one pass takes <= 2 rows.  Rows per block: 16 for
+    // one matrix; for a gate/up pair 4 (8 weight loads in flight per lane:
+    // twice the waves, each with half the dot products left to do once its
+    // data is in, which shortens the kernel's tail), or 8 when the epilogue
+    // writes records (16-row pieces: with 4 rows that takes 8-wave blocks).
     if (p.m <= 1) {
-        const int j = p.rows_j ? p.rows_j : (DUAL ? 8 : 16);
+        const int j = p.rows_j ? p.rows_j : (DUAL ? (p.rec_out ? 8 : 4) : 16);
         if (j == 4) return launch<1, 4, DUAL, EPI, V2>(p, st);
         if (j == 16) return launch<1, 16, DUAL, EPI, V2>(p, st);
         return launch<1, 8, DUAL, EPI, V2>(p, st);
