@@ -6,9 +6,14 @@
 // fused_swiglu_mlp_w8a32 (src/quantization/fused_ops.rs:8-133), and the fp32
 // lm_head of the per-layer Python path (python/torchburn/llm/model.py:499-500).
 //
-// Same work mapping as the INT4 kernel (w4_gemv.hip): 32-element chunks, one per
-// lane for the life of the block, split-K over waves, J rows per block, a
-// transpose reduction and one epilogue.  Differences:
+// Same work mapping as the INT4 kernel (w4_gemv.hip): 32 elements per lane for
+// the life of the block, split-K over waves, J rows per block, a transpose
+// reduction and one epilogue.  Differences:
+//   * a lane's 32 elements are LD 16-byte pieces strided by the lanes of its
+//     row (piece cl + sw * i of its wave's K slice), so each load instruction
+//     reads one contiguous run of the row; 32 contiguous elements per lane
+//     would spread one instruction over 64 cache lines (fp32 lm_head: 2.2
+//     TB/s);
 //   * x stays in VGPRs as f32 (32 per activation row), loaded from x directly;
 //   * INT8: two non-temporal 16-byte loads per chunk; w ^ 0x80808080 turns each
 //     signed byte into w + 128, which v_cvt_f32_ubyte{0..3} converts in one
@@ -38,13 +43,17 @@ struct DenseGemv {
         uint32_t ok;
     };
 
+    static constexpr int PE = 16 / BPE;             // elements per 16-byte piece
+
     const DenseParams &p;
     const Layout &L;
-    int lane, wave, grp, rr, cl, chunk;
+    int lane, wave, grp, rr, cl;
     bool act;
-    size_t bpr, boff;
+    size_t bpr;
+    int piece[LD];        // the lane's pieces (clamped into the row)
+    uint32_t pmask;       // bit i: piece i lies inside K
     float xr[M][32];
-    float xs[M];   // 128 * sum of the chunk (INT8 offset correction)
+    float xs[M];   // 128 * sum of the lane's elements (INT8 offset correction)
 
     __device__ __forceinline__ DenseGemv(const DenseParams &pp, const Layout &ll) : p(pp), L(ll) {
         lane = threadIdx.x & 63;
@@ -52,20 +61,33 @@ struct DenseGemv {
         grp = wave / L.nks;
         rr = lane >> L.b;
         cl = lane & ((1 << L.b) - 1);
-        const int chunk_raw = (wave - grp * L.nks) * L.sw + cl;
-        act = (cl < L.sw) && (chunk_raw < L.c);
-        chunk = act ? chunk_raw : 0;
+        const int pbase = (wave - grp * L.nks) * L.sw * LD;   // first piece of the K slice
+        const int npieces = L.c * LD;
+        pmask = 0u;
+#pragma unroll
+        for (int i = 0; i < LD; ++i) {
+            const int pc = pbase + cl + L.sw * i;
+            const bool in = cl < L.sw && pc < npieces;
+            pmask |= in ? (1u << i) : 0u;
+            piece[i] = in ? pc : npieces - 1;
+        }
+        act = pmask != 0u;
         bpr = (size_t)p.k * BPE;
-        boff = (size_t)chunk * 32 * BPE;
     }
 
+    // x pieces of the lane (PE floats each); pieces past K read as zero.
     __device__ __forceinline__ void issue_x(float4 (&raw)[M][8]) const {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const bool live = act && m < p.m;
-            const float4 *xp = reinterpret_cast<const float4 *>(p.x + (size_t)m * p.k + chunk * 32);
+            const float *xm = p.x + (size_t)(m < p.m ? m : 0) * p.k;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) raw[m][i] = live ? xp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int i = 0; i < LD; ++i) {
+                const float4 *xp = reinterpret_cast<const float4 *>(xm + (size_t)piece[i] * PE);
+                const bool live = ((pmask >> i) & 1u) && m < p.m;
+#pragma unroll
+                for (int t = 0; t < PE / 4; ++t)
+                    raw[m][i * (PE / 4) + t] = live ? xp[t] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
     }
 
@@ -97,7 +119,7 @@ struct DenseGemv {
                 const uint8_t *w = static_cast<const uint8_t *>(d ? p.w1 : p.w0);
 #pragma unroll
                 for (int i = 0; i < LD; ++i)
-                    bt.q[d][j][i] = load_nt16(w + (size_t)row * bpr + boff + 16 * i);
+                    bt.q[d][j][i] = load_nt16(w + (size_t)row * bpr + (size_t)piece[i] * 16);
             }
         }
     }
