@@ -207,7 +207,8 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
  * projections (no reference counterpart: the reference converts x inside each
  * GEMV).  A record holds 32 activations as 24-bit fixed-point integers in six
  * 4-bit limb planes plus a power-of-two step and an integer sum per 16-element
- * half: 112 bytes per 32 elements, tb_x_records_bytes(m, k) in total.  tb_xquant builds them from x [M, K];
+ * half: 112 bytes per 32 elements, tb_x_records_bytes(m, k) in total, laid out per row as 7 planes
+ * of 16 bytes per chunk.  The layout is internal to this library.  tb_xquant builds them from x [M, K];
  * the *_xq GEMVs read them instead of building their own (x itself is still
  * read when a chunk holds NaN/Inf).  residual may be NULL.
  */

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const DecState *__restrict__ st
         o.w = __fmul_rn(__fmul_rn(v.w, inv), ww.w);
         reinterpret_cast<float4 *>(xn)[i4] = o;
     }
-    if (xq) build_xrec8(o, sub, live, xq + (size_t)rec * kXRecDwords);
+    if (xq) build_xrec8(o, sub, live, xq, c, live ? rec : 0);
 }
 
 // First input of the fused-RMSNorm step: x = embed[token], x * w in f32 and as
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void k_embed_rec(const DecState *__restrict__ 
     }
     const float4 p = make_float4(v.x * ww.x, v.y * ww.y, v.z * ww.z, v.w * ww.w);
     if (live) reinterpret_cast<float4 *>(xw)[rec * 8 + sub] = p;
-    build_xrec8(p, sub, live, xq + (size_t)rec * kXRecDwords);
+    build_xrec8(p, sub, live, xq, H / 32, live ? rec : 0);
     float sq = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, v.w * v.w)));
     sq += __shfl_xor(sq, 1);
     sq += __shfl_xor(sq, 2);
@@ -492,7 +492,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(const DecState *__restrict__ 
         const bool live = rc < NREC;
         const float4 vv = live ? reinterpret_cast<const float4 *>(so + rc * 32)[sub]
                                : make_float4(0.f, 0.f, 0.f, 0.f);
-        build_xrec8(vv, sub, live, xq + ((size_t)h * NREC + rc) * kXRecDwords);
+        build_xrec8(vv, sub, live, xq, (int)gridDim.x * NREC, h * NREC + (live ? rc : 0));
     }
 }
 
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restr
         reinterpret_cast<float4 *>(out + (size_t)h * HD + 32 * ck)[tid] = o;
     }
     // the whole wave takes part (8-lane groups); lanes 0..7 hold the chunk
-    if (xq) build_xrec8(o, tid & 7, tid < 8, xq + ((size_t)h * (HD / 32) + ck) * kXRecDwords);
+    if (xq) build_xrec8(o, tid & 7, tid < 8, xq, (int)(gridDim.x * gridDim.y), h * (HD / 32) + ck);
 }
 
 // Greedy argmax, stage 1: per block the largest logit, lowest index on ties

@@ -320,8 +320,8 @@ __device__ __forceinline__ int quad_xor2(int v) {
     return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
 }
 
-__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *rec,
-                                                int half);
+__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *row, int nc,
+                                                int chunk, int half);
 
 // LDS a GEMV block needs besides the partials: wave sums of squares, and the
 // block's outputs while their records are built.
@@ -432,8 +432,7 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
             if (ok && e.rec_w) wv = *reinterpret_cast<const float4 *>(e.rec_w + base + 4 * q);
             const float4 xv = make_float4(yv.x * wv.x, yv.y * wv.y, yv.z * wv.z, yv.w * wv.w);
             if (e.rec_out)
-                build_half_rec4(xv, q, ok, e.rec_out + (size_t)(base >> 5) * kXRecDwords,
-                                (base >> 4) & 1);
+                build_half_rec4(xv, q, ok, e.rec_out, e.n >> 5, base >> 5, (base >> 4) & 1);
             if (ok && e.xw_out) *reinterpret_cast<float4 *>(e.xw_out + base + 4 * q) = xv;
             if (e.ssq_out) {
                 float sq = fmaf(yv.x, yv.x, fmaf(yv.y, yv.y, fmaf(yv.z, yv.z, yv.w * yv.w)));
@@ -452,13 +451,16 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
 // 2^(e - 23), the precision an f32 partial sum of these elements has.  Limb l
 // of U_i = X_i + 2^23 (bits [4l, 4l + 4)) goes to nibble (i & 7) of dword
 // limb[l][i >> 3] (i = element index in the 32-element chunk), the nibble
-// order of the packed weights.  Record layout (kXRecDwords): 24 limb dwords
-// (limb l at 4l .. 4l + 3; dwords 0-1 of a limb hold half 0, 2-3 half 1), then
+// order of the packed weights.  A record (kXRecDwords) is 7 quads of 4
+// dwords: quad l < 6 holds limb l (dwords 0-1 half 0, 2-3 half 1), quad 6
 // {step of half 0, step of half 1, sum X of half 0, sum X of half 1}; a step is
-// NaN when its half holds NaN/Inf.  All 4 lanes must call this; `rec` is
+// NaN when its half holds NaN/Inf.  The records of a row of nc chunks are
+// stored by quad: quad i of chunk c at row + (i * nc + c) * 4, so a GEMV wave,
+// one chunk per lane, reads each quad of 64 consecutive chunks as one
+// contiguous KiB.  All 4 lanes must call this; the record of `chunk` is
 // written when `live`.
-__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *rec,
-                                                int half) {
+__device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *row, int nc,
+                                                int chunk, int half) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
     int fin = 1;
     float amax = 0.f;
@@ -492,20 +494,23 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
 #pragma unroll
     for (int l = 0; l < 6; ++l) lw[l] |= (uint32_t)quad_xor1((int)lw[l]);
     if (!live) return;
+    uint32_t *rec = row + (size_t)chunk * 4;
+    const size_t quad = (size_t)nc * 4;   // dwords between quads of one record
     if ((q & 1) == 0) {
 #pragma unroll
-        for (int l = 0; l < 6; ++l) rec[l * 4 + half * 2 + (q >> 1)] = lw[l];
+        for (int l = 0; l < 6; ++l) rec[l * quad + half * 2 + (q >> 1)] = lw[l];
     }
     if (q == 0) {
-        rec[24 + half] = __float_as_uint(fin ? ldexpf(1.0f, e - 23) : __builtin_nanf(""));
-        rec[26 + half] = (uint32_t)ssum;
+        rec[6 * quad + half] = __float_as_uint(fin ? ldexpf(1.0f, e - 23) : __builtin_nanf(""));
+        rec[6 * quad + 2 + half] = (uint32_t)ssum;
     }
 }
 
 // One whole chunk record from 8 consecutive lanes; lane `sub` (0..7) holds
-// elements 4*sub .. 4*sub + 3 of the 32-element chunk.
-__device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32_t *out) {
-    build_half_rec4(v, sub & 3, live, out, sub >> 2);
+// elements 4*sub .. 4*sub + 3 of chunk `chunk` of a row of nc chunks.
+__device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32_t *row, int nc,
+                                            int chunk) {
+    build_half_rec4(v, sub & 3, live, row, nc, chunk, sub >> 2);
 }
 
 }  // namespace gemv

@@ -101,10 +101,12 @@ struct W4Gemv {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const int mm = m < p.m ? m : 0;
-            const uint32_t *rp = p.xq + ((size_t)mm * L.c + chunk) * kXRecDwords;
+            // quad i of this chunk's record: row base + (i * c + chunk) * 4 dwords
+            const u32x4 *rp = reinterpret_cast<const u32x4 *>(p.xq + (size_t)mm * L.c * kXRecDwords) +
+                              chunk;
 #pragma unroll
-            for (int i = 0; i < 6; ++i) xr.limbs[m][i] = reinterpret_cast<const u32x4 *>(rp)[i];
-            xr.tail[m] = reinterpret_cast<const u32x4 *>(rp)[6];
+            for (int i = 0; i < 6; ++i) xr.limbs[m][i] = rp[(size_t)i * L.c];
+            xr.tail[m] = rp[(size_t)6 * L.c];
         }
     }
 
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(256) void k_xquant(const float *__restrict__ x,
     const int row = live ? rec / c : 0, ch = live ? rec - row * c : 0;
     const float4 v = live ? reinterpret_cast<const float4 *>(x + (size_t)row * k + ch * 32)[sub]
                           : make_float4(0.f, 0.f, 0.f, 0.f);
-    build_xrec8(v, sub, live, xq + (size_t)rec * kXRecDwords);
+    build_xrec8(v, sub, live, xq + (size_t)row * c * kXRecDwords, c, ch);
 }
 
 template <int M, int J, bool DUAL, int EPI, bool V2 = false>

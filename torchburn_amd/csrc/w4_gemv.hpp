@@ -26,13 +26,16 @@ constexpr int kMaxRowsPerPass = 2;
 // An x chunk record: 32 activations as 24-bit fixed-point integers in six
 // 4-bit limb planes (24 dwords), then {step of elements 0-15, step of 16-31,
 // integer sum of 0-15, of 16-31} (steps as f32 bits, NaN when the half holds
-// NaN/Inf): 112 bytes, 16-byte aligned.  Built once per activation vector by
-// xquant() or by the producing kernel, read by every block of the GEMV.
+// NaN/Inf): 112 bytes in 7 quads of 4 dwords.  A row's records are stored by
+// quad (quad i of chunk c at (i * k/32 + c) * 4 dwords from the row's start),
+// so a GEMV wave, one chunk per lane, reads each quad of 64 chunks as one
+// contiguous KiB.  Built once per activation vector by xquant() or by the
+// producing kernel, read by every block of the GEMV.
 constexpr int kXRecDwords = 28;
 
 struct W4Params {
     const float *x;    // [m, k] activations (read only by the NaN/Inf path)
-    const uint32_t *xq; // [m, k/32, kXRecDwords] chunk records of x (xquant)
+    const uint32_t *xq; // [m, 7, k/32, 4] chunk records of x (xquant), by quad
     const uint8_t *w0; // [n, k/2] packed nibbles (gate when dual)
     const float *s0;   // [n, k/group] scales
     const float *b0;   // [n] bias or null
@@ -66,7 +69,7 @@ struct W4Params {
 // p.w1 is set.  Shapes are validated by the caller.
 int w4_gemv(W4Params p, int epi, hipStream_t st);
 
-// Chunk records of x [m, k] (k % 32 == 0) into xq [m, k/32, kXRecDwords].
+// Chunk records of x [m, k] (k % 32 == 0) into xq [m, 7, k/32, 4] (by quad).
 int xquant(const float *x, uint32_t *xq, int m, int k, hipStream_t st);
 
 }  // namespace tb
