@@ -89,6 +89,18 @@ def test_small_decoder_variants(cuda, variant):
 
 
 @pytest.mark.parametrize("variant", [
+    dict(wkind=8, lmkind=32, gs=32),
+    dict(wkind=4, lmkind=8, gs=32),
+])
+def test_decoder_ragged_k_slices(cuda, variant):
+    """hidden = intermediate = 2080 (65 chunks: two waves of 33 lanes, the last
+    lane of the second idle): the INT8 / fp32 GEMVs' strided 16-byte pieces
+    end inside a wave, and the fused-RMSNorm producers write 130 16-row pieces."""
+    run_parity(small(hidden=2080, intermediate=2080, vocab=777), 12, prefill=19, steps=6,
+               **variant)
+
+
+@pytest.mark.parametrize("variant", [
     dict(wkind=4, lmkind=32, gs=32),
     dict(wkind=8, lmkind=8, gs=32),
 ])

@@ -19,7 +19,10 @@ def rel(a, b):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 128256, 4096), (2, 1000, 896),
-                                   (3, 77, 64), (1, 4096, 14336)])
+                                   (3, 77, 64), (1, 4096, 14336),
+                                   # K slices that end inside a wave's pieces: 152 chunks on
+                                   # 3 waves of 51 lanes, 65 chunks on 2 waves of 33
+                                   (1, 300, 4864), (2, 77, 2080), (1, 50, 96)])
 def test_w8_linear_matches_oracle(cuda, m, n, k):
     print(f"case w8a32_linear m={m} n={n} k={k}", flush=True)
     g = synth.rng(21, m, n, k)
