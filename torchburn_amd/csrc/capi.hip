@@ -129,7 +129,7 @@ static size_t xq_bytes(int64_t m, int64_t k) {
     return (size_t)m * (size_t)(k / 32) * kXRecDwords * sizeof(uint32_t);
 }
 
-// M rows in passes of at most kMaxRowsPerPass (the GEMV keeps x in VGPRs).
+// M rows in passes of at most kMaxW4RowsPerPass (the GEMV keeps x in VGPRs).
 // xq: chunk records of all m rows of p.x (built here when build_xq is set).
 static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
                    hipStream_t st) {
@@ -138,9 +138,9 @@ static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
         if (rc) return rc;
     }
     const int64_t rec = (int64_t)(p.k / 32) * kXRecDwords;
-    for (int64_t r0 = 0; r0 < m; r0 += kMaxRowsPerPass) {
+    for (int64_t r0 = 0; r0 < m; r0 += kMaxW4RowsPerPass) {
         W4Params q = p;
-        q.m = (int)((m - r0) < kMaxRowsPerPass ? (m - r0) : kMaxRowsPerPass);
+        q.m = (int)((m - r0) < kMaxW4RowsPerPass ? (m - r0) : kMaxW4RowsPerPass);
         q.x = p.x + r0 * p.k;
         q.xq = xq + r0 * rec;
         q.y = p.y + r0 * (int64_t)p.n;

@@ -312,7 +312,7 @@ int launch(const W4Params &p, hipStream_t st) {
 
 template <bool DUAL, int EPI, bool V2 = false>
 int dispatch_m(const W4Params &p, hipStream_t st) {
-    // x stays in VGPRs, so one pass takes <= 2 rows.  Rows per block: 16 for
+    // x stays in VGPRs, so one pass takes <= 4 rows.  Rows per block: 16 for
     // one matrix; for a gate/up pair 4 (8 weight loads in flight per lane:
     // twice the waves, each with half the dot products left to do once its
     // data is in, which shortens the kernel's tail), or 8 when the epilogue
@@ -323,7 +323,10 @@ int dispatch_m(const W4Params &p, hipStream_t st) {
         if (j == 16) return launch<1, 16, DUAL, EPI, V2>(p, st);
         return launch<1, 8, DUAL, EPI, V2>(p, st);
     }
-    return launch<2, DUAL ? 4 : 8, DUAL, EPI, V2>(p, st);
+    // 2 and 3-4 activation rows: fewer weight rows per block as the records
+    // (28 VGPRs per activation row) and the dot products grow with M.
+    if (p.m <= 2) return launch<2, DUAL ? 4 : 8, DUAL, EPI, V2>(p, st);
+    return launch<4, DUAL ? 2 : 4, DUAL, EPI, V2>(p, st);
 }
 
 }  // namespace
@@ -337,8 +340,8 @@ int xquant(const float *x, uint32_t *xq, int m, int k, hipStream_t st) {
 }
 
 int w4_gemv(W4Params p, int epi, hipStream_t st) {
-    TB_REQUIRE(p.m >= 1 && p.m <= kMaxRowsPerPass, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: w4 GEMV pass takes 1..2 rows");
+    TB_REQUIRE(p.m >= 1 && p.m <= kMaxW4RowsPerPass, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4 GEMV pass takes 1..4 rows");
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4 GEMV needs K % 32 == 0");
     if (p.v2) {
         TB_REQUIRE(p.w1 == nullptr, TB_ERR_UNSUPPORTED,

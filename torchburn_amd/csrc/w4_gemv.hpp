@@ -21,7 +21,8 @@ struct RopeArgs {
 };
 
 // Activation rows per GEMV pass (x is held in VGPRs).
-constexpr int kMaxRowsPerPass = 2;
+constexpr int kMaxRowsPerPass = 2;     // INT8 / fp32 GEMV
+constexpr int kMaxW4RowsPerPass = 4;   // INT4 GEMV
 
 // An x chunk record: 32 activations as 24-bit fixed-point integers in six
 // 4-bit limb planes (24 dwords), then {step of elements 0-15, step of 16-31,
@@ -65,7 +66,7 @@ struct W4Params {
     float *ssq_out;
 };
 
-// One pass over m <= kMaxRowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
+// One pass over m <= kMaxW4RowsPerPass activation rows.  Epilogue EPI_SWIGLU is implied when
 // p.w1 is set.  Shapes are validated by the caller.
 int w4_gemv(W4Params p, int epi, hipStream_t st);
 
