@@ -64,7 +64,7 @@ TB_API const char *tb_version(void);
  * x f32 [M, K], w u8 [N, ceil(K/2)], scales f32 [N, ceil(K/gs)], bias f32 [N]
  * or NULL, out f32 [M, N].  group_size is 32 or 64 and must divide K (the
  * reference's quantizer requires the same, python/torchburn/quantization.py:75-79).
- * M <= 4 runs the GEMV kernels (passes of 2 rows); M >= 5 the FP32-MFMA
+ * M <= 4 runs the GEMV kernels (one pass of up to 4 rows); M >= 5 the FP32-MFMA
  * projection (weights dequantized in registers into the MFMA operand).
  */
 TB_API int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float *scales,
