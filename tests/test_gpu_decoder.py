@@ -83,6 +83,7 @@ def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=
     dict(wkind=8, lmkind=8, gs=32),
     dict(wkind=8, lmkind=32, gs=32),
     dict(wkind=4, lmkind=8, gs=32),
+    dict(wkind=8, lmkind=4, gs=32),
 ])
 def test_small_decoder_variants(cuda, variant):
     run_parity(small(), 5, prefill=37, steps=12, **variant)

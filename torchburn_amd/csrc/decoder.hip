@@ -304,7 +304,9 @@ struct Decoder {
     // Enqueues one decoder step (reference step_internal) on `st`.
     int enqueue_step(bool sampled = false) {
         const bool q4 = wbits == 4;
-        if (fused) return enqueue_step_fused(sampled);
+        // INT8 layers write no records, which an INT4 lm_head reads: that pair
+        // keeps the separate final RMSNorm of the unfused step.
+        if (fused && (wbits == 4 || lmbits != 4)) return enqueue_step_fused(sampled);
         int rc;
         for (int l = 0; l < L; ++l) {
             const Layer &y = layers[l];
