@@ -185,8 +185,10 @@ struct Decoder {
         return bits == 4 ? (size_t)n * (size_t)(k / gs) * 4 : (bits == 8 ? (size_t)n * 4 : 0);
     }
 
-    // Fused-RMSNorm wiring of an INT4 projection: the input side (records of
-    // x * xw, sums of squares) and the output side (records of y * rec_w).
+    // Fused-RMSNorm wiring of a projection: the input side (sums of squares of
+    // x; x * w_norm as records for INT4, in f32 for INT8 / fp32) and the output
+    // side (y * rec_w as records (INT4 only) and in f32, and the 16-row sums of
+    // squares of y).
     struct Fuse {
         const float *ssq_in = nullptr;
         uint32_t *rec_out = nullptr;
