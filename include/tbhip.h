@@ -62,10 +62,11 @@ TB_API const char *tb_version(void);
  * src/ffi/quantization_ffi.rs:56-85 -> src/quantization/packed_v2.rs:557-624
  * -> gemm_w4a32_grouped / gemv_w4a32_grouped (src/quantization/gemv.rs:1514-1725).
  * x f32 [M, K], w u8 [N, ceil(K/2)], scales f32 [N, ceil(K/gs)], bias f32 [N]
- * or NULL, out f32 [M, N].  group_size is 32 or 64 and must divide K (the
- * reference's quantizer requires the same, python/torchburn/quantization.py:75-79).
- * M <= 4 runs the GEMV kernels (one pass of up to 4 rows); M >= 5 the FP32-MFMA
- * projection (weights dequantized in registers into the MFMA operand).
+ * or NULL, out f32 [M, N].  Any K >= 1 and any even group_size (a short last
+ * group, as gemv.rs:1650-1660; groups start on byte boundaries).  K a multiple of 32 with a power-of-two group_size >= 32
+ * dividing K runs the streaming kernels: M <= 4 the GEMV (one pass of up to 4
+ * rows, K <= 16384), M >= 5 the FP32-MFMA projection (weights dequantized in
+ * registers into the MFMA operand); other shapes run the any-shape GEMV.
  */
 TB_API int tb_w4a32_grouped_linear(const float *x, const uint8_t *w_packed, const float *scales,
                             const float *bias, float *out, int64_t m, int64_t n, int64_t k,
@@ -224,10 +225,32 @@ TB_API int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t 
                               int64_t k, int64_t inter, int64_t group_size, void *stream);
 
 /*
+ * out[m, n] = (sum_k (nib(w[n, k]) - 8) * x[m, k]) * s[n] + bias[n]: the
+ * reference's per-channel w4a32_linear (binding src/ffi/quantization_ffi.rs:32-54,
+ * kernel src/quantization/gemv.rs:1066-1182; dispatched by the compile engine,
+ * src/engine/dispatch_op/d_quant.rs:109-125).  w u8 [N, ceil(K/2)] (v1 nibbles),
+ * s_len 1 (one per-tensor scale) or N; bias NULL or [N]; any K.
+ */
+TB_API int tb_w4a32_linear(const float *x, const uint8_t *w_packed, const float *scales,
+                           int64_t s_len, const float *bias, float *out, int64_t m, int64_t n,
+                           int64_t k, void *stream);
+
+/*
+ * f32 weights [N, K] -> v1 nibbles [N, ceil(K/2)] + one f32 scale per row [N] on
+ * the device: quantize_linear_weights_int4 (binding quantize_linear_int4,
+ * python/torchburn/quantization.py:44-50 -> src/quantization/fused_ops.rs:592-639),
+ * s = max|w| / 7 (1 when max|w| <= 1e-8), q = clamp(round_half_away(w * (1 / s)),
+ * -8, 7); an odd K pads the last byte with the nibble 8.
+ */
+TB_API int tb_quantize_weight_int4(const float *w, uint8_t *packed, float *scales, int64_t n,
+                                   int64_t k, void *stream);
+
+/*
  * out[m, n] = (sum_k x[m, k] * w[n, k]) * s[n] + bias[n]: the reference's
  * w8a32_linear (binding src/ffi/quantization_ffi.rs:8-30, kernel
  * src/quantization/gemv.rs:733-1061).  w i8 [N, K]; s_len 1 (one per-tensor
- * scale) or N; K must be a multiple of 32.
+ * scale) or N; any K (K a multiple of 32 up to 16384 runs the streaming GEMV,
+ * others the any-shape GEMV).
  */
 TB_API int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_t s_len,
                            const float *bias, float *out, int64_t m, int64_t n, int64_t k,
@@ -235,15 +258,21 @@ TB_API int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales,
 
 /*
  * INT8 SwiGLU MLP, fused_swiglu_mlp_w8a32 (binding src/ffi/quantization_ffi.rs:150-201,
- * kernel src/quantization/fused_ops.rs:8-133), with an optional residual add.
- * Per-channel scales [I] / [n_out]; h [M, I] in the library workspace.
+ * kernel src/quantization/fused_ops.rs:8-133), with an optional residual add:
+ *   h[j] = silu(dot(x, gate_j) * gs + gb[j]) * (dot(x, up_j) * us + ub[j]),
+ *   out = dot(h, down_n) * ds + db[n] [+ residual].
+ * Each projection's scales have *_s_len = 1 (one per-tensor scalar,
+ * fused_ops.rs:80-97) or N (per row) elements; biases may be NULL; any K and
+ * inter.  h [M, I] lives in the library workspace.
  */
 TB_API int tb_fused_swiglu_mlp_w8a32(const float *x, const int8_t *gate_w, const float *gate_s,
-                                     const float *gate_b, const int8_t *up_w, const float *up_s,
+                                     int64_t gate_s_len, const float *gate_b,
+                                     const int8_t *up_w, const float *up_s, int64_t up_s_len,
                                      const float *up_b, const int8_t *down_w,
-                                     const float *down_s, const float *down_b,
-                                     const float *residual, float *out, int64_t m, int64_t k,
-                                     int64_t inter, int64_t n_out, void *stream);
+                                     const float *down_s, int64_t down_s_len,
+                                     const float *down_b, const float *residual, float *out,
+                                     int64_t m, int64_t k, int64_t inter, int64_t n_out,
+                                     void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Decoder (replaces RustQwenDecoder, reference src/llm/decoder.rs:176-1374)   */
@@ -413,6 +442,15 @@ TB_API int tb_decoder_get_logits(tb_decoder *d, float *out);
 /* Seed of the sampling generator (no reference counterpart: the reference draws
  * from an unseeded rand::random). */
 TB_API int tb_decoder_set_seed(tb_decoder *d, uint64_t seed);
+
+/* Replaces the RoPE tables, which tb_decoder_create builds in f64 as
+ * RustQwenDecoder::new does (decoder.rs:334-350), with caller-built cos / sin
+ * [max_seq_len, head_dim] (host or device memory).  The reference's per-layer
+ * Python path, which runs INT8 and fp32-lm_head models, takes its tables from
+ * RotaryEmbedding in f32 (python/torchburn/llm/model.py:108-122); no
+ * counterpart on RustQwenDecoder. */
+TB_API int tb_decoder_set_rope_tables(tb_decoder *d, const float *cos_t, const float *sin_t,
+                                      int64_t rows, int64_t head_dim);
 
 /* Benchmark helper (no reference counterpart): n_steps greedy steps from
  * (first_token, offset) as back-to-back graph replays, timed with HIP events on

@@ -49,7 +49,16 @@ def lib():
         L.orc_swiglu_mlp_w4.argtypes = [_vp] * 11 + [_i64] * 5
         L.orc_gemv_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64]
         L.orc_quantize_int8.argtypes = [_f32p, _i8p, _f32p, _i64, _i64]
-        L.orc_swiglu_h_w8.argtypes = [_vp] * 6 + [_i64, _i64]
+        L.orc_swiglu_h_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
+                                      _i64]
+        L.orc_swiglu_mlp_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                                        _i64, _vp, _vp, _i64, _i64, _i64, _i64]
+        L.orc_gemv_w4_rows.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64]
+        L.orc_quantize_int4_rows.argtypes = [_f32p, _u8p, _f32p, _i64, _i64]
+        L.orc_rms_norm_torch.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
+        L.orc_attention_layer.argtypes = [_f32p, _vp, _vp, _f32p, _i64, _i64, _i64, _i64, _i64]
+        L.orc_decoder_set_rope_tables.argtypes = [_vp, _f32p, _f32p]
+        L.orc_decoder_set_layer_path.argtypes = [_vp, C.c_int]
         L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
         L.orc_gemv_f32.argtypes = [_vp, _vp, _vp, _i64, _i64]
         L.orc_rope_tables.argtypes = [_f32p, _f32p, _i64, _i64, C.c_double]
@@ -291,6 +300,62 @@ def gemv_w8(x, w, s, bias=None) -> np.ndarray:
     return y.reshape(*x.shape[:-1], n)
 
 
+def gemv_w4_rows(x, w, s, bias=None, k=None) -> np.ndarray:
+    """Per-channel w4a32_linear (gemv.rs:1066-1182), any number of x rows:
+    y = dot_f32_u4(x, w_row) * s + b, s of 1 or N elements."""
+    x = _c(x, np.float32)
+    k = x.shape[-1] if k is None else k
+    m = x.size // k
+    w, s, bias = _c(w, np.uint8), _c(s, np.float32).reshape(-1), _c(bias, np.float32)
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    xf = x.reshape(m, k)
+    for i in range(m):
+        row = np.ascontiguousarray(xf[i])
+        lib().orc_gemv_w4_rows(_p(row), _p(w), _p(s), s.size, _p(bias), y[i].ctypes.data, n, k)
+    return y.reshape(*x.shape[:-1], n)
+
+
+def quantize_int4_rows(w: np.ndarray):
+    """quantize_linear_weights_int4 (fused_ops.rs:592-639): packed (N, ceil(K/2))
+    and one scale per row."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    q = np.empty((n, (k + 1) // 2), np.uint8)
+    s = np.empty(n, np.float32)
+    lib().orc_quantize_int4_rows(w, q, s, n, k)
+    return q, s
+
+
+def swiglu_h_w8(x, gw, gsc, uw, usc, gb=None, ub=None) -> np.ndarray:
+    """The neuron loop of fused_swiglu_mlp_w8a32 (fused_ops.rs:71-113) for one
+    token: scales of 1 element are per-tensor scalars, biases may be None."""
+    x = _c(x, np.float32).reshape(-1)
+    gw, uw = _c(gw, np.int8), _c(uw, np.int8)
+    gsc, usc = _c(gsc, np.float32).reshape(-1), _c(usc, np.float32).reshape(-1)
+    gb, ub = _c(gb, np.float32), _c(ub, np.float32)
+    inter = gw.shape[0]
+    h = np.empty(inter, np.float32)
+    lib().orc_swiglu_h_w8(_p(x), _p(gw), _p(gsc), gsc.size, _p(gb), _p(uw), _p(usc), usc.size,
+                          _p(ub), _p(h), inter, x.size)
+    return h
+
+
+def swiglu_mlp_w8(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None) -> np.ndarray:
+    """fused_swiglu_mlp_w8a32 (fused_ops.rs:8-133) over every row of x."""
+    x = _c(x, np.float32)
+    k = x.shape[-1]
+    m = x.size // k
+    gw, uw, dw = _c(gw, np.int8), _c(uw, np.int8), _c(dw, np.int8)
+    gsc, usc, dsc = (_c(a, np.float32).reshape(-1) for a in (gsc, usc, dsc))
+    gb, ub, db = _c(gb, np.float32), _c(ub, np.float32), _c(db, np.float32)
+    inter, nout = gw.shape[0], dw.shape[0]
+    out = np.empty((m, nout), np.float32)
+    lib().orc_swiglu_mlp_w8(_p(x), _p(gw), _p(gsc), gsc.size, _p(gb), _p(uw), _p(usc), usc.size,
+                            _p(ub), _p(dw), _p(dsc), dsc.size, _p(db), _p(out), m, k, inter, nout)
+    return out.reshape(*x.shape[:-1], nout)
+
+
 def quantize_int8(w: np.ndarray):
     w = _c(w, np.float32)
     n, k = w.shape
@@ -304,6 +369,14 @@ def rms_norm(x, w, eps) -> np.ndarray:
     x, w = _c(x, np.float32), _c(w, np.float32)
     out = np.empty_like(x)
     lib().orc_rms_norm(x, w, out, x.size, eps)
+    return out
+
+
+def rms_norm_torch(x, w, eps) -> np.ndarray:
+    """F.rms_norm numerics of the per-layer Python path (model.py:91-98)."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rms_norm_torch(x, w, out, x.size, eps)
     return out
 
 
@@ -338,6 +411,17 @@ def attention(q, k_cache, v_cache, seq_len: int) -> np.ndarray:
     return out
 
 
+def attention_layer(q, k_cache, v_cache, seq_len: int) -> np.ndarray:
+    """The per-layer steps' attention (fused_ops.rs:823-858, 997-1040)."""
+    q = _c(q, np.float32)
+    k_cache, v_cache = _c(k_cache, np.float32), _c(v_cache, np.float32)
+    hq, hd = q.shape
+    hkv, max_seq, _ = k_cache.shape
+    out = np.empty_like(q)
+    lib().orc_attention_layer(q, _p(k_cache), _p(v_cache), out, hq, hkv, hd, max_seq, seq_len)
+    return out
+
+
 def argmax(v) -> int:
     return int(lib().orc_argmax(_c(v, np.float32), np.asarray(v).size))
 
@@ -347,9 +431,12 @@ class Decoder:
 
     Borrows the numpy weight arrays held in ``weights`` (kept alive here).
     wkind: 4 (INT4 grouped) or 8 (INT8 per-channel); lmkind: 4, 8 or 32 (fp32).
+    rope_tables: (cos, sin) f32 [max_seq, head_dim] replacing the f64 tables.
+    layer_path: the numerics of the reference's per-layer Python path
+    (orc_decoder_set_layer_path), which runs INT8 and fp32-lm_head models.
     """
 
-    def __init__(self, weights: dict, cfg: dict):
+    def __init__(self, weights: dict, cfg: dict, rope_tables=None, layer_path=False):
         self.cfg = cfg
         self.w = weights
         L = lib()
@@ -366,6 +453,11 @@ class Decoder:
                 _p(lw["o_s"]), _p(lw["post_norm"]), _p(lw["gate_w"]), _p(lw["gate_s"]),
                 _p(lw["up_w"]), _p(lw["up_s"]), _p(lw["down_w"]), _p(lw["down_s"]),
                 _p(lw.get("qkv_b")))
+        if rope_tables is not None:
+            c, sn = (_c(t, np.float32) for t in rope_tables)
+            assert c.shape == (cfg["max_seq"], cfg["head_dim"]) == sn.shape
+            L.orc_decoder_set_rope_tables(self.h, c, sn)
+        L.orc_decoder_set_layer_path(self.h, 1 if layer_path else 0)
 
     def step(self, token: int, offset: int) -> np.ndarray:
         L = lib()

@@ -433,6 +433,93 @@ ORC_API void orc_swiglu_mlp_w4(const float *x, const uint8_t *gw, const float *g
 }
 
 /* ------------------------------------------------------------------------ */
+/* Per-channel INT4: w4a32_linear, gemv.rs:1066-1182 (the compile engine's    */
+/* d_quant.rs:109-125 and python/torchburn/quantization.py:219-243):           */
+/*   y[r] = dot_f32_u4(x, w[r], k) * s + b,  s = s[r] (or s[0] when 1 element) */
+/* dot_f32_u4 AVX2 tier, gemv.rs:643-704: per 32-element chunk elements 0-7    */
+/* and 16-23 feed accumulator 0, 8-15 and 24-31 accumulator 1 (8 lanes each,  */
+/* fma); the two are added lane-wise, hsum256_ps_avx (gemv.rs:11-19: high +   */
+/* low 128, then movehl, then lane 1 + lane 0), then the scalar tail adds     */
+/* x * q element by element.                                                  */
+/* ------------------------------------------------------------------------ */
+static float hsum8(const float *v) {
+    float s4[4];
+    for (int i = 0; i < 4; ++i) s4[i] = v[i + 4] + v[i];
+    float a = s4[0] + s4[2], b = s4[1] + s4[3];
+    return a + b;
+}
+
+static inline float dot_f32_u4(const float *x, const uint8_t *w, int64_t len) {
+    float s0[8] = {0}, s1[8] = {0};
+    int64_t off = 0;
+    for (; off + 32 <= len; off += 32) {
+        float q[32];
+        for (int j = 0; j < 16; ++j) {
+            uint8_t b = w[off / 2 + j];
+            q[2 * j] = (float)((int)(b & 15) - 8);
+            q[2 * j + 1] = (float)((int)(b >> 4) - 8);
+        }
+        for (int l = 0; l < 8; ++l) s0[l] = fmaf(q[l], x[off + l], s0[l]);
+        for (int l = 0; l < 8; ++l) s1[l] = fmaf(q[8 + l], x[off + 8 + l], s1[l]);
+        for (int l = 0; l < 8; ++l) s0[l] = fmaf(q[16 + l], x[off + 16 + l], s0[l]);
+        for (int l = 0; l < 8; ++l) s1[l] = fmaf(q[24 + l], x[off + 24 + l], s1[l]);
+    }
+    float sum[8];
+    for (int l = 0; l < 8; ++l) sum[l] = s0[l] + s1[l];
+    float t = hsum8(sum);
+    for (; off < len; ++off) {
+        uint8_t b = w[off / 2];
+        int q = (off % 2 == 0) ? (int)(b & 15) - 8 : (int)(b >> 4) - 8;
+        t += x[off] * (float)q;
+    }
+    return t;
+}
+
+ORC_API void orc_gemv_w4_rows(const float *x, const uint8_t *w, const float *s, int64_t s_len,
+                              const float *bias, float *y, int64_t n, int64_t k) {
+    int64_t bpr = (k + 1) / 2;
+#pragma omp parallel for schedule(dynamic, 8)
+    for (int64_t r = 0; r < n; ++r) {
+        float sc = s_len > 1 ? s[r] : s[0];
+        y[r] = dot_f32_u4(x, w + r * bpr, k) * sc + (bias ? bias[r] : 0.f);
+    }
+}
+
+/* quantize_linear_weights_int4, fused_ops.rs:592-639: per row               */
+/* s = amax / 7 (1 when amax <= 1e-8), inv = 1 / s,                           */
+/* q = clamp(round_half_away(w * inv), -8, 7) + 8, two per byte (low nibble   */
+/* first), an odd K's last byte padded with the nibble 8.                     */
+ORC_API void orc_quantize_int4_rows(const float *w, uint8_t *packed, float *s, int64_t n,
+                                    int64_t k) {
+    int64_t kp = (k + 1) / 2;
+    for (int64_t r = 0; r < n; ++r) {
+        const float *row = w + r * k;
+        float amax = 0.f;
+        for (int64_t i = 0; i < k; ++i) {
+            float a = fabsf(row[i]);
+            if (a > amax) amax = a;
+        }
+        float sc = amax > 1e-8f ? amax / 7.0f : 1.0f;
+        float inv = 1.0f / sc;
+        s[r] = sc;
+        for (int64_t b = 0; b < kp; ++b) {
+            int q[2];
+            for (int h = 0; h < 2; ++h) {
+                int64_t e = 2 * b + h;
+                if (e < k) {
+                    float v = roundf(row[e] * inv);
+                    v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
+                    q[h] = (int)v + 8;
+                } else {
+                    q[h] = 8;
+                }
+            }
+            packed[r * kp + b] = (uint8_t)((q[0] & 15) | ((q[1] & 15) << 4));
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* a18: INT8 W8A32.  dot_f32_i8_avx512 gemv.rs:280-324 and the 8-row kernel   */
 /* gemv.rs:147-270 share one per-row structure: two 16-lane accumulators over */
 /* 32-element chunks, summed, then 16-element chunks, lane reduce, scalar     */
@@ -493,27 +580,50 @@ ORC_API void orc_quantize_int8(const float *w, int8_t *q, float *s, int64_t n, i
     }
 }
 
-/* SwiGLU MLP with INT8 weights, fused_ops.rs:8-133: the same neuron formula  */
-/* with the a18 row dot, then the INT8 down GEMV.                             */
+/* SwiGLU MLP with INT8 weights, fused_ops.rs:8-133: per neuron j            */
+/*   g = dot(x, gate_j) * gs + gb,  u = dot(x, up_j) * us + ub                 */
+/* (fused_ops.rs:101-105; a scale slice of one element is a per-tensor scalar, */
+/* fused_ops.rs:80-97; absent biases are 0), h_j = silu(g) * u, then the INT8  */
+/* down GEMV with its own scale length and bias (fused_ops.rs:117-128).        */
 HOT static void swiglu_w8_rows(const float *x, const int8_t *gw, const float *gsc,
-                               const int8_t *uw, const float *usc, float *h, int64_t j0,
-                               int64_t j1, int64_t k) {
+                               int64_t gs_len, const float *gb, const int8_t *uw,
+                               const float *usc, int64_t us_len, const float *ub, float *h,
+                               int64_t j0, int64_t j1, int64_t k) {
     for (int64_t j = j0; j < j1; ++j) {
-        float g = dot_i8_row(x, gw + j * k, k) * gsc[j];
-        float u = dot_i8_row(x, uw + j * k, k) * usc[j];
+        float gsj = gs_len > 1 ? gsc[j] : gsc[0];
+        float usj = us_len > 1 ? usc[j] : usc[0];
+        float g = dot_i8_row(x, gw + j * k, k) * gsj + (gb ? gb[j] : 0.f);
+        float u = dot_i8_row(x, uw + j * k, k) * usj + (ub ? ub[j] : 0.f);
         float silu = g / (1.0f + expf(-g));
         h[j] = silu * u;
     }
 }
 
-ORC_API void orc_swiglu_h_w8(const float *x, const int8_t *gw, const float *gsc,
-                             const int8_t *uw, const float *usc, float *h, int64_t inter,
+ORC_API void orc_swiglu_h_w8(const float *x, const int8_t *gw, const float *gsc, int64_t gs_len,
+                             const float *gb, const int8_t *uw, const float *usc,
+                             int64_t us_len, const float *ub, float *h, int64_t inter,
                              int64_t k) {
     int64_t ch = rayon_chunk(inter);
 #pragma omp parallel for schedule(dynamic, 1)
     for (int64_t c = 0; c < (inter + ch - 1) / ch; ++c)
-        swiglu_w8_rows(x, gw, gsc, uw, usc, h, c * ch, (c + 1) * ch < inter ? (c + 1) * ch : inter,
-                       k);
+        swiglu_w8_rows(x, gw, gsc, gs_len, gb, uw, usc, us_len, ub, h, c * ch,
+                       (c + 1) * ch < inter ? (c + 1) * ch : inter, k);
+}
+
+/* fused_swiglu_mlp_w8a32 over m tokens (fused_ops.rs:52-131: one token at a  */
+/* time, h then gemv_w8a32 of the down projection).                           */
+ORC_API void orc_swiglu_mlp_w8(const float *x, const int8_t *gw, const float *gsc,
+                               int64_t gs_len, const float *gb, const int8_t *uw,
+                               const float *usc, int64_t us_len, const float *ub,
+                               const int8_t *dw, const float *dsc, int64_t ds_len,
+                               const float *db, float *out, int64_t m, int64_t k, int64_t inter,
+                               int64_t nout) {
+    float *h = (float *)malloc((size_t)(inter > 0 ? inter : 1) * sizeof(float));
+    for (int64_t t = 0; t < m; ++t) {
+        orc_swiglu_h_w8(x + t * k, gw, gsc, gs_len, gb, uw, usc, us_len, ub, h, inter, k);
+        orc_gemv_w8(h, dw, dsc, ds_len, db, out + t * nout, nout, inter);
+    }
+    free(h);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -530,6 +640,22 @@ ORC_API void orc_rms_norm(const float *x, const float *w, float *out, int64_t n,
     float inv = 1.0f / rms;
     for (int64_t i = 0; i < nc * 16; ++i) out[i] = (x[i] * inv) * w[i];
     for (int64_t i = nc * 16; i < n; ++i) out[i] = (x[i] / rms) * w[i];
+}
+
+/* RMSNorm of the reference's per-layer Python path, python/torchburn/llm/    */
+/* model.py:91-98 (F.rms_norm): y = (x * rsqrt(mean(x^2) + eps)) * w in f32.  */
+/* The sum of squares is taken in 16 lanes and a tree, as a vectorised CPU    */
+/* reduction does; torch's exact lane order is not pinned at the bit level.   */
+ORC_API void orc_rms_norm_torch(const float *x, const float *w, float *out, int64_t n,
+                                float eps) {
+    float acc[L16] = {0};
+    int64_t nc = n / 16;
+    for (int64_t c = 0; c < nc; ++c)
+        for (int i = 0; i < L16; ++i) acc[i] = fmaf(x[c * 16 + i], x[c * 16 + i], acc[i]);
+    float tot = tree16(acc);
+    for (int64_t i = nc * 16; i < n; ++i) tot += x[i] * x[i];
+    float r = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int64_t i = 0; i < n; ++i) out[i] = (x[i] * r) * w[i];
 }
 
 /* dot_f32_f32 AVX-512 tier, fused_ops.rs:646-664 (len >= 16), else scalar.  */
@@ -624,10 +750,37 @@ static void attend_head(const float *q, const float *kb, const float *vb, float 
     }
 }
 
+/* The attention of the per-layer steps, fused_ops.rs:997-1040 (INT4) and     */
+/* 823-858 (INT8): every position 0..seq_len-1 (no single-position shortcut,  */
+/* no 32768 cap), inv = 1 / sum with no clamp, out += w * v rounded twice.    */
+static void attend_head_layer(const float *q, const float *kb, const float *vb, float *out,
+                              float *scores, int64_t seq_len, int64_t hd) {
+    for (int64_t d = 0; d < hd; ++d) out[d] = 0.f;
+    float scale = 1.0f / sqrtf((float)hd);
+    float mx = -INFINITY;
+    for (int64_t t = 0; t < seq_len; ++t) {
+        float sc = dot_f32(q, kb + t * hd, hd) * scale;
+        scores[t] = sc;
+        if (sc > mx) mx = sc;
+    }
+    float sum = 0.f;
+    for (int64_t t = 0; t < seq_len; ++t) {
+        float e = expf(scores[t] - mx);
+        scores[t] = e;
+        sum += e;
+    }
+    float inv = 1.0f / sum;
+    for (int64_t t = 0; t < seq_len; ++t) {
+        float wt = scores[t] * inv;
+        const float *v = vb + t * hd;
+        for (int64_t d = 0; d < hd; ++d) out[d] += wt * v[d];
+    }
+}
+
 /* q: [hq, hd]; k_cache/v_cache: [hkv, max_seq, hd]; out: [hq, hd]. */
-ORC_API void orc_attention(const float *q, const float *k_cache, const float *v_cache,
-                           float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
-                           int64_t seq_len) {
+static void attention_any(const float *q, const float *k_cache, const float *v_cache,
+                          float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
+                          int64_t seq_len, int layer_path) {
     int64_t per = hq / (hkv > 0 ? hkv : 1);
     if (per < 1) per = 1;
 #pragma omp parallel
@@ -636,11 +789,28 @@ ORC_API void orc_attention(const float *q, const float *k_cache, const float *v_
 #pragma omp for schedule(static)
         for (int64_t h = 0; h < hq; ++h) {
             int64_t kvh = h / per;
-            attend_head(q + h * hd, k_cache + kvh * max_seq * hd, v_cache + kvh * max_seq * hd,
-                        out + h * hd, scores, seq_len, hd);
+            if (layer_path)
+                attend_head_layer(q + h * hd, k_cache + kvh * max_seq * hd,
+                                  v_cache + kvh * max_seq * hd, out + h * hd, scores, seq_len, hd);
+            else
+                attend_head(q + h * hd, k_cache + kvh * max_seq * hd,
+                            v_cache + kvh * max_seq * hd, out + h * hd, scores, seq_len, hd);
         }
         free(scores);
     }
+}
+
+ORC_API void orc_attention(const float *q, const float *k_cache, const float *v_cache,
+                           float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
+                           int64_t seq_len) {
+    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 0);
+}
+
+/* The per-layer steps' attention (attend_head_layer) for q [hq, hd]. */
+ORC_API void orc_attention_layer(const float *q, const float *k_cache, const float *v_cache,
+                                 float *out, int64_t hq, int64_t hkv, int64_t hd,
+                                 int64_t max_seq, int64_t seq_len) {
+    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 1);
 }
 
 /* a17: greedy argmax, decoder.rs:914-925 (strict >, lowest index wins).      */
@@ -674,8 +844,9 @@ ORC_API void orc_repetition_penalty(float *logits, int64_t V, const int64_t *rec
 }
 
 /* sample_logits, decoder.rs:908-1020, with the uniform u supplied:          */
-/*  greedy (temperature not finite or <= 0, or top_k == 1): first index of   */
-/*  the largest raw logit (NaN never chosen);                                */
+/*  greedy (temperature not finite or <= 0, or top_k == 1): orc_argmax, the  */
+/*  reference's scan from logits[0] with strict > (a NaN at index 0 wins, a  */
+/*  NaN elsewhere is never chosen);                                          */
 /*  else k = clamp(top_k, 1, V) candidates, non-finite logits as -inf, taken */
 /*  by (value descending, index ascending) and visited in that order;         */
 /*  p_i = exp((v_i - v_0) * (1/T)); nucleus: keep while the normalised mass  */
@@ -693,11 +864,8 @@ ORC_API int64_t orc_sample_logits(const float *logits, int64_t V, float temperat
                                   int64_t top_k, float top_p, float u, int64_t *kept_out) {
     if (V <= 0) return 0;
     if (!isfinite(temperature) || temperature <= 0.f || top_k == 1) {
-        int64_t bi = -1;
-        for (int64_t i = 0; i < V; ++i)
-            if (!isnan(logits[i]) && (bi < 0 || logits[i] > logits[bi])) bi = i;
         if (kept_out) *kept_out = 1;
-        return bi < 0 ? 0 : bi;
+        return orc_argmax(logits, V); /* decoder.rs:914-925: a NaN at index 0 wins */
     }
     int64_t k = top_k < 1 ? 1 : (top_k > V ? V : top_k);
     orc_item *it = (orc_item *)malloc((size_t)V * sizeof(orc_item));
@@ -869,7 +1037,8 @@ typedef struct {
 typedef struct {
     int64_t L, H, I, hq, hkv, hd, V, gs, max_seq;
     int wkind, lmkind;
-    int use_v2; /* decoder.rs:361-390 */
+    int use_v2;     /* decoder.rs:361-390 */
+    int layer_path; /* numerics of the per-layer Python path (orc_decoder_set_layer_path) */
     uint8_t *lm_w2;
     float eps;
     const float *embed, *final_norm;
@@ -967,6 +1136,24 @@ ORC_API void orc_decoder_set_kv_len(orc_decoder *d, int64_t n) {
     if (n > d->kv_used) d->kv_used = n;
 }
 
+/* Caller-built RoPE tables [max_seq, hd] replace the f64 ones of           */
+/* decoder.rs:334-350: the per-layer Python path takes cos / sin from         */
+/* RotaryEmbedding (python/torchburn/llm/model.py:108-122), whose angle       */
+/* pos * inv_freq is an f32 product.                                          */
+ORC_API void orc_decoder_set_rope_tables(orc_decoder *d, const float *cos_t,
+                                         const float *sin_t) {
+    memcpy(d->cos_t, cos_t, (size_t)(d->max_seq * d->hd) * sizeof(float));
+    memcpy(d->sin_t, sin_t, (size_t)(d->max_seq * d->hd) * sizeof(float));
+}
+
+/* 1: the step composes the per-layer Python path that the reference runs    */
+/* when its native decoder does not apply (INT8 weights or an fp32 lm_head,  */
+/* python/torchburn/llm/engine.py:133-151): F.rms_norm (model.py:91-98,      */
+/* orc_rms_norm_torch) and the per-layer steps' attention (fused_ops.rs:      */
+/* 823-858, 997-1040); the residual adds, projections and MLP are the same   */
+/* kernels as the native step.  0 (default): RustQwenDecoder::step_internal. */
+ORC_API void orc_decoder_set_layer_path(orc_decoder *d, int on) { d->layer_path = on; }
+
 /* projection_gemv, decoder.rs:1029-1049 (v1 path). */
 static void proj(const orc_decoder *d, int kind, const float *x, const void *w, const float *s,
                  const float *b, float *y, int64_t n, int64_t k) {
@@ -995,7 +1182,10 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
     if (offset + 1 > d->kv_used) d->kv_used = offset + 1;
     for (int64_t l = 0; l < d->L; ++l) {
         const orc_layer *y = &d->layers[l];
-        orc_rms_norm(d->x, y->in_norm, d->xn, H, d->eps);
+        if (d->layer_path)
+            orc_rms_norm_torch(d->x, y->in_norm, d->xn, H, d->eps);
+        else
+            orc_rms_norm(d->x, y->in_norm, d->xn, H, d->eps);
         if (d->use_v2)
             orc_gemv_w4_v2(d->xn, y->qkv_w2, y->qkv_b, d->qkv, tq, H);
         else
@@ -1008,26 +1198,32 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
             memcpy(kc + (h * d->max_seq + offset) * hd, k + h * hd, (size_t)hd * 4);
             memcpy(vc + (h * d->max_seq + offset) * hd, v + h * hd, (size_t)hd * 4);
         }
-        orc_attention(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1);
+        attention_any(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1, d->layer_path);
         if (d->use_v2)
             orc_gemv_w4_v2(d->att, y->o_w2, NULL, d->o, H, qd);
         else
             proj(d, d->wkind, d->att, y->o_w, y->o_s, NULL, d->o, H, qd);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->o[i];
-        orc_rms_norm(d->x, y->post_norm, d->xn, H, d->eps);
+        if (d->layer_path)
+            orc_rms_norm_torch(d->x, y->post_norm, d->xn, H, d->eps);
+        else
+            orc_rms_norm(d->x, y->post_norm, d->xn, H, d->eps);
         if (d->wkind == 4)
             orc_swiglu_h_w4(d->xn, (const uint8_t *)y->gate_w, y->gate_s, NULL,
                             (const uint8_t *)y->up_w, y->up_s, NULL, d->h, d->I, H, d->gs);
         else
-            orc_swiglu_h_w8(d->xn, (const int8_t *)y->gate_w, y->gate_s,
-                            (const int8_t *)y->up_w, y->up_s, d->h, d->I, H);
+            orc_swiglu_h_w8(d->xn, (const int8_t *)y->gate_w, y->gate_s, d->I, NULL,
+                            (const int8_t *)y->up_w, y->up_s, d->I, NULL, d->h, d->I, H);
         if (d->use_v2)
             orc_gemv_w4_v2(d->h, y->down_w2, NULL, d->dn, H, d->I);
         else
             proj(d, d->wkind, d->h, y->down_w, y->down_s, NULL, d->dn, H, d->I);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->dn[i];
     }
-    orc_rms_norm(d->x, d->final_norm, d->xn, H, d->eps);
+    if (d->layer_path)
+        orc_rms_norm_torch(d->x, d->final_norm, d->xn, H, d->eps);
+    else
+        orc_rms_norm(d->x, d->final_norm, d->xn, H, d->eps);
     if (d->lm_w2)
         orc_gemv_w4_v2(d->xn, d->lm_w2, NULL, d->logits, d->V, H);
     else

@@ -6,6 +6,13 @@ the same seeded weights and the same prefilled KV cache (copy_kv_cache_from_tens
 decoder.rs:479-523); every step's logits are compared (max|d| / max|ref|) and the
 greedy token sequences must be identical.  The top-1/top-2 logit margin of the
 oracle is printed per run.
+
+Configs 4 (fp32 lm_head) and 5-INT8 are models the reference's native decoder
+does not take (decoder.rs:252-256; engine.py:133-151 routes them through the
+per-layer Python path), so those runs compare against the oracle in its
+per-layer-path mode: RoPE tables built as RotaryEmbedding builds them
+(model.py:108-122, f32 angle; passed to both decoders), F.rms_norm numerics
+and the per-layer steps' attention (fused_ops.rs:823-858, 997-1040).
 """
 import numpy as np
 import pytest
@@ -13,7 +20,7 @@ import torch
 
 from oracle import oracle as O
 from torchburn_amd import synth
-from torchburn_amd.decoder import decoder_from_weights
+from torchburn_amd.decoder import decoder_from_weights, rotary_tables_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -28,17 +35,20 @@ def small(**kw):
 
 
 def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=256,
-               check_generate=True):
+               check_generate=True, layer_path=False):
     print(f"case decoder cfg={cfg} wkind={wkind} lmkind={lmkind} gs={gs} prefill={prefill} "
-          f"steps={steps}", flush=True)
+          f"steps={steps} layer_path={layer_path}", flush=True)
     w = synth.decoder_weights(cfg, seed, wkind, lmkind, gs)
     ocfg = dict(num_layers=cfg["num_layers"], hidden=cfg["hidden"],
                 intermediate=cfg["intermediate"], num_heads=cfg["num_heads"],
                 num_kv_heads=cfg["num_kv_heads"], head_dim=cfg["head_dim"], vocab=cfg["vocab"],
                 group_size=gs, max_seq=max_seq, rope_theta=cfg["rope_theta"], eps=cfg["eps"],
                 wkind=wkind, lmkind=lmkind)
-    ref = O.Decoder(w, ocfg)
+    tabs = rotary_tables_f32(max_seq, cfg["head_dim"], cfg["rope_theta"]) if layer_path else None
+    ref = O.Decoder(w, ocfg, rope_tables=tabs, layer_path=layer_path)
     dec = decoder_from_weights(w, cfg, group_size=gs, max_seq_len=max_seq)
+    if layer_path:
+        dec.set_rope_tables(*tabs)
     if prefill:
         kv = synth.kv_prefill(cfg, seed, prefill, max_seq)
         for li, (k, v) in enumerate(kv):
@@ -55,6 +65,9 @@ def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=
         worst = max(worst, float(np.abs(lg - lo).max() / np.abs(lo).max()))
         srt = np.sort(lo)
         margins.append(float(srt[-1] - srt[-2]))
+        if steps >= 32:
+            print(f"step {i}: token {O.argmax(lo)} top-1/top-2 margin {margins[-1]:.4g} "
+                  f"rel err {float(np.abs(lg - lo).max() / np.abs(lo).max()):.3g}", flush=True)
         nxt = O.argmax(lo)
         assert am == nxt, f"step {i}: GPU argmax {am} != oracle {nxt} (margin {margins[-1]})"
         ref_tokens.append(tok)
@@ -180,9 +193,10 @@ def test_decoder_eos_and_sampling(cuda):
 
 @pytest.mark.timeout(900)
 def test_config4_qwen05b_fp32_lm_head_greedy_64(cuda):
-    """Qwen2.5-0.5B shape, INT4 g32, fp32 lm_head, KV 2048, 64 steps."""
+    """Qwen2.5-0.5B shape, INT4 g32, fp32 lm_head, KV 2048, 64
+    steps, against the per-layer-path oracle (the path the reference runs it on)."""
     run_parity(synth.QWEN_0_5B, 0x7B + 4, wkind=4, lmkind=32, gs=32, prefill=2048, steps=64,
-               max_seq=2048 + 64, check_generate=True)
+               max_seq=2048 + 64, check_generate=True, layer_path=True)
 
 
 @pytest.mark.timeout(900)
@@ -194,6 +208,15 @@ def test_config5_llama8b_int4_greedy_64(cuda):
 
 @pytest.mark.timeout(900)
 def test_config5_llama8b_int8_greedy_64(cuda):
-    """BASELINE config 5 repeat: INT8 per-channel weights and lm_head."""
+    """BASELINE config 5 repeat: INT8 per-channel weights and lm_head, against the
+    per-layer-path oracle (the path the reference runs INT8 on)."""
     run_parity(synth.LLAMA3_8B, 0x7B + 5, wkind=8, lmkind=8, prefill=4096, steps=64,
-               max_seq=4096 + 64, check_generate=False)
+               max_seq=4096 + 64, check_generate=False, layer_path=True)
+
+
+@pytest.mark.parametrize("variant", [dict(wkind=4, lmkind=32), dict(wkind=8, lmkind=8)])
+def test_small_decoder_layer_path(cuda, variant):
+    """Caller-built f32 RoPE tables (set_rope_tables) at positions in the
+    thousands, where they differ from the f64 tables by ~1e-4, against the
+    per-layer-path oracle; check_generate replays the graphs with the new tables."""
+    run_parity(small(), 13, prefill=3000, steps=6, max_seq=3010, layer_path=True, **variant)

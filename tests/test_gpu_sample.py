@@ -30,7 +30,7 @@ CASES = [
 def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
     print(f"case sample_logits V={V} T={T} top_k={k} top_p={top_p} penalty={pen}", flush=True)
     g = np.random.default_rng(V + k)
-    for trial in range(6):
+    for trial in range(7):
         lg = (g.standard_normal(V) * 3).astype(np.float32)
         if trial == 1:
             lg[g.integers(0, V, 20)] = np.nan
@@ -39,6 +39,9 @@ def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
             lg[:] = np.round(lg)                  # many ties
         if trial == 3:
             lg[:] = 0.0                           # all equal
+        if trial == 4:
+            lg[0] = np.nan                        # greedy keeps index 0 (decoder.rs:914-925)
+            lg[g.integers(1, V, 3)] = np.nan
         recent = list(g.integers(0, V, 30)) + [V + 5, -1]
         seed, counter = int(g.integers(0, 2 ** 63)), int(g.integers(0, 1000))
         tok, u = tb.sample_logits(torch.from_numpy(lg).to(cuda), T, k, top_p, pen, recent,

@@ -45,19 +45,47 @@ def test_w8_per_tensor_scale(cuda):
     assert rel(y, O.gemv_w8(x, w, s)) < 1e-4
 
 
-def test_w8_swiglu_mlp_matches_oracle(cuda):
-    g = synth.rng(23)
-    m, k, inter = 1, 1024, 2048
+@pytest.mark.parametrize("m,k,inter,bias,scalar", [
+    (1, 1024, 2048, False, ""),          # per-row scales, no biases
+    (1, 1024, 2048, True, ""),           # biases on gate, up and down
+    (1, 1024, 2048, True, "gud"),        # one per-tensor scale on every projection
+    (3, 512, 1536, True, "g"),           # mixed: scalar gate scale, per-row up / down
+    (2, 4096, 14336, False, "d"),        # Llama-3-8B MLP shape, scalar down scale
+])
+def test_w8_swiglu_mlp_matches_oracle(cuda, m, k, inter, bias, scalar):
+    """fused_swiglu_mlp_w8a32 (fused_ops.rs:8-133) with the reference's optional
+    biases and its per-tensor scale branch (gs_len == 1, fused_ops.rs:80-97)."""
+    print(f"case w8 swiglu mlp m={m} k={k} inter={inter} bias={bias} scalar={scalar}", flush=True)
+    g = synth.rng(23, m, k, inter)
     x = synth.activations(g, m, k)
     gw, gsc = synth.int8_weight(g, inter, k)
     uw, usc = synth.int8_weight(g, inter, k)
     dw, dsc = synth.int8_weight(g, k, inter)
-    h = O.lib()  # noqa: F841  (loads the oracle)
-    hh = np.empty(inter, np.float32)
-    O.lib().orc_swiglu_h_w8(x.ctypes.data, gw.ctypes.data, gsc.ctypes.data, uw.ctypes.data,
-                            usc.ctypes.data, hh.ctypes.data, inter, k)
-    ref = O.gemv_w8(hh[None], dw, dsc)
-    T = lambda a: torch.from_numpy(a).to(cuda)
-    out = tb.fused_swiglu_mlp_w8a32(T(x), T(gw), T(gsc), None, T(uw), T(usc), None, T(dw),
-                                    T(dsc), None).cpu().numpy()
+    one = lambda s: s[:1].copy()
+    gsc = one(gsc) if "g" in scalar else gsc
+    usc = one(usc) if "u" in scalar else usc
+    dsc = one(dsc) if "d" in scalar else dsc
+    nb = lambda n: g.normal(0, 0.1, n).astype(np.float32) if bias else None
+    gb, ub, db = nb(inter), nb(inter), nb(k)
+    ref = O.swiglu_mlp_w8(x, gw, gsc, uw, usc, dw, dsc, gb=gb, ub=ub, db=db)
+    T = lambda a: None if a is None else torch.from_numpy(a).to(cuda)
+    out = tb.fused_swiglu_mlp_w8a32(T(x), T(gw), T(gsc), T(gb), T(uw), T(usc), T(ub), T(dw),
+                                    T(dsc), T(db)).cpu().numpy()
     assert rel(out, ref) < 1e-4
+
+
+def test_w8_swiglu_mlp_rejects_bad_scales(cuda):
+    """A scale vector that is neither per-tensor nor per-row is refused before
+    any device read (the kernel would otherwise read past it)."""
+    g = synth.rng(24)
+    x = synth.activations(g, 1, 256)
+    gw, gsc = synth.int8_weight(g, 512, 256)
+    uw, usc = synth.int8_weight(g, 512, 256)
+    dw, dsc = synth.int8_weight(g, 256, 512)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    with pytest.raises(tb.UnsupportedOpError):
+        tb.fused_swiglu_mlp_w8a32(T(x), T(gw), T(gsc[:7]), None, T(uw), T(usc), None, T(dw),
+                                  T(dsc), None)
+    with pytest.raises(tb.UnsupportedOpError):
+        tb.fused_swiglu_mlp_w8a32(T(x), T(gw[:, :128]), T(gsc), None, T(uw), T(usc), None,
+                                  T(dw), T(dsc), None)

@@ -14,17 +14,35 @@ budgets are reproduced here):
   swiglu             float64 closed form via torch.nn.functional.silu
   gemv_w8            the dot_f32_i8 KAT (tests/parity/int8.rs:24-37), float64,
                      quality budget (int8.rs:41-67)
+  swiglu_w8          float64 closed form with biases, per-row and per-tensor
+                     scales (fused_ops.rs:8-133); a dropped bias or a per-row
+                     read of a scalar scale fails it
+  gemv_w4_rows       per-channel w4a32_linear (gemv.rs:1066-1182): float64 with
+                     odd K and short K, per-row and scalar scales, bias;
+                     one-hot x returns (q - 8) * s exactly
+  quantize_int4_rows numpy closed form, ties away from zero, odd-K padding
+                     nibble 8, zero rows -> scale 1 (fused_ops.rs:592-639)
+  gemv_f32           float64; one-hot x returns a column exactly; integer
+                     weights and x = 1 give exact row sums
   quantize_int8      numpy closed form with ties away from zero and the 1e-8
                      zero-row threshold (fused_ops.rs:554-589)
   rms_norm           the reference's KAT (tests/parity/decoder.rs:14-29) and
                      torch.nn.functional.rms_norm in float64
+  rms_norm_torch     torch.nn.functional.rms_norm in float32 on the CPU (the
+                     per-layer path's own op) within 2 ulp, and float64
   rope               RoPE as a complex rotation in float64 (a different formula),
                      pos 0 is the identity, pair norms preserved
   attention          torch scaled_dot_product_attention(enable_gqa) in float64;
-                     seq_len 1 returns v; identical keys give mean(V)
+                     seq_len 1 returns v; identical keys give mean(V); the same
+                     for the per-layer steps' variant (attention_layer)
   argmax             decoder.rs:32-40 KAT, ties -> lowest index
+  f32 RoPE tables    (torchburn_amd.decoder.rotary_tables_f32, the per-layer
+                     path's tables) cos / sin of the float32 angle within 1 ulp,
+                     the angle within f32 rounding of pos * theta^(-2i/d)
   decoder step       an independent float64 torch model built from library ops
-                     (rms_norm, complex RoPE, SDPA, silu) on a small config; at
+                     (rms_norm, complex RoPE, SDPA, silu) on a small config, for
+                     INT4 and INT8 projections and INT4 / INT8 / fp32 lm_heads,
+                     and with caller tables + the per-layer numerics; at
                      group 64 with every dimension a multiple of 64 the model uses
                      binary16-rounded QKV / O / down / lm_head scales (the
                      reference's v2 repack) and the f32-scale model is shown to differ
@@ -182,6 +200,94 @@ def test_swiglu_mlp_vs_float64():
     assert rel(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("k", [1000, 7, 64])
+def test_gemv_f32_vs_float64(k):
+    """orc_gemv_f32 (fp32 lm_head, model.py:499-500): float64, exact special cases.
+    k = 1000 ends in an 8-element tail, k = 7 takes the scalar branch."""
+    g = np.random.default_rng(k)
+    n = 37
+    x = g.standard_normal(k).astype(np.float32)
+    w = g.standard_normal((n, k)).astype(np.float32)
+    assert rel(O.gemv_f32(x, w), w.astype(np.float64) @ x.astype(np.float64)) < 1e-6
+    for j in (0, k // 2, k - 1):
+        e = np.zeros(k, np.float32)
+        e[j] = 1.0
+        assert np.array_equal(O.gemv_f32(e, w), w[:, j])
+    wi = g.integers(-50, 50, (n, k)).astype(np.float32)
+    assert np.array_equal(O.gemv_f32(np.ones(k, np.float32), wi), wi.sum(1))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("scalar", ["", "gud", "u"])
+def test_swiglu_w8_vs_float64(bias, scalar):
+    """fused_swiglu_mlp_w8a32 (fused_ops.rs:8-133): g = dot * gs + gb,
+    u = dot * us + ub (a 1-element scale is one per-tensor scalar,
+    fused_ops.rs:80-97), h = silu(g) * u, out = dot(h, down) * ds + db."""
+    g = np.random.default_rng(11 + bias + len(scalar))
+    m, k, inter = 2, 160, 96
+    x = g.standard_normal((m, k)).astype(np.float32)
+    gw, gsc = synth.int8_weight(g, inter, k)
+    uw, usc = synth.int8_weight(g, inter, k)
+    dw, dsc = synth.int8_weight(g, k, inter)
+    gsc = gsc[:1].copy() if "g" in scalar else gsc
+    usc = usc[:1].copy() if "u" in scalar else usc
+    dsc = dsc[:1].copy() if "d" in scalar else dsc
+    nb = (lambda n: g.normal(0, 0.5, n).astype(np.float32)) if bias else (lambda n: None)
+    gb, ub, db = nb(inter), nb(inter), nb(k)
+    D = lambda a: np.asarray(a, np.float64)
+    z = lambda b, n: np.zeros(n) if b is None else D(b)
+    sc = lambda s, n: np.broadcast_to(D(s), (n,))
+    ref = []
+    for r in range(m):
+        gg = (D(gw) @ D(x[r])) * sc(gsc, inter) + z(gb, inter)
+        uu = (D(uw) @ D(x[r])) * sc(usc, inter) + z(ub, inter)
+        h = F.silu(torch.from_numpy(gg)).numpy() * uu
+        assert rel(O.swiglu_h_w8(x[r], gw, gsc, uw, usc, gb, ub), h) < 1e-5
+        ref.append((D(dw) @ h) * sc(dsc, k) + z(db, k))
+    out = O.swiglu_mlp_w8(x, gw, gsc, uw, usc, dw, dsc, gb=gb, ub=ub, db=db)
+    assert rel(out, np.stack(ref)) < 1e-5
+
+
+@pytest.mark.parametrize("k,scalar", [(896, False), (1001, False), (31, True), (4096, True)])
+def test_gemv_w4_rows_vs_float64(k, scalar):
+    """Per-channel w4a32_linear: y = dot_f32_u4(x, row) * s + b."""
+    g = np.random.default_rng(k)
+    n = 45
+    q = g.integers(-8, 8, (n, k)).astype(np.int8)
+    w = O.pack_int4(q)
+    s = (np.abs(g.normal(0, 0.02, 1 if scalar else n)) + 1e-3).astype(np.float32)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    x = g.standard_normal((2, k)).astype(np.float32)
+    y = O.gemv_w4_rows(x, w, s, b)
+    ref = (x.astype(np.float64) @ q.astype(np.float64).T) * np.broadcast_to(s, (n,)) + b
+    assert rel(y, ref) < 1e-6
+    for j in (0, k - 1):
+        e = np.zeros((1, k), np.float32)
+        e[0, j] = 1.0
+        assert np.array_equal(O.gemv_w4_rows(e, w, s)[0],
+                              (q[:, j].astype(np.float32) * np.broadcast_to(s, (n,))))
+
+
+def test_quantize_int4_rows_closed_form():
+    """quantize_linear_weights_int4 (fused_ops.rs:592-639)."""
+    g = np.random.default_rng(9)
+    n, k = 5, 37                                   # odd K: last byte padded with 8
+    w = g.standard_normal((n, k)).astype(np.float32)
+    w[1] = 0.0                                     # amax 0 -> scale 1, q 0
+    w[2, :3] = [7.0, 3.5, -3.5]                    # scale 1: ties away from zero
+    w[2, 3:] = 0.0
+    q, s = O.quantize_int4_rows(w)
+    amax = np.abs(w).max(1)
+    s_want = np.where(amax > np.float32(1e-8), amax / np.float32(7.0), np.float32(1.0))
+    assert np.array_equal(s, s_want.astype(np.float32))
+    t = (w * (np.float32(1.0) / s_want.astype(np.float32))[:, None]).astype(np.float32)
+    t = t.astype(np.float64)
+    r = np.clip(np.where(t >= 0, np.floor(t + 0.5), np.ceil(t - 0.5)), -8, 7).astype(np.int8)
+    assert np.array_equal(O.unpack_int4(q, k), r)
+    assert np.all((q[:, -1] >> 4) == 8)
+    assert list(O.unpack_int4(q, k)[2, :3]) == [7, 4, -4] and not O.unpack_int4(q, k)[1].any()
+
+
 # ------------------------------------------------------------------- int8 ---
 
 def test_dot_i8_reference_kat():
@@ -247,6 +353,56 @@ def test_rms_norm_reference_kat():
     assert rel(out, want) < 1e-6
 
 
+@pytest.mark.parametrize("n", [896, 4096, 100])
+def test_rms_norm_torch_vs_f_rms_norm(n):
+    """orc_rms_norm_torch is the per-layer path's F.rms_norm (model.py:91-98):
+    within 2 ulp of torch's own float32 result, and of float64."""
+    g = np.random.default_rng(n)
+    x = (g.standard_normal(n) * 2).astype(np.float32)
+    w = (1 + g.standard_normal(n) * 0.1).astype(np.float32)
+    out = O.rms_norm_torch(x, w, 1e-5)
+    t32 = F.rms_norm(torch.from_numpy(x), (n,), torch.from_numpy(w), eps=1e-5).numpy()
+    ulp = np.spacing(np.abs(t32).astype(np.float32))
+    assert np.all(np.abs(out - t32) <= 2 * ulp)
+    t64 = F.rms_norm(torch.from_numpy(x.astype(np.float64)), (n,),
+                     torch.from_numpy(w.astype(np.float64)), eps=1e-5).numpy()
+    assert rel(out, t64) < 1e-6
+
+
+def test_rotary_tables_f32():
+    """The per-layer path's tables: cos / sin of the float32 angle pos * inv_freq
+    (model.py:108-122), against float64 mathematics -- and visibly not the
+    native decoder's f64 tables at thousands of positions."""
+    from torchburn_amd.decoder import rotary_tables_f32
+    hd, theta, max_seq = 128, 5e5, 4200
+    c, s = rotary_tables_f32(max_seq, hd, theta)
+    assert c.dtype == np.float32 and c.shape == (max_seq, hd)
+    half = hd // 2
+    assert np.array_equal(c[:, :half], c[:, half:]) and np.array_equal(s[:, :half], s[:, half:])
+    freq64 = theta ** (-(2.0 * np.arange(half)) / hd)
+    pos32 = np.arange(max_seq, dtype=np.float32)
+    one = np.spacing(np.float32(1)) * 1.01
+    for i in range(half):
+        # some float32 inv_freq within 3 ulp of theta^(-2i/d) reproduces the whole
+        # column as cos / sin (within 1 ulp) of the float32 product pos * inv_freq
+        up, dn = [np.float32(freq64[i])], [np.float32(freq64[i])]
+        for _ in range(3):
+            up.append(np.nextafter(up[-1], np.float32(np.inf)))
+            dn.append(np.nextafter(dn[-1], np.float32(-np.inf)))
+        cands = up + dn[1:]
+        ok = False
+        for inv in cands:
+            a = (pos32 * inv).astype(np.float32).astype(np.float64)
+            if (np.abs(c[:, i] - np.cos(a)).max() <= one and
+                    np.abs(s[:, i] - np.sin(a)).max() <= one):
+                ok = True
+                break
+        assert ok, f"column {i}: no float32 angle pos * inv_freq reproduces the table"
+    c64, s64 = O.rope_tables(max_seq, hd, theta)
+    assert np.abs(c[4096:] - c64[4096:]).max() > 1e-5   # the two table builds differ
+    assert np.abs(c[:8] - c64[:8]).max() < 1e-6
+
+
 @pytest.mark.parametrize("hd,theta", [(64, 1e6), (128, 5e5)])
 def test_rope_vs_complex_rotation(hd, theta):
     c, s = O.rope_tables(300, hd, theta)
@@ -278,6 +434,24 @@ def test_attention_vs_sdpa(hq, hkv, hd, seq):
     assert rel(out, ref) < 1e-5
 
 
+@pytest.mark.parametrize("hq,hkv,hd,seq", [(14, 2, 64, 300), (32, 8, 128, 97), (4, 4, 64, 1)])
+def test_attention_layer_vs_sdpa(hq, hkv, hd, seq):
+    """The per-layer steps' attention (fused_ops.rs:823-858, 997-1040): no
+    single-position shortcut, no clamp, out += w * v."""
+    g = np.random.default_rng(seq + 1)
+    max_seq = seq + 5
+    q = g.standard_normal((hq, hd), dtype=np.float32)
+    kc = g.standard_normal((hkv, max_seq, hd), dtype=np.float32)
+    vc = g.standard_normal((hkv, max_seq, hd), dtype=np.float32)
+    out = O.attention_layer(q, kc, vc, seq)
+    T = lambda a: torch.from_numpy(a.astype(np.float64))
+    ref = F.scaled_dot_product_attention(T(q)[None, :, None], T(kc[:, :seq])[None],
+                                         T(vc[:, :seq])[None], enable_gqa=True)[0, :, 0].numpy()
+    assert rel(out, ref) < 1e-5
+    if seq == 1:
+        assert np.array_equal(out, np.repeat(vc[:, 0], hq // hkv, 0))
+
+
 def test_attention_special_cases():
     g = np.random.default_rng(0)
     q = g.standard_normal((4, 64), dtype=np.float32)
@@ -302,26 +476,42 @@ def test_argmax_kat_and_ties():
 
 # ------------------------------------------------------------ decoder step ---
 
-def torch_step(w, cfg, kv, tok, pos, gs, f16=False):
+def torch_step(w, cfg, kv, tok, pos, gs, f16=False, wkind=4, lmkind=4, tables=None):
     """One decoder step in float64 from torch library ops (independent of the
-    oracle's C code): rms_norm, complex RoPE, SDPA with GQA, silu.  f16: QKV, O,
-    down and lm_head use binary16-rounded scales (numpy's float16), the effect
-    of the reference's v2 repack at group 64 (decoder.rs:361-390)."""
+    oracle's C code): rms_norm, RoPE, SDPA with GQA, silu.  f16: QKV, O, down
+    and lm_head use binary16-rounded scales (numpy's float16), the effect of the
+    reference's v2 repack at group 64 (decoder.rs:361-390).  wkind / lmkind: 4
+    INT4 grouped, 8 INT8 per-row, 32 fp32.  tables: (cos, sin) [max_seq, hd] for a
+    rotate-half RoPE (model.py:125-136); None = the exact complex rotation."""
     D = lambda a: torch.from_numpy(np.asarray(a, np.float64))
     r16 = (lambda s: s.astype(np.float16).astype(np.float32)) if f16 else (lambda s: s)
+
+    def deq(wt, sc, k, kind, f16s=False):
+        if kind == 4:
+            return D(dequant(wt, r16(sc) if f16s else sc, k, gs))
+        if kind == 8:
+            return D(wt.astype(np.float64) * np.asarray(sc, np.float64).reshape(-1, 1))
+        return D(wt)
+
     H, hq, hkv, hd = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     half = hd // 2
-    freq = D(cfg["rope_theta"] ** (-(2.0 * np.arange(half)) / hd))
-    rot = torch.exp(1j * pos * freq)
+    if tables is None:
+        freq = D(cfg["rope_theta"] ** (-(2.0 * np.arange(half)) / hd))
+        rot = torch.exp(1j * pos * freq)
 
-    def rope(t):   # [heads, hd]
-        z = torch.complex(t[:, :half], t[:, half:]) * rot
-        return torch.cat([z.real, z.imag], -1)
+        def rope(t):   # [heads, hd]
+            z = torch.complex(t[:, :half], t[:, half:]) * rot
+            return torch.cat([z.real, z.imag], -1)
+    else:
+        cr, sr = D(tables[0][pos]), D(tables[1][pos])
+
+        def rope(t):
+            return t * cr + torch.cat([-t[:, half:], t[:, :half]], -1) * sr
 
     x = D(w["embed"][tok])
     for li, lw in enumerate(w["layers"]):
         xn = F.rms_norm(x, (H,), D(lw["in_norm"]), eps=cfg["eps"])
-        qkv = D(dequant(lw["qkv_w"], r16(lw["qkv_s"]), H, gs)) @ xn
+        qkv = deq(lw["qkv_w"], lw["qkv_s"], H, wkind, True) @ xn
         if lw.get("qkv_b") is not None:
             qkv = qkv + D(lw["qkv_b"])
         q = rope(qkv[:hq * hd].reshape(hq, hd))
@@ -332,13 +522,13 @@ def torch_step(w, cfg, kv, tok, pos, gs, f16=False):
         vc[:, pos] = v
         att = F.scaled_dot_product_attention(q[None, :, None], kc[None, :, :pos + 1],
                                              vc[None, :, :pos + 1], enable_gqa=True)[0, :, 0]
-        x = x + D(dequant(lw["o_w"], r16(lw["o_s"]), hq * hd, gs)) @ att.reshape(-1)
+        x = x + deq(lw["o_w"], lw["o_s"], hq * hd, wkind, True) @ att.reshape(-1)
         xn = F.rms_norm(x, (H,), D(lw["post_norm"]), eps=cfg["eps"])
-        h = F.silu(D(dequant(lw["gate_w"], lw["gate_s"], H, gs)) @ xn) * \
-            (D(dequant(lw["up_w"], lw["up_s"], H, gs)) @ xn)
-        x = x + D(dequant(lw["down_w"], r16(lw["down_s"]), cfg["intermediate"], gs)) @ h
+        h = F.silu(deq(lw["gate_w"], lw["gate_s"], H, wkind) @ xn) * \
+            (deq(lw["up_w"], lw["up_s"], H, wkind) @ xn)
+        x = x + deq(lw["down_w"], lw["down_s"], cfg["intermediate"], wkind, True) @ h
     xn = F.rms_norm(x, (H,), D(w["final_norm"]), eps=cfg["eps"])
-    return (D(dequant(w["lm_head_w"], r16(w["lm_head_s"]), H, gs)) @ xn).numpy()
+    return (deq(w["lm_head_w"], w["lm_head_s"], H, lmkind, True) @ xn).numpy()
 
 
 @pytest.mark.parametrize("gs,vocab,v2", [(32, 300, False), (64, 300, False), (64, 320, True)])
@@ -373,4 +563,40 @@ def test_decoder_step_vs_torch_float64(gs, vocab, v2):
     assert dec.kv_len() == pre + 4
     # out-of-range token / position -> zeroed logits (decoder.rs:1066-1089)
     assert not dec.step(vocab, 3).any() and not dec.step(1, max_seq).any()
+    dec.close()
+
+
+@pytest.mark.parametrize("wkind,lmkind,layer_path", [(4, 32, True), (8, 8, True), (8, 32, False),
+                                                      (4, 8, False), (4, 4, True)])
+def test_decoder_kinds_and_layer_path_vs_torch_float64(wkind, lmkind, layer_path):
+    """INT8 projections and INT8 / fp32 lm_heads (configs 4 and 5-INT8), with the
+    per-layer path's f32 RoPE tables passed in and its numerics
+    (orc_decoder_set_layer_path), against the float64 torch model using the
+    same tables; a model with the exact rotation is visibly different once the
+    position is in the thousands."""
+    from torchburn_amd.decoder import rotary_tables_f32
+    cfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
+               head_dim=64, vocab=300, eps=1e-5, rope_theta=5e5, qkv_bias=wkind == 4)
+    max_seq, pre = 3010, 3000
+    w = synth.decoder_weights(cfg, 31 + wkind + lmkind, wkind, lmkind, 32)
+    ocfg = dict(cfg, group_size=32, max_seq=max_seq, wkind=wkind, lmkind=lmkind)
+    tabs = rotary_tables_f32(max_seq, 64, 5e5)
+    dec = O.Decoder(w, ocfg, rope_tables=tabs, layer_path=layer_path)
+    kvp = synth.kv_prefill(cfg, 5, pre, max_seq)
+    tkv = []
+    for li, (k, v) in enumerate(kvp):
+        dec.copy_kv(li, k, v, pre)
+        tkv.append((torch.from_numpy(k.astype(np.float64)), torch.from_numpy(v.astype(np.float64))))
+    tok = 17
+    for step in range(3):
+        pos = pre + step
+        lo = dec.step(tok, pos)
+        exact = [(k.clone(), v.clone()) for k, v in tkv]
+        lt = torch_step(w, cfg, tkv, tok, pos, 32, wkind=wkind, lmkind=lmkind, tables=tabs)
+        assert rel(lo, lt) < 1e-5, f"step {step}"
+        if step == 0:
+            le = torch_step(w, cfg, exact, tok, pos, 32, wkind=wkind, lmkind=lmkind)
+            assert rel(lt, le) > 1e-5
+        assert O.argmax(lo) == int(np.argmax(lt))
+        tok = O.argmax(lo)
     dec.close()

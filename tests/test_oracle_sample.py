@@ -1,7 +1,8 @@
 """Pins the oracle's sampling restatement (orc_sample_logits, orc_repetition_penalty;
 decoder.rs:878-1020) before it checks the device sampler.
 
-  greedy        numpy argmax (first index); NaN skipped, +inf taken; the
+  greedy        numpy argmax (first index); NaN past index 0 skipped, a NaN
+                at index 0 kept (the reference's scan), +inf taken; the
                 temperature / top_k conditions of decoder.rs:919-931
   distribution  the fraction of a fine grid of u that lands on each token equals
                 a float64 numpy softmax over the top-k with the nucleus cut
@@ -30,6 +31,12 @@ def test_greedy_cases():
     assert O.sample_logits(lg2, 0.0, 40, 1.0, 0.0)[0] == 9
     ties = np.zeros(50, np.float32)
     assert O.sample_logits(ties, 0.0, 5, 1.0, 0.0)[0] == 0
+    # decoder.rs:914-925 starts from logits[0] and compares with strict >: a NaN
+    # there is never replaced, a NaN elsewhere never taken
+    lg3 = lg.copy()
+    lg3[0] = np.nan
+    assert O.sample_logits(lg3, 0.0, 40, 1.0, 0.0)[0] == 0
+    assert O.argmax(lg3) == 0
 
 
 def expected_probs(lg, T, k, top_p):

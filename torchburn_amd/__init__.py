@@ -17,11 +17,13 @@ from .quantization import (
     fused_transformer_layer_step_w4a32,
     fused_swiglu_mlp,
     fused_swiglu_mlp_w4a32,
+    fused_swiglu_mlp_batched,
     fused_swiglu_mlp_batched_w4a32,
     fused_swiglu_mlp_w8a32,
     dequantize_int4_grouped_v2,
     pack_rows_w4a32_group64_v1_to_v2,
     quantize_model,
+    quantize_weight_int4,
     quantize_weight_int4_grouped,
     quantize_weight_int4_grouped_v2,
     quantize_weight_int8,
@@ -30,8 +32,10 @@ from .quantization import (
     w4a32_grouped_linear,
     w4a32_grouped_linear_residual,
     w4a32_grouped_linear_v2,
+    w4a32_linear,
     w8a32_linear,
 )
+from .decoder import rotary_tables_f32
 
 __all__ = [
     "RustQwenDecoder",
@@ -47,13 +51,17 @@ __all__ = [
     "fused_transformer_layer_step_w4a32",
     "fused_swiglu_mlp",
     "fused_swiglu_mlp_w4a32",
+    "fused_swiglu_mlp_batched",
     "fused_swiglu_mlp_batched_w4a32",
     "quantize_model",
+    "quantize_weight_int4",
     "quantize_weight_int4_grouped",
     "quantize_weight_int8",
     "w4a32_grouped_linear",
     "w4a32_grouped_linear_residual",
     "w4a32_grouped_linear_v2",
+    "w4a32_linear",
+    "rotary_tables_f32",
     "quantize_weight_int4_grouped_v2",
     "dequantize_int4_grouped_v2",
     "pack_rows_w4a32_group64_v1_to_v2",

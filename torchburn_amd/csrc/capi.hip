@@ -10,11 +10,14 @@
 #include <algorithm>
 #include <atomic>
 
+#include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
 
 #include "gemv_dense.hpp"
+#include "gemv_generic.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
 #include "w4_mfma.hpp"
@@ -27,13 +30,29 @@ namespace tb {
 namespace {
 thread_local std::string g_last_error;
 
-// Device workspace (grow-only, one per device) for intermediates of fused ops.
-std::mutex g_ws_mu;
-std::vector<std::pair<void *, size_t>> g_ws;
+// Per-(device, stream) scratch for intermediates of the stateless ops.
+struct StreamScratch {
+    std::mutex mu;        // held by the op enqueueing on this stream
+    void *ptr = nullptr;
+    size_t size = 0;
+};
+std::mutex g_ws_mu;       // guards the two containers below
+std::map<std::pair<int, uintptr_t>, std::unique_ptr<StreamScratch>> g_ws;
+std::vector<void *> g_retired;   // replaced buffers: kept until the process exits
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-int gshift_of(int64_t gs) { return gs == 32 ? 5 : (gs == 64 ? 6 : -1); }
+// log2 of a power-of-two group size of at least 32 (the streaming kernels'
+// chunk), else -1.
+int gshift_of(int64_t gs) {
+    if (gs < 32 || gs > (1 << 20) || (gs & (gs - 1)) != 0) return -1;
+    int b = 0;
+    while ((1ll << b) < gs) ++b;
+    return b;
+}
+
+// K range of one GEMV pass (kMaxWaves K-slices of 64 chunks of 32 elements).
+constexpr int64_t kMaxGemvK = 8 * 64 * 32;
 
 // GEMV rows per block; TB_W4_J overrides the default (tuning sweeps only).
 int env_int(const char *name, int dflt) {
@@ -59,52 +78,68 @@ int fail(int code, const std::string &msg) {
     return code;
 }
 
-int workspace(size_t bytes, void **out) {
+int workspace(size_t bytes, hipStream_t st, WsLease &out) {
     int dev = 0;
     TB_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
-    auto &slot = g_ws[dev];
-    if (slot.second < bytes) {
-        // A stream may still be using the old buffer; free it only after the
-        // device is idle.
-        if (slot.first) {
-            TB_HIP(hipDeviceSynchronize());
-            TB_HIP(hipFree(slot.first));
-            slot = {nullptr, 0};
-        }
-        size_t sz = bytes < (1u << 20) ? (1u << 20) : bytes;
-        TB_HIP(hipMalloc(&slot.first, sz));
-        slot.second = sz;
+    StreamScratch *sc;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        auto &slot = g_ws[{dev, reinterpret_cast<uintptr_t>(st)}];
+        if (!slot) slot.reset(new StreamScratch);
+        sc = slot.get();
     }
-    *out = slot.first;
+    out.lock = std::unique_lock<std::mutex>(sc->mu);
+    if (sc->size < bytes) {
+        size_t sz = std::max<size_t>({bytes, 2 * sc->size, (size_t)1 << 20});
+        void *p = nullptr;
+        TB_HIP(hipMalloc(&p, sz));
+        if (sc->ptr) {
+            std::lock_guard<std::mutex> lk(g_ws_mu);
+            g_retired.push_back(sc->ptr);
+        }
+        sc->ptr = p;
+        sc->size = sz;
+    }
+    out.ptr = sc->ptr;
     return TB_OK;
 }
 
-// Validates a grouped INT4 projection and fills the common W4Params fields.
+// Validates a grouped INT4 projection: any K >= 1 and any group size >= 1 (the
+// reference's GEMV takes tail groups, src/quantization/gemv.rs:1650-1660).
 static int check_w4(const float *x, const uint8_t *w, const float *s, int64_t m, int64_t n,
                     int64_t k, int64_t gs, const char *what) {
     const std::string op(what);
     TB_REQUIRE(x && w && s, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": null pointer");
     TB_REQUIRE(m >= 0 && n >= 0 && k > 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: " + op + ": negative or empty dimension");
-    TB_REQUIRE(gshift_of(gs) > 0, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": group_size must be 32 or 64, got " + std::to_string(gs));
-    TB_REQUIRE(k % gs == 0, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": K=" + std::to_string(k) +
-                   " must be a multiple of group_size=" + std::to_string(gs));
-    TB_REQUIRE(k <= (1 << 20) && n < (1ll << 31) && m < (1ll << 31), TB_ERR_UNSUPPORTED,
+    // Groups start on byte boundaries (gemv.rs:1514-1530 steps group_size / 2
+    // bytes per group), so an odd group size has no consistent layout.
+    TB_REQUIRE(gs >= 2 && gs % 2 == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": group_size must be a positive even number, got " +
+                   std::to_string(gs));
+    TB_REQUIRE(k <= (1 << 30) && n < (1ll << 31) && m < (1ll << 31), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: " + op + ": dimension too large");
-    TB_REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(s, 4), TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": x and w must be 16-byte aligned device pointers");
+    TB_REQUIRE(aligned(x, 4) && aligned(s, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": x and scales must be 4-byte aligned device pointers");
     return TB_OK;
+}
+
+// Shapes the streaming kernels take: K a multiple of 32 and of a power-of-two
+// group of at least 32, 16-byte aligned x and w, and (GEMV passes, M below the
+// MFMA threshold) K within one pass's split-K range.  Other shapes run the
+// any-shape GEMV (gemv_generic.hip).
+static bool w4_fast(const float *x, const void *w, int64_t m, int64_t k, int64_t gs,
+                    bool per_row) {
+    if (k % 32 != 0 || (!per_row && (gshift_of(gs) < 0 || k % gs != 0))) return false;
+    if (!aligned(x, 16) || !aligned(w, 16)) return false;
+    return m >= mfma_min_m() || k <= kMaxGemvK;
 }
 
 static W4Params w4_params(const float *x, const uint8_t *w, const float *s, const float *b,
                           float *y, int64_t m, int64_t n, int64_t k, int64_t gs) {
     W4Params p{};
     p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
-    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = std::max(gshift_of(gs), 5);
     p.rows_j = rows_j_env();
     return p;
 }
@@ -113,15 +148,16 @@ static MfmaParams mfma_params(const float *x, const uint8_t *w, const float *s, 
                               float *y, int64_t m, int64_t n, int64_t k, int64_t gs) {
     MfmaParams p{};
     p.x = x; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
-    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = gshift_of(gs);
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.gshift = std::max(gshift_of(gs), 5);
     return p;
 }
 
 // The MFMA projection with its split-K partials in the library workspace.
 static int mfma_ws(const MfmaParams &p, int epi, hipStream_t st) {
-    void *ws = nullptr;
-    int rc = workspace(w4_mfma_partials_bytes(p.m, p.n, p.k, p.w1 != nullptr), &ws);
+    WsLease lease;
+    int rc = workspace(w4_mfma_partials_bytes(p.m, p.n, p.k, p.w1 != nullptr), st, lease);
     if (rc) return rc;
+    void *ws = lease.ptr;
     return w4_mfma(p, epi, static_cast<float *>(ws), st);
 }
 
@@ -162,18 +198,27 @@ static size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 // the weights as v1 nibbles + f32 scales or as v2 blocks.  Under W4A8
 // semantics (group 64) each row of x is first replaced by its byte
 // quantization q * s_x.  Workspace: [x' | records or split-K partials].
+static int generic(const float *x, const void *w0, const float *s0, int mode0, const float *b0,
+                   const void *w1, const float *s1, int mode1, const float *b1,
+                   const float *res, float *y, int64_t m, int64_t n, int64_t k, int64_t gs,
+                   int bits, hipStream_t st);
+
 static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
                      const float *bias, const float *res, float *out, int64_t m, int64_t n,
-                     int64_t k, int64_t gs, hipStream_t st) {
-    const bool a8 = gs == 64 && g_vnni.load(std::memory_order_relaxed) != 0;
+                     int64_t k, int64_t gs, hipStream_t st, int scale_mode = 0) {
+    if (!v2 && !w4_fast(x, w, m, k, gs, scale_mode != 0))
+        return generic(x, w, s, scale_mode, bias, nullptr, nullptr, 0, nullptr, res, out, m, n, k,
+                       scale_mode ? k : gs, 4, st);
+    const bool a8 = gs == 64 && scale_mode == 0 && g_vnni.load(std::memory_order_relaxed) != 0;
     const size_t xb = a8 ? up256((size_t)m * (size_t)k * sizeof(float)) : 0;
     const int epi = res ? EPI_RESID : EPI_PLAIN;
     const bool mf = m >= mfma_min_m();
     const size_t rest = mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
                            : xq_bytes(m, k);
-    void *ws = nullptr;
-    int rc = workspace(xb + rest, &ws);
+    WsLease lease;
+    int rc = workspace(xb + rest, st, lease);
     if (rc) return rc;
+    void *ws = lease.ptr;
     const float *xin = x;
     if (a8) {
         if ((rc = act_u8(x, static_cast<float *>(ws), m, k, st))) return rc;
@@ -184,11 +229,13 @@ static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
         MfmaParams q = mfma_params(xin, w, s, bias, out, m, n, k, gs);
         q.res = res;
         q.v2 = v2 ? 1 : 0;
+        q.scale_mode = scale_mode;
         return w4_mfma(q, epi, static_cast<float *>(tail), st);
     }
     W4Params p = w4_params(xin, w, s, bias, out, m, n, k, gs);
     p.res = res;
     p.v2 = v2 ? 1 : 0;
+    p.scale_mode = scale_mode;
     return w4_rows(p, epi, m, static_cast<uint32_t *>(tail), true, st);
 }
 
@@ -222,11 +269,17 @@ static int check_w8(const float *x, const int8_t *w, const float *s, int64_t s_l
                "TB_UNSUPPORTED: " + op + ": negative or empty dimension");
     TB_REQUIRE(s_len == 1 || s_len == n, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: " + op + ": scales must have 1 or N elements");
-    TB_REQUIRE(k % 32 == 0 && k <= (1 << 20) && n < (1ll << 31), TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": K must be a multiple of 32");
-    TB_REQUIRE(aligned(x, 16) && aligned(w, 16), TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: " + op + ": x and w must be 16-byte aligned device pointers");
+    TB_REQUIRE(k <= (1 << 30) && n < (1ll << 31) && m < (1ll << 31), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": dimension too large");
+    TB_REQUIRE(aligned(x, 4) && aligned(s, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: " + op + ": x and scales must be 4-byte aligned device pointers");
     return TB_OK;
+}
+
+// INT8 shapes the streaming GEMV takes: K a multiple of 32 within one pass's
+// split-K range, 16-byte aligned x and w.  Others run the any-shape GEMV.
+static bool w8_fast(const float *x, const void *w, int64_t k) {
+    return k % 32 == 0 && k <= kMaxGemvK && aligned(x, 16) && aligned(w, 16);
 }
 
 static int dense_rows(DenseParams p, int wt, int epi, int64_t m, hipStream_t st) {
@@ -240,6 +293,113 @@ static int dense_rows(DenseParams p, int wt, int epi, int64_t m, hipStream_t st)
         if (rc) return rc;
     }
     return TB_OK;
+}
+
+// The any-shape GEMV over INT4 grouped (scale_mode 0), per-row (1) or scalar
+// (2) scales, or INT8 (bits 8, scale_mode 1 / 2).
+static int generic(const float *x, const void *w0, const float *s0, int mode0, const float *b0,
+                   const void *w1, const float *s1, int mode1, const float *b1,
+                   const float *res, float *y, int64_t m, int64_t n, int64_t k, int64_t gs,
+                   int bits, hipStream_t st) {
+    GenericParams g{};
+    g.x = x; g.w0 = w0; g.s0 = s0; g.b0 = b0; g.w1 = w1; g.s1 = s1; g.b1 = b1;
+    g.res = res; g.y = y; g.m = m; g.n = n; g.k = k; g.group = gs;
+    g.scale_mode0 = mode0; g.scale_mode1 = mode1; g.bits = bits;
+    return gemv_generic(g, st);
+}
+
+// ---- fused SwiGLU MLP (INT4), shared by the workspace and no-alloc entries ----
+struct MlpW4 {
+    const float *x;
+    const uint8_t *gate_w;
+    const float *gate_s, *gate_b;
+    const uint8_t *up_w;
+    const float *up_s, *up_b;
+    const uint8_t *down_w;
+    const float *down_s, *down_b, *residual;
+    float *out;
+    int64_t m, k, inter, n_out, gs;
+};
+
+static int mlp_w4_check(const MlpW4 &a, const char *op) {
+    int rc = check_w4(a.x, a.gate_w, a.gate_s, a.m, a.inter, a.k, a.gs, op);
+    if (rc) return rc;
+    rc = check_w4(a.x, a.up_w, a.up_s, a.m, a.inter, a.k, a.gs, op);
+    if (rc) return rc;
+    TB_REQUIRE(a.down_w && a.down_s && a.out && a.inter > 0 && a.n_out >= 0, TB_ERR_UNSUPPORTED,
+               std::string("TB_UNSUPPORTED: ") + op + ": null down weight or output");
+    return TB_OK;
+}
+
+// 0: any-shape GEMVs; 1: FP32-MFMA pair; 2: GEMV passes
+static int mlp_w4_path(const MlpW4 &a) {
+    if (!w4_fast(a.x, a.gate_w, a.m, a.k, a.gs, false) || !aligned(a.up_w, 16) ||
+        !w4_fast(a.x, a.down_w, a.m, a.inter, a.gs, false))
+        return 0;
+    return a.m >= mfma_min_m() ? 1 : 2;
+}
+
+// Scratch: h [m, inter] f32, then the MFMA split-K partials (path 1) or the
+// chunk records of x and of h (path 2).
+static size_t mlp_w4_scratch_bytes(const MlpW4 &a) {
+    const size_t hb = up256((size_t)a.m * (size_t)a.inter * sizeof(float));
+    switch (mlp_w4_path(a)) {
+        case 0: return hb;
+        case 1: {
+            const size_t pg = w4_mfma_partials_bytes((int)a.m, (int)a.inter, (int)a.k, true);
+            const size_t pd = w4_mfma_partials_bytes((int)a.m, (int)a.n_out, (int)a.inter, false);
+            return hb + std::max(pg, pd);
+        }
+        default: return hb + up256(xq_bytes(a.m, a.k)) + xq_bytes(a.m, a.inter);
+    }
+}
+
+// out = [residual +] down(silu(gate(x)) * up(x)) with `ws` of at least
+// mlp_w4_scratch_bytes(a) bytes (fused_swiglu_mlp_w4a32, fused_ops.rs:138-424).
+static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
+    int rc;
+    const int64_t m = a.m, k = a.k, inter = a.inter, n_out = a.n_out, gs = a.gs;
+    float *h = static_cast<float *>(ws);
+    const size_t hb = up256((size_t)m * (size_t)inter * sizeof(float));
+    const int path = mlp_w4_path(a);
+    if (path == 0) {
+        // Shapes outside the streaming kernels: h by the any-shape GEMV, then the
+        // down projection by whichever path its own shape takes.
+        rc = generic(a.x, a.gate_w, a.gate_s, 0, a.gate_b, a.up_w, a.up_s, 0, a.up_b, nullptr, h,
+                     m, inter, k, gs, 4, st);
+        if (rc) return rc;
+        return generic(h, a.down_w, a.down_s, 0, a.down_b, nullptr, nullptr, 0, nullptr,
+                       a.residual, a.out, m, n_out, inter, gs, 4, st);
+    }
+    if (path == 1) {
+        float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + hb);
+        MfmaParams g = mfma_params(a.x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+        g.w1 = a.up_w; g.s1 = a.up_s; g.b1 = a.up_b;
+        if ((rc = w4_mfma(g, EPI_SWIGLU, part, st))) return rc;
+        MfmaParams d = mfma_params(h, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
+        d.res = a.residual;
+        return w4_mfma(d, a.residual ? EPI_RESID : EPI_PLAIN, part, st);
+    }
+    uint32_t *xq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb);
+    uint32_t *hq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb +
+                                                up256(xq_bytes(m, k)));
+    W4Params p = w4_params(a.x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+    p.w1 = a.up_w; p.s1 = a.up_s; p.b1 = a.up_b;
+    W4Params d = w4_params(h, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
+    d.res = a.residual;
+    const int depi = a.residual ? EPI_RESID : EPI_PLAIN;
+    if (m == 1) {
+        // One row: the gate/up epilogue writes h's chunk records as well, so the
+        // down projection needs no separate record pass.
+        if ((rc = xquant(a.x, xq, 1, (int)k, st))) return rc;
+        p.xq = xq;
+        p.rec_out = hq;
+        if ((rc = w4_gemv(p, EPI_SWIGLU, st))) return rc;
+        d.xq = hq;
+        return w4_gemv(d, depi, st);
+    }
+    if ((rc = w4_rows(p, EPI_SWIGLU, m, xq, true, st))) return rc;
+    return w4_rows(d, depi, m, hq, true, st);
 }
 
 }  // namespace tb
@@ -371,9 +531,10 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     const size_t cand = (size_t)kSampleCand;
     const size_t bytes = up256(sizeof(SampleParams)) + up256(sizeof(SampleOut)) +
                          up256(cand * 4) + up256(cand * 4) + up256(kSampleMaxBlocks * 4);
-    void *ws = nullptr;
-    int rc = workspace(bytes, &ws);
+    WsLease lease;
+    int rc = workspace(bytes, (hipStream_t)stream, lease);
     if (rc) return rc;
+    void *ws = lease.ptr;
     char *w = static_cast<char *>(ws);
     SampleParams *dprm = reinterpret_cast<SampleParams *>(w);
     w += up256(sizeof(SampleParams));
@@ -424,14 +585,18 @@ int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
     if (rc) return rc;
     TB_REQUIRE(h, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: swiglu_w4a32: null output");
     if (m == 0 || inter == 0) return TB_OK;
+    if (!w4_fast(x, gate_w, m, k, group_size, false) || !aligned(up_w, 16))
+        return generic(x, gate_w, gate_s, 0, gate_b, up_w, up_s, 0, up_b, nullptr, h, m, inter, k,
+                       group_size, 4, (hipStream_t)stream);
     if (m >= mfma_min_m()) {
         MfmaParams q = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
         q.w1 = up_w; q.s1 = up_s; q.b1 = up_b;
         return mfma_ws(q, EPI_SWIGLU, (hipStream_t)stream);
     }
-    void *ws = nullptr;
-    rc = workspace(xq_bytes(m, k), &ws);
+    WsLease lease;
+    rc = workspace(xq_bytes(m, k), (hipStream_t)stream, lease);
     if (rc) return rc;
+    void *ws = lease.ptr;
     W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
     p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
     return w4_rows(p, EPI_SWIGLU, m, (uint32_t *)ws, true, (hipStream_t)stream);
@@ -443,68 +608,14 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
                               const float *down_b, const float *residual, float *out,
                               int64_t m, int64_t k, int64_t inter, int64_t n_out,
                               int64_t group_size, void *stream) {
-    int rc = check_w4(x, gate_w, gate_s, m, inter, k, group_size, "fused_swiglu_mlp_w4a32");
-    if (rc) return rc;
-    rc = check_w4(x, up_w, up_s, m, inter, k, group_size, "fused_swiglu_mlp_w4a32");
-    if (rc) return rc;
-    TB_REQUIRE(inter % group_size == 0 && inter % 32 == 0, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: intermediate size must be a multiple "
-               "of group_size");
-    TB_REQUIRE(down_w && down_s && out, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32: null down weight or output");
-    if (m == 0 || n_out == 0) return TB_OK;
-    // Workspace: h [m, inter] f32 | chunk records of x | chunk records of h,
-    // or on the MFMA path h | split-K partials.
-    const size_t hb = ((size_t)m * (size_t)inter * sizeof(float) + 255) & ~(size_t)255;
-    if (m >= mfma_min_m()) {
-        const size_t pg = w4_mfma_partials_bytes((int)m, (int)inter, (int)k, true);
-        const size_t pd = w4_mfma_partials_bytes((int)m, (int)n_out, (int)inter, false);
-        void *ws = nullptr;
-        rc = workspace(hb + (pg > pd ? pg : pd), &ws);
-        if (rc) return rc;
-        float *h = static_cast<float *>(ws);
-        float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + hb);
-        hipStream_t st = (hipStream_t)stream;
-        MfmaParams g = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
-        g.w1 = up_w; g.s1 = up_s; g.b1 = up_b;
-        rc = w4_mfma(g, EPI_SWIGLU, part, st);
-        if (rc) return rc;
-        MfmaParams d = mfma_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
-        d.res = residual;
-        return w4_mfma(d, residual ? EPI_RESID : EPI_PLAIN, part, st);
-    }
-    const size_t xb = (xq_bytes(m, k) + 255) & ~(size_t)255;
-    void *ws = nullptr;
-    rc = workspace(hb + xb + xq_bytes(m, inter), &ws);
-    if (rc) return rc;
-    float *h = static_cast<float *>(ws);
-    uint32_t *xq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb);
-    uint32_t *hq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb + xb);
+    const MlpW4 a{x, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
+                  residual, out, m, k, inter, n_out, group_size};
+    int rc = mlp_w4_check(a, "fused_swiglu_mlp_w4a32");
+    if (rc || m == 0 || n_out == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
-    W4Params p = w4_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
-    p.w1 = up_w; p.s1 = up_s; p.b1 = up_b;
-    if (m == 1) {
-        // One row: the gate/up epilogue writes h's chunk records as well, so the
-        // down projection needs no separate record pass.
-        rc = xquant(x, xq, 1, (int)k, st);
-        if (rc) return rc;
-        p.xq = xq;
-        p.rec_out = hq;
-        rc = w4_gemv(p, EPI_SWIGLU, st);
-        if (rc) return rc;
-        W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
-        d.xq = hq;
-        d.res = residual;
-        return w4_gemv(d, residual ? EPI_RESID : EPI_PLAIN, st);
-    }
-    rc = w4_rows(p, EPI_SWIGLU, m, xq, true, st);
-    if (rc) return rc;
-    W4Params d = w4_params(h, down_w, down_s, down_b, out, m, n_out, inter, group_size);
-    if (residual) {
-        d.res = residual;
-        return w4_rows(d, EPI_RESID, m, hq, true, st);
-    }
-    return w4_rows(d, EPI_PLAIN, m, hq, true, st);
+    WsLease lease;
+    if ((rc = workspace(mlp_w4_scratch_bytes(a), st, lease))) return rc;
+    return mlp_w4_run(a, lease.ptr, st);
 }
 
 int64_t tb_x_records_bytes(int64_t m, int64_t k) {
@@ -527,6 +638,9 @@ int tb_w4a32_gemv_xq(const float *x, const uint32_t *xq, const uint8_t *w_packed
     if (rc) return rc;
     TB_REQUIRE(out && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32_gemv_xq: null output or unaligned records");
+    TB_REQUIRE(w4_fast(x, w_packed, m, k, group_size, false), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4a32_gemv_xq: records need K % 32 == 0, a power-of-two group "
+               ">= 32 and K <= " + std::to_string(kMaxGemvK));
     if (m == 0 || n == 0) return TB_OK;
     if (m >= mfma_min_m()) {
         MfmaParams q = mfma_params(x, w_packed, scales, bias, out, m, n, k, group_size);
@@ -549,6 +663,10 @@ int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t *gate_w
     if (rc) return rc;
     TB_REQUIRE(h && xq && aligned(xq, 16), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: swiglu_w4a32_xq: null output or unaligned records");
+    TB_REQUIRE(w4_fast(x, gate_w, m, k, group_size, false) && aligned(up_w, 16),
+               TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: swiglu_w4a32_xq: records need K % 32 == 0, a power-of-two group "
+               ">= 32 and K <= " + std::to_string(kMaxGemvK));
     if (m == 0 || inter == 0) return TB_OK;
     if (m >= mfma_min_m()) {
         MfmaParams q = mfma_params(x, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
@@ -560,6 +678,30 @@ int tb_swiglu_w4a32_xq(const float *x, const uint32_t *xq, const uint8_t *gate_w
     return w4_rows(p, EPI_SWIGLU, m, const_cast<uint32_t *>(xq), false, (hipStream_t)stream);
 }
 
+int tb_w4a32_linear(const float *x, const uint8_t *w_packed, const float *scales, int64_t s_len,
+                    const float *bias, float *out, int64_t m, int64_t n, int64_t k, void *stream) {
+    int rc = check_w4(x, w_packed, scales, m, n, k, 2, "w4a32_linear");
+    if (rc) return rc;
+    TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4a32_linear: null output");
+    TB_REQUIRE(s_len == 1 || s_len == n, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4a32_linear: scales must have 1 or N elements");
+    if (m == 0 || n == 0) return TB_OK;
+    // y = dot * s + b with one scale per row or one scalar (gemv.rs:1114-1180)
+    return linear_w4(x, w_packed, scales, false, bias, nullptr, out, m, n, k, 32,
+                     (hipStream_t)stream, s_len > 1 ? 1 : 2);
+}
+
+int tb_quantize_weight_int4(const float *w, uint8_t *packed, float *scales, int64_t n, int64_t k,
+                            void *stream) {
+    TB_REQUIRE(w && packed && scales, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4: null pointer");
+    TB_REQUIRE(n >= 0 && k > 0 && k <= (1 << 30) && n < (1ll << 31), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4: bad shape");
+    TB_REQUIRE(aligned(w, 4) && aligned(scales, 4), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: quantize_weight_int4: misaligned device pointer");
+    return quantize_int4_rows(w, packed, scales, n, k, (hipStream_t)stream);
+}
+
 int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_t s_len,
                     const float *bias, float *out, int64_t m, int64_t n, int64_t k,
                     void *stream) {
@@ -567,6 +709,9 @@ int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_
     if (rc) return rc;
     TB_REQUIRE(out, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w8a32_linear: null output");
     if (m == 0 || n == 0) return TB_OK;
+    if (!w8_fast(x, w, k))
+        return generic(x, w, scales, s_len > 1 ? 1 : 2, bias, nullptr, nullptr, 0, nullptr,
+                       nullptr, out, m, n, k, 1, 8, (hipStream_t)stream);
     DenseParams p{};
     p.x = x; p.w0 = w; p.rs0 = scales; p.rs0_len = (int)s_len; p.b0 = bias; p.y = out;
     p.m = (int)m; p.n = (int)n; p.k = (int)k;
@@ -574,31 +719,44 @@ int tb_w8a32_linear(const float *x, const int8_t *w, const float *scales, int64_
 }
 
 int tb_fused_swiglu_mlp_w8a32(const float *x, const int8_t *gate_w, const float *gate_s,
-                              const float *gate_b, const int8_t *up_w, const float *up_s,
-                              const float *up_b, const int8_t *down_w, const float *down_s,
-                              const float *down_b, const float *residual, float *out,
-                              int64_t m, int64_t k, int64_t inter, int64_t n_out,
-                              void *stream) {
-    int rc = check_w8(x, gate_w, gate_s, inter, m, inter, k, "fused_swiglu_mlp_w8a32");
+                              int64_t gate_s_len, const float *gate_b, const int8_t *up_w,
+                              const float *up_s, int64_t up_s_len, const float *up_b,
+                              const int8_t *down_w, const float *down_s, int64_t down_s_len,
+                              const float *down_b, const float *residual, float *out, int64_t m,
+                              int64_t k, int64_t inter, int64_t n_out, void *stream) {
+    // Each projection's scales are per row (N elements) or one per-tensor
+    // scalar (fused_ops.rs:80-97 and gemv_w8a32's s_len).
+    int rc = check_w8(x, gate_w, gate_s, gate_s_len, m, inter, k, "fused_swiglu_mlp_w8a32 gate");
     if (rc) return rc;
-    rc = check_w8(x, up_w, up_s, inter, m, inter, k, "fused_swiglu_mlp_w8a32");
+    rc = check_w8(x, up_w, up_s, up_s_len, m, inter, k, "fused_swiglu_mlp_w8a32 up");
     if (rc) return rc;
-    TB_REQUIRE(down_w && down_s && out && inter % 32 == 0, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: fused_swiglu_mlp_w8a32: bad down projection or output");
+    TB_REQUIRE(out && (inter > 0 || n_out == 0), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused_swiglu_mlp_w8a32: null output");
     if (m == 0 || n_out == 0) return TB_OK;
-    void *ws = nullptr;
-    rc = workspace((size_t)m * (size_t)inter * sizeof(float), &ws);
+    // down reads h [m, inter] from the workspace (x stands in for its checks)
+    rc = check_w8(x, down_w, down_s, down_s_len, m, n_out, inter, "fused_swiglu_mlp_w8a32 down");
     if (rc) return rc;
+    WsLease lease;
+    rc = workspace((size_t)m * (size_t)inter * sizeof(float), (hipStream_t)stream, lease);
+    if (rc) return rc;
+    void *ws = lease.ptr;
     float *h = static_cast<float *>(ws);
     hipStream_t st = (hipStream_t)stream;
+    if (!w8_fast(x, gate_w, k) || !aligned(up_w, 16) || !w8_fast(h, down_w, inter)) {
+        rc = generic(x, gate_w, gate_s, gate_s_len > 1 ? 1 : 2, gate_b, up_w, up_s,
+                     up_s_len > 1 ? 1 : 2, up_b, nullptr, h, m, inter, k, 1, 8, st);
+        if (rc) return rc;
+        return generic(h, down_w, down_s, down_s_len > 1 ? 1 : 2, down_b, nullptr, nullptr, 0,
+                       nullptr, residual, out, m, n_out, inter, 1, 8, st);
+    }
     DenseParams p{};
-    p.x = x; p.w0 = gate_w; p.rs0 = gate_s; p.rs0_len = (int)inter; p.b0 = gate_b;
-    p.w1 = up_w; p.rs1 = up_s; p.rs1_len = (int)inter; p.b1 = up_b;
+    p.x = x; p.w0 = gate_w; p.rs0 = gate_s; p.rs0_len = (int)gate_s_len; p.b0 = gate_b;
+    p.w1 = up_w; p.rs1 = up_s; p.rs1_len = (int)up_s_len; p.b1 = up_b;
     p.y = h; p.m = (int)m; p.n = (int)inter; p.k = (int)k;
     rc = dense_rows(p, W_I8, EPI_SWIGLU, m, st);
     if (rc) return rc;
     DenseParams d{};
-    d.x = h; d.w0 = down_w; d.rs0 = down_s; d.rs0_len = (int)n_out; d.b0 = down_b;
+    d.x = h; d.w0 = down_w; d.rs0 = down_s; d.rs0_len = (int)down_s_len; d.b0 = down_b;
     d.res = residual; d.y = out; d.m = (int)m; d.n = (int)n_out; d.k = (int)inter;
     return dense_rows(d, W_I8, residual ? EPI_RESID : EPI_PLAIN, m, st);
 }

@@ -1273,6 +1273,21 @@ int tb_decoder_set_seed(tb_decoder *d, uint64_t seed) {
     return TB_OK;
 }
 
+int tb_decoder_set_rope_tables(tb_decoder *d, const float *cos_t, const float *sin_t,
+                               int64_t rows, int64_t head_dim) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    TB_REQUIRE(cos_t && sin_t, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: set_rope_tables: null table");
+    TB_REQUIRE(rows == d->max_seq && head_dim == d->hd, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: set_rope_tables: tables must be [max_seq_len=" +
+                   std::to_string(d->max_seq) + ", head_dim=" + std::to_string(d->hd) + "]");
+    const size_t bytes = (size_t)rows * (size_t)head_dim * sizeof(float);
+    // The step graphs read the tables through these same buffers.
+    TB_HIP(hipStreamSynchronize(d->st));
+    TB_HIP(hipMemcpy(d->cos_t, cos_t, bytes, hipMemcpyDefault));
+    TB_HIP(hipMemcpy(d->sin_t, sin_t, bytes, hipMemcpyDefault));
+    return TB_OK;
+}
+
 int tb_decoder_time_greedy(tb_decoder *d, int64_t first_token, int64_t offset, int64_t n_steps,
                            float *ms_out) {
     TB_REQUIRE(d && ms_out, TB_ERR_VALUE, "null argument");

@@ -45,7 +45,8 @@ struct LayerWs {
     uint32_t *xq_i;   // records of h (INT4)
 };
 
-int layer_ws(int64_t H, int64_t I, int hq, int hkv, int hd, int max_seq, LayerWs &w) {
+int layer_ws(int64_t H, int64_t I, int hq, int hkv, int hd, int max_seq, LayerWs &w,
+             WsLease &lease, hipStream_t st) {
     const size_t qkv_n = (size_t)(hq + 2 * hkv) * hd;
     const size_t part_n = (size_t)hq * attn_nsplit(max_seq) * (hd + 4);
     size_t off[9], o = 0;
@@ -57,10 +58,9 @@ int layer_ws(int64_t H, int64_t I, int hq, int hkv, int hd, int max_seq, LayerWs
         off[i] = o;
         o += sz[i];
     }
-    void *ws = nullptr;
-    int rc = workspace(o, &ws);
+    int rc = workspace(o, st, lease);
     if (rc) return rc;
-    char *b = static_cast<char *>(ws);
+    char *b = static_cast<char *>(lease.ptr);
     w.state = reinterpret_cast<DecState *>(b + off[0]);
     w.qkv = reinterpret_cast<float *>(b + off[1]);
     w.part = reinterpret_cast<float *>(b + off[2]);
@@ -180,7 +180,8 @@ int attention_step(const char *what, int bits, const float *x, const void *qkv_w
                    is_aligned(out, 16),
                TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": 16-byte aligned device pointers required");
     LayerWs w;
-    if ((rc = layer_ws(H, 0, (int)hq, (int)hkv, (int)hd, (int)max_seq, w))) return rc;
+    WsLease lease;
+    if ((rc = layer_ws(H, 0, (int)hq, (int)hkv, (int)hd, (int)max_seq, w, lease, st))) return rc;
     if ((rc = set_pos(w, offset, st))) return rc;
     if (bits == 4 && (rc = xquant(x, w.xq_h, 1, (int)H, st))) return rc;
     const Proj qkv{bits, qkv_w, qkv_s, qkv_s_len, qkv_b};
@@ -251,8 +252,9 @@ int tb_fused_transformer_layer_step_w4a32(
                    is_aligned(up_w, 16) && is_aligned(down_w, 16),
                TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: " + op + ": 16-byte aligned device pointers required");
     LayerWs w;
+    WsLease lease;
     if ((rc = layer_ws(hidden, intermediate, (int)num_heads, (int)num_kv_heads, (int)head_dim,
-                       (int)max_seq, w)))
+                       (int)max_seq, w, lease, st)))
         return rc;
     if ((rc = set_pos(w, offset, st))) return rc;
     const float e = (float)eps;

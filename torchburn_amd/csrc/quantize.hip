@@ -9,6 +9,10 @@
 //   * per-channel INT8 (src/quantization/fused_ops.rs:554-589): s = max|w| / 127
 //     (1 when max|w| <= 1e-8), q = clamp(round_half_away(w * (1 / s)), -127, 127).
 //     One block per row.
+//   * per-channel INT4 (quantize_linear_weights_int4, src/quantization/fused_ops.rs:
+//     592-639): s = max|w| / 7 (1 when max|w| <= 1e-8), q = clamp(round_half_away(
+//     w * (1 / s)), -8, 7) + 8 packed two per byte; an odd K pads its last byte
+//     with the nibble 8.  One block per row.
 //   * v2 -> v1 (python/torchburn/llm/loader.py:540-561, the cache migration):
 //     32 nibble bytes copied, the binary16 scale widened to f32.
 #include <math.h>
@@ -70,6 +74,36 @@ __global__ __launch_bounds__(256) void k_quant_int8(const float *__restrict__ w,
     }
 }
 
+__global__ __launch_bounds__(256) void k_quant_int4_rows(const float *__restrict__ w,
+                                                         uint8_t *__restrict__ packed,
+                                                         float *__restrict__ scales, int k) {
+    __shared__ float red[4];
+    const float *wr = w + (size_t)blockIdx.x * k;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(wr[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = mx > 1e-8f ? __fdiv_rn(mx, 7.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, s);
+    if (threadIdx.x == 0) scales[blockIdx.x] = s;
+    const int kp = (k + 1) / 2;
+    uint8_t *pr = packed + (size_t)blockIdx.x * kp;
+    for (int j = threadIdx.x; j < kp; j += blockDim.x) {
+        uint32_t nib[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e = 2 * j + h;
+            // roundf: ties away from zero, as Rust's f32::round
+            const float q = e < k ? fminf(fmaxf(roundf(__fmul_rn(wr[e], inv)), -8.0f), 7.0f) : 0.f;
+            nib[h] = (uint32_t)((int)q + 8) & 15u;
+        }
+        pr[j] = (uint8_t)(nib[0] | (nib[1] << 4));
+    }
+}
+
 // One thread per block: 32 nibble bytes, then the f16 scale as f32.
 __global__ __launch_bounds__(256) void k_unpack_v2(const uint8_t *__restrict__ blocked,
                                                    uint8_t *__restrict__ w,
@@ -95,6 +129,15 @@ int quantize_int4_grouped(const float *w, uint8_t *packed, float *scales, int64_
         hipLaunchKernelGGL(k_quant_int4<32>, grid, dim3(256), 0, st, w, packed, scales, n, (int)k);
     else
         hipLaunchKernelGGL(k_quant_int4<64>, grid, dim3(256), 0, st, w, packed, scales, n, (int)k);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int quantize_int4_rows(const float *w, uint8_t *packed, float *scales, int64_t n, int64_t k,
+                       hipStream_t st) {
+    if (n == 0) return TB_OK;
+    hipLaunchKernelGGL(k_quant_int4_rows, dim3((unsigned)n), dim3(256), 0, st, w, packed, scales,
+                       (int)k);
     TB_LAUNCHED();
     return TB_OK;
 }

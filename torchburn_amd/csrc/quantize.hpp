@@ -10,6 +10,11 @@ namespace tb {
 int quantize_int4_grouped(const float *w, uint8_t *packed, float *scales, int64_t n, int64_t k,
                           int gs, hipStream_t st);
 
+// f32 [n, k] -> v1 nibbles [n, ceil(k/2)] + one f32 scale per row [n]
+// (quantize_linear_weights_int4, fused_ops.rs:592-639).
+int quantize_int4_rows(const float *w, uint8_t *packed, float *scales, int64_t n, int64_t k,
+                       hipStream_t st);
+
 // f32 [n, k] -> int8 [n, k] + per-row f32 scales [n].
 int quantize_int8(const float *w, int8_t *q, float *scales, int64_t n, int64_t k,
                   hipStream_t st);

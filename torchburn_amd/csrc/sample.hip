@@ -35,7 +35,7 @@ constexpr int kThreads = 256;
 
 // Order-preserving key of a logit.  Sampling treats every non-finite logit as
 // -inf (decoder.rs:951-997); greedy keeps +inf (the reference's argmax compares
-// raw values) and never picks NaN.
+// raw values) and never picks a NaN past index 0.
 __device__ __forceinline__ uint32_t fkey(float f, bool greedy) {
     if (greedy ? isnan(f) : !isfinite(f)) f = -INFINITY;
     const uint32_t b = __float_as_uint(f);
@@ -168,7 +168,12 @@ __global__ __launch_bounds__(kThreads) void k_topk_slice(const float *__restrict
     const bool greedy = prm->greedy != 0;
     const int b = blockIdx.x, base = b * kSampleSlice;
     const int n = min(kSampleSlice, V - base);
-    for (int i = threadIdx.x; i < n; i += kThreads) keys[i] = fkey(logits[base + i], greedy);
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = logits[base + i];
+        // greedy scans from logits[0] with strict > (decoder.rs:914-925): a NaN
+        // there is never replaced, so it takes the largest key
+        keys[i] = (greedy && base + i == 0 && isnan(v)) ? 0xFFFFFFFFu : fkey(v, greedy);
+    }
     __syncthreads();
     const int kk = min(k, n);
     int need;

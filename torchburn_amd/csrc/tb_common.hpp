@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/tbhip.h"
@@ -13,8 +14,20 @@ namespace tb {
 // Records the message of the last failing call on this thread and returns code.
 int fail(int code, const std::string &msg);
 
-// The library's device scratch (grow-only, one per device) of at least `bytes`.
-int workspace(size_t bytes, void **out);
+// A stream's device scratch, held by one op while it enqueues its kernels.
+struct WsLease {
+    std::unique_lock<std::mutex> lock;
+    void *ptr = nullptr;
+};
+
+// The scratch of stream `st` on the current device, at least `bytes` long.
+// One buffer per (device, stream): ops on different streams never share
+// scratch, and ops that share a stream are stream-ordered -- the lease keeps a
+// second thread on the same stream from interleaving its enqueue.  The buffer
+// grows geometrically; a replaced buffer is never freed while the process
+// lives (a graph captured earlier may still read it), and growth never
+// synchronizes, so it is legal during stream capture.
+int workspace(size_t bytes, hipStream_t st, WsLease &out);
 
 #define TB_HIP(expr)                                                                   \
     do {                                                                               \

@@ -84,8 +84,9 @@ struct W4Gemv {
         act = (cl < L.sw) && (chunk_raw < L.c);
         // Idle lanes read a valid chunk and contribute zero (scale forced to 0).
         chunk = act ? chunk_raw : 0;
-        gcols = p.k >> p.gshift;
-        sg = (chunk * 32) >> p.gshift;
+        // scale of (row, chunk) at s[row * gcols + sg]: per group, per row or one
+        gcols = p.scale_mode == 0 ? p.k >> p.gshift : (p.scale_mode == 1 ? 1 : 0);
+        sg = p.scale_mode == 0 ? (chunk * 32) >> p.gshift : 0;
         if (V2) {
             bpr = (size_t)(p.k >> 6) * kV2Block;
             soff = (size_t)(chunk >> 1) * kV2Block;   // the chunk's block

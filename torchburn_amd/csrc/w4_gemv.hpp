@@ -47,6 +47,8 @@ struct W4Params {
     float *y;          // [m, n] output
     int m, n, k;
     int gshift;        // log2(group_size)
+    int scale_mode;    // 0: grouped scales [n, k/group]; 1: one scale per row [n]
+                       // (per-channel w4a32_linear); 2: one per-tensor scalar
     int v2;            // 1: w0 is the v2 stream of 34-byte group-64 blocks (f16
                        // scales inside, s0 unused; K % 64 == 0, 4-byte aligned)
     int rows_j;        // rows per block (tuning: 4, 8 or 16; 0 = default)

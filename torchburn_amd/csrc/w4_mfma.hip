@@ -63,7 +63,8 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
                                                  const uint8_t *__restrict__ w1,
                                                  const float *__restrict__ s1,
                                                  float *__restrict__ part, int m, int n, int k,
-                                                 int gshift, int klen, int nbx, int splits) {
+                                                 int scols, int gshift, int klen, int nbx,
+                                                 int splits) {
     constexpr int XV = MT * 2;             // float4 of the X tile per thread
     constexpr int NACC = MT <= 2 ? 4 : 2;  // independent accumulation chains per M tile
     constexpr int NB = MT <= 2 ? 2 : 1;    // X tile buffers (two cost occupancy at MT >= 3)
@@ -81,7 +82,9 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
     const int q = lane >> 4;
     const bool rok = row < n;
     const uint8_t *wrow = w + (size_t)(rok ? row : 0) * (size_t)(k >> 1);
-    const float *srow = V2 ? nullptr : s + (size_t)(rok ? row : 0) * (size_t)(k >> gshift);
+    // scales of the row at srow[kk >> gshift]: scols per row (k / group, or 1 per
+    // row / 0 for one scalar with gshift 31)
+    const float *srow = V2 ? nullptr : s + (size_t)(rok ? row : 0) * (size_t)scols;
     const uint32_t vrow = (uint32_t)(rok ? row : 0) * (uint32_t)((k >> 6) * kV2Block);
 
     float4 xr[XV];
@@ -252,14 +255,16 @@ int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
                    "under 4 GiB");
     const Plan pl = plan(p.m, p.n, p.k, dual);
     dim3 grid(pl.nbx * (dual ? 2 : 1), pl.splits, pl.mz);
+    const int scols = p.scale_mode == 0 ? p.k >> p.gshift : (p.scale_mode == 1 ? 1 : 0);
+    const int gsh = p.scale_mode == 0 ? p.gshift : 31;
 #define TB_MFMA_LAUNCH(MT)                                                                   \
     if (p.v2)                                                                                \
         hipLaunchKernelGGL((k_w4_mfma<MT, true>), grid, dim3(256), 0, st, p.x, p.w0, p.s0,   \
-                           p.w1, p.s1, part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx,        \
+                           p.w1, p.s1, part, p.m, p.n, p.k, scols, gsh, pl.klen, pl.nbx,     \
                            pl.splits);                                                       \
     else                                                                                     \
         hipLaunchKernelGGL((k_w4_mfma<MT, false>), grid, dim3(256), 0, st, p.x, p.w0, p.s0,  \
-                           p.w1, p.s1, part, p.m, p.n, p.k, p.gshift, pl.klen, pl.nbx,        \
+                           p.w1, p.s1, part, p.m, p.n, p.k, scols, gsh, pl.klen, pl.nbx,     \
                            pl.splits)
     switch (pl.mt) {
         case 1: TB_MFMA_LAUNCH(1); break;

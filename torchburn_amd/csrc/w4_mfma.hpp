@@ -19,6 +19,7 @@ struct MfmaParams {
     float *y;            // [m, n]
     int m, n, k;
     int gshift;          // log2(group_size)
+    int scale_mode;      // 0: grouped [n, k/group]; 1: one scale per row; 2: one scalar
     int v2;              // 1: w0 / w1 are v2 streams of 34-byte group-64 blocks
                          // (f16 scales inside, s0 / s1 unused)
 };

@@ -53,6 +53,7 @@ def _bind():
         "tb_decoder_kv_len": [p, C.POINTER(i64)],
         "tb_decoder_get_logits": [p, p],
         "tb_decoder_set_seed": [p, C.c_uint64],
+        "tb_decoder_set_rope_tables": [p, p, p, i64, i64],
         "tb_decoder_time_greedy": [p, i64, i64, i64, C.POINTER(C.c_float)],
         "tb_decoder_destroy": [p],
     }
@@ -93,26 +94,82 @@ def decoder_symbols() -> list:
             "tb_decoder_reset_kv", "tb_decoder_copy_kv", "tb_decoder_kv_len",
             "tb_decoder_get_logits", "tb_decoder_set_seed", "tb_decoder_time_greedy",
             "tb_decoder_destroy", "tb_decoder_generate_sampled", "tb_decoder_verify",
-            "tb_decoder_speculative_accept", "tb_speculative_accept_rows", "tb_spec_uniform"]
+            "tb_decoder_speculative_accept", "tb_speculative_accept_rows", "tb_spec_uniform",
+            "tb_decoder_set_rope_tables"]
 
 
-def _as_buffer(t: Any, dtype=None):
-    """(pointer, keep-alive object, numpy dtype) of a contiguous tensor/array."""
+_NP_TO_TORCH = {"float32": "float32", "uint8": "uint8", "int8": "int8", "int64": "int64"}
+
+
+def _as_buffer(t: Any, dtype=None, numel: Optional[int] = None, what: str = "tensor"):
+    """(pointer, keep-alive object, dtype name) of a contiguous tensor/array.
+
+    ``dtype`` (a numpy dtype) converts the data first, for torch tensors as for
+    arrays; ``numel`` is the element count the C side will read, checked here
+    because the C ABI receives no lengths (a short or mis-typed buffer would be
+    over-read), as the reference's typed_slice rejects a wrong element size
+    (src/llm/decoder.rs:77-89)."""
     if t is None:
         return None, None, None
     try:
         import torch
         if isinstance(t, torch.Tensor):
-            t = t.detach().contiguous()
-            return t.data_ptr(), t, str(t.dtype).replace("torch.", "")
+            t = t.detach()
+            if dtype is not None:
+                t = t.to(getattr(torch, _NP_TO_TORCH[np.dtype(dtype).name]))
+            t = t.contiguous()
+            name = str(t.dtype).replace("torch.", "")
+            if numel is not None and t.numel() != numel:
+                raise _lib.UnsupportedOpError(
+                    f"{_lib.UNSUPPORTED_MARKER} {what}: expected {numel} elements, got {t.numel()}")
+            return t.data_ptr(), t, name
     except ImportError:
         pass
     a = np.ascontiguousarray(t if dtype is None else np.asarray(t, dtype=dtype))
+    if numel is not None and a.size != numel:
+        raise _lib.UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {what}: expected {numel} elements, got {a.size}")
     return a.ctypes.data, a, str(a.dtype)
 
 
 def _bits_of(dtype: str) -> int:
-    return {"uint8": 4, "int8": 8, "float32": 32}[dtype]
+    bits = {"uint8": 4, "int8": 8, "float32": 32}.get(dtype)
+    if bits is None:
+        raise _lib.UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} projection weights must be uint8 (INT4 packed), int8 or "
+            f"float32, got {dtype}")
+    return bits
+
+
+def _proj_sizes(bits: int, n: int, k: int, gs: int) -> Tuple[int, int]:
+    """(weight elements, scale elements) the decoder reads for a projection [n, k]."""
+    if bits == 4:
+        return n * ((k + 1) // 2), n * (k // gs)
+    if bits == 8:
+        return n * k, n
+    return n * k, 0
+
+
+def _row_scales(s: Any, n: int):
+    """INT8 scales as n per-row values: a 1-element (per-tensor) scale is repeated."""
+    a = s.detach().float().reshape(-1).cpu().numpy() if hasattr(s, "detach") else \
+        np.asarray(s, np.float32).reshape(-1)
+    return np.repeat(a, n) if a.size == 1 and n != 1 else a
+
+
+def rotary_tables_f32(max_seq: int, head_dim: int, theta: float) -> Tuple[np.ndarray, np.ndarray]:
+    """cos / sin [max_seq, head_dim] exactly as the reference's per-layer Python
+    path builds them (RotaryEmbedding, python/torchburn/llm/model.py:108-122):
+    inv_freq = 1 / theta ** (arange(0, d, 2) / d) in float32, the angle
+    t * inv_freq as a float32 product, cos / sin in float32, halves duplicated.
+    The native decoder instead builds its tables in f64 (decoder.rs:334-350);
+    the two differ by up to ~1e-4 at positions in the thousands."""
+    import torch
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    t = torch.arange(0, max_seq, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().numpy().astype(np.float32), emb.sin().numpy().astype(np.float32)
 
 
 class RustQwenDecoder:
@@ -133,36 +190,77 @@ class RustQwenDecoder:
                  rope_theta: float = 1e6):
         L = _bind()
         self._h = None
-        emb_p, emb_k, _ = _as_buffer(embed_tokens, np.float32)
-        fn_p, fn_k, _ = _as_buffer(final_norm_w, np.float32)
-        lm_p, lm_k, lm_dt = _as_buffer(lm_head_w)
-        ls_p, ls_k, _ = _as_buffer(lm_head_s, np.float32) if lm_head_s is not None else (None, None, None)
         vocab = int(embed_tokens.shape[0])
+        H, I, gs = int(hidden_size), int(intermediate_size), int(group_size)
+        qd, tq = num_heads * head_dim, (num_heads + 2 * num_kv_heads) * head_dim
         if len(layers_data) != num_layers:
             raise ValueError(f"expected {num_layers} layers, got {len(layers_data)}")
+        emb_p, emb_k, _ = _as_buffer(embed_tokens, np.float32, vocab * H, "embed_tokens")
+        fn_p, fn_k, _ = _as_buffer(final_norm_w, np.float32, H, "final_norm_w")
+        lm_dt = _as_buffer(lm_head_w)[2]
+        lmbits = _bits_of(lm_dt)
+        lw_n, ls_n = _proj_sizes(lmbits, vocab, H, gs)
+        lm_p, lm_k, _ = _as_buffer(lm_head_w, None, lw_n, "lm_head_w")
+        if lmbits == 8 and lm_head_s is not None:
+            lm_head_s = _row_scales(lm_head_s, vocab)
+        ls_p, ls_k, _ = (_as_buffer(lm_head_s, np.float32, ls_n, "lm_head_s")
+                         if lm_head_s is not None and lmbits != 32 else (None, None, None))
         wdt = _as_buffer(layers_data[0][1])[2] if num_layers else "uint8"
+        wbits = _bits_of(wdt)
+        if wbits == 32:
+            raise _lib.UnsupportedOpError(
+                f"{_lib.UNSUPPORTED_MARKER} decoder projections must be INT4 or INT8")
         cfg = _Config(num_layers, hidden_size, intermediate_size, num_heads, num_kv_heads,
                       head_dim, vocab, group_size, max_seq_len, float(rms_norm_eps),
-                      float(rope_theta), _bits_of(wdt), _bits_of(lm_dt))
+                      float(rope_theta), wbits, lmbits)
         h = C.c_void_p()
         _lib.check(L.tb_decoder_create(C.byref(cfg), emb_p, fn_p, lm_p, ls_p, C.byref(h)))
         self._h = h
         self.vocab_size = vocab
         self.hidden_size = hidden_size
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads
         self.num_layers = num_layers
         self.max_seq_len = max_seq_len
         self.weight_bits = cfg.weight_bits
         self.lm_head_bits = cfg.lm_head_bits
         del emb_k, fn_k, lm_k, ls_k
+        # (name, projection rows, K) of the weight / scale pairs in capsule order
+        shapes = {1: ("qkv", tq, H), 3: ("o", H, qd), 6: ("gate", I, H), 8: ("up", I, H),
+                  10: ("down", H, I)}
+        wdtype = np.uint8 if wbits == 4 else np.int8
         for li, caps in enumerate(layers_data):
             if len(caps) < 12:
                 raise _lib.UnsupportedOpError(
                     f"{_lib.UNSUPPORTED_MARKER} Each layer requires 12 capsules: input_norm, "
                     "qkv_w, qkv_s, o_w, o_s, post_norm, gate_w, gate_s, up_w, up_s, down_w, down_s")
-            bufs = [_as_buffer(caps[i]) for i in range(12)]
-            qkv_b = _as_buffer(caps[12], np.float32) if len(caps) >= 13 and caps[12] is not None \
-                else (None, None, None)
+            bufs = [None] * 12
+            for i in (0, 5):
+                bufs[i] = _as_buffer(caps[i], np.float32, H, f"layer {li} norm")
+            for i, (name, n, k) in shapes.items():
+                wn, sn = _proj_sizes(wbits, n, k, gs)
+                if _as_buffer(caps[i])[2] != np.dtype(wdtype).name:
+                    raise _lib.UnsupportedOpError(
+                        f"{_lib.UNSUPPORTED_MARKER} layer {li} {name}_w must be "
+                        f"{np.dtype(wdtype).name} like the other projections")
+                bufs[i] = _as_buffer(caps[i], None, wn, f"layer {li} {name}_w")
+                sc = _row_scales(caps[i + 1], n) if wbits == 8 else caps[i + 1]
+                bufs[i + 1] = _as_buffer(sc, np.float32, sn, f"layer {li} {name}_s")
+            qkv_b = _as_buffer(caps[12], np.float32, tq, f"layer {li} qkv_b") \
+                if len(caps) >= 13 and caps[12] is not None else (None, None, None)
             _lib.check(L.tb_decoder_set_layer(self._h, li, *[b[0] for b in bufs], qkv_b[0]))
+
+    def set_rope_tables(self, cos, sin) -> None:
+        """Replace the decoder's f64-built RoPE tables (decoder.rs:334-350) with
+        caller-built cos / sin [max_seq_len, head_dim], e.g. rotary_tables_f32(),
+        the tables of the reference's per-layer Python path (no reference
+        counterpart on RustQwenDecoder)."""
+        n = self.max_seq_len * self.head_dim
+        cp, ck, _ = _as_buffer(cos, np.float32, n, "cos")
+        sp, sk, _ = _as_buffer(sin, np.float32, n, "sin")
+        _lib.check(_bind().tb_decoder_set_rope_tables(self._h, cp, sp, self.max_seq_len,
+                                                      self.head_dim))
+        del ck, sk
 
     # -- stepping -----------------------------------------------------------
 
@@ -274,9 +372,16 @@ class RustQwenDecoder:
         """Per-layer [.., kv_heads, src_max, head_dim] f32 tensors (decoder.rs:479-523)."""
         L = _bind()
         for li in range(min(self.num_layers, len(k_tensors))):
-            kp, kk, _ = _as_buffer(k_tensors[li], np.float32)
-            vp, vk, _ = _as_buffer(v_tensors[li], np.float32)
-            src_max = int(k_tensors[li].shape[-2]) if len(k_tensors[li].shape) >= 2 else seq_len
+            shp = tuple(k_tensors[li].shape)
+            if len(shp) < 2 or shp[-1] != self.head_dim or tuple(v_tensors[li].shape) != shp:
+                raise _lib.UnsupportedOpError(
+                    f"{_lib.UNSUPPORTED_MARKER} layer {li} KV tensors must be "
+                    f"[.., {self.num_kv_heads}, src_max, {self.head_dim}], got {list(shp)} / "
+                    f"{list(v_tensors[li].shape)}")
+            src_max = int(shp[-2])
+            n = self.num_kv_heads * src_max * self.head_dim
+            kp, kk, _ = _as_buffer(k_tensors[li], np.float32, n, f"layer {li} k")
+            vp, vk, _ = _as_buffer(v_tensors[li], np.float32, n, f"layer {li} v")
             _lib.check(L.tb_decoder_copy_kv(self._h, li, kp, vp, src_max, int(seq_len)))
             del kk, vk
 

@@ -99,6 +99,23 @@ def quantize_weight_int4_grouped(
     return packed.to(weight.device), scales.to(weight.device)
 
 
+def quantize_weight_int4(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(N, K) float -> (packed uint8 (N, (K+1)//2), per-channel float32 scales (N,))
+    on the GPU (tb_quantize_weight_int4): s = amax / 7 (1 when amax <= 1e-8),
+    q = clamp(round_half_away(w * (1/s)), -8, 7) + 8, two per byte (reference
+    python/torchburn/quantization.py:44-50 -> src/quantization/fused_ops.rs:592-639).
+    The result is on w's device."""
+    if w.ndim != 2:
+        raise ValueError(f"Expected 2D weight, got {w.shape}")
+    n, k = w.shape
+    dev = _target(w)
+    wc = _on_gpu(w.detach(), torch.float32, dev)
+    q = torch.empty((n, (k + 1) // 2), dtype=torch.uint8, device=dev)
+    s = torch.empty(n, dtype=torch.float32, device=dev)
+    _lib.call("tb_quantize_weight_int4", _ptr(wc), _ptr(q), _ptr(s), n, k, _stream(dev))
+    return q.to(w.device), s.to(w.device)
+
+
 def pack_rows_w4a32_group64_v1_to_v2(w_packed: torch.Tensor, scales: torch.Tensor,
                                      k: int) -> torch.Tensor:
     """v1 nibbles (N, K/2) + f32 scales (N, K/64) -> v2 blocks (N, (K/64) * 34) uint8:
@@ -203,6 +220,45 @@ def unpack_rows_w4a32_group64_v2_to_v1(blocked: torch.Tensor) -> Tuple[torch.Ten
 # --------------------------------------------------------------------------
 # Linear ops (reference quantization.py:193-269 -> src/ffi/quantization_ffi.rs)
 # --------------------------------------------------------------------------
+
+def w4a32_linear(
+    x: torch.Tensor,
+    w_packed: torch.Tensor,
+    scales: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Per-channel INT4 linear: out[..., N] = (x @ unpack(w).T) * scales + bias
+    (reference quantization.py:219-243 -> gemv.rs:1066-1182); scales of N
+    elements or one per-tensor scalar."""
+    if x.dim() < 1:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_linear requires x with at least 1 dimension")
+    dev = _target(x)
+    k = x.shape[-1]
+    x2 = _on_gpu(x.reshape(-1, k), torch.float32, dev)
+    m = x2.shape[0]
+    w = _on_gpu(w_packed, torch.uint8, dev)
+    s = _on_gpu(scales, torch.float32, dev).reshape(-1)
+    b = _on_gpu(bias, torch.float32, dev)
+    if w.ndim != 2:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_linear requires 2D packed weight matrix")
+    n = w.shape[0]
+    if w.shape[1] != (k + 1) // 2:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_linear dimension mismatch: x K={k}, "
+            f"w packed K={w.shape[1]} (expected {(k + 1) // 2})")
+    if s.numel() not in (1, n):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} w4a32_linear scales must have 1 or {n} elements, "
+            f"got {s.numel()}")
+    if b is not None and b.numel() != n:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} bias must have {n} elements")
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _lib.call("tb_w4a32_linear", _ptr(x2), _ptr(w), _ptr(s), s.numel(), _ptr(b), _ptr(out),
+              m, n, k, _stream(dev))
+    return out.reshape(*x.shape[:-1], n).to(x.device)
+
 
 def w4a32_grouped_linear(
     x: torch.Tensor,
@@ -315,12 +371,10 @@ def fused_swiglu_mlp_w4a32(
     gs, us, ds = (_on_gpu(t, torch.float32, dev) for t in (gate_s, up_s, down_s))
     gb, ub, db = (_on_gpu(t, torch.float32, dev) for t in (gate_b, up_b, down_b))
     inter, n_out = gw.shape[0], dw.shape[0]
-    for name, w_, rows, kk in (("gate", gw, inter, k), ("up", uw, inter, k),
-                               ("down", dw, n_out, inter)):
-        if w_.ndim != 2 or w_.shape[0] != rows or w_.shape[1] != (kk + 1) // 2:
-            raise UnsupportedOpError(
-                f"{_lib.UNSUPPORTED_MARKER} fused_swiglu_mlp_w4a32 {name} weight shape "
-                f"{list(w_.shape)} does not match ({rows}, {(kk + 1) // 2})")
+    op = "fused_swiglu_mlp_w4a32"
+    _check_w4(op, "gate", gw, gs, gb, inter, k, group_size)
+    _check_w4(op, "up", uw, us, ub, inter, k, group_size)
+    _check_w4(op, "down", dw, ds, db, n_out, inter, group_size)
     r = None if residual is None else _on_gpu(residual.reshape(m, n_out), torch.float32, dev)
     out = torch.empty((m, n_out), dtype=torch.float32, device=dev)
     _lib.call("tb_fused_swiglu_mlp_w4a32", _ptr(x2), _ptr(gw), _ptr(gs), _ptr(gb), _ptr(uw),
@@ -367,10 +421,48 @@ def w8a32_linear(
             f"{_lib.UNSUPPORTED_MARKER} w8a32_linear dimension mismatch: x K={k}, "
             f"w {list(wt.shape)}")
     n = wt.shape[0]
+    _check_w8("w8a32_linear", "w", wt, s, b, n, k)
     out = torch.empty((m, n), dtype=torch.float32, device=dev)
     _lib.call("tb_w8a32_linear", _ptr(x2), _ptr(wt), _ptr(s), s.numel(), _ptr(b), _ptr(out),
               m, n, k, _stream(dev))
     return out.reshape(*x.shape[:-1], n).to(x.device)
+
+
+def _check_w4(op: str, name: str, w: torch.Tensor, s: torch.Tensor, b: Optional[torch.Tensor],
+              n: int, k: int, gs: int) -> None:
+    """Grouped INT4 projection operands: packed w (n, ceil(k/2)), scales of
+    n * ceil(k/gs) elements, bias of n elements or None (the reference's checks,
+    src/quantization/packed_v2.rs:565-596)."""
+    if w.ndim != 2 or tuple(w.shape) != (n, (k + 1) // 2):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} weight shape {list(w.shape)} does not "
+            f"match ({n}, {(k + 1) // 2})")
+    ng = (k + gs - 1) // gs
+    if s.numel() != n * ng:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} scales must be [{n}, {ng}], got "
+            f"{list(s.shape)}")
+    if b is not None and b.numel() != n:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} bias must have {n} elements, got {b.numel()}")
+
+
+def _check_w8(op: str, name: str, w: torch.Tensor, s: torch.Tensor, b: Optional[torch.Tensor],
+              n: int, k: int) -> None:
+    """INT8 projection operands: w (n, k); 1 (per-tensor) or n (per-row) scales;
+    bias of n elements or None (the reference's gemv_w8a32 s_len rule,
+    src/quantization/fused_ops.rs:80-97)."""
+    if w.ndim != 2 or tuple(w.shape) != (n, k):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} weight shape {list(w.shape)} does not "
+            f"match ({n}, {k})")
+    if s.numel() not in (1, n):
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} scales must have 1 or {n} elements, "
+            f"got {s.numel()}")
+    if b is not None and b.numel() != n:
+        raise UnsupportedOpError(
+            f"{_lib.UNSUPPORTED_MARKER} {op} {name} bias must have {n} elements, got {b.numel()}")
 
 
 def fused_swiglu_mlp_w8a32(
@@ -380,7 +472,9 @@ def fused_swiglu_mlp_w8a32(
     down_w: torch.Tensor, down_s: torch.Tensor, down_b: Optional[torch.Tensor],
     residual: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """INT8 down(silu(gate(x)) * up(x)) [+ residual] (reference fused_ops.rs:8-133)."""
+    """INT8 down(silu(gate(x)) * up(x)) [+ residual] (reference fused_ops.rs:8-133).
+    Each projection's scales are per row or one per-tensor scalar; biases are
+    optional."""
     dev = _target(x)
     k = x.shape[-1]
     x2 = _on_gpu(x.reshape(-1, k), torch.float32, dev)
@@ -389,12 +483,28 @@ def fused_swiglu_mlp_w8a32(
     gs, us, ds = (_on_gpu(t, torch.float32, dev).reshape(-1) for t in (gate_s, up_s, down_s))
     gb, ub, db = (_on_gpu(t, torch.float32, dev) for t in (gate_b, up_b, down_b))
     inter, n_out = gw.shape[0], dw.shape[0]
+    op = "fused_swiglu_mlp_w8a32"
+    _check_w8(op, "gate", gw, gs, gb, inter, k)
+    _check_w8(op, "up", uw, us, ub, inter, k)
+    _check_w8(op, "down", dw, ds, db, n_out, inter)
     r = None if residual is None else _on_gpu(residual.reshape(m, n_out), torch.float32, dev)
     out = torch.empty((m, n_out), dtype=torch.float32, device=dev)
-    _lib.call("tb_fused_swiglu_mlp_w8a32", _ptr(x2), _ptr(gw), _ptr(gs), _ptr(gb), _ptr(uw),
-              _ptr(us), _ptr(ub), _ptr(dw), _ptr(ds), _ptr(db), _ptr(r), _ptr(out),
-              m, k, inter, n_out, _stream(dev))
+    _lib.call("tb_fused_swiglu_mlp_w8a32", _ptr(x2), _ptr(gw), _ptr(gs), gs.numel(), _ptr(gb),
+              _ptr(uw), _ptr(us), us.numel(), _ptr(ub), _ptr(dw), _ptr(ds), ds.numel(), _ptr(db),
+              _ptr(r), _ptr(out), m, k, inter, n_out, _stream(dev))
     return out.reshape(*x.shape[:-1], n_out).to(x.device)
+
+
+def fused_swiglu_mlp_batched(x: torch.Tensor, gate: Any, up: Any, down: Any) -> torch.Tensor:
+    """Prefill SwiGLU MLP over three QuantizedLinear modules (reference
+    quantization.py:358-405, called at python/torchburn/llm/model.py:359): INT4
+    runs fused_swiglu_mlp_batched_w4a32 (all T rows as one FP32-MFMA GEMM pair
+    from 5 rows), INT8 the per-token fused_swiglu_mlp."""
+    if gate.bits != 4:
+        return fused_swiglu_mlp(x, gate, up, down)
+    return fused_swiglu_mlp_batched_w4a32(
+        x, gate.qweight, gate.scales, gate.bias, up.qweight, up.scales, up.bias, down.qweight,
+        down.scales, down.bias, gate.group_size)
 
 
 def fused_swiglu_mlp(x: torch.Tensor, gate: Any, up: Any, down: Any) -> torch.Tensor:
@@ -415,12 +525,17 @@ def fused_swiglu_mlp(x: torch.Tensor, gate: Any, up: Any, down: Any) -> torch.Te
 # fused_ops.rs:718-1062, fused_transformer.rs:16-376)
 # --------------------------------------------------------------------------
 
-def _cache_on_gpu(c: torch.Tensor, dev: torch.device, name: str) -> Tuple[torch.Tensor, int]:
-    """The KV cache as a contiguous f32 GPU tensor (the caller's own storage when
-    it already is one) and its max_seq (the length of dim -2: [.., Hkv, max, hd])."""
-    if c.ndim < 3:
+def _cache_on_gpu(c: torch.Tensor, dev: torch.device, name: str, num_kv_heads: int,
+                  head_dim: int):
+    """The cache as a contiguous f32 device tensor (the caller's own tensor when
+    it already is one) and its max_seq (the length of dim -2: [.., Hkv, max, hd]).
+    The kernels write k / v at `offset` of every KV head, so the shape is checked
+    against num_kv_heads and head_dim here (the reference's slices are
+    bounds-checked, fused_ops.rs:981-994)."""
+    if c.ndim < 3 or int(c.shape[-3]) != num_kv_heads or int(c.shape[-1]) != head_dim:
         raise UnsupportedOpError(
-            f"{_lib.UNSUPPORTED_MARKER} {name} must be [..., num_kv_heads, max_seq, head_dim]")
+            f"{_lib.UNSUPPORTED_MARKER} {name} must be [..., num_kv_heads={num_kv_heads}, "
+            f"max_seq, head_dim={head_dim}], got {list(c.shape)}")
     g = c if (c.device == dev and c.dtype == torch.float32 and c.is_contiguous()) else \
         c.detach().to(device=dev, dtype=torch.float32).contiguous()
     return g, int(c.shape[-2])
@@ -447,15 +562,20 @@ def _attention_step(bits: int, x, qkv_w, qkv_s, qkv_b, o_w, o_s, o_b, k_cache, v
     qw, ow = _on_gpu(qkv_w, wdt, dev), _on_gpu(o_w, wdt, dev)
     qs, os_ = _on_gpu(qkv_s, torch.float32, dev), _on_gpu(o_s, torch.float32, dev)
     qb, ob = _on_gpu(qkv_b, torch.float32, dev), _on_gpu(o_b, torch.float32, dev)
-    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache")
-    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache")
+    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache", num_kv_heads, head_dim)
+    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache", num_kv_heads, head_dim)
+    if tuple(vc.shape[-3:]) != tuple(kc.shape[-3:]):
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: k / v caches differ in shape")
     cs = _on_gpu(cos.reshape(-1), torch.float32, dev)
     sn = _on_gpu(sin.reshape(-1), torch.float32, dev)
     nq = (num_heads + 2 * num_kv_heads) * head_dim
-    if qw.shape[0] != nq or ow.shape[0] != h:
-        raise UnsupportedOpError(
-            f"{_lib.UNSUPPORTED_MARKER} {name}: qkv rows {qw.shape[0]} (expected {nq}) / "
-            f"o rows {ow.shape[0]} (expected {h})")
+    qd = num_heads * head_dim
+    if bits == 4:
+        _check_w4(name, "qkv", qw, qs, qb, nq, h, group_size)
+        _check_w4(name, "o", ow, os_, ob, h, qd, group_size)
+    else:
+        _check_w8(name, "qkv", qw, qs.reshape(-1), qb, nq, h)
+        _check_w8(name, "o", ow, os_.reshape(-1), ob, h, qd)
     if cs.numel() < head_dim or sn.numel() < head_dim:
         raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: cos / sin need head_dim values")
     out = torch.empty(h, dtype=torch.float32, device=dev)
@@ -514,14 +634,22 @@ def fused_transformer_layer_step_w4a32(x, input_norm_w, qkv_w, qkv_s, qkv_b, o_w
     qs, os_, gs, us, ds = (g(t) for t in (qkv_s, o_s, gate_s, up_s, down_s))
     qb, ob, gb, ub, db = (g(t) for t in (qkv_b, o_b, gate_b, up_b, down_b))
     inw, pnw = g(input_norm_w), g(post_norm_w)
-    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache")
-    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache")
+    kc, max_seq = _cache_on_gpu(k_cache, dev, "k_cache", num_kv_heads, head_dim)
+    vc, _ = _cache_on_gpu(v_cache, dev, "v_cache", num_kv_heads, head_dim)
+    if tuple(vc.shape[-3:]) != tuple(kc.shape[-3:]):
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: k / v caches differ in shape")
     cs, sn = g(cos.reshape(-1)), g(sin.reshape(-1))
+    if cs.numel() < head_dim or sn.numel() < head_dim:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: cos / sin need head_dim values")
     inter = gw.shape[0]
-    if dw.shape[0] != h or dw.shape[1] != (inter + 1) // 2:
-        raise UnsupportedOpError(
-            f"{_lib.UNSUPPORTED_MARKER} {name}: down weight {list(dw.shape)} does not match "
-            f"({h}, {(inter + 1) // 2})")
+    nq, qd = (num_heads + 2 * num_kv_heads) * head_dim, num_heads * head_dim
+    _check_w4(name, "qkv", qw, qs, qb, nq, h, group_size)
+    _check_w4(name, "o", ow, os_, ob, h, qd, group_size)
+    _check_w4(name, "gate", gw, gs, gb, inter, h, group_size)
+    _check_w4(name, "up", uw, us, ub, inter, h, group_size)
+    _check_w4(name, "down", dw, ds, db, h, inter, group_size)
+    if inw.numel() != h or pnw.numel() != h:
+        raise UnsupportedOpError(f"{_lib.UNSUPPORTED_MARKER} {name}: norm weights need {h} values")
     _lib.call("tb_fused_transformer_layer_step_w4a32", _ptr(xg), _ptr(inw), _ptr(qw), _ptr(qs),
               _ptr(qb), _ptr(ow), _ptr(os_), _ptr(ob), _ptr(pnw), _ptr(gw), _ptr(gs), _ptr(gb),
               _ptr(uw), _ptr(us), _ptr(ub), _ptr(dw), _ptr(ds), _ptr(db), _ptr(kc), _ptr(vc),
