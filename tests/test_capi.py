@@ -40,17 +40,26 @@ def test_argument_errors_before_any_gpu_call():
     L = _lib.lib()
     buf = (C.c_float * 64)()
     p = C.cast(buf, C.c_void_p).value
-    # group size 16 is not supported by the kernels -> UnsupportedOpError
-    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, 1, 1, 64, 16, None)
-    assert rc == _lib.TB_ERR_UNSUPPORTED
+    # an odd group size has no byte-aligned layout -> UnsupportedOpError
+    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, 1, 1, 64, 9, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"even" in L.tb_last_error()
     with pytest.raises(_lib.UnsupportedOpError, match="TB_UNSUPPORTED"):
         _lib.check(rc)
-    # K not a multiple of the group
-    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, 1, 1, 48, 32, None)
-    assert rc == _lib.TB_ERR_UNSUPPORTED and b"multiple" in L.tb_last_error()
-    # misaligned pointers
-    rc = L.tb_w4a32_grouped_linear(p + 4, p, p, None, p, 1, 1, 64, 32, None)
+    # negative dimension, null weight
+    rc = L.tb_w4a32_grouped_linear(p, p, p, None, p, -1, 1, 64, 32, None)
     assert rc == _lib.TB_ERR_UNSUPPORTED
+    rc = L.tb_w4a32_grouped_linear(p, None, p, None, p, 1, 1, 64, 32, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"null" in L.tb_last_error()
+    # misaligned activations
+    rc = L.tb_w4a32_grouped_linear(p + 2, p, p, None, p, 1, 1, 64, 32, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED
+    # per-channel scales: 1 or N elements
+    rc = L.tb_w4a32_linear(p, p, p, 3, None, p, 1, 2, 64, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"1 or N" in L.tb_last_error()
+    # INT8 MLP scale lengths (fused_ops.rs:80-97)
+    rc = L.tb_fused_swiglu_mlp_w8a32(p, p, p, 5, None, p, p, 8, None, p, p, 8, None, None, p,
+                                     1, 32, 8, 8, None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"1 or N" in L.tb_last_error()
 
 
 @pytest.mark.parametrize("field,value,msg", [
