@@ -127,8 +127,16 @@ def test_errors_match_reference_contract(cuda):
     w = T(np.zeros((8, 32), np.uint8))
     with pytest.raises(tb.UnsupportedOpError, match="scales mismatch"):
         tb.w4a32_grouped_linear(x, w, T(np.ones((8, 3), np.float32)), group_size=32)
+    # groups start on byte boundaries: an odd group size is refused, an even one
+    # that the streaming kernels do not take runs the any-shape GEMV
     with pytest.raises(tb.UnsupportedOpError, match="group_size"):
-        tb.w4a32_grouped_linear(x, w, T(np.ones((8, 4), np.float32)), group_size=16)
+        tb.w4a32_grouped_linear(x, w, T(np.ones((8, 8), np.float32)), group_size=9)
+    g = synth.rng(15)
+    xs = synth.activations(g, 1, 64)
+    q = g.integers(-8, 8, (8, 64)).astype(np.int8)
+    ss = (np.abs(g.normal(0, 0.02, (8, 4))) + 1e-3).astype(np.float32)
+    y = tb.w4a32_grouped_linear(T(xs), T(O.pack_int4(q)), T(ss), group_size=16).cpu().numpy()
+    assert rel(y, O.gemm_w4(xs, O.pack_int4(q), ss, None, group_size=16)) < TOL
 
 
 def test_non_finite_activations_propagate(cuda):
