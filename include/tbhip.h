@@ -204,6 +204,27 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
                               int64_t group_size, void *stream);
 
 /*
+ * tb_fused_swiglu_mlp_w4a32 without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * intermediates (h, the x / h chunk records or the MFMA split-K partials) live
+ * in a 4 MiB static device array, one per GPU, instead of the per-stream
+ * workspace: shapes needing more return TB_ERR_UNSUPPORTED with the byte count
+ * (the Llama-3-8B MLP needs about 121 KB per activation row on the GEMV path,
+ * M <= 4).  Every call on one GPU shares that array, so calls that overlap on
+ * one GPU (two streams, or two threads) race; nothing in it needs clearing
+ * between calls.  Same arguments and results as tb_fused_swiglu_mlp_w4a32.
+ */
+TB_API int tb_fused_swiglu_mlp_w4a32_noalloc(const float *x, const uint8_t *gate_w,
+                                             const float *gate_s, const float *gate_b,
+                                             const uint8_t *up_w, const float *up_s,
+                                             const float *up_b, const uint8_t *down_w,
+                                             const float *down_s, const float *down_b,
+                                             const float *residual, float *out, int64_t m,
+                                             int64_t k, int64_t inter, int64_t n_out,
+                                             int64_t group_size, void *stream);
+
+/*
  * Activation chunk records, for callers that reuse one x across several INT4
  * projections (no reference counterpart: the reference converts x inside each
  * GEMV).  A record holds 32 activations as 24-bit fixed-point integers in six

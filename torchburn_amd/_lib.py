@@ -50,6 +50,7 @@ _SIGS = {
                          C.c_uint64, C.c_uint64, _p, _p, _p],
     "tb_swiglu_w4a32": [_p] * 8 + [_i64] * 4 + [_p],
     "tb_fused_swiglu_mlp_w4a32": [_p] * 12 + [_i64] * 5 + [_p],
+    "tb_fused_swiglu_mlp_w4a32_noalloc": [_p] * 12 + [_i64] * 5 + [_p],
     "tb_w8a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "tb_w4a32_linear": [_p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "tb_quantize_weight_int4": [_p, _p, _p, _i64, _i64, _p],

@@ -402,6 +402,39 @@ static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
     return w4_rows(d, depi, m, hq, true, st);
 }
 
+// ---- the no-allocation MLP entry point ----
+// Scratch of tb_fused_swiglu_mlp_w4a32_noalloc, in the code object's static
+// device memory: every GPU the library runs on holds one copy of
+// kNoAllocScratchBytes until the process ends.  `scratch` names the host-side
+// stand-in of the array; its device address (per device) comes from
+// hipGetSymbolAddress and is the only form passed to kernels.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];   // device address of `scratch` per device, or null
+}  // namespace
+
+// The current device's address of `scratch`, looked up on the first call per
+// device with that device current (no allocation).
+static int noalloc_scratch(void **out) {
+    int dev = 0;
+    TB_HIP(hipGetDevice(&dev));
+    TB_REQUIRE(dev >= 0 && dev < kMaxDevices, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: no-alloc entry points support device ids below " +
+                   std::to_string(kMaxDevices));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        TB_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TB_OK;
+}
+
 }  // namespace tb
 
 using namespace tb;
@@ -616,6 +649,28 @@ int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, const float
     WsLease lease;
     if ((rc = workspace(mlp_w4_scratch_bytes(a), st, lease))) return rc;
     return mlp_w4_run(a, lease.ptr, st);
+}
+
+int tb_fused_swiglu_mlp_w4a32_noalloc(const float *x, const uint8_t *gate_w,
+                                      const float *gate_s, const float *gate_b,
+                                      const uint8_t *up_w, const float *up_s, const float *up_b,
+                                      const uint8_t *down_w, const float *down_s,
+                                      const float *down_b, const float *residual, float *out,
+                                      int64_t m, int64_t k, int64_t inter, int64_t n_out,
+                                      int64_t group_size, void *stream) {
+    const MlpW4 a{x, gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
+                  residual, out, m, k, inter, n_out, group_size};
+    int rc = mlp_w4_check(a, "fused_swiglu_mlp_w4a32_noalloc");
+    if (rc || m == 0 || n_out == 0) return rc;
+    const size_t need = mlp_w4_scratch_bytes(a);
+    TB_REQUIRE(need <= kNoAllocScratchBytes, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: fused_swiglu_mlp_w4a32_noalloc: this shape needs " +
+                   std::to_string(need) + " bytes of scratch; the static scratch holds " +
+                   std::to_string(kNoAllocScratchBytes) +
+                   " (use tb_fused_swiglu_mlp_w4a32, which allocates)");
+    void *ws = nullptr;
+    if ((rc = noalloc_scratch(&ws))) return rc;
+    return mlp_w4_run(a, ws, (hipStream_t)stream);
 }
 
 int64_t tb_x_records_bytes(int64_t m, int64_t k) {
