@@ -95,6 +95,34 @@ def test_speculative_accept_matches_oracle(cuda, T, top_p):
     print(f"accepted counts seen: {sorted(outcomes)}", flush=True)
 
 
+def test_speculative_accept_at_cache_end(cuda):
+    """Drafts running past max_seq_len: the reference's step_internal gives zero
+    logits there (decoder.rs:1066-1089) and acceptance proceeds
+    (decoder.rs:588-612), so no error -- the same (accepted, bonus) as the oracle
+    over the two verified rows and two zero rows."""
+    print("case speculative_accept at the cache end", flush=True)
+    V, K, max_seq = 1000, 4, 16
+    g = np.random.default_rng(77)
+    for trial in range(4):
+        ref, dec = make(small(), 4, 4, max_seq=max_seq, seed=60 + trial)
+        pre = [int(t) for t in g.integers(0, V, 14)]
+        for i, t in enumerate(pre):
+            ref.step(t, i)
+        dec.prefill_tokens(pre, 0)
+        draft = [int(t) for t in g.integers(0, V, K)]
+        dp = g.random((K, V)).astype(np.float32) ** 6
+        dp /= dp.sum(1, keepdims=True)
+        dec.set_seed(5 + trial)
+        got = dec.speculative_accept(14, draft, dp.reshape(-1), 1.0, 1.0)
+        rows = np.stack([ref.step(t, 14 + i) for i, t in enumerate(draft)])
+        assert not rows[2:].any()
+        u = [spec_uniform(5 + trial, i) for i in range(K + 1)]
+        assert got == O.speculative_accept(rows, draft, dp, u, 1.0, 1.0), trial
+        assert dec.kv_len() == max_seq
+        ref.close()
+        dec.close()
+
+
 @pytest.mark.parametrize("n,start", [(3, 40), (6, 2400)])
 def test_verify_llama_heads_long_prefix(cuda, n, start):
     """head_dim 128, 4 query heads per KV head: 12 and 24 query rows per KV

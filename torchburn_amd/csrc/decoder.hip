@@ -1189,9 +1189,15 @@ int tb_decoder_speculative_accept(tb_decoder *d, int64_t offset, const int64_t *
         return TB_OK;
     }
     TB_REQUIRE(draft_tokens && draft_probs, TB_ERR_VALUE, "draft_probs must be K×V row-major");
-    std::vector<float> rows((size_t)k * d->V);
-    int rc = tb_decoder_verify(d, offset, draft_tokens, k, rows.data());
-    if (rc) return rc;
+    // step_internal zeroes the logits of positions past the cache and changes
+    // nothing else (decoder.rs:1066-1089), so the reference's acceptance runs on
+    // zero rows there instead of failing: verify only the positions inside.
+    std::vector<float> rows((size_t)k * d->V, 0.f);
+    const int64_t inside = std::max<int64_t>(0, std::min<int64_t>(k, d->max_seq - offset));
+    if (inside > 0) {
+        int rc = tb_decoder_verify(d, offset, draft_tokens, inside, rows.data());
+        if (rc) return rc;
+    }
     std::vector<double> u((size_t)k + 1);
     for (auto &v : u) v = spec_uniform(d->seed, d->draws++);
     return spec_accept(rows.data(), draft_tokens, draft_probs, k, d->V, temperature, top_p,
