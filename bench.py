@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--copies", type=int, default=4, help="weight copies rotated (> 256 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-decode", default="llama4,qwen",
+                    help="decode configs whose CPU-oracle tok/s is sampled, or 'none'")
+    ap.add_argument("--no-config1", action="store_true", help="skip the config-1 GEMV line")
     ap.add_argument("--decode", default="llama4,llama8,qwen,qwen64",
                     help="decode runs: comma list of llama4, llama8, qwen, qwen64, or 'none'")
     ap.add_argument("--decode-steps", type=int, default=64)
@@ -61,7 +64,10 @@ def parse():
 
 
 def cpu_info():
-    model, flags = "", set()
+    """Host CPU facts for the baseline: model, SIMD flags, logical CPUs (nproc),
+    physical cores, and the CPUs this process may run on (affinity)."""
+    model, flags, cores = "", set(), set()
+    phys = core = None
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -69,10 +75,26 @@ def cpu_info():
                     model = line.split(":", 1)[1].strip()
                 if line.startswith("flags") and not flags:
                     flags = set(line.split(":", 1)[1].split())
+                if line.startswith("physical id"):
+                    phys = line.split(":", 1)[1].strip()
+                if line.startswith("core id"):
+                    core = line.split(":", 1)[1].strip()
+                if not line.strip():
+                    if core is not None:
+                        cores.add((phys, core))
+                    phys = core = None
+            if core is not None:
+                cores.add((phys, core))
     except OSError:
         pass
     keep = ("avx2", "fma", "avx512f", "avx512bw", "avx512_vnni")
-    return model, sorted(f for f in flags if f in keep)
+    try:
+        affinity = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = list(range(os.cpu_count() or 1))
+    return dict(model=model, flags=sorted(f for f in flags if f in keep),
+                nproc=os.cpu_count(), physical_cores=len(cores) or os.cpu_count(),
+                affinity=f"{len(affinity)} CPUs: {affinity[0]}-{affinity[-1]}" if affinity else "")
 
 
 PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -98,11 +120,12 @@ def pmc_traffic():
         return None
 
 
-def graph_time(torch, fn, reps, warmup, inner=1):
+def graph_time(torch, fn, reps, warmup, inner=1, spread=False):
     """Capture `inner` back-to-back calls of fn() as one graph, replay it `reps`
     times; returns ms per fn() call.  A graph replay costs a few microseconds
     of its own at its start and end, so short kernels are timed with enough of
-    them per replay that this stays a small share of each."""
+    them per replay that this stays a small share of each.  spread: also
+    returns the per-replay ms per call (one event pair around each replay)."""
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(st):
@@ -116,13 +139,20 @@ def graph_time(torch, fn, reps, warmup, inner=1):
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record()
+    for i in range(reps):
         g.replay()
-    e1.record()
+        if spread:
+            ev[i + 1].record()
+    if not spread:
+        ev[reps].record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * inner), g
+    ms = ev[0].elapsed_time(ev[reps]) / (reps * inner)
+    if spread:
+        per = [ev[i].elapsed_time(ev[i + 1]) / inner for i in range(reps)]
+        return ms, g, per
+    return ms, g
 
 
 INNER = 10   # rotations of the weight copies per captured graph (MLP and GEMV timing)
@@ -164,8 +194,10 @@ def mlp_section(torch, args, dev):
     inner = max(1, min(INNER, args.steps // len(sets)))
     per = inner * len(sets)
     reps = max(1, args.steps // per)
-    ms_graph, _ = graph_time(torch, all_steps, reps, max(1, -(-args.warmup // per)), inner)
+    ms_graph, _, per_rep = graph_time(torch, all_steps, reps, max(1, -(-args.warmup // per)),
+                                      inner, spread=True)
     ms = ms_graph / len(sets)
+    per_step = sorted(v / len(sets) for v in per_rep)
     timed_steps = reps * per
     w_bytes = 3 * (I * K // 2 + 4 * I * (K // GS))
     act_bytes = 4 * (M * K + 2 * M * I + 2 * M * K)
@@ -204,6 +236,9 @@ def mlp_section(torch, args, dev):
 
     cpu = None
     if not args.no_cpu:
+        info = cpu_info()
+        threads = info["physical_cores"]   # the reference's default pool size
+        O.set_num_threads(threads)
         n, t0 = 0, time.perf_counter()
         while True:
             O.swiglu_mlp_w4(xs, ws[0], ws[1], ws[2], ws[3], ws[4], ws[5], group_size=GS)
@@ -211,15 +246,19 @@ def mlp_section(torch, args, dev):
             el = time.perf_counter() - t0
             if el > args.cpu_seconds:
                 break
-        model, flags = cpu_info()
         cpu = {"value": round(step_bytes * n / el / 1e9, 3), "unit": "GB/s",
                "cores": O.num_threads(), "kind": "port",
                "sample": f"{n} M={M} MLP passes of the C oracle (restated reference CPU path) "
-                         f"in {el:.1f} s on {model} [{' '.join(flags)}]",
-               "ms_per_step": round(el / n * 1e3, 3)}
+                         f"in {el:.1f} s",
+               "ms_per_step": round(el / n * 1e3, 3),
+               "host": info}
     del sets
     return dict(ms=ms, step_bytes=step_bytes, gu_us=gu_us, gu_bytes=gu_bytes, dn_us=dn_us,
-                dn_bytes=dn_bytes, max_rel=max_rel, cpu=cpu, steps=timed_steps)
+                dn_bytes=dn_bytes, max_rel=max_rel, cpu=cpu, steps=timed_steps,
+                spread={"replays": len(per_step),
+                        "median_ms_per_step": round(per_step[len(per_step) // 2], 5),
+                        "min_ms_per_step": round(per_step[0], 5),
+                        "max_ms_per_step": round(per_step[-1], 5)})
 
 
 def int4_set(torch, dev, gen, n, k, gs=32):
@@ -292,6 +331,87 @@ def mlp_batch_section(torch, args, dev):
     del sets
     torch.cuda.empty_cache()
     return out
+
+
+def config1_line(torch, dev):
+    """BASELINE config 1 (report only): one INT4 g32 GEMV, Qwen2.5-0.5B up-proj
+    shape [4864, 896], M = 1, through tb_w4a32_grouped_linear (x records + GEMV),
+    over > 256 MB of rotating weight copies."""
+    from torchburn_amd import _lib
+    N, K, GS = 4864, 896, 32
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x7B + 1)
+    wbytes = N * K // 2 + 4 * N * (K // GS)
+    copies = -(-300 * 2**20 // wbytes)
+    sets = [int4_set(torch, dev, gen, N, K, GS) for _ in range(copies)]
+    x = torch.randn((1, K), device=dev, generator=gen)
+    y = torch.empty((1, N), device=dev)
+    S = lambda: torch.cuda.current_stream(dev).cuda_stream
+
+    def run():
+        for w, sc in sets:
+            _lib.call("tb_w4a32_grouped_linear", x.data_ptr(), w.data_ptr(), sc.data_ptr(), None,
+                      y.data_ptr(), 1, N, K, GS, S())
+
+    ms, _ = graph_time(torch, run, 5, 1)
+    us = ms * 1e3 / len(sets)
+    byts = wbytes + 4 * (K + N)
+    del sets
+    torch.cuda.empty_cache()
+    return {"workload": "config 1: INT4 g32 GEMV [4864, 896], M=1 (report only)", "us": round(us, 3),
+            "gbs": round(byts / us / 1e3, 1), "frac_hbm_peak": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+            "weight_copies_rotated": copies}
+
+
+def cpu_decode(name):
+    """The C oracle's decode step (the restated reference CPU decoder) for a
+    decode config, on a bounded sample: a decoder of 2 layers of the real shape
+    over the real KV length (greedy steps) and the lm_head GEMV alone; the
+    per-layer time (2-layer step minus lm_head, halved) x the layer count plus
+    the lm_head gives the full model's time per token."""
+    from oracle import oracle as O
+    from torchburn_amd import synth
+    cfg, wk, lk, kvlen, seed = {
+        "llama4": (synth.LLAMA3_8B, 4, 4, 4096, 0x7B + 5),
+        "llama8": (synth.LLAMA3_8B, 8, 8, 4096, 0x7B + 5),
+        "qwen": (synth.QWEN_0_5B, 4, 32, 2048, 0x7B + 4),
+    }[name]
+    info = cpu_info()
+    O.set_num_threads(info["physical_cores"])
+    c = dict(cfg, num_layers=2)
+    w = synth.decoder_weights(c, seed, wk, lk, 32)
+    max_seq = kvlen + 8
+    dec = O.Decoder(w, dict(c, group_size=32, max_seq=max_seq, wkind=wk, lmkind=lk))
+    for li, (k, v) in enumerate(synth.kv_prefill(c, seed, kvlen, max_seq)):
+        dec.copy_kv(li, k, v, kvlen)
+    tok = seed % cfg["vocab"]
+    dec.step(tok, kvlen)                          # warm-up: touches every page once
+    steps = []
+    for i in range(1, 6):
+        t0 = time.perf_counter()
+        dec.step(tok, kvlen + i)
+        steps.append(time.perf_counter() - t0)
+    xn = np.random.default_rng(1).standard_normal((1, cfg["hidden"])).astype(np.float32)
+    lm = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        if lk == 4:
+            O.gemm_w4(xn, w["lm_head_w"], w["lm_head_s"], None, group_size=32)
+        elif lk == 8:
+            O.gemv_w8(xn, w["lm_head_w"], w["lm_head_s"])
+        else:
+            O.gemv_f32(xn[0], w["lm_head_w"])
+        lm.append(time.perf_counter() - t0)
+    dec.close()
+    t2, t_lm = min(steps), min(lm)
+    t_layer = max(t2 - t_lm, 0.0) / 2
+    t_tok = cfg["num_layers"] * t_layer + t_lm
+    return {"tok_s": round(1.0 / t_tok, 3), "ms_per_token": round(t_tok * 1e3, 2),
+            "cores": O.num_threads(), "kind": "port",
+            "sample": f"oracle decoder of 2 {name} layers at KV {kvlen} (best of 5 steps "
+                      f"{t2 * 1e3:.1f} ms) and its lm_head alone (best of 5, {t_lm * 1e3:.1f} ms); "
+                      f"per-layer time x {cfg['num_layers']} layers + lm_head",
+            "host": info}
 
 
 def decode_run(torch, name, steps, prefill_tokens=0):
@@ -428,11 +548,16 @@ def main():
     gu_gbs = r["gu_bytes"] / (r["gu_us"] * 1e-6) / 1e9
     batched = batched_section(torch, args, dev) if args.batched != "none" else {}
     mlp_batches = mlp_batch_section(torch, args, dev) if args.mlp_batches != "none" else {}
+    cfg1 = None if args.no_config1 else config1_line(torch, dev)
     decode = {}
     if args.decode != "none":
         for name in args.decode.split(","):
             decode[name] = decode_run(torch, name.strip(), args.decode_steps,
                                       args.prefill_tokens if name.strip() == "llama4" else 0)
+    if not args.no_cpu and args.cpu_decode != "none":
+        for name in args.cpu_decode.split(","):
+            if name in decode:
+                decode[name]["cpu_baseline"] = cpu_decode(name)
     line = {
         "metric": "INT4 GEMV HBM GB/s (% of 8 TB/s); decode tokens/sec at 8B shape, 1 GPU",
         "value": round(gbs, 1),
@@ -440,6 +565,7 @@ def main():
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
         "ms_per_step": round(r["ms"], 5),
+        "ms_per_step_spread": r["spread"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int4 weights, f32 activations, f32 accumulate",
         "data": "synthetic (seeded random weights and activations)",
@@ -460,6 +586,7 @@ def main():
         "decode": decode,
         "batched_mfma": batched,
         "mlp_batches": mlp_batches,
+        "config1": cfg1,
         "cpu_baseline": r["cpu"],
         "parity_max_rel": r["max_rel"],
         "wall_s": round(time.perf_counter() - t_start, 1),

@@ -83,6 +83,7 @@ def lib():
         L.orc_decoder_copy_kv.argtypes = [_vp, _i64, _vp, _vp, _i64, _i64]
         L.orc_decoder_copy_kv.restype = C.c_int
         L.orc_num_threads.restype = C.c_int
+        L.orc_set_num_threads.argtypes = [C.c_int]
         _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
         L.orc_f16_to_f32.restype = C.c_float
@@ -116,6 +117,11 @@ def _c(a, dt):
 
 def num_threads() -> int:
     return int(lib().orc_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    """OpenMP threads of the oracle's parallel loops (the Rayon pool size)."""
+    lib().orc_set_num_threads(int(n))
 
 
 def pack_int4(q: np.ndarray) -> np.ndarray:

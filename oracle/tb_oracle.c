@@ -128,12 +128,14 @@ static float dot_u4_group_scalar(const float *x, const uint8_t *w, int64_t len) 
 /* a3: unpack_and_fma_32_avx512, gemv.rs:1190-1211.  16 bytes -> elements     */
 /* 0..15 (lane i) and 16..31 (lane i); result lane i = fma(w1, x1, w0 * x0).   */
 static inline void unpack_fma32(const float *x, const uint8_t *w, float *out16) {
+    float q[32];
+    for (int j = 0; j < 16; ++j) {   /* element 2j: low nibble, 2j+1: high nibble */
+        q[2 * j] = (float)((int)(w[j] & 0x0F) - 8);
+        q[2 * j + 1] = (float)((int)(w[j] >> 4) - 8);
+    }
     for (int i = 0; i < L16; ++i) {
-        int e0 = i, e1 = 16 + i;
-        int q0 = ((e0 & 1) ? (w[e0 / 2] >> 4) : (w[e0 / 2] & 0x0F)) - 8;
-        int q1 = ((e1 & 1) ? (w[e1 / 2] >> 4) : (w[e1 / 2] & 0x0F)) - 8;
-        float m0 = (float)q0 * x[e0];
-        out16[i] = fmaf((float)q1, x[e1], m0);
+        float m0 = q[i] * x[i];
+        out16[i] = fmaf(q[16 + i], x[16 + i], m0);
     }
 }
 
@@ -1244,6 +1246,14 @@ ORC_API int orc_decoder_copy_kv(orc_decoder *d, int64_t l, const float *k, const
         }
     if (seq_len > d->kv_used) d->kv_used = seq_len;
     return 0;
+}
+
+ORC_API void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
 }
 
 ORC_API int orc_num_threads(void) {
