@@ -131,3 +131,32 @@ def test_quantized_linear_graph_capture(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert rel(y_static.cpu().numpy(), O.gemm_w4(xv, wq, sq, bq, group_size=32)) < 1e-4, rep
+
+
+def test_capture_on_a_fresh_stream(cuda):
+    """torch.cuda.graph on its own capture stream, never used before: the op's
+    first call on that stream allocates its scratch during the capture; the
+    replays match the oracle."""
+    print("case capture on a fresh stream (scratch allocated under capture)", flush=True)
+    g = synth.rng(53)
+    K, I = 1024, 2048
+    x = synth.activations(g, 1, K)
+    gw, gsc = w4(g, I, K)
+    uw, usc = w4(g, I, K)
+    dw, dsc = w4(g, K, I)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    args = [T(a) for a in (gw, gsc)] + [None] + [T(a) for a in (uw, usc)] + [None] + \
+        [T(a) for a in (dw, dsc)] + [None]
+    dx = T(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):       # torch's capture stream, no warm-up on it
+        y = tb.fused_swiglu_mlp_w4a32(dx, *args, 32)
+    gen = np.random.default_rng(5)
+    for rep in range(3):
+        xv = gen.standard_normal((1, K)).astype(np.float32)
+        dx.copy_(torch.from_numpy(xv))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = O.swiglu_mlp_w4(xv, gw, gsc, uw, usc, dw, dsc, group_size=32)
+        assert rel(y.cpu().numpy(), ref) < 1e-4, rep

@@ -92,7 +92,14 @@ int workspace(size_t bytes, hipStream_t st, WsLease &out) {
     if (sc->size < bytes) {
         size_t sz = std::max<size_t>({bytes, 2 * sc->size, (size_t)1 << 20});
         void *p = nullptr;
-        TB_HIP(hipMalloc(&p, sz));
+        // A stream first seen under graph capture (e.g. a capture stream that
+        // was never warmed up) allocates here: hipMalloc is not a stream
+        // operation, so this thread's capture mode is relaxed around it.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        TB_HIP(hipThreadExchangeStreamCaptureMode(&mode));
+        const hipError_t e = hipMalloc(&p, sz);
+        TB_HIP(hipThreadExchangeStreamCaptureMode(&mode));
+        TB_HIP(e);
         if (sc->ptr) {
             std::lock_guard<std::mutex> lk(g_ws_mu);
             g_retired.push_back(sc->ptr);
