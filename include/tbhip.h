@@ -208,7 +208,7 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
  * intermediates (h, the x / h chunk records or the MFMA split-K partials) live
- * in a 4 MiB static device array, one per GPU, instead of the per-stream
+ * in an 8 MiB static device array, one per GPU, instead of the per-stream
  * workspace: shapes needing more return TB_ERR_UNSUPPORTED with the byte count
  * (the Llama-3-8B MLP needs about 121 KB per activation row on the GEMV path,
  * M <= 4).  Every call on one GPU shares that array, so calls that overlap on

@@ -43,9 +43,10 @@ def call(name, t, m, k, inter, gs, dev):
 
 
 def test_noalloc_matches_allocating_entry(cuda):
-    # first a Llama-3-8B MLP at M = 2 (GEMV passes), then a smaller one at M = 1
-    # (the fused record path): the scratch keeps the first call's contents.
-    for seed, m, k, inter in ((61, 2, 4096, 14336), (62, 1, 1024, 2048)):
+    # first a Llama-3-8B MLP at M = 8 (small-batch f16 MFMA), then smaller ones
+    # at M = 3 (same path) and M = 1 (the fused record path): the scratch keeps
+    # the previous call's contents.
+    for seed, m, k, inter in ((61, 8, 4096, 14336), (63, 3, 1024, 2048), (62, 1, 1024, 2048)):
         print(f"case noalloc mlp m={m} k={k} inter={inter}", flush=True)
         t, ref = mlp_case(cuda, seed, m, k, inter, 32)
         rc, got = call("tb_fused_swiglu_mlp_w4a32_noalloc", t, m, k, inter, 32, cuda)
@@ -59,8 +60,8 @@ def test_noalloc_matches_allocating_entry(cuda):
 
 
 def test_noalloc_rejects_oversized_scratch(cuda):
-    # M = 16 runs the FP32-MFMA pair, whose split-K partials exceed the 4 MiB scratch
-    m, k, inter = 16, 4096, 14336
+    # M = 32 runs the FP32-MFMA pair, whose split-K partials exceed the 8 MiB scratch
+    m, k, inter = 32, 4096, 14336
     print(f"case noalloc size limit m={m} k={k} inter={inter}", flush=True)
     dev = cuda
     x = torch.zeros((m, k), device=dev)

@@ -35,9 +35,17 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libtbhip.so)")
 
 
+# Per-source extra flags.  w4_limb: MFMA results in VGPRs (the kernel scales
+# every result with VALU; accumulators in AGPRs would cost a copy each).
+EXTRA_FLAGS = {
+    "w4_limb.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(PKG, ".."), "-c", src, "-o", obj]
+    extra = EXTRA_FLAGS.get(os.path.basename(src), [])
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", os.path.join(PKG, ".."), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")

@@ -20,6 +20,7 @@
 #include "gemv_generic.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
+#include "w4_limb.hpp"
 #include "w4_mfma.hpp"
 #include "v2_layout.hpp"
 #include "quantize.hpp"
@@ -70,6 +71,18 @@ int rows_j_env() {
 int64_t mfma_min_m() {
     static int v = env_int("TB_MFMA_MIN_M", 5);
     return v < 1 ? 1 : v;
+}
+// Batches of the small-batch f16-MFMA projection (w4_limb.hip), which reads
+// the weights once for 3..16 activation rows (at 2 rows the two-row GEMV
+// pass is faster: 41 vs 54 us for a Llama-3-8B MLP); TB_LIMB_MIN_M /
+// TB_LIMB_MAX_M override (max 1 turns it off), for tuning sweeps only.
+int64_t limb_min_m() {
+    static int v = env_int("TB_LIMB_MIN_M", 3);
+    return std::max(v, 2);
+}
+int64_t limb_max_m() {
+    static int v = env_int("TB_LIMB_MAX_M", kLimbMaxM);
+    return std::min<int64_t>(v, kLimbMaxM);
 }
 }  // namespace
 
@@ -168,6 +181,29 @@ static int mfma_ws(const MfmaParams &p, int epi, hipStream_t st) {
     return w4_mfma(p, epi, static_cast<float *>(ws), st);
 }
 
+// Shapes of the small-batch f16-MFMA projection: limb_min_m() <= m <= limb_max_m(),
+// K % 128 == 0 (a SwiGLU pair: N % 128 == 0), 16-byte aligned x and w, a power-of-two
+// group >= 32 dividing K (or per-row / scalar scales).
+static bool limb_fast(const float *x, const void *w, int64_t m, int64_t n, int64_t k,
+                      int64_t gs, bool per_row, bool pair, bool records = false) {
+    if (m < limb_min_m() || m > limb_max_m() || !limb_shape_ok(m, n, k, pair, records))
+        return false;
+    if (!per_row && (gshift_of(gs) < 0 || k % gs != 0)) return false;
+    return aligned(x, 16) && aligned(w, 16);
+}
+
+// scale_mode 0: grouped scales [n, k / gs]; 1: one per row; 2: one scalar.
+static LimbParams limb_params(const float *x, const uint8_t *rec, const uint8_t *w,
+                              const float *s, const float *b, float *y, int64_t m, int64_t n,
+                              int64_t k, int64_t gs, int scale_mode = 0) {
+    LimbParams p{};
+    p.x = x; p.rec = rec; p.w0 = w; p.s0 = s; p.b0 = b; p.y = y;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k;
+    p.scols = scale_mode == 0 ? (int)(k / gs) : (scale_mode == 1 ? 1 : 0);
+    p.gshift = scale_mode == 0 ? gshift_of(gs) : 31;
+    return p;
+}
+
 static size_t xq_bytes(int64_t m, int64_t k) {
     return (size_t)m * (size_t)(k / 32) * kXRecDwords * sizeof(uint32_t);
 }
@@ -213,15 +249,18 @@ static int generic(const float *x, const void *w0, const float *s0, int mode0, c
 static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
                      const float *bias, const float *res, float *out, int64_t m, int64_t n,
                      int64_t k, int64_t gs, hipStream_t st, int scale_mode = 0) {
-    if (!v2 && !w4_fast(x, w, m, k, gs, scale_mode != 0))
+    const bool lb = !v2 && limb_fast(x, w, m, n, k, gs, scale_mode != 0, false);
+    if (!v2 && !lb && !w4_fast(x, w, m, k, gs, scale_mode != 0))
         return generic(x, w, s, scale_mode, bias, nullptr, nullptr, 0, nullptr, res, out, m, n, k,
                        scale_mode ? k : gs, 4, st);
     const bool a8 = gs == 64 && scale_mode == 0 && g_vnni.load(std::memory_order_relaxed) != 0;
     const size_t xb = a8 ? up256((size_t)m * (size_t)k * sizeof(float)) : 0;
     const int epi = res ? EPI_RESID : EPI_PLAIN;
-    const bool mf = m >= mfma_min_m();
-    const size_t rest = mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
-                           : xq_bytes(m, k);
+    const bool mf = !lb && m >= mfma_min_m();
+    const size_t rest = lb ? up256(limb_records_bytes((int)m, (int)k)) +
+                                 limb_partials_bytes((int)m, (int)n, (int)k, false)
+                           : mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
+                                : xq_bytes(m, k);
     WsLease lease;
     int rc = workspace(xb + rest, st, lease);
     if (rc) return rc;
@@ -232,6 +271,15 @@ static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
         xin = static_cast<const float *>(ws);
     }
     void *tail = static_cast<char *>(ws) + xb;
+    if (lb) {
+        uint8_t *rec = static_cast<uint8_t *>(tail);
+        float *part =
+            reinterpret_cast<float *>(rec + up256(limb_records_bytes((int)m, (int)k)));
+        if ((rc = limb_prep(xin, rec, (int)m, (int)k, st))) return rc;
+        LimbParams q = limb_params(xin, rec, w, s, bias, out, m, n, k, gs, scale_mode);
+        q.res = res;
+        return w4_limb(q, part, st);
+    }
     if (mf) {
         MfmaParams q = mfma_params(xin, w, s, bias, out, m, n, k, gs);
         q.res = res;
@@ -338,20 +386,30 @@ static int mlp_w4_check(const MlpW4 &a, const char *op) {
     return TB_OK;
 }
 
-// 0: any-shape GEMVs; 1: FP32-MFMA pair; 2: GEMV passes
+// 0: any-shape GEMVs; 1: FP32-MFMA pair; 2: GEMV passes; 3: small-batch f16 MFMA
 static int mlp_w4_path(const MlpW4 &a) {
+    if (limb_fast(a.x, a.gate_w, a.m, a.inter, a.k, a.gs, false, true, true) &&
+        aligned(a.up_w, 16) &&
+        limb_fast(a.x, a.down_w, a.m, a.n_out, a.inter, a.gs, false, false))
+        return 3;
     if (!w4_fast(a.x, a.gate_w, a.m, a.k, a.gs, false) || !aligned(a.up_w, 16) ||
         !w4_fast(a.x, a.down_w, a.m, a.inter, a.gs, false))
         return 0;
     return a.m >= mfma_min_m() ? 1 : 2;
 }
 
-// Scratch: h [m, inter] f32, then the MFMA split-K partials (path 1) or the
-// chunk records of x and of h (path 2).
+// Scratch: h [m, inter] f32, then the MFMA split-K partials (path 1), the
+// chunk records of x and of h (path 2) or their f16-limb records (path 3).
 static size_t mlp_w4_scratch_bytes(const MlpW4 &a) {
     const size_t hb = up256((size_t)a.m * (size_t)a.inter * sizeof(float));
     switch (mlp_w4_path(a)) {
         case 0: return hb;
+        case 3: {
+            return hb + up256(limb_records_bytes((int)a.m, (int)a.k)) +
+                   up256(limb_records_bytes((int)a.m, (int)a.inter)) +
+                   std::max(limb_partials_bytes((int)a.m, (int)a.inter, (int)a.k, true),
+                            limb_partials_bytes((int)a.m, (int)a.n_out, (int)a.inter, false));
+        }
         case 1: {
             const size_t pg = w4_mfma_partials_bytes((int)a.m, (int)a.inter, (int)a.k, true);
             const size_t pd = w4_mfma_partials_bytes((int)a.m, (int)a.n_out, (int)a.inter, false);
@@ -377,6 +435,22 @@ static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
         if (rc) return rc;
         return generic(h, a.down_w, a.down_s, 0, a.down_b, nullptr, nullptr, 0, nullptr,
                        a.residual, a.out, m, n_out, inter, gs, 4, st);
+    }
+    if (path == 3) {
+        // prep(x) -> gate/up + SwiGLU, which also writes h's records -> down
+        uint8_t *xr = static_cast<uint8_t *>(ws) + hb;
+        uint8_t *hr = xr + up256(limb_records_bytes((int)m, (int)k));
+        float *part =
+            reinterpret_cast<float *>(hr + up256(limb_records_bytes((int)m, (int)inter)));
+        if ((rc = limb_prep(a.x, xr, (int)m, (int)k, st))) return rc;
+        LimbParams g = limb_params(a.x, xr, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+        g.w1 = a.up_w; g.s1 = a.up_s; g.b1 = a.up_b;
+        g.rec_out = hr;
+        if ((rc = w4_limb(g, part, st))) return rc;
+        LimbParams d = limb_params(h, hr, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter,
+                                   gs);
+        d.res = a.residual;
+        return w4_limb(d, part, st);
     }
     if (path == 1) {
         float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + hb);
@@ -415,7 +489,7 @@ static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
 // kNoAllocScratchBytes until the process ends.  `scratch` names the host-side
 // stand-in of the array; its device address (per device) comes from
 // hipGetSymbolAddress and is the only form passed to kernels.
-constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
@@ -625,6 +699,18 @@ int tb_swiglu_w4a32(const float *x, const uint8_t *gate_w, const float *gate_s,
     if (rc) return rc;
     TB_REQUIRE(h, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: swiglu_w4a32: null output");
     if (m == 0 || inter == 0) return TB_OK;
+    if (limb_fast(x, gate_w, m, inter, k, group_size, false, true) && aligned(up_w, 16)) {
+        WsLease lease;
+        const size_t rb = up256(limb_records_bytes((int)m, (int)k));
+        if ((rc = workspace(rb + limb_partials_bytes((int)m, (int)inter, (int)k, true),
+                            (hipStream_t)stream, lease)))
+            return rc;
+        uint8_t *rec = static_cast<uint8_t *>(lease.ptr);
+        if ((rc = limb_prep(x, rec, (int)m, (int)k, (hipStream_t)stream))) return rc;
+        LimbParams q = limb_params(x, rec, gate_w, gate_s, gate_b, h, m, inter, k, group_size);
+        q.w1 = up_w; q.s1 = up_s; q.b1 = up_b;
+        return w4_limb(q, reinterpret_cast<float *>(rec + rb), (hipStream_t)stream);
+    }
     if (!w4_fast(x, gate_w, m, k, group_size, false) || !aligned(up_w, 16))
         return generic(x, gate_w, gate_s, 0, gate_b, up_w, up_s, 0, up_b, nullptr, h, m, inter, k,
                        group_size, 4, (hipStream_t)stream);

@@ -1,0 +1,599 @@
+// Small-batch grouped-INT4 projection Y[M, N] = X[M, K] . deq(W)^T for up to
+// 16 activation rows on f16 MFMA (v_mfma_f32_16x16x32_f16), reading every
+// weight byte once (the C ABI routes 3..16 rows here).
+//
+// Replaces the M > 1 path of the reference's w4a32_grouped_linear
+// (src/quantization/packed_v2.rs:557-624 -> gemm_w4a32_grouped,
+// src/quantization/gemv.rs:1690-1725), which runs one GEMV per activation row,
+// and the batched MLP of fused_swiglu_mlp_batched_w4a32
+// (src/quantization/fused_ops.rs:1267-1319) at decode-size batches.
+//
+// Arithmetic.  The contraction of one 32-element group is
+//     sum_k (q_k - 8) x_k
+// with q_k the stored nibble, computed exactly on the MFMA:
+//   * weights: a nibble q placed in the low bits of an f16 is the subnormal
+//     q * 2^-24 (nibbles at bits 4-7 of a byte give 16 q * 2^-24), so a dword
+//     of 8 nibbles becomes 8 exact f16 operands with 4 ANDs and one shift;
+//   * activations: each batch of 128 elements of a row (4 groups) is scaled by
+//     a power of two 2^e (its largest magnitude lands in [2^14, 2^15)) and
+//     split into two fixed-point limbs on that grid: h1 a multiple of 16
+//     (|h1 / 16| <= 2048) and h2 a multiple of 2^-7 (|h2 2^7| <= 1024), both
+//     exact in f16, with |x 2^e - h1 - h2| <= 2^-8, i.e. 2^-23 of the batch's
+//     largest term;
+//   * the -8 of every weight is one more MFMA of the limbs against a constant
+//     B of -8 * 2^-24, shared by all weight rows, whose result is the C
+//     operand of the weight MFMA.  Each limb has its own accumulation, so every
+//     product and partial sum is an integer multiple of the limb's quantum below
+//     2^21 quanta: the MFMA result is exact whatever the order and rounding of
+//     its internal additions (they are not IEEE round-to-nearest, which a
+//     float split of x would expose);
+//   * per 32-element group the limb results are scaled by the weight row's
+//     group scale and accumulated in f32; per batch the sum is scaled by
+//     2^(24 - e) into the running total.
+// The error of a batch's contribution is the limb quantization, ~2^-23 of its
+// largest term, the order of the f32 reference's own rounding.  A batch
+// holding NaN / Inf, or a largest magnitude outside [2^-100, 2^100], is
+// flagged and runs an f32 MFMA path on the raw activations, so non-finite
+// values propagate as in the reference's unpack-and-fma.
+//
+// Activation records (limb_prep, or the SwiGLU reduce for the next
+// projection), one per 128-element batch: for each of its 4 groups T f16 A
+// tiles of 64 lanes x 16 bytes, then 16 bytes, one per A-row, holding the
+// biased f32 exponent of 2^(24 - e).  After the records, one flag byte per
+// batch (1: take the f32 path).
+//   * M <= 8 (T = 1): A-row i of the MFMA is limb (i >> 3) of row i & 7, so one
+//     MFMA covers both limbs in separate output rows; the two limb halves of the
+//     output are added at the end (lanes l and l + 32).
+//   * 9 <= M <= 16 (T = 2): A-row i is row i; tile t is limb t (two MFMAs).
+//   * Lane l (i = l % 16, k-slot q = l / 16) holds elements 8q + {0,4,1,5,2,6,
+//     3,7} of the group (odd ones pre-divided by 16), the order in which
+//     expand_nibbles unpacks a dword of nibbles.
+//
+// Work split.  The grid is (row chunks) x (K splits).  A block copies the
+// records of its K range to LDS once, then each of its waves streams the
+// weights of R 16-row blocks over that range: per batch a lane loads one
+// 16-byte chunk per row block, lane (i, q) group g0 + q of row i, and a 4x4
+// transpose across the lane quarters (v_permlane32_swap, v_permlane16_swap)
+// leaves dword q of group g0 + t in register t, the MFMA B operand layout.
+// Weights and scales stream DEPTH - 1 batches ahead through a register ring;
+// since the records come from LDS, each wait is for the oldest weights only
+// (vector loads retire in order).  The per-split partial sums go to a scratch
+// buffer and a small reduce kernel sums them in split order (deterministic)
+// and runs the epilogue: bias (+ residual), or for a SwiGLU pair, whose gate
+// and up rows are stacked as one 2n-row matrix, h = silu(g) * u plus the
+// records of h for the next projection.
+#include <math.h>
+
+#include <algorithm>
+
+#include "gemv_common.hpp"
+#include "tb_common.hpp"
+#include "w4_limb.hpp"
+
+namespace tb {
+
+using namespace gemv;
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 1024;          // one A tile: 64 lanes x 8 f16
+constexpr int kBatch = 128;          // K per batch: one 16-byte chunk per lane
+constexpr int kTargetWaves = 2048;   // 8 per CU
+constexpr int kDepthMax = 4;         // weight batches held in registers
+constexpr int kRecTail = 16;         // 16 signed exponent bytes
+constexpr int kLdsBudget = 64 << 10; // records per block (two blocks per CU)
+
+__host__ __device__ constexpr int tiles_of(int m) { return m <= 8 ? 1 : 2; }
+// bytes of one batch record (4 groups)
+__host__ __device__ constexpr int rec_stride(int tiles) { return 4 * tiles * kTile + kRecTail; }
+
+// 8 nibbles of a dword -> the f16 B operand (subnormals q * 2^-24; the odd
+// nibbles come out 16x larger, which their pre-divided activations undo).
+// Slot order: n0, n4, 16 n1, 16 n5, n2, n6, 16 n3, 16 n7.
+__device__ __forceinline__ h8 expand_nibbles(uint32_t d) {
+    const uint32_t u = d >> 8;
+    const u32x4 v = {d & 0x000F000Fu, d & 0x00F000F0u, u & 0x000F000Fu, u & 0x00F000F0u};
+    return __builtin_bit_cast(h8, v);
+}
+
+// The B operand of the offset MFMA: -8 * 2^-24 in the slots of even elements,
+// -128 * 2^-24 in those of the pre-divided odd ones (f16 subnormals).
+__device__ __forceinline__ h8 offset_operand() {
+    const u32x4 v = {0x80088008u, 0x80808080u, 0x80088008u, 0x80808080u};
+    return __builtin_bit_cast(h8, v);
+}
+
+// Lane (i, q) holds dwords 0..3 of group g0 + q of its row; afterwards
+// register t holds dword q of group g0 + t.  Transpose of 4 x 4 dwords across
+// the lane quarters: v_permlane32_swap exchanges the upper half's first
+// operand with the lower half's second, v_permlane16_swap the same between
+// the 16-lane rows of each half.
+__device__ __forceinline__ void transpose4(u32x4 &v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    v.x = c[0]; v.y = c[1]; v.z = d[0]; v.w = d[1];
+}
+
+// The record of one 128-element batch, built by one wave.  Lane (i, q) holds
+// v[g][e] = element 32 g + 8 q + e of the batch for its row (row i & 7 when
+// T = 1, row i when T = 2; zeros beyond m).  flag: the batch's flag byte.
+template <int T>
+__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg, uint8_t *flag) {
+    const int i = lane & 15, q = lane >> 4;
+    float mx = 0.f;
+    bool fin = true;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            fin = fin && __builtin_isfinite(v[g][e]);
+            mx = fmaxf(mx, fabsf(v[g][e]));
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    int E = 0;
+    (void)frexpf(mx, &E);   // mx = f 2^E, f in [0.5, 1)
+    const bool out_of_range = mx > 0.f && (E > 100 || E < -100);
+    const bool bad = __any((!fin || out_of_range) ? 1 : 0) != 0;
+    const int e = (mx > 0.f && !out_of_range) ? 15 - E : 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        h8 l1, l2;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int el = (j >> 1) | ((j & 1) << 2);
+            const bool odd = ((j >> 1) & 1) != 0;
+            const float xs = (fin && !out_of_range) ? ldexpf(v[g][el], e) : 0.f;
+            const float j1 = rintf(xs * 0.0625f);               // h1 = 16 j1
+            const float j2 = rintf((xs - 16.0f * j1) * 128.0f);  // h2 = 2^-7 j2
+            l1[j] = (_Float16)(odd ? j1 : 16.0f * j1);
+            l2[j] = (_Float16)ldexpf(j2, odd ? -11 : -7);
+        }
+        uint8_t *tg = rg + (size_t)g * T * kTile;
+        if (T == 1) {
+            *reinterpret_cast<h8 *>(tg + lane * 16) = i < 8 ? l1 : l2;
+        } else {
+            *reinterpret_cast<h8 *>(tg + lane * 16) = l1;
+            *reinterpret_cast<h8 *>(tg + kTile + lane * 16) = l2;
+        }
+    }
+    // biased f32 exponent of 2^(24 - e): e in [-85, 115] -> [36, 236]
+    if (q == 0) rg[4 * T * kTile + i] = (uint8_t)(151 - e);
+    if (lane == 0) *flag = bad ? 1 : 0;
+}
+
+template <int T>
+__device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict__ rec, int m,
+                               int k, int batches) {
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= batches) return;   // whole waves
+    const int i = lane & 15, q = lane >> 4;
+    const int row = T == 1 ? (i & 7) : i;
+    float v[4][8];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (row < m) {
+            const float *xp = x + (size_t)row * k + 128 * b + 32 * g + 8 * q;
+            const float4 a = *reinterpret_cast<const float4 *>(xp);
+            const float4 c = *reinterpret_cast<const float4 *>(xp + 4);
+            v[g][0] = a.x; v[g][1] = a.y; v[g][2] = a.z; v[g][3] = a.w;
+            v[g][4] = c.x; v[g][5] = c.y; v[g][6] = c.z; v[g][7] = c.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[g][e] = 0.f;
+        }
+    }
+    build_batch<T>(v, lane, rec + (size_t)b * rec_stride(T),
+                   rec + (size_t)batches * rec_stride(T) + b);
+}
+
+// Partial sums of one block: rows [row0, row0 + 16 R NW) of the stacked
+// weights (rows past n come from w1 / s1 for a SwiGLU pair) over the K range
+// [ks, ks + ksl) of split blockIdx.y.  The records of that range are copied to
+// LDS first (one pass, one barrier); the loop then waits only for weights.
+template <int T, int R, int NW, int DEPTH>
+__global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__restrict__ part,
+                                                   int ksl, int ntot) {
+    constexpr int BS = rec_stride(T);
+    constexpr int ROWS = 16 * R * NW;
+    extern __shared__ __align__(16) uint8_t lrec[];   // the (ksl / 128) batch records
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, q = lane >> 4;
+    const int split = blockIdx.y;
+    const int ks = split * ksl;
+    const int ke = min(p.k, ks + ksl);
+    const int b0 = ks / kBatch, nb = (ke - ks) / kBatch;
+    const uint8_t *flags = p.rec + (size_t)(p.k / kBatch) * BS;
+
+    // the weight and scale rows of block row rl (rows past the stacked
+    // [w0; w1] read row 0 and are never stored)
+    auto row_ptrs = [&](int rl, const uint8_t *&w, const float *&sc) {
+        const int row = blockIdx.x * ROWS + rl;
+        const bool second = row >= p.n && row < ntot;
+        const int rr = row < ntot ? (second ? row - p.n : row) : 0;
+        w = (second ? p.w1 : p.w0) + (size_t)rr * (size_t)(p.k >> 1);
+        sc = (second ? p.s1 : p.s0) + (size_t)rr * (size_t)p.scols;
+    };
+    {   // records of this K range -> LDS: every load in flight at once, then
+        // the stores (a load-store loop would pay one memory latency per pass)
+        constexpr int kChunks = (kLdsBudget / 16 + NW * 64 - 1) / (NW * 64);
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(p.rec + (size_t)b0 * BS);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(lrec);
+        const int n16 = nb * BS / 16;
+        u32x4 tmp[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+            if (tid + c * NW * 64 < n16) tmp[c] = src[tid + c * NW * 64];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+            if (tid + c * NW * 64 < n16) dst[tid + c * NW * 64] = tmp[c];
+    }
+    // NaN / Inf flags of the range, once, one byte per lane (nb <= 64): the
+    // common all-finite case needs no per-batch test.  (A loop of byte loads
+    // here would pay one memory latency per batch.)
+    const bool any_bad = __any(lane < nb && flags[b0 + (lane < nb ? lane : 0)] != 0) != 0;
+
+    const uint8_t *wr[R];
+    const float *sr[R];
+    int rows[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        const int rl = wave * 16 * R + 16 * rb + i;
+        rows[rb] = blockIdx.x * ROWS + rl;
+        row_ptrs(rl, wr[rb], sr[rb]);
+    }
+    f32x4 acc[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Weights of one batch: lane (i, q) takes group g + q of its row and that
+    // group's scale (one dword per lane: the four lanes of a row would
+    // otherwise each fetch the same four scales).
+    auto load_w = [&](int k0, u32x4 (&wv)[R], float (&sv)[R]) {
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            // cached, not non-temporal: each load takes half of a row's
+            // 128-byte line and the next batch takes the other half
+            wv[rb] = *reinterpret_cast<const u32x4 *>(wr[rb] + (k0 >> 1) + 16 * q);
+            sv[rb] = sr[rb][(k0 + 32 * q) >> p.gshift];
+        }
+    };
+
+    // The f32 path of a flagged batch: (q - 8) x in IEEE arithmetic on the raw
+    // activations (v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16]
+    // and B[l / 16][l % 16]).
+    auto compute_f32 = [&](int k0, const u32x4 (&wv)[R], const f32x4 (&st)[R]) {
+        const int xr = T == 1 ? (i < 8 ? i : kLimbMaxM) : i;
+        const float *xrow = p.x + (size_t)(xr < p.m ? xr : 0) * p.k;
+        const bool live = xr < p.m;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float *xp = xrow + k0 + 32 * t + 8 * q;
+            const float4 a = *reinterpret_cast<const float4 *>(xp);
+            const float4 b = *reinterpret_cast<const float4 *>(xp + 4);
+            const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    D = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        live ? xv[e] : 0.f, (float)((wv[rb][t] >> (4 * e)) & 15u) - 8.0f, D, 0,
+                        0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(D[r], st[rb][t], acc[rb][r]);
+            }
+        }
+    };
+    const h8 boff = offset_operand();
+    // The four steps of a batch are independent until the accumulation: all
+    // LDS reads first, then the four offset MFMAs, then per row block the four
+    // weight MFMAs; the batch's partial sum takes the batch exponent once.
+    auto compute = [&](int k0, const u32x4 (&wv)[R], const f32x4 (&st)[R]) {
+        const uint8_t *rg = lrec + (size_t)((k0 - ks) / kBatch) * BS;
+        h8 A[4][T];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < T; ++u)
+                A[t][u] = *reinterpret_cast<const h8 *>(rg + (t * T + u) * kTile + lane * 16);
+        const uint32_t pw = *reinterpret_cast<const uint32_t *>(rg + 4 * T * kTile + 4 * q);
+        f32x4 off[4][T];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < T; ++u)
+                off[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    A[t][u], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        float pf[4];   // 2^(24 - e) of the lane's four A-rows
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            pf[r] = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(pw, 8 * r, 8) << 23);
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            f32x4 D[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const h8 B = expand_nibbles(wv[rb][t]);
+                D[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][0], B, off[t][0], 0, 0, 0);
+                if (T == 2)
+                    D[t] += __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][T - 1], B, off[t][T - 1],
+                                                                   0, 0, 0);
+            }
+            f32x4 bs = D[0] * st[rb][0];
+#pragma unroll
+            for (int t = 1; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[t][r], st[rb][t], bs[r]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(bs[r], pf[r], acc[rb][r]);
+        }
+    };
+    // One batch: transpose its weights, gather the row's four scales from the
+    // lanes that loaded them (ds_bpermute), then the f16 MFMA or, for a
+    // flagged batch, the f32 path.
+    auto step = [&](int k0, u32x4 (&wv)[R], const float (&sv)[R]) {
+        f32x4 st[R];
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            transpose4(wv[rb]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) st[rb][t] = __shfl(sv[rb], i + 16 * t);
+        }
+        if (any_bad && flags[k0 / kBatch])
+            compute_f32(k0, wv, st);
+        else
+            compute(k0, wv, st);
+    };
+
+    // Weights and scales DEPTH - 1 batches ahead in a register ring; the
+    // records come from LDS, so each wait is for the oldest weights only.
+    u32x4 wq[DEPTH][R];
+    float sq[DEPTH][R];
+#pragma unroll
+    for (int j = 0; j < DEPTH - 1; ++j)
+        if (ks + j * kBatch < ke) load_w(ks + j * kBatch, wq[j], sq[j]);
+    __syncthreads();   // the records are in LDS
+    for (int k0 = ks; k0 < ke; k0 += DEPTH * kBatch) {
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) {
+            const int kc = k0 + j * kBatch;
+            if (kc >= ke) break;
+            const int kn = kc + (DEPTH - 1) * kBatch;
+            if (kn < ke) load_w(kn, wq[(j + DEPTH - 1) % DEPTH], sq[(j + DEPTH - 1) % DEPTH]);
+            step(kc, wq[j], sq[j]);
+        }
+    }
+
+    // Lane l's register r holds A-row 4 (l / 16) + r of weight row l % 16; for
+    // T = 1 rows 8..15 are the second limbs of rows 0..7 (lanes l + 32).
+    float *pp = part + (size_t)split * (size_t)p.m * (size_t)ntot;
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        f32x4 v = acc[rb];
+        if (T == 1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] += __shfl_down(v[r], 32);
+        }
+        if (rows[rb] < ntot && (T == 2 || q < 2)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 4 * q + r;
+                if (tok < p.m) pp[(size_t)tok * ntot + rows[rb]] = v[r];
+            }
+        }
+    }
+}
+
+// y = sum of the split partials (split order) + bias (+ residual).
+__global__ __launch_bounds__(256) void k_limb_reduce(const float *__restrict__ part, int splits,
+                                                     int m, int n, const float *__restrict__ b0,
+                                                     const float *__restrict__ res,
+                                                     float *__restrict__ y) {
+    const size_t total = (size_t)m * n;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const int row = (int)(e % (size_t)n);
+        float g = 0.f;
+        for (int s = 0; s < splits; ++s) g += part[(size_t)s * total + e];
+        if (b0) g += b0[row];
+        if (res) g += res[e];
+        y[e] = g;
+    }
+}
+
+// SwiGLU pair: h = silu(gate + b0) * (up + b1) from the split partials of the
+// stacked [gate; up] rows.  One block per 128-row batch of h: each thread sums
+// 4 T contiguous values of one token over the splits (four splits' loads in
+// flight at a time) and writes them to y and LDS; wave 0 then writes the
+// batch's record for the next projection (rec_out, K = n).
+template <int T>
+__global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restrict__ part,
+                                                          int splits, int m, int n,
+                                                          const float *__restrict__ b0,
+                                                          const float *__restrict__ b1,
+                                                          float *__restrict__ y,
+                                                          uint8_t *__restrict__ rec_out) {
+    constexpr int TOKS = 8 * T;           // tokens of the batch
+    constexpr int PER = 32 / T;           // threads per token
+    __shared__ __align__(16) float hs[TOKS][kBatch];
+    const int tid = threadIdx.x, bt = blockIdx.x;
+    const int tok = tid / PER, c0 = (tid % PER) * 4 * T;   // 4 T values at rows c0..
+    const int row0 = kBatch * bt + c0;
+    const size_t ntot = 2 * (size_t)n;
+    const size_t plane = (size_t)m * ntot;
+    const bool live = tok < m;
+    f32x4 gs[T] = {}, us[T] = {};
+    if (live) {
+        const float *pg = part + (size_t)tok * ntot + row0;
+        int s = 0;
+        for (; s + 4 <= splits; s += 4) {
+            f32x4 lg[4][T], lu[4][T];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int h = 0; h < T; ++h) {
+                    lg[j][h] = *reinterpret_cast<const f32x4 *>(pg + (s + j) * plane + 4 * h);
+                    lu[j][h] = *reinterpret_cast<const f32x4 *>(pg + (s + j) * plane + n + 4 * h);
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int h = 0; h < T; ++h) {
+                    gs[h] += lg[j][h];
+                    us[h] += lu[j][h];
+                }
+        }
+        for (; s < splits; ++s)
+#pragma unroll
+            for (int h = 0; h < T; ++h) {
+                gs[h] += *reinterpret_cast<const f32x4 *>(pg + s * plane + 4 * h);
+                us[h] += *reinterpret_cast<const f32x4 *>(pg + s * plane + n + 4 * h);
+            }
+        // biases before any store: on this GPU loads and stores retire through
+        // one in-order counter, so a load issued after a store waits for it
+        f32x4 bg[T] = {}, bu[T] = {};
+#pragma unroll
+        for (int h = 0; h < T; ++h) {
+            if (b0) bg[h] = *reinterpret_cast<const f32x4 *>(b0 + row0 + 4 * h);
+            if (b1) bu[h] = *reinterpret_cast<const f32x4 *>(b1 + row0 + 4 * h);
+        }
+#pragma unroll
+        for (int h = 0; h < T; ++h) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = silu(gs[h][e] + bg[h][e]) * (us[h][e] + bu[h][e]);
+            *reinterpret_cast<f32x4 *>(y + (size_t)tok * n + row0 + 4 * h) = v;
+            *reinterpret_cast<f32x4 *>(&hs[tok][c0 + 4 * h]) = v;
+        }
+    }
+    if (!rec_out) return;
+    __syncthreads();
+    if (tid >= 64) return;
+    const int lane = tid, i = lane & 15, q = lane >> 4;
+    const int tr = T == 1 ? (i & 7) : i;
+    float v[4][8];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[g][e] = tr < m ? hs[tr][32 * g + 8 * q + e] : 0.f;
+    build_batch<T>(v, lane, rec_out + (size_t)bt * rec_stride(T),
+                   rec_out + (size_t)(n / kBatch) * rec_stride(T) + bt);
+}
+
+constexpr int kTargetBlocks = 512;
+
+struct Plan {
+    int ksl, splits, r, chunks;
+    size_t lds;
+};
+
+// Four waves per block, each over R 16-row blocks (R = 2 when the grid would
+// otherwise exceed about kTargetBlocks blocks); the K split is as long as the
+// block's records fit kLdsBudget.
+Plan plan(int m, int n, int k, bool pair) {
+    Plan pl;
+    const int bs = rec_stride(tiles_of(m));
+    const int batches = k / kBatch;
+    const long ntot = pair ? 2L * n : n;
+    int per = kLdsBudget / bs;
+    if (per < 1) per = 1;
+    if (per > batches) per = batches;
+    pl.splits = (batches + per - 1) / per;
+    per = (batches + pl.splits - 1) / pl.splits;   // even out the splits
+    pl.splits = (batches + per - 1) / per;
+    pl.ksl = per * kBatch;
+    pl.lds = (size_t)per * bs;
+    const long want_rows = (ntot * pl.splits + kTargetBlocks - 1) / kTargetBlocks;
+    pl.r = want_rows > 96 ? 2 : 1;
+    const int rows = 16 * pl.r * 4;
+    pl.chunks = (int)((ntot + rows - 1) / rows);
+    return pl;
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void k_limb_prep(const float *__restrict__ x,
+                                                   uint8_t *__restrict__ rec, int m, int k,
+                                                   int batches) {
+    limb_prep_body<T>(x, rec, m, k, batches);
+}
+
+}  // namespace
+
+size_t limb_records_bytes(int m, int k) {
+    const size_t b = (size_t)(k / kBatch);
+    return b * (size_t)rec_stride(tiles_of(m)) + ((b + 15) & ~(size_t)15);
+}
+
+size_t limb_partials_bytes(int m, int n, int k, bool pair) {
+    const Plan pl = plan(m, n, k, pair);
+    return (size_t)pl.splits * (size_t)m * (size_t)(pair ? 2 * n : n) * sizeof(float);
+}
+
+bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair, bool records) {
+    if (m < 1 || m > kLimbMaxM || n < 1 || k < kBatch || k % kBatch != 0) return false;
+    if (k > (int64_t)1 << 24 || n > (int64_t)1 << 23) return false;
+    (void)records;
+    return !pair || n % kBatch == 0;   // whole 128-row batches of h per pair block
+}
+
+int limb_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st) {
+    TB_REQUIRE(m >= 1 && m <= kLimbMaxM && k % kBatch == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: activation records need 1 <= M <= 16 and K % 128 == 0");
+    const int batches = k / kBatch;
+    const dim3 grid((unsigned)((batches + 3) / 4));
+    if (tiles_of(m) == 1)
+        hipLaunchKernelGGL(k_limb_prep<1>, grid, dim3(256), 0, st, x, rec, m, k, batches);
+    else
+        hipLaunchKernelGGL(k_limb_prep<2>, grid, dim3(256), 0, st, x, rec, m, k, batches);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int w4_limb(const LimbParams &p, float *part, hipStream_t st) {
+    const bool pair = p.w1 != nullptr;
+    TB_REQUIRE(limb_shape_ok(p.m, p.n, p.k, pair, pair && p.rec_out), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: small-batch MFMA projection needs 1 <= M <= 16, K % 128 == 0 "
+               "(and N % 128 == 0 for a SwiGLU pair)");
+    const bool t1 = tiles_of(p.m) == 1;
+    const int ntot = pair ? 2 * p.n : p.n;
+    const Plan pl = plan(p.m, p.n, p.k, pair);
+    const dim3 grid((unsigned)pl.chunks, (unsigned)pl.splits), block(256);
+#define TB_LIMB_LAUNCH(T_, R_, D_)                                                            \
+    hipLaunchKernelGGL((k_w4_limb<T_, R_, 4, D_>), grid, block, pl.lds, st, p, part, pl.ksl, \
+                       ntot)
+    if (pl.r == 2) {
+        if (t1) TB_LIMB_LAUNCH(1, 2, 4);
+        else TB_LIMB_LAUNCH(2, 2, 4);
+    } else {
+        if (t1) TB_LIMB_LAUNCH(1, 1, 6);
+        else TB_LIMB_LAUNCH(2, 1, 6);
+    }
+#undef TB_LIMB_LAUNCH
+    TB_LAUNCHED();
+    if (pair) {
+        const dim3 rg((unsigned)(p.n / kBatch));
+        if (t1)
+            hipLaunchKernelGGL(k_limb_reduce_pair<1>, rg, dim3(256), 0, st, part, pl.splits, p.m,
+                               p.n, p.b0, p.b1, p.y, p.rec_out);
+        else
+            hipLaunchKernelGGL(k_limb_reduce_pair<2>, rg, dim3(256), 0, st, part, pl.splits, p.m,
+                               p.n, p.b0, p.b1, p.y, p.rec_out);
+    } else {
+        const size_t total = (size_t)p.m * (size_t)p.n;
+        const unsigned nb = (unsigned)std::min<size_t>((total + 255) / 256, 2048);
+        hipLaunchKernelGGL(k_limb_reduce, dim3(nb), dim3(256), 0, st, part, pl.splits, p.m, p.n,
+                           p.b0, p.res, p.y);
+    }
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+}  // namespace tb
