@@ -171,3 +171,46 @@ def test_extreme_activation_ranges(cuda):
     ref = O.gemm_w4(x, w, s, None, group_size=32)
     y = tb.w4a32_grouped_linear(T(x), T(w), T(s), None, 32).cpu().numpy()
     assert rel(y, ref) < TOL
+
+
+@pytest.mark.parametrize("n,k,gs", [(4864, 896, 32), (4096, 14336, 32), (300, 2048, 64),
+                                    (896, 4864, 32), (7, 64, 32)])
+def test_in_kernel_records_match_prebuilt(cuda, n, k, gs):
+    """One activation row of a single projection without x records: the GEMV
+    builds each chunk's record from x itself.  Bit-identical to the same kernel
+    fed the records of tb_xquant, including zero, tiny, huge and non-finite
+    chunks."""
+    from torchburn_amd import _lib
+    print(f"case in-kernel records n={n} k={k} gs={gs}", flush=True)
+    g = synth.rng(16, n, k, gs)
+    x = synth.activations(g, 1, k)
+    x[0, :32] = 0.0
+    x[0, 32:48] *= 1e-33
+    x[0, 48:64] *= 3e28
+    x[0, k - 24:] = np.round(x[0, k - 24:] * 8) / 8   # exact small-step values
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    P = lambda t: t.data_ptr()
+    S = torch.cuda.current_stream(cuda).cuda_stream
+    w, s = synth.int4_weight(g, n, k, gs)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    r = synth.activations(g, 1, n)
+    xt, wt, st, bt, rt = T(x), T(w), T(s), T(b), T(r)
+    xq = torch.empty(_lib.lib().tb_x_records_bytes(1, k) // 4, dtype=torch.int32, device=cuda)
+    want = torch.empty((1, n), device=cuda)
+
+    def both():
+        _lib.check(_lib.lib().tb_xquant(P(xt), P(xq), 1, k, S))
+        _lib.check(_lib.lib().tb_w4a32_gemv_xq(P(xt), P(xq), P(wt), P(st), P(bt), P(rt),
+                                               P(want), 1, n, k, gs, S))
+        got = tb.w4a32_grouped_linear_residual(xt, wt, st, rt, bt, group_size=gs)
+        torch.cuda.synchronize()
+        return got.cpu().numpy(), want.cpu().numpy()
+
+    gv, wv = both()
+    np.testing.assert_array_equal(gv.view(np.uint32), wv.view(np.uint32))
+    assert rel(gv, O.gemm_w4(x, w, s, b, group_size=gs) + r) < TOL
+    # a NaN chunk reaches every output row on both paths
+    x[0, k - 40] = np.nan
+    xt.copy_(T(x))
+    gv, wv = both()
+    assert np.isnan(wv).all() and np.isnan(gv).all()

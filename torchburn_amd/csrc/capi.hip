@@ -209,9 +209,18 @@ static size_t xq_bytes(int64_t m, int64_t k) {
 }
 
 // M rows in passes of at most kMaxW4RowsPerPass (the GEMV keeps x in VGPRs).
-// xq: chunk records of all m rows of p.x (built here when build_xq is set).
+// xq: chunk records of all m rows of p.x (built here when build_xq is set).  A
+// single row of a single projection builds them inside the GEMV instead, one
+// chunk per lane while its weights load (Qwen2.5-0.5B up-projection
+// [4864, 896]: 7.0 -> 6.0 us); a gate/up pair keeps the record pass, since
+// the build lengthens each of its two rounds of blocks (Llama-3-8B: +4 us
+// against the pass's 2-4 us).
 static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
                    hipStream_t st) {
+    if (build_xq && m == 1 && p.w1 == nullptr && epi != EPI_ROPE && p.ssq_in == nullptr) {
+        p.xq = nullptr;
+        return w4_gemv(p, epi, st);
+    }
     if (build_xq) {
         int rc = xquant(p.x, xq, (int)m, p.k, st);
         if (rc) return rc;

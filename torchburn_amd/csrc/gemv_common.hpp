@@ -446,19 +446,22 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
 
 // Builds one half (16 elements) of an x chunk record in a quad of 4
 // consecutive lanes; lane q (0..3) holds elements 4q .. 4q + 3 of the half in v.
-// x_i ~= sx * X_i with sx = 2^(e - 23), amax < 2^e, |X_i| < 2^23: the
+// x_i ~= sx * X_i with sx = 2^(e - 22), amax < 2^e, |X_i| <= 2^22: the
 // power-of-two step makes the scaling exact and rounds off only bits below
-// 2^(e - 23), the precision an f32 partial sum of these elements has.  Limb l
-// of U_i = X_i + 2^23 (bits [4l, 4l + 4)) goes to nibble (i & 7) of dword
-// limb[l][i >> 3] (i = element index in the 32-element chunk), the nibble
-// order of the packed weights.  A record (kXRecDwords) is 7 quads of 4
-// dwords: quad l < 6 holds limb l (dwords 0-1 half 0, 2-3 half 1), quad 6
-// {step of half 0, step of half 1, sum X of half 0, sum X of half 1}; a step is
-// NaN when its half holds NaN/Inf.  The records of a row of nc chunks are
-// stored by quad: quad i of chunk c at row + (i * nc + c) * 4, so a GEMV wave,
-// one chunk per lane, reads each quad of 64 consecutive chunks as one
-// contiguous KiB.  All 4 lanes must call this; the record of `chunk` is
-// written when `live`.
+// 2^(e - 23), about the precision an f32 partial sum of these elements has.
+// X_i is written as six signed base-16 digits d_l in [-8, 7] (X_i = sum_l
+// 16^l d_l; six digits reach +-8947848 > 2^22): digit l of X is nibble l of
+// X + 0x888888 minus 8, and its 4-bit two's complement that nibble XOR 8, so
+// the digit planes are the nibble planes of U_i = (X_i + 0x888888) ^ 0x888888.
+// Digit l of element i goes to nibble (i & 7) of dword limb[l][i >> 3] (i =
+// element index in the 32-element chunk), the nibble order of the packed
+// weights.  A record (kXRecDwords) is 7 quads of 4 dwords: quad l < 6 holds
+// digit plane l (dwords 0-1 half 0, 2-3 half 1), quad 6 {step of half 0, step
+// of half 1, 0, 0}; a step is NaN when its half holds NaN/Inf.  The records of
+// a row of nc chunks are stored by quad: quad i of chunk c at
+// row + (i * nc + c) * 4, so a GEMV wave, one chunk per lane, reads each quad
+// of 64 consecutive chunks as one contiguous KiB.  All 4 lanes must call this;
+// the record of `chunk` is written when `live`.
 __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint32_t *row, int nc,
                                                 int chunk, int half) {
     const float xv[4] = {v.x, v.y, v.z, v.w};
@@ -476,21 +479,17 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
     int e = 0;
     (void)frexpf(amax, &e);
     e = e < -100 ? -100 : e;
-    const float inv = ldexpf(1.0f, 23 - e);
+    const float inv = ldexpf(1.0f, 22 - e);
     uint32_t lw[6] = {0u, 0u, 0u, 0u, 0u, 0u};
-    int ssum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         int X = fin ? (int)rintf(xv[i] * inv) : 0;
-        X = X > 8388607 ? 8388607 : (X < -8388607 ? -8388607 : X);
-        ssum += X;
-        const uint32_t U = (uint32_t)(X + 8388608);
+        X = X > 4194304 ? 4194304 : (X < -4194304 ? -4194304 : X);
+        const uint32_t U = (uint32_t)(X + 0x888888) ^ 0x888888u;
         const int nib = (q & 1) * 4 + i;   // nibble of element 4q + i in its dword
 #pragma unroll
         for (int l = 0; l < 6; ++l) lw[l] |= ((U >> (4 * l)) & 15u) << (4 * nib);
     }
-    ssum += quad_xor1(ssum);
-    ssum += quad_xor2(ssum);
 #pragma unroll
     for (int l = 0; l < 6; ++l) lw[l] |= (uint32_t)quad_xor1((int)lw[l]);
     if (!live) return;
@@ -501,8 +500,8 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
         for (int l = 0; l < 6; ++l) rec[l * quad + half * 2 + (q >> 1)] = lw[l];
     }
     if (q == 0) {
-        rec[6 * quad + half] = __float_as_uint(fin ? ldexpf(1.0f, e - 23) : __builtin_nanf(""));
-        rec[6 * quad + 2 + half] = (uint32_t)ssum;
+        rec[6 * quad + half] = __float_as_uint(fin ? ldexpf(1.0f, e - 22) : __builtin_nanf(""));
+        rec[6 * quad + 2 + half] = 0u;
     }
 }
 
@@ -511,6 +510,67 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
 __device__ __forceinline__ void build_xrec8(float4 v, int sub, bool live, uint32_t *row, int nc,
                                             int chunk) {
     build_half_rec4(v, sub & 3, live, row, nc, chunk, sub >> 2);
+}
+
+// The six digit-plane dwords of 8 consecutive elements (U[e] of
+// build_half_rec4, 24 bits): out[l] nibble e = bits [4l, 4l + 4) of U[e].
+// Pairs of elements first merge into bytes (pe: even planes, po: odd planes;
+// byte b of pair p holds plane 2b or 2b + 1 of elements 2p, 2p + 1), then
+// v_perm_b32 gathers byte b of the four pairs into one dword: 42 VALU
+// operations instead of 96 nibble inserts.
+__device__ __forceinline__ void pack_limbs8(const uint32_t *U, uint32_t (&out)[6]) {
+    uint32_t pe[4], po[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        pe[p] = (U[2 * p] & 0x0F0F0Fu) | ((U[2 * p + 1] << 4) & 0xF0F0F0u);
+        po[p] = ((U[2 * p] >> 4) & 0x0F0F0Fu) | (U[2 * p + 1] & 0xF0F0F0u);
+    }
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+        // selector bytes: b picks byte b of the second operand, 4 + b of the
+        // first, 0x0c a zero byte
+        const uint32_t slo = 0x0c0c0000u | ((4u + b) << 8) | (uint32_t)b;
+        const uint32_t shi = ((4u + b) << 24) | ((uint32_t)b << 16) | 0x0c0cu;
+        out[2 * b] = __builtin_amdgcn_perm(pe[1], pe[0], slo) | __builtin_amdgcn_perm(pe[3], pe[2], shi);
+        out[2 * b + 1] =
+            __builtin_amdgcn_perm(po[1], po[0], slo) | __builtin_amdgcn_perm(po[3], po[2], shi);
+    }
+}
+
+// The record of one whole chunk (x[e], e = 0..31) built by a single lane, in
+// registers: the values build_half_rec4 stores, limb[l][d] = dword d of digit
+// plane l, step[h] the step of half h.
+__device__ __forceinline__ void lane_chunk_rec(const float (&x)[32], uint32_t (&limb)[6][4],
+                                               float (&step)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        bool fin = true;
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            fin = fin && __builtin_isfinite(x[16 * h + j]);
+            amax = fmaxf(amax, fabsf(x[16 * h + j]));
+        }
+        int e = 0;
+        (void)frexpf(amax, &e);
+        e = e < -100 ? -100 : e;
+        const float inv = ldexpf(1.0f, 22 - e);
+        uint32_t U[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int X = fin ? (int)rintf(x[16 * h + j] * inv) : 0;
+            X = X > 4194304 ? 4194304 : (X < -4194304 ? -4194304 : X);
+            U[j] = (uint32_t)(X + 0x888888) ^ 0x888888u;
+        }
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            uint32_t o[6];
+            pack_limbs8(U + 8 * d, o);
+#pragma unroll
+            for (int l = 0; l < 6; ++l) limb[l][2 * h + d] = o[l];
+        }
+        step[h] = fin ? ldexpf(1.0f, e - 22) : __builtin_nanf("");
+    }
 }
 
 }  // namespace gemv

@@ -16,13 +16,18 @@
 //   * Each row step a lane issues one coalesced non-temporal 128-bit load of
 //     packed nibbles (consecutive lanes read consecutive 16-byte pieces of the
 //     same row: a wave instruction covers 1 KiB of one row) and one f32 scale.
-//   * x arrives as chunk records (k_xquant / fused producers): a 24-bit
-//     fixed-point integer per element in six 4-bit limb planes.  Then
-//        sum_i n_i U_i = sum_l 16^l * v_dot8_u32_u4(q, limb_l)
-//     directly on the packed nibbles -- no unpacking -- plus one dot8 against
-//     0x11111111 for sum n_i; the "-8" of the stored nibble and the limb offset
-//     are removed in exact integer arithmetic and the chunk partial is rounded
-//     to f32 once, then multiplied by its group scale.
+//   * x arrives as chunk records (k_xquant / fused producers): a 23-bit
+//     fixed-point integer per element as six signed base-16 digit planes
+//     (two's complement nibbles, [-8, 7]).  With no
+//     records given (XR: one activation row, one matrix), each lane builds
+//     its chunk's record itself from the raw x it loads, while its weight
+//     loads are in flight, which saves the separate record pass.  The stored
+//     nibble q becomes the signed nibble q - 8 with one XOR by 8 per nibble,
+//     and then
+//        sum_i (q_i - 8) X_i = sum_l 16^l * v_dot8_i32_i4(q ^ 0x8..8, digit_l)
+//     directly on the packed nibbles -- no unpacking, no correction terms --
+//     exact in 32-bit integers; each 16-element half is rounded to f32 once,
+//     scaled by its step, and the chunk partial by its group scale.
 //   * The per-lane partials of J rows are transpose-reduced across lanes,
 //     summed across waves through LDS, and the epilogue (bias, residual add, or
 //     silu(g)*u of a gate/up pair) writes the outputs.
@@ -42,7 +47,7 @@ using namespace gemv;
 
 namespace {
 
-template <int M, int J, bool DUAL, int EPI, bool V2>
+template <int M, int J, bool DUAL, int EPI, bool V2, bool XR>
 struct W4Gemv {
     static constexpr int D = DUAL ? 2 : 1;
     static constexpr int V = D * J * M;
@@ -57,10 +62,12 @@ struct W4Gemv {
         uint32_t ok;
     };
 
-    // The lane's x chunk records (one per activation row).
+    // The lane's x chunk records (one per activation row), or with XR its
+    // 32 raw activations.
     struct XRec {
         u32x4 limbs[M][6];
         u32x4 tail[M];   // {step 0-15, step 16-31, sum 0-15, sum 16-31}
+        float4 raw[XR ? M : 1][8];
     };
 
     const W4Params &p;
@@ -69,8 +76,7 @@ struct W4Gemv {
     bool act;
     size_t bpr, boff, soff;
     int gcols, sg;
-    uint32_t limb[M][6][NDW];   // limb[m][l][d] nibble e = bits [4l, 4l+4) of U_{8d+e}
-    int sxq[M][2];              // sum_i X_i of each 16-element half
+    uint32_t limb[M][6][NDW];   // limb[m][l][d] nibble e = digit l of X_{8d+e}
     float sx[M][2];             // power-of-two step of each half
     bool finite;                // false -> the wave takes the f32 path
 
@@ -99,6 +105,17 @@ struct W4Gemv {
     }
 
     __device__ __forceinline__ void issue_x(XRec &xr) const {
+        if (XR) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const int mm = m < p.m ? m : 0;
+                const float4 *xp =
+                    reinterpret_cast<const float4 *>(p.x + (size_t)mm * p.k + chunk * 32);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xr.raw[m][i] = xp[i];
+            }
+            return;
+        }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const int mm = m < p.m ? m : 0;
@@ -115,6 +132,17 @@ struct W4Gemv {
         bool fin = true;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
+            if (XR) {
+                float v[32];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    v[4 * i] = xr.raw[m][i].x; v[4 * i + 1] = xr.raw[m][i].y;
+                    v[4 * i + 2] = xr.raw[m][i].z; v[4 * i + 3] = xr.raw[m][i].w;
+                }
+                lane_chunk_rec(v, limb[m], sx[m]);
+                fin = fin && (m >= p.m || !(__builtin_isnan(sx[m][0]) || __builtin_isnan(sx[m][1])));
+                continue;
+            }
 #pragma unroll
             for (int l = 0; l < 6; ++l) {
                 const u32x4 t = xr.limbs[m][l];
@@ -122,8 +150,6 @@ struct W4Gemv {
             }
             sx[m][0] = __uint_as_float(xr.tail[m].x);
             sx[m][1] = __uint_as_float(xr.tail[m].y);
-            sxq[m][0] = (int)xr.tail[m].z;
-            sxq[m][1] = (int)xr.tail[m].w;
             fin = fin && (m >= p.m || !(__builtin_isnan(sx[m][0]) || __builtin_isnan(sx[m][1])));
         }
         // One vote per wave, so the integer path runs without per-lane branches.
@@ -179,9 +205,10 @@ struct W4Gemv {
     }
 
     // Dot products of the batch, per 16-element half h of the chunk:
-    //   sum_i (n_i - 8) X_i = 4096 * (hi - 2048 * sum n) + lo - 8 * sum X
-    // with lo / hi the limb sums 0..2 / 3..5 (all exact in 32-bit integers);
-    // one f32 rounding per half, then * step, summed, * group scale.
+    //   sum_i (n_i - 8) X_i = sum_l 16^l a_l,  a_l = signed dot8 of (n - 8, digit l)
+    // exact in 32-bit integers (|a_l| <= 1024, every Horner partial below 2^31,
+    // the sum below 2^29); one f32 rounding per half, then * step, summed,
+    // * group scale.
     __device__ __forceinline__ void dots(const Batch &bt, float (&v)[V]) const {
         if (!finite) {
 #pragma unroll
@@ -196,39 +223,49 @@ struct W4Gemv {
                                 : 0.f;
             return;
         }
+        // signed nibbles n - 8 of every chunk of the batch
+        int qs[J][D][NDW];
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-            for (int d = 0; d < D; ++d) {
-                const uint32_t(&q)[NDW] = bt.q[d][j];
-                uint32_t sn[2];
+            for (int d = 0; d < D; ++d)
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
-                    sn[h] = __builtin_amdgcn_udot8(
-                        q[2 * h + 1], 0x11111111u,
-                        __builtin_amdgcn_udot8(q[2 * h], 0x11111111u, 0u, false), false);
+                for (int dw = 0; dw < NDW; ++dw) qs[j][d][dw] = (int)(bt.q[d][j][dw] ^ 0x88888888u);
+        // Horner from the top digit, all (row, matrix, activation row, half)
+        // chains side by side: the shifted running sum is the accumulator of
+        // the next dot8 (the accumulate-in-place v_dot8c needs no zeroed
+        // register), and consecutive dot8s never depend on each other, so the
+        // dot-to-dot accumulator hazard costs no wait states.
+        int t[J][D][M][2];
+#pragma unroll
+        for (int l = 5; l >= 0; --l) {
+#pragma unroll
+            for (int hw = 0; hw < 2; ++hw)   // dword 2h + hw of each half
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+#pragma unroll
+                    for (int d = 0; d < D; ++d)
+#pragma unroll
+                        for (int m = 0; m < M; ++m)
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                int &a = t[j][d][m][h];
+                                const int acc = l == 5 ? (hw ? a : 0)
+                                                       : (hw ? a : (int)((uint32_t)a << 4));
+                                a = __builtin_amdgcn_sdot8(qs[j][d][2 * h + hw],
+                                                           (int)limb[m][l][2 * h + hw], acc, false);
+                            }
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int d = 0; d < D; ++d)
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    float r[2];
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        uint32_t a[6];
-#pragma unroll
-                        for (int l = 0; l < 6; ++l)
-                            a[l] = __builtin_amdgcn_udot8(
-                                q[2 * h + 1], limb[m][l][2 * h + 1],
-                                __builtin_amdgcn_udot8(q[2 * h], limb[m][l][2 * h], 0u, false),
-                                false);
-                        const int lo = (int)(a[0] + 16u * a[1] + 256u * a[2]);
-                        const int hi = (int)(a[3] + 16u * a[4] + 256u * a[5]);
-                        const int t = hi - 2048 * (int)sn[h];
-                        r[h] = 8.0f * (float)(512 * t - sxq[m][h]) + (float)lo;
-                    }
                     const float sc = ((bt.ok >> j) & 1u) ? bt.sc[d][j] : 0.f;
-                    v[(d * J + j) * M + m] = sc * fmaf(sx[m][0], r[0], sx[m][1] * r[1]);
+                    v[(d * J + j) * M + m] =
+                        sc * fmaf(sx[m][0], (float)t[j][d][m][0], sx[m][1] * (float)t[j][d][m][1]);
                 }
-            }
-        }
     }
 };
 
@@ -237,9 +274,9 @@ struct W4Gemv {
 // products (which wait only for what they read, since loads retire in issue
 // order).  Straight-line code: a
 // loop back-edge would make the compiler drain the load counter early.
-template <int M, int J, bool DUAL, int EPI, bool V2>
+template <int M, int J, bool DUAL, int EPI, bool V2, bool XR>
 __global__ __launch_bounds__(512) void k_w4_gemv(W4Params p, Layout L, Epi e) {
-    using G = W4Gemv<M, J, DUAL, EPI, V2>;
+    using G = W4Gemv<M, J, DUAL, EPI, V2, XR>;
     __shared__ float red[kMaxWaves * 64];
     __shared__ EpiShared sh;
     G g(p, L);
@@ -272,7 +309,7 @@ __global__ __launch_bounds__(256) void k_xquant(const float *__restrict__ x,
     build_xrec8(v, sub, live, xq + (size_t)row * c * kXRecDwords, c, ch);
 }
 
-template <int M, int J, bool DUAL, int EPI, bool V2 = false>
+template <int M, int J, bool DUAL, int EPI, bool V2 = false, bool XR = false>
 int launch(const W4Params &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
@@ -305,8 +342,12 @@ int launch(const W4Params &p, hipStream_t st) {
         TB_REQUIRE(p.k % 64 == 0 && !DUAL && ((uintptr_t)p.w0 & 3u) == 0, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: v2 blocks need K % 64 == 0 and a 4-byte aligned stream");
     const int grid = (p.n + L.rpb - 1) / L.rpb;
-    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI, V2>), dim3(grid), dim3(L.nwaves * 64), 0, st,
-                       p, L, e);
+    if (XR)
+        TB_REQUIRE(p.x && ((uintptr_t)p.x & 15u) == 0 && p.ssq_in == nullptr, TB_ERR_UNSUPPORTED,
+                   "TB_UNSUPPORTED: w4 GEMV without x records needs a 16-byte aligned x "
+                   "and no fused RMSNorm input");
+    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI, V2, XR>), dim3(grid), dim3(L.nwaves * 64), 0,
+                       st, p, L, e);
     TB_LAUNCHED();
     return TB_OK;
 }
@@ -320,6 +361,11 @@ int dispatch_m(const W4Params &p, hipStream_t st) {
     // writes records (16-row pieces: with 4 rows that takes 8-wave blocks).
     if (p.m <= 1) {
         const int j = p.rows_j ? p.rows_j : (DUAL ? (p.rec_out ? 8 : 4) : 16);
+        if (!DUAL && !p.xq) {   // records built in the kernel from x
+            if (j == 4) return launch<1, 4, false, EPI, V2, true>(p, st);
+            if (j == 16) return launch<1, 16, false, EPI, V2, true>(p, st);
+            return launch<1, 8, false, EPI, V2, true>(p, st);
+        }
         if (j == 4) return launch<1, 4, DUAL, EPI, V2>(p, st);
         if (j == 16) return launch<1, 16, DUAL, EPI, V2>(p, st);
         return launch<1, 8, DUAL, EPI, V2>(p, st);
@@ -344,6 +390,9 @@ int w4_gemv(W4Params p, int epi, hipStream_t st) {
     TB_REQUIRE(p.m >= 1 && p.m <= kMaxW4RowsPerPass, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4 GEMV pass takes 1..4 rows");
     TB_REQUIRE(p.k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: w4 GEMV needs K % 32 == 0");
+    TB_REQUIRE(p.xq || (p.m == 1 && epi != EPI_ROPE && p.w1 == nullptr), TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: w4 GEMV: x records are required for M > 1, gate/up pairs and "
+               "fused RoPE");
     if (p.v2) {
         TB_REQUIRE(p.w1 == nullptr, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: v2 blocks take single projections");
