@@ -14,8 +14,19 @@
  *
  * Pointer convention.  Stateless ops take DEVICE pointers (HBM-resident
  * tensors, row-major, contiguous) and a hipStream_t passed as void* (NULL = the
- * default stream); they are asynchronous on that stream and re-entrant per
- * stream.  The decoder copies HOST weights to the device once at creation, as
+ * default stream); they are asynchronous on that stream.
+ *
+ * Scratch.  An op that needs scratch (activation records, h, split-K
+ * partials) takes it from a workspace owned by the library per (device,
+ * stream): calls on different streams or threads never share scratch, and
+ * calls on one stream are ordered by that stream.  A workspace only grows; a
+ * buffer it outgrows is kept, not freed, until the process ends, so a graph
+ * captured earlier still points at valid memory.  Growth may happen while the
+ * stream is being captured (this thread's capture mode is relaxed around the
+ * allocation).  tb_fused_swiglu_mlp_w4a32_noalloc uses a fixed static scratch
+ * instead and allocates nothing.
+ *
+ * The decoder copies HOST weights to the device once at creation, as
  * RustQwenDecoder::new copies them into Rust-owned memory
  * (src/llm/decoder.rs:235-332).  A decoder handle is not thread-safe, matching
  * the reference's &mut self receivers.

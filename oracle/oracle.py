@@ -17,7 +17,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_SO = os.path.join(_HERE, "liboracle.so")
+# TB_ORACLE_SO: another build of the same source, e.g. the sanitizer build of
+# sanitize.sh; by default the Makefile's liboracle.so beside this file
+_SO = os.environ.get("TB_ORACLE_SO") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")

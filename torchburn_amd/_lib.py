@@ -10,7 +10,9 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libtbhip.so")
+# TB_LIB_SO: another build of the same sources (the host-sanitizer build of
+# tests/run_sanitized.sh); by default the in-tree libtbhip.so
+LIB_PATH = os.environ.get("TB_LIB_SO") or os.path.join(_HERE, "libtbhip.so")
 
 TB_OK = 0
 TB_ERR_UNSUPPORTED = 1

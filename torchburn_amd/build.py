@@ -35,6 +35,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libtbhip.so)")
 
 
+# Host-side sanitizer build (tests/run_sanitized.sh): AddressSanitizer and
+# UndefinedBehaviorSanitizer on the host code only -- each flag behind
+# -Xarch_host, so the gfx950 device code is built exactly as in the product.
+HOST_SANITIZE_FLAGS = [
+    "-g", "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+]
+
+
 # Per-source extra flags.  w4_limb: MFMA results in VGPRs (the kernel scales
 # every result with VALU; accumulators in AGPRs would cost a copy each).
 EXTRA_FLAGS = {
@@ -42,9 +51,11 @@ EXTRA_FLAGS = {
 }
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+def _compile(src: str, build_dir: str = BUILD, host_sanitize: bool = False) -> str:
+    obj = os.path.join(build_dir, os.path.basename(src) + ".o")
     extra = EXTRA_FLAGS.get(os.path.basename(src), [])
+    if host_sanitize:
+        extra = extra + HOST_SANITIZE_FLAGS
     cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", os.path.join(PKG, ".."), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -52,22 +63,29 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose: bool = False, out: str = LIB, host_sanitize: bool = False) -> str:
+    """Builds the library into `out`.  host_sanitize: the sanitizer build of the
+    host code (objects in csrc/_build_san/; load it with the sanitizer runtime
+    preloaded, as tests/run_sanitized.sh does)."""
+    build_dir = BUILD + "_san" if host_sanitize else BUILD
+    os.makedirs(build_dir, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, build_dir, host_sanitize), srcs))
+    tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
-    return LIB
+        print(f"built {out} from {len(srcs)} sources")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) == 3 and sys.argv[1] == "--host-sanitize":
+        build(verbose=True, out=os.path.abspath(sys.argv[2]), host_sanitize=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

@@ -423,7 +423,9 @@ __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restric
                                                           uint8_t *__restrict__ rec_out) {
     constexpr int TOKS = 8 * T;           // tokens of the batch
     constexpr int PER = 32 / T;           // threads per token
-    __shared__ __align__(16) float hs[TOKS][kBatch];
+    // rows padded by one float: the record wave reads the 8 (16) tokens of a
+    // column in one instruction, which would otherwise hit one bank
+    __shared__ float hs[TOKS][kBatch + 1];
     const int tid = threadIdx.x, bt = blockIdx.x;
     const int tok = tid / PER, c0 = (tid % PER) * 4 * T;   // 4 T values at rows c0..
     const int row0 = kBatch * bt + c0;
@@ -471,7 +473,8 @@ __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restric
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = silu(gs[h][e] + bg[h][e]) * (us[h][e] + bu[h][e]);
             *reinterpret_cast<f32x4 *>(y + (size_t)tok * n + row0 + 4 * h) = v;
-            *reinterpret_cast<f32x4 *>(&hs[tok][c0 + 4 * h]) = v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hs[tok][c0 + 4 * h + e] = v[e];
         }
     }
     if (!rec_out) return;
