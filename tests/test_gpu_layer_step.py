@@ -80,6 +80,10 @@ CASES = [
     (4096, 32, 8, 128, 4160, 4096, 32, 5e5),    # Llama-3-8B shape, KV 4096
     (512, 8, 8, 64, 80, 0, 64, 1e4),            # MHA, first position, group 64
     (1024, 16, 4, 64, 300, 200, 32, 1e4),       # ragged last tile
+    # long caches: more 64-position tiles than the 128 attention blocks per KV
+    # head, so blocks fold 2-3 tiles each (the merge reads 128 partials)
+    (1024, 16, 4, 64, 16448, 12000, 32, 1e4),
+    (2048, 16, 4, 128, 24640, 20000, 32, 5e5),
 ]
 
 

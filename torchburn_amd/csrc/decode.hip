@@ -269,6 +269,9 @@ __global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
 //     2 KB LDS table to the lanes holding V, which accumulate o per head and
 //     fold their row groups with two shuffles;
 //   * the four waves' (o, m, l) combine through LDS into the block's partial.
+// Block y folds tiles y, y + gridDim.y, ... below the sequence length into one
+// running (o, m, l) per (head, column) -- the online softmax across tiles --
+// and writes it as partial y; with one tile per block that is the tile's own.
 template <int HD, int GP>
 __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ st,
                                                   const float *__restrict__ qkv,
@@ -292,136 +295,155 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
     __shared__ float so[4][GP][HD];
     __shared__ float sml[4][GP][2];
 
-    const int kvh = blockIdx.x, spl = blockIdx.y, tid = threadIdx.x;
+    const int kvh = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int seq = st->pos + 1;
-    const int t0 = spl * T;
-    if (t0 >= seq) return;   // tile past the sequence: the merge never reads it
+    if ((int)blockIdx.y * T >= seq) return;   // no tile: the merge never reads this partial
     const int c = lane & (C4 - 1), rg = lane >> B;
-    const int pbase = t0 + wave * PW;
+    // the running (o, m, l) of this thread's (head, column) of the final fold
+    // (G * C4 <= 256: one per thread at most)
+    float4 run_o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float run_m = -FLT_MAX, run_l = 0.f;
+    for (int spl = blockIdx.y; spl * T < seq; spl += gridDim.y) {
+        const int t0 = spl * T;
+        const int pbase = t0 + wave * PW;
 
-    const float4 *k4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * max_seq * C4 + c;
-    const float4 *v4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * max_seq * C4 + c;
-    const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
-    float4 kr[NI], vr[NI], qr[GP];
-    // q, then every K row, then every V row: the scores and the softmax wait
-    // only for K, and run while V is still arriving.
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-        qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int p = pbase + i * RPL + rg;
-        kr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(k4 + (size_t)p * C4))
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int p = pbase + i * RPL + rg;
-        vr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(v4 + (size_t)p * C4))
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
-    float v[NV];
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
+        const float4 *k4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * max_seq * C4 + c;
+        const float4 *v4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * max_seq * C4 + c;
+        const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
+        float4 kr[NI], vr[NI], qr[GP];
+        // q, then every K row, then every V row: the scores and the softmax wait
+        // only for K, and run while V is still arriving.
 #pragma unroll
         for (int g = 0; g < GP; ++g)
-            v[i * GP + g] = fmaf(qr[g].w, kr[i].w,
-                                 fmaf(qr[g].z, kr[i].z, fmaf(qr[g].y, kr[i].y, qr[g].x * kr[i].x)));
-
-    // Lane l now holds, per chunk ch, the score of flat index ch * CH + (c >> RB).
-    const int vi = c >> RB;
-    const int g = vi & (GP - 1);
-    const bool rep = (c & ((1 << RB) - 1)) == 0;
-    float sc[NCH];
-    bool ok[NCH];
-    int pw[NCH];
-    float m = -FLT_MAX;
+            qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        float t[CH];
-#pragma unroll
-        for (int j = 0; j < CH; ++j) t[j] = v[ch * CH + j];
-        transpose_reduce<CH>(t, lane, B);
-        const int i = (ch * CH + vi) >> LGP;
-        pw[ch] = i * RPL + rg;
-        ok[ch] = g < G && pbase + pw[ch] < seq;
-        sc[ch] = t[0] * scale;
-        if (ok[ch]) m = fmaxf(m, sc[ch]);
-    }
-#pragma unroll
-    for (int j = 0; j < 6; ++j)
-        if (j < RB || j >= RB + LGP) m = fmaxf(m, __shfl_xor(m, 1 << j));
-    float l = 0.f;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        const float p = ok[ch] ? expf(sc[ch] - m) : 0.f;
-        if (rep) sp[wave][pw[ch]][g] = p;
-        if (rep) l += p;
-    }
-#pragma unroll
-    for (int j = 0; j < 6; ++j)
-        if (j < RB || j >= RB + LGP) l += __shfl_xor(l, 1 << j);
-    if (rg == 0 && rep && vi < GP) {
-        sml[wave][g][0] = m;
-        sml[wave][g][1] = l;
-    }
-    __syncthreads();
-
-    float4 acc[GP];
-#pragma unroll
-    for (int h = 0; h < GP; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const float *pr = sp[wave][i * RPL + rg];
-#pragma unroll
-        for (int h = 0; h < GP; ++h) {
-            const float p = pr[h];
-            acc[h].x = fmaf(p, vr[i].x, acc[h].x);
-            acc[h].y = fmaf(p, vr[i].y, acc[h].y);
-            acc[h].z = fmaf(p, vr[i].z, acc[h].z);
-            acc[h].w = fmaf(p, vr[i].w, acc[h].w);
+        for (int i = 0; i < NI; ++i) {
+            const int p = pbase + i * RPL + rg;
+            kr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(k4 + (size_t)p * C4))
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    }
 #pragma unroll
-    for (int j = B; j < 6; ++j)
-#pragma unroll
-        for (int h = 0; h < GP; ++h) {
-            acc[h].x += __shfl_xor(acc[h].x, 1 << j);
-            acc[h].y += __shfl_xor(acc[h].y, 1 << j);
-            acc[h].z += __shfl_xor(acc[h].z, 1 << j);
-            acc[h].w += __shfl_xor(acc[h].w, 1 << j);
+        for (int i = 0; i < NI; ++i) {
+            const int p = pbase + i * RPL + rg;
+            vr[i] = p < seq ? load_nt_f4(reinterpret_cast<const float *>(v4 + (size_t)p * C4))
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    if (rg == 0) {
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-            if (h < G) *reinterpret_cast<float4 *>(&so[wave][h][4 * c]) = acc[h];
-    }
-    __syncthreads();
 
-    for (int idx = tid; idx < G * C4; idx += 256) {
-        const int h = idx / C4, cc = idx - h * C4;
-        float M = -FLT_MAX;
+        float v[NV];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, sml[w][h][0]);
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        float L = 0.f;
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float e = expf(sml[w][h][0] - M);
-            const float4 ow = *reinterpret_cast<const float4 *>(&so[w][h][4 * cc]);
-            o.x = fmaf(e, ow.x, o.x);
-            o.y = fmaf(e, ow.y, o.y);
-            o.z = fmaf(e, ow.z, o.z);
-            o.w = fmaf(e, ow.w, o.w);
-            L = fmaf(e, sml[w][h][1], L);
+            for (int g = 0; g < GP; ++g)
+                v[i * GP + g] =
+                    fmaf(qr[g].w, kr[i].w,
+                         fmaf(qr[g].z, kr[i].z, fmaf(qr[g].y, kr[i].y, qr[g].x * kr[i].x)));
+
+        // Lane l now holds, per chunk ch, the score of flat index ch * CH + (c >> RB).
+        const int vi = c >> RB;
+        const int g = vi & (GP - 1);
+        const bool rep = (c & ((1 << RB) - 1)) == 0;
+        float sc[NCH];
+        bool ok[NCH];
+        int pw[NCH];
+        float m = -FLT_MAX;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            float t[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) t[j] = v[ch * CH + j];
+            transpose_reduce<CH>(t, lane, B);
+            const int i = (ch * CH + vi) >> LGP;
+            pw[ch] = i * RPL + rg;
+            ok[ch] = g < G && pbase + pw[ch] < seq;
+            sc[ch] = t[0] * scale;
+            if (ok[ch]) m = fmaxf(m, sc[ch]);
         }
-        float *dst = part + ((size_t)(kvh * G + h) * nsplit + spl) * (HD + 4);
-        *reinterpret_cast<float4 *>(dst + 4 * cc) = o;
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            if (j < RB || j >= RB + LGP) m = fmaxf(m, __shfl_xor(m, 1 << j));
+        float l = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const float p = ok[ch] ? expf(sc[ch] - m) : 0.f;
+            if (rep) sp[wave][pw[ch]][g] = p;
+            if (rep) l += p;
+        }
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            if (j < RB || j >= RB + LGP) l += __shfl_xor(l, 1 << j);
+        if (rg == 0 && rep && vi < GP) {
+            sml[wave][g][0] = m;
+            sml[wave][g][1] = l;
+        }
+        __syncthreads();
+
+        float4 acc[GP];
+#pragma unroll
+        for (int h = 0; h < GP; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float *pr = sp[wave][i * RPL + rg];
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                const float p = pr[h];
+                acc[h].x = fmaf(p, vr[i].x, acc[h].x);
+                acc[h].y = fmaf(p, vr[i].y, acc[h].y);
+                acc[h].z = fmaf(p, vr[i].z, acc[h].z);
+                acc[h].w = fmaf(p, vr[i].w, acc[h].w);
+            }
+        }
+#pragma unroll
+        for (int j = B; j < 6; ++j)
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                acc[h].x += __shfl_xor(acc[h].x, 1 << j);
+                acc[h].y += __shfl_xor(acc[h].y, 1 << j);
+                acc[h].z += __shfl_xor(acc[h].z, 1 << j);
+                acc[h].w += __shfl_xor(acc[h].w, 1 << j);
+            }
+        if (rg == 0) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h)
+                if (h < G) *reinterpret_cast<float4 *>(&so[wave][h][4 * c]) = acc[h];
+        }
+        __syncthreads();
+
+        if (tid < G * C4) {
+            const int h = tid / C4, cc = tid - h * C4;
+            float M = -FLT_MAX;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) M = fmaxf(M, sml[w][h][0]);
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+            float L = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float e = expf(sml[w][h][0] - M);
+                const float4 ow = *reinterpret_cast<const float4 *>(&so[w][h][4 * cc]);
+                o.x = fmaf(e, ow.x, o.x);
+                o.y = fmaf(e, ow.y, o.y);
+                o.z = fmaf(e, ow.z, o.z);
+                o.w = fmaf(e, ow.w, o.w);
+                L = fmaf(e, sml[w][h][1], L);
+            }
+            // fold the tile into the running state (first tile: a = 0, b = 1,
+            // so a single tile passes through unchanged)
+            const float mn = fmaxf(run_m, M);
+            const float a = expf(run_m - mn), b = expf(M - mn);
+            run_o = make_float4(fmaf(run_o.x, a, o.x * b), fmaf(run_o.y, a, o.y * b),
+                                fmaf(run_o.z, a, o.z * b), fmaf(run_o.w, a, o.w * b));
+            run_l = fmaf(run_l, a, L * b);
+            run_m = mn;
+        }
+        __syncthreads();   // the next tile rewrites sp, so and sml
+    }
+    if (tid < G * C4) {
+        const int h = tid / C4, cc = tid - h * C4;
+        float *dst = part + ((size_t)(kvh * G + h) * nsplit + blockIdx.y) * (HD + 4);
+        *reinterpret_cast<float4 *>(dst + 4 * cc) = run_o;
         if (cc == 0) {
-            dst[HD] = M;
-            dst[HD + 1] = L;
+            dst[HD] = run_m;
+            dst[HD + 1] = run_l;
         }
     }
 }
@@ -513,7 +535,8 @@ __global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restr
     __shared__ float smx[NSG], sl[NSG];
     const int h = blockIdx.x, ck = blockIdx.y, tid = threadIdx.x;
     const int c = tid & 7, sg = tid >> 3;
-    const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;
+    // partials written: one per attention block that had a tile
+    const int used = min(nsplit, (st->pos + 1 + kAttnTile - 1) / kAttnTile);
     const float *ph = part + (size_t)h * nsplit * rec;
     float M = -FLT_MAX, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1020,9 +1043,12 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
                "TB_UNSUPPORTED: attention tile does not fit in LDS for this head layout");
     const int gp = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 0;
     if (gp && (hd == 128 || hd == 64)) {
+        // at most kAttnMaxSplits blocks per KV head, each folding every
+        // nb-th tile: the partials (and the merge) stay bounded for long caches
+        const int nb = std::min(ns, kAttnMaxSplits);
 #define TB_ATTN_REG(HD, GP)                                                                    \
-    hipLaunchKernelGGL((k_attn_reg<HD, GP>), dim3(hkv, ns), dim3(256), 0, s, st, qkv, kc, vc, \
-                       part, G, max_seq, ns, scale)
+    hipLaunchKernelGGL((k_attn_reg<HD, GP>), dim3(hkv, nb), dim3(256), 0, s, st, qkv, kc, vc, \
+                       part, G, max_seq, nb, scale)
         if (hd == 128) {
             if (gp == 1) TB_ATTN_REG(128, 1);
             else if (gp == 2) TB_ATTN_REG(128, 2);
@@ -1030,7 +1056,7 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
             else TB_ATTN_REG(128, 8);
             TB_LAUNCHED();
             hipLaunchKernelGGL(k_attn_merge_chunk<128>, dim3(hq, 4), dim3(64), 0, s, st, part, out,
-                               xq, ns);
+                               xq, nb);
         } else {
             if (gp == 1) TB_ATTN_REG(64, 1);
             else if (gp == 2) TB_ATTN_REG(64, 2);
@@ -1038,7 +1064,7 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
             else TB_ATTN_REG(64, 8);
             TB_LAUNCHED();
             hipLaunchKernelGGL(k_attn_merge_chunk<64>, dim3(hq, 2), dim3(64), 0, s, st, part, out,
-                               xq, ns);
+                               xq, nb);
         }
 #undef TB_ATTN_REG
     } else if (hd == 128) {

@@ -20,6 +20,9 @@ constexpr int kNormChunks = 32;    // 32-element chunks normalised per RMSNorm b
 constexpr int kAttnTile = 64;      // KV positions per attention block
 constexpr int kArgmaxBlocks = 256;
 constexpr int kMaxTiles = 1024;     // max_seq_len <= kMaxTiles * kAttnTile
+// Attention blocks per KV head: a longer cache has each block fold several
+// tiles, so the grid and the merge stay this size whatever max_seq_len is.
+constexpr int kAttnMaxSplits = 128;
 
 int launch_rmsnorm(const DecState *st, const float *embed, float *x, const float *w, float *xn,
                    uint32_t *xq, int H, float eps, hipStream_t s);
