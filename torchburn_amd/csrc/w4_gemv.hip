@@ -223,49 +223,59 @@ struct W4Gemv {
                                 : 0.f;
             return;
         }
-        // signed nibbles n - 8 of every chunk of the batch
-        int qs[J][D][NDW];
+        // Rows in load order, JG at a time: the dots of the first rows start
+        // as soon as their weights are in (loads retire in issue order).
+        // Within a group, Horner from the top digit with every (row, matrix,
+        // activation row, half) chain side by side: the shifted running sum is
+        // the accumulator of the next dot8 (the accumulate-in-place v_dot8c
+        // needs no zeroed register), and with at least 4 chains consecutive
+        // dot8s never depend on each other, so the dot-to-dot accumulator
+        // hazard costs no wait states.
+        constexpr int JG = (D * M * 2 >= 4 || J < 2) ? 1 : 2;
 #pragma unroll
-        for (int j = 0; j < J; ++j)
+        for (int j0 = 0; j0 < J; j0 += JG) {
+            int qs[JG][D][NDW];   // signed nibbles n - 8
 #pragma unroll
-            for (int d = 0; d < D; ++d)
+            for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
-                for (int dw = 0; dw < NDW; ++dw) qs[j][d][dw] = (int)(bt.q[d][j][dw] ^ 0x88888888u);
-        // Horner from the top digit, all (row, matrix, activation row, half)
-        // chains side by side: the shifted running sum is the accumulator of
-        // the next dot8 (the accumulate-in-place v_dot8c needs no zeroed
-        // register), and consecutive dot8s never depend on each other, so the
-        // dot-to-dot accumulator hazard costs no wait states.
-        int t[J][D][M][2];
+                for (int d = 0; d < D; ++d)
 #pragma unroll
-        for (int l = 5; l >= 0; --l) {
+                    for (int dw = 0; dw < NDW; ++dw)
+                        qs[jj][d][dw] = (int)(bt.q[d][j0 + jj][dw] ^ 0x88888888u);
+            int t[JG][D][M][2];
 #pragma unroll
-            for (int hw = 0; hw < 2; ++hw)   // dword 2h + hw of each half
+            for (int l = 5; l >= 0; --l) {
 #pragma unroll
-                for (int j = 0; j < J; ++j)
+                for (int hw = 0; hw < 2; ++hw)   // dword 2h + hw of each half
 #pragma unroll
-                    for (int d = 0; d < D; ++d)
+                    for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
-                        for (int m = 0; m < M; ++m)
+                        for (int d = 0; d < D; ++d)
 #pragma unroll
-                            for (int h = 0; h < 2; ++h) {
-                                int &a = t[j][d][m][h];
-                                const int acc = l == 5 ? (hw ? a : 0)
-                                                       : (hw ? a : (int)((uint32_t)a << 4));
-                                a = __builtin_amdgcn_sdot8(qs[j][d][2 * h + hw],
-                                                           (int)limb[m][l][2 * h + hw], acc, false);
-                            }
+                            for (int m = 0; m < M; ++m)
+#pragma unroll
+                                for (int h = 0; h < 2; ++h) {
+                                    int &a = t[jj][d][m][h];
+                                    const int acc = l == 5 ? (hw ? a : 0)
+                                                           : (hw ? a : (int)((uint32_t)a << 4));
+                                    a = __builtin_amdgcn_sdot8(qs[jj][d][2 * h + hw],
+                                                               (int)limb[m][l][2 * h + hw], acc,
+                                                               false);
+                                }
+            }
+#pragma unroll
+            for (int jj = 0; jj < JG; ++jj)
+#pragma unroll
+                for (int d = 0; d < D; ++d)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const int j = j0 + jj;
+                        const float sc = ((bt.ok >> j) & 1u) ? bt.sc[d][j] : 0.f;
+                        v[(d * J + j) * M + m] =
+                            sc * fmaf(sx[m][0], (float)t[jj][d][m][0],
+                                      sx[m][1] * (float)t[jj][d][m][1]);
+                    }
         }
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-#pragma unroll
-            for (int d = 0; d < D; ++d)
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float sc = ((bt.ok >> j) & 1u) ? bt.sc[d][j] : 0.f;
-                    v[(d * J + j) * M + m] =
-                        sc * fmaf(sx[m][0], (float)t[j][d][m][0], sx[m][1] * (float)t[j][d][m][1]);
-                }
     }
 };
 
