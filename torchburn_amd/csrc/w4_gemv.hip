@@ -362,20 +362,30 @@ int launch(const W4Params &p, hipStream_t st) {
     return TB_OK;
 }
 
+// Blocks of a single-matrix M = 1 launch at j rows per block.
+int blocks_at(const W4Params &p, int j) {
+    Layout L;
+    if (!make_layout(p.k / 32, ceil_log2(j), j, L, 0)) return 0;
+    return (p.n + L.rpb - 1) / L.rpb;
+}
+
 template <bool DUAL, int EPI, bool V2 = false>
 int dispatch_m(const W4Params &p, hipStream_t st) {
-    // x stays in VGPRs, so one pass takes <= 4 rows.  Rows per block: 16 for
-    // one matrix, 8 when K needs 4 or more K-slice waves and no records are
-    // written (two blocks per CU instead of one: Llama-3-8B down projection
-    // 10.0 -> 9.55 us); for a gate/up pair 4 (8 weight loads in flight per
-    // lane: twice the waves, each with half the dot products left to do once
-    // its data is in, which shortens the kernel's tail), or 8 when the
-    // epilogue writes records (16-row pieces: with 4 rows that takes 8-wave
-    // blocks).
+    // x stays in VGPRs, so one pass takes <= 4 rows.  Rows per block at M = 1:
+    // 8 for a gate/up pair (with the dots in load order, 8 rows measured
+    // 15.4 us against 16.0 at 4 and 16.7 at 16 for Llama-3-8B); 16 for one
+    // matrix whose epilogue writes records (16-row pieces); otherwise the
+    // largest of 16, 8, 4 that still gives 512 blocks (two per CU: the
+    // Qwen2.5-0.5B up-projection [4864, 896] 5.9 -> 4.7 us at 4 rows, the
+    // Llama-3-8B down projection 10.0 -> 9.0 us at 8).
     if (p.m <= 1) {
         const bool prod = p.rec_out || p.xw_out || p.ssq_out;
-        const int j = p.rows_j ? p.rows_j
-                               : (DUAL ? (p.rec_out ? 8 : 4) : (p.k >= 8192 && !prod ? 8 : 16));
+        int j = p.rows_j;
+        if (!j) {
+            j = DUAL ? 8 : 16;
+            if (!DUAL && !prod)
+                while (j > 4 && blocks_at(p, j) < 512) j /= 2;
+        }
         if (!DUAL && !p.xq) {   // records built in the kernel from x
             if (j == 4) return launch<1, 4, false, EPI, V2, true>(p, st);
             if (j == 16) return launch<1, 16, false, EPI, V2, true>(p, st);
