@@ -297,9 +297,16 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
 
     const int kvh = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & (C4 - 1), rg = lane >> B;
+    // column c of the G query heads: the same for every tile, and loaded
+    // before the step position is known
+    const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
+    float4 qr[GP];
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+        qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
     const int seq = st->pos + 1;
     if ((int)blockIdx.y * T >= seq) return;   // no tile: the merge never reads this partial
-    const int c = lane & (C4 - 1), rg = lane >> B;
     // the running (o, m, l) of this thread's (head, column) of the final fold
     // (G * C4 <= 256: one per thread at most)
     float4 run_o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -310,13 +317,9 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
 
         const float4 *k4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * max_seq * C4 + c;
         const float4 *v4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * max_seq * C4 + c;
-        const float4 *q4 = reinterpret_cast<const float4 *>(qkv) + (size_t)kvh * G * C4 + c;
-        float4 kr[NI], vr[NI], qr[GP];
-        // q, then every K row, then every V row: the scores and the softmax wait
-        // only for K, and run while V is still arriving.
-#pragma unroll
-        for (int g = 0; g < GP; ++g)
-            qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 kr[NI], vr[NI];
+        // every K row, then every V row: the scores and the softmax wait only
+        // for K, and run while V is still arriving.
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int p = pbase + i * RPL + rg;
@@ -540,18 +543,22 @@ __global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restr
     const float *ph = part + (size_t)h * nsplit * rec;
     float M = -FLT_MAX, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < used; s0 += NSG * NB) {
+    // The passes cover all nsplit slots of the buffer: a pass's loads do not
+    // wait for the step position, which only masks the slots not written
+    // this step afterwards.
+    for (int s0 = 0; s0 < nsplit; s0 += NSG * NB) {
         float4 ov[NB];
         float mv[NB], lv[NB];
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const int sp = s0 + sg + u * NSG;
+            const float *pp = ph + (size_t)(sp < nsplit ? sp : 0) * rec;
+            const float4 o4 = *reinterpret_cast<const float4 *>(pp + 32 * ck + 4 * c);
+            const float m4 = pp[HD], l4 = pp[HD + 1];
             const bool ok = sp < used;
-            const float *pp = ph + (size_t)(ok ? sp : 0) * rec;
-            ov[u] = ok ? *reinterpret_cast<const float4 *>(pp + 32 * ck + 4 * c)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-            mv[u] = ok ? pp[HD] : -FLT_MAX;
-            lv[u] = ok ? pp[HD + 1] : 0.f;
+            ov[u] = ok ? o4 : make_float4(0.f, 0.f, 0.f, 0.f);
+            mv[u] = ok ? m4 : -FLT_MAX;
+            lv[u] = ok ? l4 : 0.f;
         }
         float mn = M;
 #pragma unroll
