@@ -185,9 +185,8 @@ static int mfma_ws(const MfmaParams &p, int epi, hipStream_t st) {
 // K % 128 == 0 (a SwiGLU pair: N % 128 == 0), 16-byte aligned x and w, a power-of-two
 // group >= 32 dividing K (or per-row / scalar scales).
 static bool limb_fast(const float *x, const void *w, int64_t m, int64_t n, int64_t k,
-                      int64_t gs, bool per_row, bool pair, bool records = false) {
-    if (m < limb_min_m() || m > limb_max_m() || !limb_shape_ok(m, n, k, pair, records))
-        return false;
+                      int64_t gs, bool per_row, bool pair) {
+    if (m < limb_min_m() || m > limb_max_m() || !limb_shape_ok(m, n, k, pair)) return false;
     if (!per_row && (gshift_of(gs) < 0 || k % gs != 0)) return false;
     return aligned(x, 16) && aligned(w, 16);
 }
@@ -397,7 +396,7 @@ static int mlp_w4_check(const MlpW4 &a, const char *op) {
 
 // 0: any-shape GEMVs; 1: FP32-MFMA pair; 2: GEMV passes; 3: small-batch f16 MFMA
 static int mlp_w4_path(const MlpW4 &a) {
-    if (limb_fast(a.x, a.gate_w, a.m, a.inter, a.k, a.gs, false, true, true) &&
+    if (limb_fast(a.x, a.gate_w, a.m, a.inter, a.k, a.gs, false, true) &&
         aligned(a.up_w, 16) &&
         limb_fast(a.x, a.down_w, a.m, a.n_out, a.inter, a.gs, false, false))
         return 3;

@@ -540,11 +540,10 @@ size_t limb_partials_bytes(int m, int n, int k, bool pair) {
     return (size_t)pl.splits * (size_t)m * (size_t)(pair ? 2 * n : n) * sizeof(float);
 }
 
-bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair, bool records) {
+bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair) {
     if (m < 1 || m > kLimbMaxM || n < 1 || k < kBatch || k % kBatch != 0) return false;
     if (k > (int64_t)1 << 24 || n > (int64_t)1 << 23) return false;
-    (void)records;
-    return !pair || n % kBatch == 0;   // whole 128-row batches of h per pair block
+    return !pair || n % kBatch == 0;   // the pair reduce takes whole 128-row batches of h
 }
 
 int limb_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st) {
@@ -562,7 +561,7 @@ int limb_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st) {
 
 int w4_limb(const LimbParams &p, float *part, hipStream_t st) {
     const bool pair = p.w1 != nullptr;
-    TB_REQUIRE(limb_shape_ok(p.m, p.n, p.k, pair, pair && p.rec_out), TB_ERR_UNSUPPORTED,
+    TB_REQUIRE(limb_shape_ok(p.m, p.n, p.k, pair), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: small-batch MFMA projection needs 1 <= M <= 16, K % 128 == 0 "
                "(and N % 128 == 0 for a SwiGLU pair)");
     const bool t1 = tiles_of(p.m) == 1;

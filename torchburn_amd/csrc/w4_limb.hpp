@@ -38,7 +38,7 @@ int limb_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st);
 
 // Shapes the kernels take: 1 <= m <= 16, k % 128 == 0; a SwiGLU pair needs
 // n % 128 == 0.  Pointers: x, w 16-byte aligned (checked by callers).
-bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair, bool records);
+bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair);
 
 // y = epilogue(x . deq(W)^T): plain / + bias / + residual for one projection,
 // silu(x W0^T + b0) * (x W1^T + b1) for a pair (plus rec_out when set).
