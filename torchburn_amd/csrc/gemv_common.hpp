@@ -11,6 +11,9 @@ namespace tb {
 namespace gemv {
 
 constexpr int kMaxWaves = 8;   // 512 threads per block: 256 VGPRs per lane available
+// 1024-thread blocks (at most 128 VGPRs per lane): more row groups per block
+// for kernels whose epilogue needs 16-row blocks
+constexpr int kMaxWavesWide = 16;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -145,7 +148,8 @@ struct Layout {
 // Picks the split of a row of `c` chunks over waves and lanes for V partials
 // per lane, with at least `min_rows` rows per block when the wave budget allows
 // (row groups).  Returns false when the row needs more than kMaxWaves slices.
-inline bool make_layout(int c, int logv, int j, Layout &L, int min_rows = 0) {
+inline bool make_layout(int c, int logv, int j, Layout &L, int min_rows = 0,
+                        int max_waves = kMaxWaves) {
     int bnat;
     if (c <= 64) {
         L.nks = 1;
@@ -162,7 +166,7 @@ inline bool make_layout(int c, int logv, int j, Layout &L, int min_rows = 0) {
     L.rps = 64 >> L.b;
     L.jr = j * L.rps;
     L.ng = 1;
-    while (L.jr * L.ng < min_rows && L.nks * L.ng * 2 <= kMaxWaves) L.ng *= 2;
+    while (L.jr * L.ng < min_rows && L.nks * L.ng * 2 <= max_waves) L.ng *= 2;
     L.nwaves = L.nks * L.ng;
     L.rpb = L.jr * L.ng;
     return true;
@@ -327,7 +331,7 @@ __device__ __forceinline__ void build_half_rec4(float4 v, int q, bool live, uint
 // block's outputs while their records are built.
 constexpr int kMaxRecRows = 256;
 struct EpiShared {
-    float ssq[kMaxWaves];
+    float ssq[kMaxWavesWide];
     float out[kMaxRecRows];
 };
 

@@ -284,10 +284,10 @@ struct W4Gemv {
 // products (which wait only for what they read, since loads retire in issue
 // order).  Straight-line code: a
 // loop back-edge would make the compiler drain the load counter early.
-template <int M, int J, bool DUAL, int EPI, bool V2, bool XR>
-__global__ __launch_bounds__(512) void k_w4_gemv(W4Params p, Layout L, Epi e) {
+template <int M, int J, bool DUAL, int EPI, bool V2, bool XR, int NW>
+__global__ __launch_bounds__(NW * 64) void k_w4_gemv(W4Params p, Layout L, Epi e) {
     using G = W4Gemv<M, J, DUAL, EPI, V2, XR>;
-    __shared__ float red[kMaxWaves * 64];
+    __shared__ float red[NW * 64];
     __shared__ EpiShared sh;
     G g(p, L);
     typename G::Batch a;
@@ -319,13 +319,15 @@ __global__ __launch_bounds__(256) void k_xquant(const float *__restrict__ x,
     build_xrec8(v, sub, live, xq + (size_t)row * c * kXRecDwords, c, ch);
 }
 
-template <int M, int J, bool DUAL, int EPI, bool V2 = false, bool XR = false>
+// NW: the block's wave limit (kMaxWaves, or kMaxWavesWide for more row
+// groups per block in kernels within 128 VGPRs).
+template <int M, int J, bool DUAL, int EPI, bool V2 = false, bool XR = false, int NW = kMaxWaves>
 int launch(const W4Params &p, hipStream_t st) {
     constexpr int V = (DUAL ? 2 : 1) * J * M;
     static_assert(V <= 64, "at most 64 partials per lane");
     Layout L;
     const bool prod = p.rec_out || p.xw_out || p.ssq_out;
-    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, prod ? 16 : 0), TB_ERR_UNSUPPORTED,
+    TB_REQUIRE(make_layout(p.k / 32, Log2<V>::value, J, L, prod ? 16 : 0, NW), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: w4a32 GEMV supports K <= " + std::to_string(kMaxWaves * 64 * 32));
     Epi e{};
     e.b0 = p.b0; e.b1 = p.b1; e.res = p.res; e.y = p.y; e.n = p.n; e.m = p.m; e.rope = p.rope;
@@ -356,8 +358,8 @@ int launch(const W4Params &p, hipStream_t st) {
         TB_REQUIRE(p.x && ((uintptr_t)p.x & 15u) == 0 && p.ssq_in == nullptr, TB_ERR_UNSUPPORTED,
                    "TB_UNSUPPORTED: w4 GEMV without x records needs a 16-byte aligned x "
                    "and no fused RMSNorm input");
-    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI, V2, XR>), dim3(grid), dim3(L.nwaves * 64), 0,
-                       st, p, L, e);
+    hipLaunchKernelGGL((k_w4_gemv<M, J, DUAL, EPI, V2, XR, NW>), dim3(grid), dim3(L.nwaves * 64),
+                       0, st, p, L, e);
     TB_LAUNCHED();
     return TB_OK;
 }
@@ -380,6 +382,15 @@ int dispatch_m(const W4Params &p, hipStream_t st) {
     // Llama-3-8B down projection 10.0 -> 9.0 us at 8).
     if (p.m <= 1) {
         const bool prod = p.rec_out || p.xw_out || p.ssq_out;
+        // A single matrix whose epilogue writes records needs 16-row blocks;
+        // with 3 or more K-slice waves, row groups of 8 or 4 rows in
+        // 1024-thread blocks give it two to four times the waves of 16 rows
+        // in one group (Llama-3-8B down: 7 K-slices x 2 groups of 8 rows).
+        const int nks = (p.k / 32 + 63) / 64;
+        if (!DUAL && !V2 && prod && !p.rows_j && p.xq && EPI != EPI_ROPE && nks >= 3) {
+            if (nks > 4) return launch<1, 8, false, EPI, false, false, kMaxWavesWide>(p, st);
+            return launch<1, 4, false, EPI, false, false, kMaxWavesWide>(p, st);
+        }
         int j = p.rows_j;
         if (!j) {
             j = DUAL ? 8 : 16;
