@@ -50,21 +50,29 @@
 //     expand_nibbles unpacks a dword of nibbles.
 //
 // Work split.  The grid is (row chunks) x (K splits).  A block copies the
-// records of its K range to LDS once, then each of its waves streams the
-// weights of R 16-row blocks over that range: per batch a lane loads one
-// 16-byte chunk per row block, lane (i, q) group g0 + q of row i, and a 4x4
-// transpose across the lane quarters (v_permlane32_swap, v_permlane16_swap)
-// leaves dword q of group g0 + t in register t, the MFMA B operand layout.
-// Weights and scales stream DEPTH - 1 batches ahead through a register ring;
-// since the records come from LDS, each wait is for the oldest weights only
-// (vector loads retire in order).  The per-split partial sums go to a scratch
-// buffer and a small reduce kernel sums them in split order (deterministic)
-// and runs the epilogue: bias (+ residual), or for a SwiGLU pair, whose gate
-// and up rows are stacked as one 2n-row matrix, h = silu(g) * u plus the
-// records of h for the next projection.
+// records of its K range to LDS once (direct global-to-LDS loads, issued with
+// the first weight loads so the block pays one memory latency), then each of
+// its waves streams the weights of R 16-row blocks over that range: per batch
+// a lane loads one 16-byte chunk per row block, lane (i, q) group g0 + q of
+// row i, and a 4x4 transpose across the lane quarters (v_permlane32_swap,
+// v_permlane16_swap) leaves dword q of group g0 + t in register t, the MFMA B
+// operand layout.  Group scales come per quad of 4 batches, lane (i, q) the 4
+// scales of batch q of row i in one 16-byte load, and reach the lanes of the
+// row by ds_bpermute.  Weights and scales stream a few quads ahead through a
+// register ring; since the records come from LDS, each wait is for the oldest
+// weights only (vector loads retire in order).  When the records of the whole
+// K fit in LDS (M <= 8, K <= 4224) and the matrix has enough 16-row blocks,
+// one block of seven waves per CU covers the whole K with no split.
+// Otherwise the per-split partial sums go to a scratch buffer and a small
+// reduce kernel sums them in split order (deterministic).  The reduce (or,
+// with no split, the same kernel over one split) runs the epilogue: bias
+// (+ residual), or for a SwiGLU pair, whose gate and up rows are stacked as
+// one 2n-row matrix, h = silu(g) * u plus the records of h for the next
+// projection.
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
@@ -81,8 +89,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 1024;          // one A tile: 64 lanes x 8 f16
 constexpr int kBatch = 128;          // K per batch: one 16-byte chunk per lane
-constexpr int kTargetWaves = 2048;   // 8 per CU
-constexpr int kDepthMax = 4;         // weight batches held in registers
 constexpr int kRecTail = 16;         // 16 signed exponent bytes
 constexpr int kLdsBudget = 64 << 10; // records per block (two blocks per CU)
 
@@ -197,8 +203,9 @@ __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict_
 // weights (rows past n come from w1 / s1 for a SwiGLU pair) over the K range
 // [ks, ks + ksl) of split blockIdx.y.  The records of that range are copied to
 // LDS first (one pass, one barrier); the loop then waits only for weights.
-template <int T, int R, int NW, int DEPTH>
-__global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__restrict__ part,
+template <int T, int R, int NW, int DQ, bool SV>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void k_w4_limb(LimbParams p, float *__restrict__ part,
                                                    int ksl, int ntot) {
     constexpr int BS = rec_stride(T);
     constexpr int ROWS = 16 * R * NW;
@@ -210,6 +217,7 @@ __global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__rest
     const int ks = split * ksl;
     const int ke = min(p.k, ks + ksl);
     const int b0 = ks / kBatch, nb = (ke - ks) / kBatch;
+    const int klast = ke - kBatch;
     const uint8_t *flags = p.rec + (size_t)(p.k / kBatch) * BS;
 
     // the weight and scale rows of block row rl (rows past the stacked
@@ -221,19 +229,14 @@ __global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__rest
         w = (second ? p.w1 : p.w0) + (size_t)rr * (size_t)(p.k >> 1);
         sc = (second ? p.s1 : p.s0) + (size_t)rr * (size_t)p.scols;
     };
-    {   // records of this K range -> LDS: every load in flight at once, then
-        // the stores (a load-store loop would pay one memory latency per pass)
-        constexpr int kChunks = (kLdsBudget / 16 + NW * 64 - 1) / (NW * 64);
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(p.rec + (size_t)b0 * BS);
-        u32x4 *dst = reinterpret_cast<u32x4 *>(lrec);
-        const int n16 = nb * BS / 16;
-        u32x4 tmp[kChunks];
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c)
-            if (tid + c * NW * 64 < n16) tmp[c] = src[tid + c * NW * 64];
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c)
-            if (tid + c * NW * 64 < n16) dst[tid + c * NW * 64] = tmp[c];
+    {   // records of this K range -> LDS by direct loads (a wave instruction
+        // moves one KiB: lane l's 16 bytes land at lrec + 1024 c + 16 l)
+        const uint8_t *src = p.rec + (size_t)b0 * BS;
+        const int bytes = nb * BS;   // a multiple of 16
+        for (int c = wave; c * 1024 < bytes; c += NW)
+            if (c * 1024 + lane * 16 < bytes)
+                __builtin_amdgcn_global_load_lds(src + c * 1024 + lane * 16, lrec + c * 1024, 16,
+                                                 0, 0);
     }
     // NaN / Inf flags of the range, once, one byte per lane (nb <= 64): the
     // common all-finite case needs no per-batch test.  (A loop of byte loads
@@ -253,16 +256,29 @@ __global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__rest
 #pragma unroll
     for (int rb = 0; rb < R; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Weights of one batch: lane (i, q) takes group g + q of its row and that
-    // group's scale (one dword per lane: the four lanes of a row would
-    // otherwise each fetch the same four scales).
-    auto load_w = [&](int k0, u32x4 (&wv)[R], float (&sv)[R]) {
+    // Weights of one batch: lane (i, q) takes the 16 bytes of group q of its
+    // row (cached, not non-temporal: each load takes half of a row's 128-byte
+    // line and the next batch takes the other half).
+    auto load_w = [&](int k0, u32x4 (&wv)[R]) {
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+            wv[rb] = *reinterpret_cast<const u32x4 *>(wr[rb] + (k0 >> 1) + 16 * q);
+    };
+    // Scales of a quad of 4 batches from k0: lane (i, q) takes the 4 group
+    // scales of batch q of its row -- one 16-byte load when SV (group 32, one
+    // 64-byte piece of a row per 4 lanes), else one load per group.  (A dword
+    // per lane per batch made every 128-byte scale line eight 16-byte
+    // requests; the streams of scales then cost almost as much as the weights.)
+    auto load_s = [&](int k0, f32x4 (&sv)[R]) {
+        const int kb = min(k0 + q * kBatch, klast);
 #pragma unroll
         for (int rb = 0; rb < R; ++rb) {
-            // cached, not non-temporal: each load takes half of a row's
-            // 128-byte line and the next batch takes the other half
-            wv[rb] = *reinterpret_cast<const u32x4 *>(wr[rb] + (k0 >> 1) + 16 * q);
-            sv[rb] = sr[rb][(k0 + 32 * q) >> p.gshift];
+            if (SV) {
+                sv[rb] = *reinterpret_cast<const f32x4 *>(sr[rb] + (kb >> 5));
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) sv[rb][t] = sr[rb][(kb + 32 * t) >> p.gshift];
+            }
         }
     };
 
@@ -336,41 +352,66 @@ __global__ __launch_bounds__(NW * 64) void k_w4_limb(LimbParams p, float *__rest
             for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(bs[r], pf[r], acc[rb][r]);
         }
     };
-    // One batch: transpose its weights, gather the row's four scales from the
-    // lanes that loaded them (ds_bpermute), then the f16 MFMA or, for a
-    // flagged batch, the f32 path.
-    auto step = [&](int k0, u32x4 (&wv)[R], const float (&sv)[R]) {
+    // Batch jj of a quad: transpose its weights, gather the row's four scales
+    // from lane (i, jj) (ds_bpermute), then the f16 MFMA or, for a flagged
+    // batch (only when CHECK), the f32 path.
+    auto step = [&](auto check, int k0, u32x4 (&wv)[R], const f32x4 (&sv)[R], int jj) {
         f32x4 st[R];
 #pragma unroll
         for (int rb = 0; rb < R; ++rb) {
             transpose4(wv[rb]);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) st[rb][t] = __shfl(sv[rb], i + 16 * t);
+            for (int t = 0; t < 4; ++t) st[rb][t] = __shfl(sv[rb][t], i + 16 * jj);
         }
-        if (any_bad && flags[k0 / kBatch])
+        if (decltype(check)::value && flags[k0 / kBatch])
             compute_f32(k0, wv, st);
         else
             compute(k0, wv, st);
     };
 
-    // Weights and scales DEPTH - 1 batches ahead in a register ring; the
-    // records come from LDS, so each wait is for the oldest weights only.
-    u32x4 wq[DEPTH][R];
-    float sq[DEPTH][R];
+    // Quads of 4 batches, DQ - 1 quads ahead in a register ring, issued with
+    // the record copy so the block pays one memory latency before its first
+    // batch; the records come from LDS, so each later wait is for the oldest
+    // weights only.  Loads past the range re-read its last batch: every pass
+    // of the main loop issues the same loads, which keeps the compiler's waits
+    // exact, and it runs whole quads only, so its batches are straight-line
+    // code the compiler can interleave (no per-batch branch).
+    const int nq = (nb + 3) / 4, nqf = nb / 4;
+    u32x4 wq[DQ][4][R];
+    f32x4 sq[DQ][R];
+    auto load_quad = [&](int qd, u32x4 (&wv)[4][R], f32x4 (&sv)[R]) {
+        const int kq = ks + 4 * min(qd, nq - 1) * kBatch;
 #pragma unroll
-    for (int j = 0; j < DEPTH - 1; ++j)
-        if (ks + j * kBatch < ke) load_w(ks + j * kBatch, wq[j], sq[j]);
-    __syncthreads();   // the records are in LDS
-    for (int k0 = ks; k0 < ke; k0 += DEPTH * kBatch) {
+        for (int j = 0; j < 4; ++j) load_w(min(kq + j * kBatch, klast), wv[j]);
+        load_s(kq, sv);
+    };
 #pragma unroll
-        for (int j = 0; j < DEPTH; ++j) {
-            const int kc = k0 + j * kBatch;
-            if (kc >= ke) break;
-            const int kn = kc + (DEPTH - 1) * kBatch;
-            if (kn < ke) load_w(kn, wq[(j + DEPTH - 1) % DEPTH], sq[(j + DEPTH - 1) % DEPTH]);
-            step(kc, wq[j], sq[j]);
+    for (int j = 0; j < DQ - 1; ++j) load_quad(j, wq[j], sq[j]);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's record copy (and weights) landed
+    __syncthreads();                 // every wave's copy landed
+    auto run = [&](auto check) {
+        int qd = 0;
+        for (; qd + DQ <= nqf; qd += DQ) {
+#pragma unroll
+            for (int j = 0; j < DQ; ++j) {
+                load_quad(qd + j + DQ - 1, wq[(j + DQ - 1) % DQ], sq[(j + DQ - 1) % DQ]);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    step(check, ks + (4 * (qd + j) + jj) * kBatch, wq[j][jj], sq[j], jj);
+            }
         }
-    }
+        // the last quads (the last may be partial): slot j holds quad qd + j
+        if (qd + DQ - 1 < nq) load_quad(qd + DQ - 1, wq[DQ - 1], sq[DQ - 1]);
+#pragma unroll
+        for (int j = 0; j < DQ; ++j)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int k0 = ks + (4 * (qd + j) + jj) * kBatch;
+                if (k0 < ke) step(check, k0, wq[j][jj], sq[j], jj);
+            }
+    };
+    if (any_bad) run(std::true_type{});
+    else run(std::false_type{});
 
     // Lane l's register r holds A-row 4 (l / 16) + r of weight row l % 16; for
     // T = 1 rows 8..15 are the second limbs of rows 0..7 (lanes l + 32).
@@ -494,18 +535,36 @@ __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restric
 constexpr int kTargetBlocks = 512;
 
 struct Plan {
-    int ksl, splits, r, chunks;
+    int ksl, splits, r, chunks, nw;
     size_t lds;
 };
 
-// Four waves per block, each over R 16-row blocks (R = 2 when the grid would
-// otherwise exceed about kTargetBlocks blocks); the K split is as long as the
-// block's records fit kLdsBudget.
+// Whole-K form: when the records of the whole K fit kLdsWhole and there are
+// enough row blocks, one block per CU (kWholeWaves waves, one 16-row block each)
+// runs the whole K with no split: every record byte is copied to LDS once per
+// CU and there are no split partials to add.
+constexpr int kWholeWaves = 7;
+constexpr int kLdsWhole = 132 << 10;
+
+// Otherwise four waves per block, each over R 16-row blocks (R = 2 when the
+// grid would otherwise exceed about kTargetBlocks blocks); the K split is as
+// long as the block's records fit kLdsBudget.
 Plan plan(int m, int n, int k, bool pair) {
     Plan pl;
     const int bs = rec_stride(tiles_of(m));
     const int batches = k / kBatch;
     const long ntot = pair ? 2L * n : n;
+    if (tiles_of(m) == 1 && (long)batches * bs <= kLdsWhole &&
+        ntot / 16 >= (long)kWholeWaves * kTargetBlocks * 3 / 8) {
+        pl.nw = kWholeWaves;
+        pl.r = 1;
+        pl.splits = 1;
+        pl.ksl = k;
+        pl.lds = (size_t)batches * bs;
+        pl.chunks = (int)((ntot + 16 * kWholeWaves - 1) / (16 * kWholeWaves));
+        return pl;
+    }
+    pl.nw = 4;
     int per = kLdsBudget / bs;
     if (per < 1) per = 1;
     if (per > batches) per = batches;
@@ -516,7 +575,7 @@ Plan plan(int m, int n, int k, bool pair) {
     pl.lds = (size_t)per * bs;
     const long want_rows = (ntot * pl.splits + kTargetBlocks - 1) / kTargetBlocks;
     pl.r = want_rows > 96 ? 2 : 1;
-    const int rows = 16 * pl.r * 4;
+    const int rows = 16 * pl.r * pl.nw;
     pl.chunks = (int)((ntot + rows - 1) / rows);
     return pl;
 }
@@ -567,18 +626,38 @@ int w4_limb(const LimbParams &p, float *part, hipStream_t st) {
     const bool t1 = tiles_of(p.m) == 1;
     const int ntot = pair ? 2 * p.n : p.n;
     const Plan pl = plan(p.m, p.n, p.k, pair);
-    const dim3 grid((unsigned)pl.chunks, (unsigned)pl.splits), block(256);
-#define TB_LIMB_LAUNCH(T_, R_, D_)                                                            \
-    hipLaunchKernelGGL((k_w4_limb<T_, R_, 4, D_>), grid, block, pl.lds, st, p, part, pl.ksl, \
-                       ntot)
-    if (pl.r == 2) {
-        if (t1) TB_LIMB_LAUNCH(1, 2, 4);
-        else TB_LIMB_LAUNCH(2, 2, 4);
+    // group-32 scales in 16-byte rows: one vector load per lane per quad
+    const bool sv = p.gshift == 5 && p.scols == (p.k >> 5) &&
+                    (reinterpret_cast<uintptr_t>(p.s0) & 15) == 0 &&
+                    (!pair || (reinterpret_cast<uintptr_t>(p.s1) & 15) == 0);
+#define TB_LIMB_GO(T_, R_, NW_, D_)                                                             \
+    do {                                                                                        \
+        const dim3 g_((unsigned)pl.chunks, (unsigned)pl.splits), b_(64 * NW_);                  \
+        if (sv)                                                                                 \
+            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, true>), g_, b_, pl.lds, st, p, part, \
+                               pl.ksl, ntot);                                                   \
+        else                                                                                    \
+            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, false>), g_, b_, pl.lds, st, p,      \
+                               part, pl.ksl, ntot);                                             \
+    } while (0)
+    if (pl.nw == kWholeWaves) {
+        // more than the default 64 KiB of dynamic LDS (set per call: the
+        // attribute belongs to the current device's code object)
+        TB_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, 4, true>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
+        TB_HIP(hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, 4, false>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
+        TB_LIMB_GO(1, 1, kWholeWaves, 4);
+    } else if (pl.r == 2) {
+        if (t1) TB_LIMB_GO(1, 2, 4, 2);
+        else TB_LIMB_GO(2, 2, 4, 2);
     } else {
-        if (t1) TB_LIMB_LAUNCH(1, 1, 6);
-        else TB_LIMB_LAUNCH(2, 1, 6);
+        if (t1) TB_LIMB_GO(1, 1, 4, 4);
+        else TB_LIMB_GO(2, 1, 4, 3);
     }
-#undef TB_LIMB_LAUNCH
+#undef TB_LIMB_GO
     TB_LAUNCHED();
     if (pair) {
         const dim3 rg((unsigned)(p.n / kBatch));
