@@ -39,8 +39,9 @@
 // Activation records (limb_prep, or the SwiGLU reduce for the next
 // projection), one per 128-element batch: for each of its 4 groups T f16 A
 // tiles of 64 lanes x 16 bytes, then 16 bytes, one per A-row, holding the
-// biased f32 exponent of 2^(24 - e).  After the records, one flag byte per
-// batch (1: take the f32 path).
+// biased f32 exponent of 2^(24 - e), or 0 in every byte for a batch that takes
+// the f32 path (a valid exponent byte is never 0, so the flag travels with the
+// record).
 //   * M <= 8 (T = 1): A-row i of the MFMA is limb (i >> 3) of row i & 7, so one
 //     MFMA covers both limbs in separate output rows; the two limb halves of the
 //     output are added at the end (lanes l and l + 32).
@@ -58,7 +59,7 @@
 // v_permlane16_swap) leaves dword q of group g0 + t in register t, the MFMA B
 // operand layout.  Group scales come per quad of 4 batches, lane (i, q) the 4
 // scales of batch q of row i in one 16-byte load, and reach the lanes of the
-// row by ds_bpermute.  Weights and scales stream a few quads ahead through a
+// row by ds_bpermute.  Weights and scales stream one quad ahead through a
 // register ring; since the records come from LDS, each wait is for the oldest
 // weights only (vector loads retire in order).  When the records of the whole
 // K fit in LDS (M <= 8, K <= 4224) and the matrix has enough 16-row blocks,
@@ -127,9 +128,9 @@ __device__ __forceinline__ void transpose4(u32x4 &v) {
 
 // The record of one 128-element batch, built by one wave.  Lane (i, q) holds
 // v[g][e] = element 32 g + 8 q + e of the batch for its row (row i & 7 when
-// T = 1, row i when T = 2; zeros beyond m).  flag: the batch's flag byte.
+// T = 1, row i when T = 2; zeros beyond m).
 template <int T>
-__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg, uint8_t *flag) {
+__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
     const int i = lane & 15, q = lane >> 4;
     float mx = 0.f;
     bool fin = true;
@@ -168,9 +169,9 @@ __device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg, uint8
             *reinterpret_cast<h8 *>(tg + kTile + lane * 16) = l2;
         }
     }
-    // biased f32 exponent of 2^(24 - e): e in [-85, 115] -> [36, 236]
-    if (q == 0) rg[4 * T * kTile + i] = (uint8_t)(151 - e);
-    if (lane == 0) *flag = bad ? 1 : 0;
+    // biased f32 exponent of 2^(24 - e): e in [-85, 115] -> [36, 236]; 0 flags
+    // the batch for the f32 path
+    if (q == 0) rg[4 * T * kTile + i] = bad ? (uint8_t)0 : (uint8_t)(151 - e);
 }
 
 template <int T>
@@ -195,8 +196,7 @@ __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict_
             for (int e = 0; e < 8; ++e) v[g][e] = 0.f;
         }
     }
-    build_batch<T>(v, lane, rec + (size_t)b * rec_stride(T),
-                   rec + (size_t)batches * rec_stride(T) + b);
+    build_batch<T>(v, lane, rec + (size_t)b * rec_stride(T));
 }
 
 // Partial sums of one block: rows [row0, row0 + 16 R NW) of the stacked
@@ -218,7 +218,6 @@ void k_w4_limb(LimbParams p, float *__restrict__ part,
     const int ke = min(p.k, ks + ksl);
     const int b0 = ks / kBatch, nb = (ke - ks) / kBatch;
     const int klast = ke - kBatch;
-    const uint8_t *flags = p.rec + (size_t)(p.k / kBatch) * BS;
 
     // the weight and scale rows of block row rl (rows past the stacked
     // [w0; w1] read row 0 and are never stored)
@@ -238,11 +237,6 @@ void k_w4_limb(LimbParams p, float *__restrict__ part,
                 __builtin_amdgcn_global_load_lds(src + c * 1024 + lane * 16, lrec + c * 1024, 16,
                                                  0, 0);
     }
-    // NaN / Inf flags of the range, once, one byte per lane (nb <= 64): the
-    // common all-finite case needs no per-batch test.  (A loop of byte loads
-    // here would pay one memory latency per batch.)
-    const bool any_bad = __any(lane < nb && flags[b0 + (lane < nb ? lane : 0)] != 0) != 0;
-
     const uint8_t *wr[R];
     const float *sr[R];
     int rows[R];
@@ -363,7 +357,7 @@ void k_w4_limb(LimbParams p, float *__restrict__ part,
 #pragma unroll
             for (int t = 0; t < 4; ++t) st[rb][t] = __shfl(sv[rb][t], i + 16 * jj);
         }
-        if (decltype(check)::value && flags[k0 / kBatch])
+        if (decltype(check)::value && lrec[(size_t)((k0 - ks) / kBatch) * BS + 4 * T * kTile] == 0)
             compute_f32(k0, wv, st);
         else
             compute(k0, wv, st);
@@ -387,8 +381,21 @@ void k_w4_limb(LimbParams p, float *__restrict__ part,
     };
 #pragma unroll
     for (int j = 0; j < DQ - 1; ++j) load_quad(j, wq[j], sq[j]);
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's record copy (and weights) landed
-    __syncthreads();                 // every wave's copy landed
+    // Wait for this wave's record copy only: vector loads retire in order, so
+    // the kAfter weight and scale loads issued after it may stay in flight.
+    // (The empty asm keeps the compiler from moving loads across the wait,
+    // which would make the count wrong.)
+    constexpr int kAfter = (DQ - 1) * (4 * R + (SV ? R : 4 * R));
+    static_assert(kAfter < 64, "vmcnt holds 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | ((kAfter >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+    __syncthreads();   // every wave's copy landed
+    // NaN / Inf flags of the range, once, from the records in LDS (a batch for
+    // the f32 path has exponent byte 0; nb <= 64): the common all-finite case
+    // needs no per-batch test.
+    const bool any_bad =
+        __any(lane < nb && lrec[(size_t)(lane < nb ? lane : 0) * BS + 4 * T * kTile] == 0) != 0;
     auto run = [&](auto check) {
         int qd = 0;
         for (; qd + DQ <= nqf; qd += DQ) {
@@ -528,8 +535,7 @@ __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restric
     for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[g][e] = tr < m ? hs[tr][32 * g + 8 * q + e] : 0.f;
-    build_batch<T>(v, lane, rec_out + (size_t)bt * rec_stride(T),
-                   rec_out + (size_t)(n / kBatch) * rec_stride(T) + bt);
+    build_batch<T>(v, lane, rec_out + (size_t)bt * rec_stride(T));
 }
 
 constexpr int kTargetBlocks = 512;
@@ -544,6 +550,10 @@ struct Plan {
 // runs the whole K with no split: every record byte is copied to LDS once per
 // CU and there are no split partials to add.
 constexpr int kWholeWaves = 7;
+// Ring depth in quads: one quad in flight while the previous one computes.
+// (Two or three quads ahead measured slower in every form, 17.7 -> 19.1 ->
+// 20.4 us for the Llama-3-8B gate/up pair at M = 8.)
+constexpr int kQuads = 2;
 constexpr int kLdsWhole = 132 << 10;
 
 // Otherwise four waves per block, each over R 16-row blocks (R = 2 when the
@@ -590,8 +600,7 @@ __global__ __launch_bounds__(256) void k_limb_prep(const float *__restrict__ x,
 }  // namespace
 
 size_t limb_records_bytes(int m, int k) {
-    const size_t b = (size_t)(k / kBatch);
-    return b * (size_t)rec_stride(tiles_of(m)) + ((b + 15) & ~(size_t)15);
+    return (size_t)(k / kBatch) * (size_t)rec_stride(tiles_of(m));
 }
 
 size_t limb_partials_bytes(int m, int n, int k, bool pair) {
@@ -644,18 +653,18 @@ int w4_limb(const LimbParams &p, float *part, hipStream_t st) {
         // more than the default 64 KiB of dynamic LDS (set per call: the
         // attribute belongs to the current device's code object)
         TB_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, 4, true>),
+            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, kQuads, true>),
             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
         TB_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, 4, false>),
+            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, kQuads, false>),
             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
-        TB_LIMB_GO(1, 1, kWholeWaves, 4);
+        TB_LIMB_GO(1, 1, kWholeWaves, kQuads);
     } else if (pl.r == 2) {
-        if (t1) TB_LIMB_GO(1, 2, 4, 2);
-        else TB_LIMB_GO(2, 2, 4, 2);
+        if (t1) TB_LIMB_GO(1, 2, 4, kQuads);
+        else TB_LIMB_GO(2, 2, 4, kQuads);
     } else {
-        if (t1) TB_LIMB_GO(1, 1, 4, 4);
-        else TB_LIMB_GO(2, 1, 4, 3);
+        if (t1) TB_LIMB_GO(1, 1, 4, kQuads);
+        else TB_LIMB_GO(2, 1, 4, kQuads);
     }
 #undef TB_LIMB_GO
     TB_LAUNCHED();
