@@ -153,3 +153,39 @@ def test_limb_deterministic(cuda):
     y0 = tb.w4a32_grouped_linear(x, w, s, None, 32).cpu().numpy()
     y1 = tb.w4a32_grouped_linear(x, w, s, None, 32).cpu().numpy()
     np.testing.assert_array_equal(y0, y1)
+
+
+def test_limb_whole_k_pair_partial_quad_and_nan(cuda):
+    """The whole-K plan (records of all of K in LDS, one block per CU, no split)
+    on a K of 31 batches (the last quad of batches is partial), with a NaN in
+    one activation row: that token's outputs are NaN, the others match."""
+    print("case limb whole-K MLP m=6 k=3968 inter=14336 + NaN row", flush=True)
+    g = synth.rng(78)
+    m, k, inter, gs = 6, 3968, 14336, 32
+    x = synth.activations(g, m, k)
+    gw, gsc = synth.int4_weight(g, inter, k, gs)
+    uw, usc = synth.int4_weight(g, inter, k, gs)
+    dw, dsc = synth.int4_weight(g, k, inter, gs)
+    x[1, 2000] = np.nan
+    ref = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, None, None, None, group_size=gs)
+    out = tb.fused_swiglu_mlp_w4a32(T(x, cuda), T(gw, cuda), T(gsc, cuda), None,
+                                    T(uw, cuda), T(usc, cuda), None, T(dw, cuda),
+                                    T(dsc, cuda), None, group_size=gs)
+    y = out.cpu().numpy()
+    assert np.isnan(ref[1]).all() and np.isnan(y[1]).all()
+    keep = [0, 2, 3, 4, 5]
+    assert np.isfinite(y[keep]).all()
+    assert rel_rows(y[keep], ref[keep]) < TOL
+
+
+def test_limb_whole_k_single_projection(cuda):
+    """A single projection with enough 16-row blocks for the whole-K plan."""
+    print("case limb whole-K linear m=5 n=24576 k=4096", flush=True)
+    g = synth.rng(79)
+    m, n, k = 5, 24576, 4096
+    w, s = synth.int4_weight(g, n, k, 32)
+    b = g.normal(0, 0.1, n).astype(np.float32)
+    x = synth.activations(g, m, k)
+    ref = O.gemm_w4(x, w, s, b, group_size=32)
+    y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), T(b, cuda), 32)
+    assert rel_rows(y.cpu().numpy(), ref) < TOL
