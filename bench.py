@@ -157,6 +157,46 @@ def graph_time(torch, fn, reps, warmup, inner=1, spread=False):
 
 INNER = 10   # rotations of the weight copies per captured graph (MLP and GEMV timing)
 
+# Grid shapes the read probe tries: (blocks of 256 threads, 16-byte loads in
+# flight per thread).
+PROBE_SHAPES = [(512, 4), (768, 4), (1024, 8), (1536, 4), (2048, 8)]
+
+
+def read_ceiling(torch, dev, sizes, copies, reps, inner):
+    """The fastest plain read (tb_read_probe: non-temporal 16-byte loads, no
+    compute) of each byte count in `sizes`, over `copies` cold buffers rotated
+    as the GEMV timing rotates its weight copies: what a read of the same bytes
+    reaches on this GPU, to set each GEMV's bandwidth beside the 8 TB/s
+    peak."""
+    from torchburn_amd import _lib
+    import ctypes
+    big = max(sizes.values())
+    buf = torch.empty(copies * big, dtype=torch.uint8, device=dev)
+    buf.fill_(3)
+    out = torch.empty(max(b for b, _ in PROBE_SHAPES) * 256, dtype=torch.int32, device=dev)
+    S = lambda: torch.cuda.current_stream(dev).cuda_stream
+    res = {}
+    for name, nbytes in sizes.items():
+        best = None
+        for blocks, loads in PROBE_SHAPES:
+            got = ctypes.c_int64(0)
+
+            def reads():
+                for c in range(copies):
+                    _lib.call("tb_read_probe", buf.data_ptr() + c * big, nbytes, blocks, loads,
+                              out.data_ptr(), ctypes.addressof(got), S())
+
+            ms, _ = graph_time(torch, reads, reps, 1, inner)
+            us = ms * 1e3 / copies
+            gbs = got.value / (us * 1e-6) / 1e9
+            if best is None or gbs > best["gbs"]:
+                best = {"bytes": nbytes, "bytes_read": got.value, "us": round(us, 3),
+                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "blocks": blocks, "loads_per_thread": loads}
+        res[name] = best
+    del buf
+    return res
+
 
 def mlp_section(torch, args, dev):
     from torchburn_amd import _lib
@@ -223,6 +263,9 @@ def mlp_section(torch, args, dev):
     dn_us = dn_ms * 1e3 / len(sets)
     gu_bytes = 2 * (I * K // 2 + 4 * I * (K // GS)) + 4 * M * K + 4 * M * I
     dn_bytes = K * I // 2 + 4 * K * (I // GS) + 4 * M * I + 8 * M * K
+    ceiling = read_ceiling(torch, dev, {"gate_up": 2 * (I * K // 2 + 4 * I * (K // GS)),
+                                        "down": K * I // 2 + 4 * K * (I // GS)},
+                           len(sets), reps, inner)
 
     # Parity guard on the measured data against the CPU oracle (set 0).
     from oracle import oracle as O
@@ -254,6 +297,7 @@ def mlp_section(torch, args, dev):
                "host": info}
     del sets
     return dict(ms=ms, step_bytes=step_bytes, gu_us=gu_us, gu_bytes=gu_bytes, dn_us=dn_us,
+                ceiling=ceiling,
                 dn_bytes=dn_bytes, max_rel=max_rel, cpu=cpu, steps=timed_steps,
                 spread={"replays": len(per_step),
                         "median_ms_per_step": round(per_step[len(per_step) // 2], 5),
@@ -582,7 +626,12 @@ def main():
                                        "profiles/k_w4_gemv_swiglu_llama8b_mlp_m1_pmc.md",
                      "avg_us": round(r["gu_us"], 3), "bytes_per_launch": r["gu_bytes"],
                      "down_kernel_avg_us": round(r["dn_us"], 3),
-                     "down_kernel_gbs": round(r["dn_bytes"] / (r["dn_us"] * 1e-6) / 1e9, 1)},
+                     "down_kernel_gbs": round(r["dn_bytes"] / (r["dn_us"] * 1e-6) / 1e9, 1),
+                     # fastest plain read of each kernel's weight + scale bytes
+                     # (tb_read_probe over the same rotation of cold copies)
+                     "read_ceiling": r["ceiling"],
+                     "frac_of_read_ceiling": round(
+                         gu_gbs / r["ceiling"]["gate_up"]["gbs"], 4)},
         "decode": decode,
         "batched_mfma": batched,
         "mlp_batches": mlp_batches,

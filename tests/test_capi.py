@@ -60,6 +60,12 @@ def test_argument_errors_before_any_gpu_call():
     rc = L.tb_fused_swiglu_mlp_w8a32(p, p, p, 5, None, p, p, 8, None, p, p, 8, None, None, p,
                                      1, 32, 8, 8, None)
     assert rc == _lib.TB_ERR_UNSUPPORTED and b"1 or N" in L.tb_last_error()
+    # the read probe: loads per thread 4, 8 or 16; a 16-byte aligned buffer
+    got = C.c_int64(0)
+    rc = L.tb_read_probe(p, 1 << 20, 8, 5, p, C.addressof(got), None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED and b"loads" in L.tb_last_error()
+    rc = L.tb_read_probe(p + 4, 1 << 20, 8, 4, p, C.addressof(got), None)
+    assert rc == _lib.TB_ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("field,value,msg", [

@@ -59,6 +59,7 @@ _SIGS = {
     "tb_fused_swiglu_mlp_w8a32": [_p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p,
                                   _p] + [_i64] * 4 + [_p],
     "tb_xquant": [_p, _p, _i64, _i64, _p],
+    "tb_read_probe": [_p, _i64, _i64, _i64, _p, _p, _p],
     "tb_w4a32_gemv_xq": [_p] * 7 + [_i64] * 4 + [_p],
     "tb_swiglu_w4a32_xq": [_p] * 9 + [_i64] * 4 + [_p],
     "tb_fused_attention_step_w4a32": [_p] * 12 + [_i64] * 7 + [_p],
