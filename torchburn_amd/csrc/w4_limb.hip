@@ -90,7 +90,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 1024;          // one A tile: 64 lanes x 8 f16
 constexpr int kBatch = 128;          // K per batch: one 16-byte chunk per lane
-constexpr int kRecTail = 16;         // 16 signed exponent bytes
+constexpr int kRecTail = 16;         // one exponent byte per A-row (0: the f32 path)
 constexpr int kLdsBudget = 64 << 10; // records per block (two blocks per CU)
 
 __host__ __device__ constexpr int tiles_of(int m) { return m <= 8 ? 1 : 2; }
@@ -205,8 +205,7 @@ __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict_
 // LDS first (one pass, one barrier); the loop then waits only for weights.
 template <int T, int R, int NW, int DQ, bool SV>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void k_w4_limb(LimbParams p, float *__restrict__ part,
-                                                   int ksl, int ntot) {
+void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
     constexpr int BS = rec_stride(T);
     constexpr int ROWS = 16 * R * NW;
     extern __shared__ __align__(16) uint8_t lrec[];   // the (ksl / 128) batch records
