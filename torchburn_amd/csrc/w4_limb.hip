@@ -378,12 +378,15 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
         for (int j = 0; j < 4; ++j) load_w(min(kq + j * kBatch, klast), wv[j]);
         load_s(kq, sv);
     };
+    // The record copy above must be issued before the kAfter weight and scale
+    // loads the wait below counts: the empty asm keeps the compiler from
+    // moving any of them across (none of them can be merged: their addresses
+    // are 64 bytes apart or runtime-strided).
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int j = 0; j < DQ - 1; ++j) load_quad(j, wq[j], sq[j]);
     // Wait for this wave's record copy only: vector loads retire in order, so
     // the kAfter weight and scale loads issued after it may stay in flight.
-    // (The empty asm keeps the compiler from moving loads across the wait,
-    // which would make the count wrong.)
     constexpr int kAfter = (DQ - 1) * (4 * R + (SV ? R : 4 * R));
     static_assert(kAfter < 64, "vmcnt holds 6 bits");
     asm volatile("" ::: "memory");
