@@ -14,12 +14,12 @@
 //   * weights: a nibble q placed in the low bits of an f16 is the subnormal
 //     q * 2^-24 (nibbles at bits 4-7 of a byte give 16 q * 2^-24), so a dword
 //     of 8 nibbles becomes 8 exact f16 operands with 4 ANDs and one shift;
-//   * activations: each batch of 128 elements of a row (4 groups) is scaled by
-//     a power of two 2^e (its largest magnitude lands in [2^14, 2^15)) and
-//     split into two fixed-point limbs on that grid: h1 a multiple of 16
-//     (|h1 / 16| <= 2048) and h2 a multiple of 2^-7 (|h2 2^7| <= 1024), both
-//     exact in f16, with |x 2^e - h1 - h2| <= 2^-8, i.e. 2^-23 of the batch's
-//     largest term;
+//   * activations: each half batch of 64 elements of a row (2 groups) is
+//     scaled by a power of two 2^e (its largest magnitude lands in
+//     [2^14, 2^15)) and split into two fixed-point limbs on that grid: h1 a
+//     multiple of 16 (|h1 / 16| <= 2048) and h2 a multiple of 2^-7
+//     (|h2 2^7| <= 1024), both exact in f16, with |x 2^e - h1 - h2| <= 2^-8,
+//     i.e. 2^-23 of the half batch's largest term;
 //   * the -8 of every weight is one more MFMA of the limbs against a constant
 //     B of -8 * 2^-24, shared by all weight rows, whose result is the C
 //     operand of the weight MFMA.  Each limb has its own accumulation, so every
@@ -28,20 +28,21 @@
 //     its internal additions (they are not IEEE round-to-nearest, which a
 //     float split of x would expose);
 //   * per 32-element group the limb results are scaled by the weight row's
-//     group scale and accumulated in f32; per batch the sum is scaled by
+//     group scale and accumulated in f32; per half batch the sum is scaled by
 //     2^(24 - e) into the running total.
-// The error of a batch's contribution is the limb quantization, ~2^-23 of its
-// largest term, the order of the f32 reference's own rounding.  A batch
-// holding NaN / Inf, or a largest magnitude outside [2^-100, 2^100], is
-// flagged and runs an f32 MFMA path on the raw activations, so non-finite
-// values propagate as in the reference's unpack-and-fma.
+// The error of a half batch's contribution is the limb quantization, ~2^-23
+// of its largest term, the order of the f32 reference's own rounding.  A half
+// batch holding NaN / Inf, or a largest magnitude outside [2^-100, 2^100], is
+// flagged, and its batch runs an f32 MFMA path on the raw activations, so
+// non-finite values propagate as in the reference's unpack-and-fma.
 //
-// Activation records (limb_prep, or the SwiGLU reduce for the next
+// Activation records (limb_prep, or the SwiGLU epilogue for the next
 // projection), one per 128-element batch: for each of its 4 groups T f16 A
-// tiles of 64 lanes x 16 bytes, then 16 bytes, one per A-row, holding the
-// biased f32 exponent of 2^(24 - e), or 0 in every byte for a batch that takes
-// the f32 path (a valid exponent byte is never 0, so the flag travels with the
-// record).
+// tiles of 64 lanes x 16 bytes, then 32 bytes, byte 2 a + h for A-row a and
+// half h (groups 2 h, 2 h + 1), holding the biased f32 exponent of
+// 2^(24 - e), or 0 for a half that takes the f32 path (a valid exponent byte
+// is never 0, so the flag travels with the record).  The two halves of a
+// record may be written by different blocks.
 //   * M <= 8 (T = 1): A-row i of the MFMA is limb (i >> 3) of row i & 7, so one
 //     MFMA covers both limbs in separate output rows; the two limb halves of the
 //     output are added at the end (lanes l and l + 32).
@@ -90,8 +91,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 1024;          // one A tile: 64 lanes x 8 f16
 constexpr int kBatch = 128;          // K per batch: one 16-byte chunk per lane
-constexpr int kRecTail = 16;         // one exponent byte per A-row (0: the f32 path)
+constexpr int kRecTail = 32;         // an exponent byte per A-row and half (0: the f32 path)
 constexpr int kLdsBudget = 64 << 10; // records per block (two blocks per CU)
+constexpr int kPairWaves = 8;        // the whole-K SwiGLU pair form
+constexpr int kPairCols = 64;        // its columns of h per block: half a record batch
 
 __host__ __device__ constexpr int tiles_of(int m) { return m <= 8 ? 1 : 2; }
 // bytes of one batch record (4 groups)
@@ -126,42 +129,73 @@ __device__ __forceinline__ void transpose4(u32x4 &v) {
     v.x = c[0]; v.y = c[1]; v.z = d[0]; v.w = d[1];
 }
 
-// The record of one 128-element batch, built by one wave.  Lane (i, q) holds
-// v[g][e] = element 32 g + 8 q + e of the batch for its row (row i & 7 when
-// T = 1, row i when T = 2; zeros beyond m).
-template <int T>
-__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
-    const int i = lane & 15, q = lane >> 4;
-    float mx = 0.f;
-    bool fin = true;
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            fin = fin && __builtin_isfinite(v[g][e]);
-            mx = fmaxf(mx, fabsf(v[g][e]));
-        }
+// The exponent of one half batch from each lane's largest magnitude mx and
+// finiteness fin over its values (the whole wave holds the half): e places
+// the largest magnitude in [2^14, 2^15); byte is the record's exponent byte,
+// the biased f32 exponent of 2^(24 - e) (e in [-85, 115] -> [36, 236]), or 0
+// when the half holds NaN / Inf or a magnitude outside [2^-100, 2^100].
+struct HalfExp {
+    int e;
+    bool ok;   // this lane's values take the limbs
+    uint8_t byte;
+};
+__device__ __forceinline__ HalfExp half_exp(float mx, bool fin) {
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     int E = 0;
     (void)frexpf(mx, &E);   // mx = f 2^E, f in [0.5, 1)
     const bool out_of_range = mx > 0.f && (E > 100 || E < -100);
     const bool bad = __any((!fin || out_of_range) ? 1 : 0) != 0;
-    const int e = (mx > 0.f && !out_of_range) ? 15 - E : 0;
+    HalfExp r;
+    r.e = (mx > 0.f && !out_of_range) ? 15 - E : 0;
+    r.ok = fin && !out_of_range;
+    r.byte = bad ? (uint8_t)0 : (uint8_t)(151 - r.e);
+    return r;
+}
+
+// The two limbs of x in slot j of a lane's 8 (odd slots pairs hold the
+// pre-divided odd elements).
+__device__ __forceinline__ void limbs_of(float x, const HalfExp &he, int j, _Float16 &l1,
+                                         _Float16 &l2) {
+    const bool odd = ((j >> 1) & 1) != 0;
+    const float xs = he.ok ? ldexpf(x, he.e) : 0.f;
+    const float j1 = rintf(xs * 0.0625f);               // h1 = 16 j1
+    const float j2 = rintf((xs - 16.0f * j1) * 128.0f);  // h2 = 2^-7 j2
+    l1 = (_Float16)(odd ? j1 : 16.0f * j1);
+    l2 = (_Float16)ldexpf(j2, odd ? -11 : -7);
+}
+
+// Element of the group held in slot j (the order expand_nibbles unpacks).
+__host__ __device__ constexpr int slot_elem(int j) { return (j >> 1) | ((j & 1) << 2); }
+
+// Half h of the record of one 128-element batch (groups 2 h, 2 h + 1), built
+// by one wave.  Lane (i, q) holds v[g][e] = element 32 (2 h + g) + 8 q + e of
+// the batch for its row (row i & 7 when T = 1, row i when T = 2; zeros beyond
+// m).
+template <int T>
+__device__ void build_half(const float (&v)[2][8], int lane, uint8_t *rg, int h) {
+    const int i = lane & 15, q = lane >> 4;
+    float mx = 0.f;
+    bool fin = true;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            fin = fin && __builtin_isfinite(v[g][e]);
+            mx = fmaxf(mx, fabsf(v[g][e]));
+        }
+    const HalfExp he = half_exp(mx, fin);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
         h8 l1, l2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int el = (j >> 1) | ((j & 1) << 2);
-            const bool odd = ((j >> 1) & 1) != 0;
-            const float xs = (fin && !out_of_range) ? ldexpf(v[g][el], e) : 0.f;
-            const float j1 = rintf(xs * 0.0625f);               // h1 = 16 j1
-            const float j2 = rintf((xs - 16.0f * j1) * 128.0f);  // h2 = 2^-7 j2
-            l1[j] = (_Float16)(odd ? j1 : 16.0f * j1);
-            l2[j] = (_Float16)ldexpf(j2, odd ? -11 : -7);
+            _Float16 a, b;
+            limbs_of(v[g][slot_elem(j)], he, j, a, b);
+            l1[j] = a;
+            l2[j] = b;
         }
-        uint8_t *tg = rg + (size_t)g * T * kTile;
+        uint8_t *tg = rg + (size_t)(2 * h + g) * T * kTile;
         if (T == 1) {
             *reinterpret_cast<h8 *>(tg + lane * 16) = i < 8 ? l1 : l2;
         } else {
@@ -169,9 +203,21 @@ __device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
             *reinterpret_cast<h8 *>(tg + kTile + lane * 16) = l2;
         }
     }
-    // biased f32 exponent of 2^(24 - e): e in [-85, 115] -> [36, 236]; 0 flags
-    // the batch for the f32 path
-    if (q == 0) rg[4 * T * kTile + i] = bad ? (uint8_t)0 : (uint8_t)(151 - e);
+    if (q == 0) rg[4 * T * kTile + 2 * i + h] = he.byte;
+}
+
+// A batch whose record flags either half (exponent byte 0 for every A-row of
+// a flagged half) runs the f32 path.
+__device__ __forceinline__ bool flagged(const uint8_t *rg_tail) {
+    const uint32_t v = *reinterpret_cast<const uint16_t *>(rg_tail);
+    return (v & 0xFFu) == 0 || (v >> 8) == 0;
+}
+
+// The whole record of a batch: v[g] holds group g (lanes as in build_half).
+template <int T>
+__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
+    build_half<T>(*reinterpret_cast<const float(*)[2][8]>(&v[0]), lane, rg, 0);
+    build_half<T>(*reinterpret_cast<const float(*)[2][8]>(&v[2]), lane, rg, 1);
 }
 
 template <int T>
@@ -203,9 +249,14 @@ __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict_
 // weights (rows past n come from w1 / s1 for a SwiGLU pair) over the K range
 // [ks, ks + ksl) of split blockIdx.y.  The records of that range are copied to
 // LDS first (one pass, one barrier); the loop then waits only for weights.
-template <int T, int R, int NW, int DQ, bool SV>
+// PE (a SwiGLU pair over the whole K, T = R = 1, NW = 8): block b takes
+// columns [64 b, 64 b + 64) of h, wave w the gate (w even) or up (w odd) rows
+// of its 16 columns 64 b + 16 (w / 2) ..; the block then writes h and half
+// b % 2 of the record of h's batch b / 2 itself (no partials, no reduce).
+template <int T, int R, int NW, int DQ, bool SV, bool PE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
+    static_assert(!PE || (T == 1 && R == 1 && NW == 8), "the pair epilogue form");
     constexpr int BS = rec_stride(T);
     constexpr int ROWS = 16 * R * NW;
     extern __shared__ __align__(16) uint8_t lrec[];   // the (ksl / 128) batch records
@@ -222,8 +273,12 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
     // [w0; w1] read row 0 and are never stored)
     auto row_ptrs = [&](int rl, const uint8_t *&w, const float *&sc) {
         const int row = blockIdx.x * ROWS + rl;
-        const bool second = row >= p.n && row < ntot;
-        const int rr = row < ntot ? (second ? row - p.n : row) : 0;
+        bool second = row >= p.n && row < ntot;
+        int rr = row < ntot ? (second ? row - p.n : row) : 0;
+        if (PE) {   // rl = 16 wave + i
+            second = (rl >> 4) & 1;
+            rr = 64 * blockIdx.x + 16 * (rl >> 5) + (rl & 15);
+        }
         w = (second ? p.w1 : p.w0) + (size_t)rr * (size_t)(p.k >> 1);
         sc = (second ? p.s1 : p.s0) + (size_t)rr * (size_t)p.scols;
     };
@@ -313,7 +368,8 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
 #pragma unroll
             for (int u = 0; u < T; ++u)
                 A[t][u] = *reinterpret_cast<const h8 *>(rg + (t * T + u) * kTile + lane * 16);
-        const uint32_t pw = *reinterpret_cast<const uint32_t *>(rg + 4 * T * kTile + 4 * q);
+        // exponent bytes of A-rows 4 q .. 4 q + 3, both halves
+        const uint2 pw = *reinterpret_cast<const uint2 *>(rg + 4 * T * kTile + 8 * q);
         f32x4 off[4][T];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -321,10 +377,14 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
             for (int u = 0; u < T; ++u)
                 off[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     A[t][u], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        float pf[4];   // 2^(24 - e) of the lane's four A-rows
+        float pf[2][4];   // 2^(24 - e) of the lane's four A-rows, per half
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            pf[r] = __builtin_bit_cast(float, __builtin_amdgcn_ubfe(pw, 8 * r, 8) << 23);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pf[h][r] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_ubfe(r < 2 ? pw.x : pw.y, 16 * (r & 1) + 8 * h, 8)
+                               << 23);
 #pragma unroll
         for (int rb = 0; rb < R; ++rb) {
             f32x4 D[4];
@@ -336,13 +396,14 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
                     D[t] += __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][T - 1], B, off[t][T - 1],
                                                                    0, 0, 0);
             }
-            f32x4 bs = D[0] * st[rb][0];
 #pragma unroll
-            for (int t = 1; t < 4; ++t)
+            for (int h = 0; h < 2; ++h) {
+                f32x4 bs = D[2 * h] * st[rb][2 * h];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[t][r], st[rb][t], bs[r]);
+                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[2 * h + 1][r], st[rb][2 * h + 1], bs[r]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(bs[r], pf[r], acc[rb][r]);
+                for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(bs[r], pf[h][r], acc[rb][r]);
+            }
         }
     };
     // Batch jj of a quad: transpose its weights, gather the row's four scales
@@ -356,7 +417,7 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) st[rb][t] = __shfl(sv[rb][t], i + 16 * jj);
         }
-        if (decltype(check)::value && lrec[(size_t)((k0 - ks) / kBatch) * BS + 4 * T * kTile] == 0)
+        if (decltype(check)::value && flagged(lrec + (size_t)((k0 - ks) / kBatch) * BS + 4 * T * kTile))
             compute_f32(k0, wv, st);
         else
             compute(k0, wv, st);
@@ -397,7 +458,7 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
     // the f32 path has exponent byte 0; nb <= 64): the common all-finite case
     // needs no per-batch test.
     const bool any_bad =
-        __any(lane < nb && lrec[(size_t)(lane < nb ? lane : 0) * BS + 4 * T * kTile] == 0) != 0;
+        __any(lane < nb && flagged(lrec + (size_t)(lane < nb ? lane : 0) * BS + 4 * T * kTile)) != 0;
     auto run = [&](auto check) {
         int qd = 0;
         for (; qd + DQ <= nqf; qd += DQ) {
@@ -424,6 +485,64 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
 
     // Lane l's register r holds A-row 4 (l / 16) + r of weight row l % 16; for
     // T = 1 rows 8..15 are the second limbs of rows 0..7 (lanes l + 32).
+    if constexpr (PE) {
+        // gate and up values to LDS past the records ([8 tokens][64 columns]
+        // each, then h in rows padded to 65), one h per thread, then the
+        // record's half by four waves, one group and four slots each
+        float *gb = reinterpret_cast<float *>(lrec + (size_t)nb * BS);
+        float *ub = gb + 8 * kPairCols, *hb = ub + 8 * kPairCols;
+        f32x4 v = acc[0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] += __shfl_down(v[r], 32);
+        if (lane < 32) {   // tokens 4 q + r of column 16 (wave / 2) + i
+            float *dst = (wave & 1) ? ub : gb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[(4 * q + r) * kPairCols + 16 * (wave >> 1) + i] = v[r];
+        }
+        const int col = kPairCols * blockIdx.x + lane, tok = wave;
+        const float bg = p.b0 ? p.b0[col] : 0.f, bu = p.b1 ? p.b1[col] : 0.f;
+        __syncthreads();
+        const float h = silu(gb[tok * kPairCols + lane] + bg) * (ub[tok * kPairCols + lane] + bu);
+        if (tok < p.m) p.y[(size_t)tok * p.n + col] = h;
+        hb[tok * (kPairCols + 1) + lane] = h;
+        if (!p.rec_out) return;
+        __syncthreads();
+        if (wave >= 4) return;
+        const int tr = i & 7;
+        float hv[2][8];
+        float mx = 0.f;
+        bool fin = true;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hv[g][e] = tr < p.m ? hb[tr * (kPairCols + 1) + 32 * g + 8 * q + e] : 0.f;
+                fin = fin && __builtin_isfinite(hv[g][e]);
+                mx = fmaxf(mx, fabsf(hv[g][e]));
+            }
+        const HalfExp he = half_exp(mx, fin);
+        const int half = blockIdx.x & 1, g = wave >> 1;
+        uint8_t *rg = p.rec_out + (size_t)(blockIdx.x >> 1) * BS;
+        auto part = [&](auto s0) {   // slots s0 .. s0 + 3 of group g
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            h4 l1, l2;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = decltype(s0)::value + jj;
+                const float x = g ? hv[1][slot_elem(j)] : hv[0][slot_elem(j)];
+                _Float16 a, b;
+                limbs_of(x, he, j, a, b);
+                l1[jj] = a;
+                l2[jj] = b;
+            }
+            *reinterpret_cast<h4 *>(rg + (size_t)(2 * half + g) * kTile + lane * 16 +
+                                    2 * decltype(s0)::value) = i < 8 ? l1 : l2;
+        };
+        if (wave & 1) part(std::integral_constant<int, 4>{});
+        else part(std::integral_constant<int, 0>{});
+        if (wave == 0 && q == 0) rg[4 * kTile + 2 * i + half] = he.byte;
+        return;
+    }
     float *pp = part + (size_t)split * (size_t)p.m * (size_t)ntot;
 #pragma unroll
     for (int rb = 0; rb < R; ++rb) {
@@ -451,10 +570,20 @@ __global__ __launch_bounds__(256) void k_limb_reduce(const float *__restrict__ p
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (size_t)gridDim.x * blockDim.x) {
         const int row = (int)(e % (size_t)n);
+        const float bias = b0 ? b0[row] : 0.f, r0 = res ? res[e] : 0.f;
+        // eight splits' loads in flight at a time, summed in split order
         float g = 0.f;
-        for (int s = 0; s < splits; ++s) g += part[(size_t)s * total + e];
-        if (b0) g += b0[row];
-        if (res) g += res[e];
+        int s = 0;
+        for (; s + 8 <= splits; s += 8) {
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = part[(size_t)(s + j) * total + e];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) g += t[j];
+        }
+        for (; s < splits; ++s) g += part[(size_t)s * total + e];
+        if (b0) g += bias;
+        if (res) g += r0;
         y[e] = g;
     }
 }
@@ -544,13 +673,17 @@ constexpr int kTargetBlocks = 512;
 
 struct Plan {
     int ksl, splits, r, chunks, nw;
+    bool pe;   // a pair whose kernel writes h and its records (no reduce)
     size_t lds;
 };
 
 // Whole-K form: when the records of the whole K fit kLdsWhole and there are
 // enough row blocks, one block per CU (kWholeWaves waves, one 16-row block each)
 // runs the whole K with no split: every record byte is copied to LDS once per
-// CU and there are no split partials to add.
+// CU and there are no split partials to add.  A SwiGLU pair takes eight waves,
+// the gate and up rows of 64 columns of h, and runs the epilogue itself (one
+// more wave per block than a single projection, about 1 us on the Llama-3-8B
+// gate/up at M = 8, against the 4.7 us of the reduce kernel it removes).
 constexpr int kWholeWaves = 7;
 // Ring depth in quads: one quad in flight while the previous one computes.
 // (Two or three quads ahead measured slower in every form, 17.7 -> 19.1 ->
@@ -568,14 +701,19 @@ Plan plan(int m, int n, int k, bool pair) {
     const long ntot = pair ? 2L * n : n;
     if (tiles_of(m) == 1 && (long)batches * bs <= kLdsWhole &&
         ntot / 16 >= (long)kWholeWaves * kTargetBlocks * 3 / 8) {
-        pl.nw = kWholeWaves;
+        pl.pe = pair;
+        pl.nw = pair ? kPairWaves : kWholeWaves;
         pl.r = 1;
         pl.splits = 1;
         pl.ksl = k;
-        pl.lds = (size_t)batches * bs;
-        pl.chunks = (int)((ntot + 16 * kWholeWaves - 1) / (16 * kWholeWaves));
+        // a pair's epilogue: gate, up and a padded h tile past the records
+        pl.lds = (size_t)batches * bs +
+                 (pair ? (size_t)(8 * (3 * kPairCols + 1)) * sizeof(float) : 0);
+        pl.chunks = pair ? n / kPairCols
+                         : (int)((ntot + 16 * kWholeWaves - 1) / (16 * kWholeWaves));
         return pl;
     }
+    pl.pe = false;
     pl.nw = 4;
     int per = kLdsBudget / bs;
     if (per < 1) per = 1;
@@ -607,6 +745,7 @@ size_t limb_records_bytes(int m, int k) {
 
 size_t limb_partials_bytes(int m, int n, int k, bool pair) {
     const Plan pl = plan(m, n, k, pair);
+    if (pl.pe) return 0;
     return (size_t)pl.splits * (size_t)m * (size_t)(pair ? 2 * n : n) * sizeof(float);
 }
 
@@ -641,35 +780,39 @@ int w4_limb(const LimbParams &p, float *part, hipStream_t st) {
     const bool sv = p.gshift == 5 && p.scols == (p.k >> 5) &&
                     (reinterpret_cast<uintptr_t>(p.s0) & 15) == 0 &&
                     (!pair || (reinterpret_cast<uintptr_t>(p.s1) & 15) == 0);
-#define TB_LIMB_GO(T_, R_, NW_, D_)                                                             \
+    // more than the default 64 KiB of dynamic LDS for the whole-K forms (set
+    // per call: the attribute belongs to the current device's code object)
+#define TB_LIMB_LDS(T_, R_, NW_, D_, SV_, PE_)                                                  \
+    TB_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_w4_limb<T_, R_, NW_, D_, SV_, PE_>), \
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds))
+#define TB_LIMB_GO(T_, R_, NW_, D_, PE_)                                                        \
     do {                                                                                        \
         const dim3 g_((unsigned)pl.chunks, (unsigned)pl.splits), b_(64 * NW_);                  \
-        if (sv)                                                                                 \
-            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, true>), g_, b_, pl.lds, st, p, part, \
-                               pl.ksl, ntot);                                                   \
-        else                                                                                    \
-            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, false>), g_, b_, pl.lds, st, p,      \
+        if (sv) {                                                                               \
+            if (pl.lds > kLdsBudget) TB_LIMB_LDS(T_, R_, NW_, D_, true, PE_);                   \
+            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, true, PE_>), g_, b_, pl.lds, st, p,  \
                                part, pl.ksl, ntot);                                             \
+        } else {                                                                                \
+            if (pl.lds > kLdsBudget) TB_LIMB_LDS(T_, R_, NW_, D_, false, PE_);                  \
+            hipLaunchKernelGGL((k_w4_limb<T_, R_, NW_, D_, false, PE_>), g_, b_, pl.lds, st, p, \
+                               part, pl.ksl, ntot);                                             \
+        }                                                                                       \
     } while (0)
-    if (pl.nw == kWholeWaves) {
-        // more than the default 64 KiB of dynamic LDS (set per call: the
-        // attribute belongs to the current device's code object)
-        TB_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, kQuads, true>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
-        TB_HIP(hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&k_w4_limb<1, 1, kWholeWaves, kQuads, false>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsWhole));
-        TB_LIMB_GO(1, 1, kWholeWaves, kQuads);
+    if (pl.pe) {
+        TB_LIMB_GO(1, 1, kPairWaves, kQuads, true);
+    } else if (pl.nw == kWholeWaves) {
+        TB_LIMB_GO(1, 1, kWholeWaves, kQuads, false);
     } else if (pl.r == 2) {
-        if (t1) TB_LIMB_GO(1, 2, 4, kQuads);
-        else TB_LIMB_GO(2, 2, 4, kQuads);
+        if (t1) TB_LIMB_GO(1, 2, 4, kQuads, false);
+        else TB_LIMB_GO(2, 2, 4, kQuads, false);
     } else {
-        if (t1) TB_LIMB_GO(1, 1, 4, kQuads);
-        else TB_LIMB_GO(2, 1, 4, kQuads);
+        if (t1) TB_LIMB_GO(1, 1, 4, kQuads, false);
+        else TB_LIMB_GO(2, 1, 4, kQuads, false);
     }
 #undef TB_LIMB_GO
+#undef TB_LIMB_LDS
     TB_LAUNCHED();
+    if (pl.pe) return TB_OK;
     if (pair) {
         const dim3 rg((unsigned)(p.n / kBatch));
         if (t1)
