@@ -64,13 +64,13 @@
 // register ring; since the records come from LDS, each wait is for the oldest
 // weights only (vector loads retire in order).  When the records of the whole
 // K fit in LDS (M <= 8, K <= 4224) and the matrix has enough 16-row blocks,
-// one block of seven waves per CU covers the whole K with no split.
-// Otherwise the per-split partial sums go to a scratch buffer and a small
-// reduce kernel sums them in split order (deterministic).  The reduce (or,
-// with no split, the same kernel over one split) runs the epilogue: bias
-// (+ residual), or for a SwiGLU pair, whose gate and up rows are stacked as
-// one 2n-row matrix, h = silu(g) * u plus the records of h for the next
-// projection.
+// one block per CU covers the whole K with no split; for a SwiGLU pair that
+// block holds the gate and up rows of 64 columns of h and writes h and its
+// half of h's records itself.  Otherwise the per-split partial sums go to a
+// scratch buffer and a small reduce kernel sums them in split order
+// (deterministic) and runs the epilogue: bias (+ residual), or for a SwiGLU
+// pair, whose gate and up rows are stacked as one 2n-row matrix,
+// h = silu(g) * u plus the records of h for the next projection.
 #include <math.h>
 
 #include <algorithm>
