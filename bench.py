@@ -27,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -367,11 +368,15 @@ def mlp_batch_section(torch, args, dev):
                           None, uw.data_ptr(), us.data_ptr(), None, dw.data_ptr(), ds.data_ptr(),
                           None, r.data_ptr(), o.data_ptr(), M, K, I, K, GS, S())
 
-        ms, _ = graph_time(torch, run, 5, 1, 5)
-        us = ms * 1e3 / len(sets)
+        # the median of 20 replays of 20 steps each (the first configuration
+        # measured otherwise read a few us slow on some boxes)
+        _, _, per = graph_time(torch, run, 20, 3, 5, spread=True)
+        us = statistics.median(per) * 1e3 / len(sets)
         byts = 3 * (I * K // 2 + 4 * I * (K // GS)) + 4 * (M * K + 2 * M * I + 2 * M * K)
         out[f"m{M}"] = {"us": round(us, 3), "gbs": round(byts / us / 1e3, 1),
-                        "tok_s": round(M / us * 1e6, 1)}
+                        "tok_s": round(M / us * 1e6, 1),
+                        "us_min_max": [round(min(per) * 1e3 / len(sets), 3),
+                                       round(max(per) * 1e3 / len(sets), 3)]}
     del sets
     torch.cuda.empty_cache()
     return out

@@ -189,3 +189,33 @@ def test_limb_whole_k_single_projection(cuda):
     ref = O.gemm_w4(x, w, s, b, group_size=32)
     y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), T(b, cuda), 32)
     assert rel_rows(y.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("m,k,inter,gs,bias", [
+    (5, 4096, 14336, 32, True),    # whole-K pair, h only (no records for a next projection)
+    (8, 4096, 12288, 32, False),   # whole-K pair at the plan's smallest size class
+    (12, 2048, 4096, 32, True),    # two tiles: split partials and the pair reduce
+    (3, 1024, 2048, 64, False),    # one tile, split partials
+])
+def test_limb_swiglu_pair_entry(cuda, m, k, inter, gs, bias):
+    """tb_swiglu_w4a32, the neuron loop of fused_swiglu_mlp_w4a32
+    (src/quantization/fused_ops.rs:244-407) on its own: h against the oracle."""
+    from torchburn_amd import _lib
+    print(f"case limb SwiGLU pair m={m} k={k} inter={inter} gs={gs} bias={bias}", flush=True)
+    g = synth.rng(83, m, k, inter, gs)
+    x = synth.activations(g, m, k)
+    gw, gsc = synth.int4_weight(g, inter, k, gs)
+    uw, usc = synth.int4_weight(g, inter, k, gs)
+    gb = g.normal(0, 0.1, inter).astype(np.float32) if bias else None
+    ub = g.normal(0, 0.1, inter).astype(np.float32) if bias else None
+    ref = np.stack([O.swiglu_h_w4(x[r], gw, gsc, uw, usc, gb, ub, group_size=gs)
+                    for r in range(m)])
+    dx, dgw, dgs, duw, dus = (T(a, cuda) for a in (x, gw, gsc, uw, usc))
+    dgb = T(gb, cuda) if bias else None
+    dub = T(ub, cuda) if bias else None
+    h = torch.full((m, inter), float("nan"), device=cuda)
+    P = lambda t: t.data_ptr() if t is not None else None
+    _lib.call("tb_swiglu_w4a32", P(dx), P(dgw), P(dgs), P(dgb), P(duw), P(dus), P(dub), P(h),
+              m, k, inter, gs, torch.cuda.current_stream(cuda).cuda_stream)
+    torch.cuda.synchronize(cuda)
+    assert rel_rows(h.cpu().numpy(), ref) < TOL
