@@ -118,8 +118,9 @@ TB_API int tb_dequantize_int4_grouped_v2(const uint8_t *w_blocked, float *out, i
  * f32 weights [N, K] -> v1 nibbles [N, K/2] + f32 scales [N, K/gs] on the device:
  * quantize_weight_int4_grouped (python/torchburn/quantization.py:53-118),
  * s = max(max|w| / 7, 1e-8) per group, q = clamp(round_half_even(w / s), -8, 7).
- * group_size 32 or 64; K % group_size != 0 is TB_ERR_VALUE with the
- * reference's message.
+ * Any group_size >= 1 that divides K (TB_ERR_VALUE with the reference's
+ * message otherwise); an odd K is TB_ERR_VALUE (the reference's nibble pairs
+ * do not line up there and torch raises).
  */
 TB_API int tb_quantize_weight_int4_grouped(const float *w, uint8_t *packed, float *scales,
                                            int64_t n, int64_t k, int64_t group_size,

@@ -2,7 +2,8 @@
 
   quantize_weight_int4_grouped   bit-exact against the oracle's restatement of
       python/torchburn/quantization.py:53-118 (pinned there against a numpy
-      closed form): ties, zero groups, K % 64 != 0 at group 32, host input
+      closed form): ties, zero groups, K % 64 != 0 at group 32, host input,
+      group sizes other than 32 / 64 (1, 3, 100, 128, 512), odd K refused
   quantize_weight_int8           bit-exact against fused_ops.rs:554-589's restatement
   unpack v2 -> v1                the loader's migration (loader.py:539-561): nibbles
       unchanged, scales = binary16 rounding of the originals
@@ -31,14 +32,16 @@ def rel(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
 
 
-@pytest.mark.parametrize("n,k,gs", [(37, 896, 64), (64, 4096, 32), (5, 96, 32), (3, 64, 64)])
+@pytest.mark.parametrize("n,k,gs", [(37, 896, 64), (64, 4096, 32), (5, 96, 32), (3, 64, 64),
+                                    (7, 768, 128), (6, 200, 100), (4, 96, 3), (3, 1536, 512),
+                                    (5, 10, 1)])
 def test_quantize_int4_bit_exact(cuda, n, k, gs):
     print(f"case quantize_weight_int4_grouped n={n} k={k} gs={gs}", flush=True)
     g = np.random.default_rng(n * k + gs)
     w = g.standard_normal((n, k)).astype(np.float32)
     w[0, :gs] = 0.0                                    # zero group -> scale 1e-8
     s0 = np.abs(w[1, :gs]).max() / np.float32(7.0)
-    w[1, 3] = np.float32(2.5) * s0                     # an exact tie (if representable)
+    w[1, min(3, gs - 1)] = np.float32(2.5) * s0        # an exact tie (if representable)
     w[2, :gs] *= np.float32(1e-12)                     # tiny group: scale clamps at 1e-8
     wq_ref, s_ref = O.quantize_int4_grouped(w, gs)
     wq, s = tb.quantize_weight_int4_grouped(torch.from_numpy(w).to(cuda), group_size=gs)
@@ -54,8 +57,8 @@ def test_quantize_int4_errors(cuda):
     w = torch.zeros((4, 96), device=cuda)
     with pytest.raises(ValueError, match="divisible"):
         tb.quantize_weight_int4_grouped(w, group_size=64)
-    with pytest.raises(tb.UnsupportedOpError):
-        tb.quantize_weight_int4_grouped(torch.zeros((4, 128), device=cuda), group_size=128)
+    with pytest.raises(RuntimeError, match="odd"):
+        tb.quantize_weight_int4_grouped(torch.zeros((4, 9), device=cuda), group_size=3)
 
 
 def test_quantize_int8_bit_exact(cuda):

@@ -89,15 +89,16 @@ def test_pack_round_trip(k):
     assert int(w[0, 0]) == (int(q[0, 0]) + 8) | ((int(q[0, 1]) + 8) << 4)
 
 
-def test_quantizer_matches_closed_form():
+@pytest.mark.parametrize("k,gs", [(128, 32), (384, 128), (96, 3), (200, 100), (10, 1)])
+def test_quantizer_matches_closed_form(k, gs):
     g = np.random.default_rng(3)
-    w = g.normal(0, 1, (9, 128)).astype(np.float32)
-    w[0, :32] = 0.0                      # all-zero group -> scale 1e-8
-    w[1, 5] = 3.5 * (np.abs(w[1, :32]).max() / 7.0)   # an exact .5 tie
-    packed, scales = O.quantize_int4_grouped(w, 32)
-    wg = w.reshape(9, 4, 32)
+    w = g.normal(0, 1, (9, k)).astype(np.float32)
+    w[0, :gs] = 0.0                      # all-zero group -> scale 1e-8
+    w[1, min(5, gs - 1)] = 3.5 * (np.abs(w[1, :gs]).max() / 7.0)   # an exact .5 tie
+    packed, scales = O.quantize_int4_grouped(w, gs)
+    wg = w.reshape(9, k // gs, gs)
     s = np.maximum(np.abs(wg).max(-1) / np.float32(7.0), np.float32(1e-8)).astype(np.float32)
-    q = np.clip(np.round(wg / s[..., None]), -8, 7).astype(np.int8).reshape(9, 128)
+    q = np.clip(np.round(wg / s[..., None]), -8, 7).astype(np.int8).reshape(9, k)
     assert np.array_equal(scales, s)
     assert np.array_equal(packed, O.pack_int4(q))
 

@@ -586,8 +586,8 @@ int tb_quantize_weight_int4_grouped(const float *w, uint8_t *packed, float *scal
                                     int64_t k, int64_t group_size, void *stream) {
     TB_REQUIRE(w && packed && scales, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: quantize_weight_int4_grouped: null pointer");
-    TB_REQUIRE(group_size == 32 || group_size == 64, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: quantize_weight_int4_grouped: group_size must be 32 or 64, got " +
+    TB_REQUIRE(group_size >= 1, TB_ERR_VALUE,
+               "quantize_weight_int4_grouped: group_size must be positive, got " +
                    std::to_string(group_size));
     TB_REQUIRE(n >= 0 && k > 0 && k <= (1 << 30), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: quantize_weight_int4_grouped: bad shape");
@@ -595,6 +595,11 @@ int tb_quantize_weight_int4_grouped(const float *w, uint8_t *packed, float *scal
                "Weight dimension K=" + std::to_string(k) + " must be divisible by group_size=" +
                    std::to_string(group_size) + ". Consider padding the weight tensor along dim 1 "
                    "to a multiple of " + std::to_string(group_size) + ".");
+    // two nibbles per byte: the reference's (low | high) has no partner for
+    // the last element of an odd K (its shapes differ and torch raises)
+    TB_REQUIRE(k % 2 == 0, TB_ERR_VALUE,
+               "quantize_weight_int4_grouped: K=" + std::to_string(k) +
+                   " is odd: the nibble pairs (K + 1) / 2 low and (K - 1) / 2 high differ");
     TB_REQUIRE(aligned(w, 4) && aligned(scales, 4), TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: quantize_weight_int4_grouped: misaligned device pointer");
     return quantize_int4_grouped(w, packed, scales, n, k, (int)group_size, (hipStream_t)stream);

@@ -1,11 +1,13 @@
 // Weight quantizers on gfx950: the formats the GEMVs read, produced on the
 // device straight from f32 checkpoint tensors.
 //
-//   * grouped INT4 (python/torchburn/quantization.py:53-118): per group of 32 or
-//     64 elements s = max(max|w| / 7, 1e-8), q = clamp(round_half_even(w / s),
-//     -8, 7), byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4.  One wavefront per
-//     64-element span of a row: lane e holds element e; the group maximum is a
-//     butterfly over the group's lanes.
+//   * grouped INT4 (python/torchburn/quantization.py:53-118): per group of
+//     group_size elements s = max(max|w| / 7, 1e-8), q = clamp(
+//     round_half_even(w / s), -8, 7), byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4.
+//     Groups of 32 or 64: one wavefront per 64-element span of a row, lane e
+//     holds element e and the group maximum is a butterfly over the group's
+//     lanes.  Any other group size: one wavefront per group for the scales,
+//     then one thread per byte (its two elements may lie in two groups).
 //   * per-channel INT8 (src/quantization/fused_ops.rs:554-589): s = max|w| / 127
 //     (1 when max|w| <= 1e-8), q = clamp(round_half_away(w * (1 / s)), -127, 127).
 //     One block per row.
@@ -16,6 +18,8 @@
 //   * v2 -> v1 (python/torchburn/llm/loader.py:540-561, the cache migration):
 //     32 nibble bytes copied, the binary16 scale widened to f32.
 #include <math.h>
+
+#include <algorithm>
 
 #include "gemv_common.hpp"
 #include "quantize.hpp"
@@ -50,6 +54,46 @@ __global__ __launch_bounds__(256) void k_quant_int4(const float *__restrict__ w,
     if (valid && (lane & 1) == 0)
         packed[row * (k / 2) + (c0 + lane) / 2] = (uint8_t)(u | (hi << 4));
     if (valid && (lane % GS) == 0) scales[row * (k / GS) + (c0 + lane) / GS] = s;
+}
+
+// Any group size: the scale of group id (row id / (k / gs)), one wavefront each.
+__global__ __launch_bounds__(256) void k_quant_int4_scales(const float *__restrict__ w,
+                                                           float *__restrict__ scales, int64_t n,
+                                                           int k, int gs) {
+    const int lane = threadIdx.x & 63;
+    const int64_t ng = k / gs;
+    for (int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); id < n * ng;
+         id += (int64_t)gridDim.x * 4) {   // wave-uniform trip count
+        const int64_t row = id / ng;
+        const float *p = w + row * k + (id - row * ng) * gs;
+        float amax = 0.f;
+        for (int e = lane; e < gs; e += 64) amax = fmaxf(amax, fabsf(p[e]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        if (lane == 0) scales[id] = fmaxf(__fdiv_rn(amax, 7.0f), 1e-8f);
+    }
+}
+
+// Any group size: byte j of a row from elements 2 j and 2 j + 1 and their
+// groups' scales.
+__global__ __launch_bounds__(256) void k_quant_int4_pack(const float *__restrict__ w,
+                                                         const float *__restrict__ scales,
+                                                         uint8_t *__restrict__ packed, int64_t n,
+                                                         int k, int gs) {
+    const int64_t bpr = k / 2;
+    for (int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x; id < n * bpr;
+         id += (int64_t)gridDim.x * 256) {
+        const int64_t row = id / bpr;
+        const int e = 2 * (int)(id - row * bpr);
+        const float *wr = w + row * k;
+        const float *sr = scales + row * (k / gs);
+        auto nib = [&](int c) {
+            float q = __builtin_rintf(__fdiv_rn(wr[c], sr[c / gs]));
+            q = fminf(fmaxf(q, -8.0f), 7.0f);
+            return (uint32_t)((int)q + 8);
+        };
+        packed[id] = (uint8_t)(nib(e) | (nib(e + 1) << 4));
+    }
 }
 
 __global__ __launch_bounds__(256) void k_quant_int8(const float *__restrict__ w,
@@ -122,6 +166,21 @@ __global__ __launch_bounds__(256) void k_unpack_v2(const uint8_t *__restrict__ b
 
 int quantize_int4_grouped(const float *w, uint8_t *packed, float *scales, int64_t n, int64_t k,
                           int gs, hipStream_t st) {
+    if (gs != 32 && gs != 64) {
+        const int64_t groups = n * (k / gs), bytes = n * (k / 2);
+        if (groups == 0) return TB_OK;
+        // grid-stride loops: at most 65536 blocks of each
+        hipLaunchKernelGGL(k_quant_int4_scales,
+                           dim3((unsigned)std::min<int64_t>((groups + 3) / 4, 65536)), dim3(256),
+                           0, st, w, scales, n, (int)k, gs);
+        TB_LAUNCHED();
+        if (bytes == 0) return TB_OK;
+        hipLaunchKernelGGL(k_quant_int4_pack,
+                           dim3((unsigned)std::min<int64_t>((bytes + 255) / 256, 65536)),
+                           dim3(256), 0, st, w, scales, packed, n, (int)k, gs);
+        TB_LAUNCHED();
+        return TB_OK;
+    }
     const int64_t waves = n * ((k + 63) / 64);
     if (waves == 0) return TB_OK;
     const dim3 grid((unsigned)((waves + 3) / 4));

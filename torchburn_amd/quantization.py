@@ -71,8 +71,8 @@ def quantize_weight_int4_grouped(
     Per group: s = max(amax / 7, 1e-8); q = clamp(round_half_even(w / s), -8, 7);
     byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4  (reference quantization.py:53-118).
     Runs on the GPU (tb_quantize_weight_int4_grouped), ``chunk_size`` rows of a
-    host tensor at a time; the result is on the weight's device.  Group sizes 32
-    and 64 (the ones the GEMVs read).
+    host tensor at a time; the result is on the weight's device.  Any group size
+    that divides K, as the reference takes (the GEMVs read even group sizes).
     """
     if weight.ndim != 2:
         raise ValueError(
@@ -83,10 +83,12 @@ def quantize_weight_int4_grouped(
         raise ValueError(
             f"Weight dimension K={k} must be divisible by group_size={group_size}. "
             f"Consider padding the weight tensor along dim 1 to a multiple of {group_size}.")
-    if group_size not in (32, 64):
-        raise UnsupportedOpError(
-            f"{_lib.UNSUPPORTED_MARKER} quantize_weight_int4_grouped: group_size must be 32 or 64, "
-            f"got {group_size}")
+    if k % 2 != 0:
+        # the reference's low | high pairs (K + 1) // 2 low nibbles with
+        # (K - 1) // 2 high ones, and torch raises on the mismatch
+        raise RuntimeError(
+            f"quantize_weight_int4_grouped: K={k} is odd: {(k + 1) // 2} low nibbles against "
+            f"{(k - 1) // 2} high ones")
     dev = _target(weight)
     packed = torch.empty((n, (k + 1) // 2), dtype=torch.uint8, device=dev)
     scales = torch.empty((n, k // group_size), dtype=torch.float32, device=dev)
