@@ -257,7 +257,12 @@ static int generic(const float *x, const void *w0, const float *s0, int mode0, c
 static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
                      const float *bias, const float *res, float *out, int64_t m, int64_t n,
                      int64_t k, int64_t gs, hipStream_t st, int scale_mode = 0) {
-    const bool lb = !v2 && limb_fast(x, w, m, n, k, gs, scale_mode != 0, false);
+    // M = 16 with N and K at most 4096 takes the FP32-MFMA projection: all 16
+    // rows share one LDS tile there, where the two-tile limb form needs five K
+    // splits (14.4 against 15.4 us at N = K = 4096; from N = 14336 the limb
+    // form is faster, 25.7 against 30.2 us)
+    const bool lb = !v2 && limb_fast(x, w, m, n, k, gs, scale_mode != 0, false) &&
+                    !(m == 16 && n <= 4096 && k <= 4096);
     if (!v2 && !lb && !w4_fast(x, w, m, k, gs, scale_mode != 0))
         return generic(x, w, s, scale_mode, bias, nullptr, nullptr, 0, nullptr, res, out, m, n, k,
                        scale_mode ? k : gs, 4, st);
