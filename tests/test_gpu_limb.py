@@ -82,7 +82,8 @@ def test_limb_per_channel(cuda, m, scalar):
 
 
 @pytest.mark.parametrize("m,k,inter,gs", [(3, 1024, 2048, 32), (8, 4096, 14336, 32),
-                                          (16, 1024, 2048, 64), (11, 512, 1024, 32)])
+                                          (16, 1024, 2048, 64), (11, 512, 1024, 32),
+                                          (4, 4096, 14336, 64)])
 def test_limb_swiglu_mlp_with_biases(cuda, m, k, inter, gs):
     print(f"case limb MLP m={m} k={k} inter={inter} gs={gs}", flush=True)
     g = synth.rng(74, m, k, inter, gs)
@@ -194,6 +195,8 @@ def test_limb_whole_k_single_projection(cuda):
 @pytest.mark.parametrize("m,k,inter,gs,bias", [
     (5, 4096, 14336, 32, True),    # whole-K pair, h only (no records for a next projection)
     (8, 4096, 12288, 32, False),   # whole-K pair at the plan's smallest size class
+    (3, 4096, 10752, 64, True),    # whole-K pair, group-64 scales (one dword per group)
+    (7, 2048, 14336, 128, False),  # whole-K pair, group 128, a short K
     (12, 2048, 4096, 32, True),    # two tiles: split partials and the pair reduce
     (3, 1024, 2048, 64, False),    # one tile, split partials
 ])
