@@ -220,19 +220,22 @@ __device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
     build_half<T>(*reinterpret_cast<const float(*)[2][8]>(&v[2]), lane, rg, 1);
 }
 
+// One wave per half batch: lane (i, q) loads elements 32 (2 h + g) + 8 q ..
+// of its row for the half's two groups g and builds that half of the record.
 template <int T>
 __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict__ rec, int m,
                                int k, int batches) {
     const int lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= batches) return;   // whole waves
+    const int hw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (hw >= 2 * batches) return;   // whole waves
+    const int b = hw >> 1, h = hw & 1;
     const int i = lane & 15, q = lane >> 4;
     const int row = T == 1 ? (i & 7) : i;
-    float v[4][8];
+    float v[2][8];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 2; ++g) {
         if (row < m) {
-            const float *xp = x + (size_t)row * k + 128 * b + 32 * g + 8 * q;
+            const float *xp = x + (size_t)row * k + 128 * b + 32 * (2 * h + g) + 8 * q;
             const float4 a = *reinterpret_cast<const float4 *>(xp);
             const float4 c = *reinterpret_cast<const float4 *>(xp + 4);
             v[g][0] = a.x; v[g][1] = a.y; v[g][2] = a.z; v[g][3] = a.w;
@@ -242,7 +245,7 @@ __device__ void limb_prep_body(const float *__restrict__ x, uint8_t *__restrict_
             for (int e = 0; e < 8; ++e) v[g][e] = 0.f;
         }
     }
-    build_batch<T>(v, lane, rec + (size_t)b * rec_stride(T));
+    build_half<T>(v, lane, rec + (size_t)b * rec_stride(T), h);
 }
 
 // Partial sums of one block: rows [row0, row0 + 16 R NW) of the stacked
@@ -759,7 +762,7 @@ int limb_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st) {
     TB_REQUIRE(m >= 1 && m <= kLimbMaxM && k % kBatch == 0, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: activation records need 1 <= M <= 16 and K % 128 == 0");
     const int batches = k / kBatch;
-    const dim3 grid((unsigned)((batches + 3) / 4));
+    const dim3 grid((unsigned)((2 * batches + 3) / 4));   // one wave per half batch
     if (tiles_of(m) == 1)
         hipLaunchKernelGGL(k_limb_prep<1>, grid, dim3(256), 0, st, x, rec, m, k, batches);
     else
