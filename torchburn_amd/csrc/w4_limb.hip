@@ -213,13 +213,6 @@ __device__ __forceinline__ bool flagged(const uint8_t *rg_tail) {
     return (v & 0xFFu) == 0 || (v >> 8) == 0;
 }
 
-// The whole record of a batch: v[g] holds group g (lanes as in build_half).
-template <int T>
-__device__ void build_batch(const float (&v)[4][8], int lane, uint8_t *rg) {
-    build_half<T>(*reinterpret_cast<const float(*)[2][8]>(&v[0]), lane, rg, 0);
-    build_half<T>(*reinterpret_cast<const float(*)[2][8]>(&v[2]), lane, rg, 1);
-}
-
 // One wave per half batch: lane (i, q) loads elements 32 (2 h + g) + 8 q ..
 // of its row for the half's two groups g and builds that half of the record.
 template <int T>
@@ -594,8 +587,9 @@ __global__ __launch_bounds__(256) void k_limb_reduce(const float *__restrict__ p
 // SwiGLU pair: h = silu(gate + b0) * (up + b1) from the split partials of the
 // stacked [gate; up] rows.  One block per 128-row batch of h: each thread sums
 // 4 T contiguous values of one token over the splits (four splits' loads in
-// flight at a time) and writes them to y and LDS; wave 0 then writes the
-// batch's record for the next projection (rec_out, K = n).
+// flight at a time) and writes them to y and LDS; waves 0 and 1 then write
+// the two halves of the batch's record for the next projection (rec_out,
+// K = n).
 template <int T>
 __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restrict__ part,
                                                           int splits, int m, int n,
@@ -661,15 +655,16 @@ __global__ __launch_bounds__(256) void k_limb_reduce_pair(const float *__restric
     }
     if (!rec_out) return;
     __syncthreads();
-    if (tid >= 64) return;
-    const int lane = tid, i = lane & 15, q = lane >> 4;
+    if (tid >= 128) return;
+    // waves 0 and 1: halves 0 and 1 of the batch's record
+    const int lane = tid & 63, h = tid >> 6, i = lane & 15, q = lane >> 4;
     const int tr = T == 1 ? (i & 7) : i;
-    float v[4][8];
+    float v[2][8];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < 2; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[g][e] = tr < m ? hs[tr][32 * g + 8 * q + e] : 0.f;
-    build_batch<T>(v, lane, rec_out + (size_t)bt * rec_stride(T));
+        for (int e = 0; e < 8; ++e) v[g][e] = tr < m ? hs[tr][32 * (2 * h + g) + 8 * q + e] : 0.f;
+    build_half<T>(v, lane, rec_out + (size_t)bt * rec_stride(T), h);
 }
 
 constexpr int kTargetBlocks = 512;
