@@ -28,6 +28,7 @@
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
+#include "w4_limb.hpp"
 #include "w4_mfma.hpp"
 #include "v2_layout.hpp"
 #include "sample.hpp"
@@ -47,6 +48,7 @@ struct Layer {
 };
 
 int gshift(int64_t gs) { return gs == 32 ? 5 : 6; }
+size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 }  // namespace
 
@@ -473,18 +475,56 @@ struct Decoder {
         part = std::max(part, w4_mfma_partials_bytes(R, H, hq * hd, false));
         part = std::max(part, w4_mfma_partials_bytes(R, I, H, true));
         part = std::max(part, w4_mfma_partials_bytes(R, H, I, false));
+        // 3..16 rows (verify_tokens, short chunks) take the small-batch
+        // projection: records + split partials of the largest of its shapes
+        size_t lb = 0;
+        for (int m = 3; m <= kLimbMaxM; ++m) {
+            auto need = [&](int n, int k, bool pair) -> size_t {
+                if (!limb_shape_ok(m, n, k, pair)) return 0;
+                return up256(limb_records_bytes(m, k)) + limb_partials_bytes(m, n, k, pair);
+            };
+            lb = std::max({lb, need((int)nq, H, false), need(H, hq * hd, false), need(I, H, true),
+                           need(H, I, false)});
+            if (m <= 8 && lmbits == 4) lb = std::max(lb, need(V, H, false));
+        }
         int rc;
         if ((rc = alloc(&pf_x, (size_t)R * H * 4)) || (rc = alloc(&pf_xn, (size_t)R * H * 4)) ||
             (rc = alloc(&pf_qkv, (size_t)R * nq * 4)) ||
             (rc = alloc(&pf_q, (size_t)R * hq * hd * 4)) ||
             (rc = alloc(&pf_a, (size_t)R * hq * hd * 4)) || (rc = alloc(&pf_h, (size_t)R * I * 4)) ||
-            (rc = alloc(&pf_part, part)) || (rc = alloc(&pf_tok, (size_t)R * 4)))
+            (rc = alloc(&pf_part, part)) || (rc = alloc(&pf_tok, (size_t)R * 4)) ||
+            (lb && (rc = alloc(&pf_limb, lb))))
             return rc;
+        pf_limb_bytes = lb;
         return TB_OK;
+    }
+
+    // The small-batch projection (records of x, then w4_limb) when it takes
+    // the shape and the buffer holds its scratch; false: use the GEMM.
+    uint8_t *pf_limb = nullptr;
+    size_t pf_limb_bytes = 0;
+    bool limb_gemm(const float *xin, const void *w, const float *s, const float *b,
+                   const void *w2, const float *s2, const float *res, float *y, int m, int n,
+                   int k, int &rc) {
+        const bool pair = w2 != nullptr;
+        if (!pf_limb || m < 3 || m > kLimbMaxM || !limb_shape_ok(m, n, k, pair)) return false;
+        const size_t rb = up256(limb_records_bytes(m, k));
+        if (rb + limb_partials_bytes(m, n, k, pair) > pf_limb_bytes) return false;
+        LimbParams p{};
+        p.x = xin; p.rec = pf_limb;
+        p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
+        p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
+        p.res = res; p.y = y; p.m = m; p.n = n; p.k = k;
+        p.scols = k / gs; p.gshift = gshift(gs);
+        if ((rc = limb_prep(xin, pf_limb, m, k, st))) return true;
+        rc = w4_limb(p, reinterpret_cast<float *>(pf_limb + rb), st);
+        return true;
     }
 
     int gemm(const float *xin, const void *w, const float *s, const float *b, const void *w2,
              const float *s2, const float *res, float *y, int m, int n, int k, int epi) {
+        int rc = TB_OK;
+        if (limb_gemm(xin, w, s, b, w2, s2, res, y, m, n, k, rc)) return rc;
         MfmaParams p{};
         p.x = xin;
         p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
@@ -512,6 +552,9 @@ struct Decoder {
     int lm_rows(const float *xr, float *y, int M) {
         int rc;
         if (lmbits == 4) {
+            if (M <= 8 && limb_gemm(xr, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, y, M, V, H,
+                                    rc))
+                return rc;
             if (!pf_lmpart &&
                 (rc = alloc(&pf_lmpart, w4_mfma_partials_bytes(64, V, H, false))))
                 return rc;
