@@ -176,6 +176,15 @@ TB_API float tb_sample_uniform(uint64_t seed, uint64_t counter);
  */
 TB_API int tb_set_vnni_semantics(int enabled);
 
+/* Frees the workspace the library keeps for `stream` on the current device (and
+ * the smaller buffers it replaced), for callers that create streams per request
+ * and would otherwise hold one workspace per stream until the process ends.  No
+ * reference counterpart (the reference allocates per call).  It waits for the
+ * device to finish its work first; a graph captured on that stream that used the
+ * library must not be replayed afterwards.  A later call on the stream gets a
+ * new workspace.  TB_OK when the stream has none. */
+TB_API int tb_release_stream_workspace(void *stream);
+
 /*
  * out = residual + w4a32_grouped_linear(x, ...).  The reference performs the
  * residual add as a separate pass after the projection
@@ -220,10 +229,11 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
  * intermediates (h, the x / h chunk records or the MFMA split-K partials) live
- * in an 8 MiB static device array, one per GPU, instead of the per-stream
+ * in a 16 MiB static device array, one per GPU, instead of the per-stream
  * workspace: shapes needing more return TB_ERR_UNSUPPORTED with the byte count
- * (the Llama-3-8B MLP needs about 121 KB per activation row on the GEMV path,
- * M <= 4).  Every call on one GPU shares that array, so calls that overlap on
+ * before any GPU work (the Llama-3-8B MLP fits at M = 1..58 and 65..97; M =
+ * 59..64 and M >= 98 are refused: the FP32-MFMA split-K partials grow with
+ * the row tiles).  Every call on one GPU shares that array, so calls that overlap on
  * one GPU (two streams, or two threads) race; nothing in it needs clearing
  * between calls.  Same arguments and results as tb_fused_swiglu_mlp_w4a32.
  */
@@ -484,6 +494,14 @@ TB_API int tb_decoder_set_seed(tb_decoder *d, uint64_t seed);
  * counterpart on RustQwenDecoder. */
 TB_API int tb_decoder_set_rope_tables(tb_decoder *d, const float *cos_t, const float *sin_t,
                                       int64_t rows, int64_t head_dim);
+
+/* Attention length of a step: the step at position p scores positions
+ * 0 .. min(p + 1, cap) - 1.  The default, 32768, is RustQwenDecoder's native
+ * step, which caps its scores at the first 32768 positions
+ * (src/llm/decoder.rs:1179-1184); cap 0 scores every position, as the
+ * reference's per-layer Python path does (fused_ops.rs:997-1040).  Batched
+ * prefill and verify chunks that reach the cap run step by step. */
+TB_API int tb_decoder_set_attention_cap(tb_decoder *d, int64_t cap);
 
 /* Benchmark helper (no reference counterpart): n_steps greedy steps from
  * (first_token, offset) as back-to-back graph replays, timed with HIP events on

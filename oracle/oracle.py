@@ -61,6 +61,7 @@ def lib():
         L.orc_attention_layer.argtypes = [_f32p, _vp, _vp, _f32p, _i64, _i64, _i64, _i64, _i64]
         L.orc_decoder_set_rope_tables.argtypes = [_vp, _f32p, _f32p]
         L.orc_decoder_set_layer_path.argtypes = [_vp, C.c_int]
+        L.orc_decoder_set_attention_cap.argtypes = [_vp, _i64]
         L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
         L.orc_gemv_f32.argtypes = [_vp, _vp, _vp, _i64, _i64]
         L.orc_rope_tables.argtypes = [_f32p, _f32p, _i64, _i64, C.c_double]
@@ -442,9 +443,12 @@ class Decoder:
     rope_tables: (cos, sin) f32 [max_seq, head_dim] replacing the f64 tables.
     layer_path: the numerics of the reference's per-layer Python path
     (orc_decoder_set_layer_path), which runs INT8 and fp32-lm_head models.
+    attention_cap: positions the native step scores (the reference's 32768,
+    decoder.rs:1179-1184, unless a test sets another).
     """
 
-    def __init__(self, weights: dict, cfg: dict, rope_tables=None, layer_path=False):
+    def __init__(self, weights: dict, cfg: dict, rope_tables=None, layer_path=False,
+                 attention_cap=32768):
         self.cfg = cfg
         self.w = weights
         L = lib()
@@ -466,6 +470,7 @@ class Decoder:
             assert c.shape == (cfg["max_seq"], cfg["head_dim"]) == sn.shape
             L.orc_decoder_set_rope_tables(self.h, c, sn)
         L.orc_decoder_set_layer_path(self.h, 1 if layer_path else 0)
+        L.orc_decoder_set_attention_cap(self.h, int(attention_cap))
 
     def step(self, token: int, offset: int) -> np.ndarray:
         L = lib()

@@ -332,9 +332,11 @@ ORC_API void orc_gemm_w4_v2(const float *x, const uint8_t *w, const float *bias,
 /* ------------------------------------------------------------------------ */
 /* f2: the W4A8 semantics of the AVX-512 VNNI tier at group 64.              */
 /* quantize_activation_to_u8_avx512, gemv.rs:1353-1389: s_x = max(max|x|,   */
-/* 1e-10) / 127; q = round-to-nearest-even(x * (1 / s_x)) (cvtps_epi32 under  */
-/* the default MXCSR); byte = q + 128.  The scalar tail (k % 16) rounds half  */
-/* away from zero and divides; it is unused for k % 64 == 0.                  */
+/* 1e-10) / 127; the first 16 * (k / 16) elements: q = round-to-nearest-even  */
+/* (x * (1 / s_x)) (cvtps_epi32 under the default MXCSR), the rest (the       */
+/* scalar tail, gemv.rs:1383-1386): q = round-half-away(x / s_x) clamped to   */
+/* +-127; byte = q + 128.  NaN gives q = 0 either way (cvtps_epi32's integer  */
+/* indefinite + 128 truncated to a byte; Rust's NaN as i16).                  */
 /* ------------------------------------------------------------------------ */
 ORC_API float orc_quantize_act_u8(const float *x, int64_t k, uint8_t *out) {
     float mx = 0.f;
@@ -344,9 +346,16 @@ ORC_API float orc_quantize_act_u8(const float *x, int64_t k, uint8_t *out) {
     }
     if (mx < 1e-10f) mx = 1e-10f;
     float sx = mx / 127.0f, inv = 1.0f / sx;
+    int64_t body = k / 16 * 16;
     for (int64_t i = 0; i < k; ++i) {
-        float q = nearbyintf(x[i] * inv);
-        out[i] = (uint8_t)((int32_t)q + 128);
+        float q;
+        if (i < body) {
+            q = nearbyintf(x[i] * inv);
+        } else {
+            q = roundf(x[i] / sx);
+            q = q > 127.f ? 127.f : (q < -127.f ? -127.f : q);
+        }
+        out[i] = isnan(q) ? (uint8_t)128 : (uint8_t)((int32_t)q + 128);
     }
     return sx;
 }
@@ -356,19 +365,23 @@ ORC_API float orc_quantize_act_u8(const float *x, int64_t k, uint8_t *out) {
 /* lane j of the 16 dpbusd lanes holds the exact integer sum over elements   */
 /* 4j..4j+3 of (byte - 128) * (nib - 8); acc_j = fma((float)lane, s_x * s_w,  */
 /* acc_j) per group; tree16 at the end.  blocked != 0: w holds v2 blocks.     */
+/* With k % 64 != 0 (v1 only) the reference's last group reads past the row  */
+/* and the activation bytes (undefined); here its missing elements count as  */
+/* zero, the library's defined form.                                         */
 HOT static void w4a8_rows(const uint8_t *xu, float sx, const uint8_t *w, const float *s,
                           int blocked, const float *bias, float *y, int64_t r0, int64_t r1,
                           int64_t k) {
-    int64_t ng = k / 64;
+    int64_t ng = (k + 63) / 64, bpr = (k + 1) / 2;
     for (int64_t r = r0; r < r1; ++r) {
         float acc[L16] = {0};
         for (int64_t g = 0; g < ng; ++g) {
-            const uint8_t *nib = blocked ? w + (r * ng + g) * 34 : w + r * (k / 2) + g * 32;
+            const uint8_t *nib = blocked ? w + (r * ng + g) * 34 : w + r * bpr + g * 32;
             float sw = blocked ? v2_scale(nib) : s[r * ng + g];
             float sc = sx * sw;
             for (int j = 0; j < L16; ++j) {
                 int32_t t = 0;
                 for (int e = 4 * j; e < 4 * j + 4; ++e) {
+                    if (g * 64 + e >= k) break;
                     uint8_t b = nib[e / 2];
                     int32_t q = (int32_t)((e & 1) ? (b >> 4) : (b & 0x0F)) - 8;
                     t += ((int32_t)xu[g * 64 + e] - 128) * q;
@@ -509,9 +522,11 @@ ORC_API void orc_quantize_int4_rows(const float *w, uint8_t *packed, float *s, i
             for (int h = 0; h < 2; ++h) {
                 int64_t e = 2 * b + h;
                 if (e < k) {
+                    /* f32::round, then clamp, which keeps a NaN, and `as i8`, */
+                    /* which maps it to 0 (fused_ops.rs:620-629)               */
                     float v = roundf(row[e] * inv);
                     v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
-                    q[h] = (int)v + 8;
+                    q[h] = isnan(v) ? 8 : (int)v + 8;
                 } else {
                     q[h] = 8;
                 }
@@ -720,14 +735,16 @@ ORC_API void orc_rope_apply(float *head, const float *c, const float *s, int64_t
 /* a12: GQA decode attention for one query head, decoder.rs:1148-1213.        */
 /* kv_base points at [seq, hd] rows of this head's KV.                       */
 /* ------------------------------------------------------------------------ */
+/* max_pos: the native step's cap, 32768 (decoder.rs:1179-1184); the oracle   */
+/* decoder takes another value only through orc_decoder_set_attention_cap.   */
 static void attend_head(const float *q, const float *kb, const float *vb, float *out,
-                        float *scores, int64_t seq_len, int64_t hd) {
+                        float *scores, int64_t seq_len, int64_t hd, int64_t max_pos) {
     for (int64_t d = 0; d < hd; ++d) out[d] = 0.f;
     if (seq_len == 1) {
         memcpy(out, vb, (size_t)hd * sizeof(float));
         return;
     }
-    int64_t cap = seq_len < 32768 ? seq_len : 32768;
+    int64_t cap = seq_len < max_pos ? seq_len : max_pos;
     float scale = 1.0f / sqrtf((float)hd);
     float mx = -INFINITY;
     for (int64_t t = 0; t < cap; ++t) {
@@ -782,7 +799,7 @@ static void attend_head_layer(const float *q, const float *kb, const float *vb, 
 /* q: [hq, hd]; k_cache/v_cache: [hkv, max_seq, hd]; out: [hq, hd]. */
 static void attention_any(const float *q, const float *k_cache, const float *v_cache,
                           float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
-                          int64_t seq_len, int layer_path) {
+                          int64_t seq_len, int layer_path, int64_t max_pos) {
     int64_t per = hq / (hkv > 0 ? hkv : 1);
     if (per < 1) per = 1;
 #pragma omp parallel
@@ -796,7 +813,8 @@ static void attention_any(const float *q, const float *k_cache, const float *v_c
                                   v_cache + kvh * max_seq * hd, out + h * hd, scores, seq_len, hd);
             else
                 attend_head(q + h * hd, k_cache + kvh * max_seq * hd,
-                            v_cache + kvh * max_seq * hd, out + h * hd, scores, seq_len, hd);
+                            v_cache + kvh * max_seq * hd, out + h * hd, scores, seq_len, hd,
+                            max_pos);
         }
         free(scores);
     }
@@ -805,14 +823,14 @@ static void attention_any(const float *q, const float *k_cache, const float *v_c
 ORC_API void orc_attention(const float *q, const float *k_cache, const float *v_cache,
                            float *out, int64_t hq, int64_t hkv, int64_t hd, int64_t max_seq,
                            int64_t seq_len) {
-    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 0);
+    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 0, 32768);
 }
 
 /* The per-layer steps' attention (attend_head_layer) for q [hq, hd]. */
 ORC_API void orc_attention_layer(const float *q, const float *k_cache, const float *v_cache,
                                  float *out, int64_t hq, int64_t hkv, int64_t hd,
                                  int64_t max_seq, int64_t seq_len) {
-    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 1);
+    attention_any(q, k_cache, v_cache, out, hq, hkv, hd, max_seq, seq_len, 1, 32768);
 }
 
 /* a17: greedy argmax, decoder.rs:914-925 (strict >, lowest index wins).      */
@@ -1041,6 +1059,7 @@ typedef struct {
     int wkind, lmkind;
     int use_v2;     /* decoder.rs:361-390 */
     int layer_path; /* numerics of the per-layer Python path (orc_decoder_set_layer_path) */
+    int64_t attn_cap; /* native step: positions scored, 32768 (orc_decoder_set_attention_cap) */
     uint8_t *lm_w2;
     float eps;
     const float *embed, *final_norm;
@@ -1061,6 +1080,7 @@ ORC_API orc_decoder *orc_decoder_create(int64_t L, int64_t H, int64_t I, int64_t
     orc_decoder *d = (orc_decoder *)calloc(1, sizeof(orc_decoder));
     d->L = L; d->H = H; d->I = I; d->hq = hq; d->hkv = hkv; d->hd = hd; d->V = V;
     d->gs = gs; d->max_seq = max_seq; d->eps = eps; d->wkind = wkind; d->lmkind = lmkind;
+    d->attn_cap = 32768;
     d->embed = embed; d->final_norm = final_norm; d->lm_w = lm_w; d->lm_s = lm_s;
     d->layers = (orc_layer *)calloc((size_t)L, sizeof(orc_layer));
     size_t kvn = (size_t)L * (size_t)hkv * (size_t)max_seq * (size_t)hd;
@@ -1156,6 +1176,13 @@ ORC_API void orc_decoder_set_rope_tables(orc_decoder *d, const float *cos_t,
 /* kernels as the native step.  0 (default): RustQwenDecoder::step_internal. */
 ORC_API void orc_decoder_set_layer_path(orc_decoder *d, int on) { d->layer_path = on; }
 
+/* The native step scores positions 0 .. min(offset + 1, cap) - 1; the        */
+/* reference's cap is the constant 32768 (decoder.rs:1179-1184), the default. */
+/* Another value lets a test show the cap's effect on a short cache.          */
+ORC_API void orc_decoder_set_attention_cap(orc_decoder *d, int64_t cap) {
+    d->attn_cap = cap > 0 ? cap : 32768;
+}
+
 /* projection_gemv, decoder.rs:1029-1049 (v1 path). */
 static void proj(const orc_decoder *d, int kind, const float *x, const void *w, const float *s,
                  const float *b, float *y, int64_t n, int64_t k) {
@@ -1200,7 +1227,8 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
             memcpy(kc + (h * d->max_seq + offset) * hd, k + h * hd, (size_t)hd * 4);
             memcpy(vc + (h * d->max_seq + offset) * hd, v + h * hd, (size_t)hd * 4);
         }
-        attention_any(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1, d->layer_path);
+        attention_any(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1, d->layer_path,
+                      d->attn_cap);
         if (d->use_v2)
             orc_gemv_w4_v2(d->att, y->o_w2, NULL, d->o, H, qd);
         else

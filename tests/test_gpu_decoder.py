@@ -35,7 +35,7 @@ def small(**kw):
 
 
 def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=256,
-               check_generate=True, layer_path=False):
+               check_generate=True, layer_path=False, cap=None):
     print(f"case decoder cfg={cfg} wkind={wkind} lmkind={lmkind} gs={gs} prefill={prefill} "
           f"steps={steps} layer_path={layer_path}", flush=True)
     w = synth.decoder_weights(cfg, seed, wkind, lmkind, gs)
@@ -45,10 +45,14 @@ def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=
                 group_size=gs, max_seq=max_seq, rope_theta=cfg["rope_theta"], eps=cfg["eps"],
                 wkind=wkind, lmkind=lmkind)
     tabs = rotary_tables_f32(max_seq, cfg["head_dim"], cfg["rope_theta"]) if layer_path else None
-    ref = O.Decoder(w, ocfg, rope_tables=tabs, layer_path=layer_path)
+    ref = O.Decoder(w, ocfg, rope_tables=tabs, layer_path=layer_path,
+                    attention_cap=cap or 32768)
     dec = decoder_from_weights(w, cfg, group_size=gs, max_seq_len=max_seq)
+    if cap:
+        dec.set_attention_cap(cap)
     if layer_path:
         dec.set_rope_tables(*tabs)
+        dec.set_attention_cap(0)   # the per-layer path scores every position
     if prefill:
         kv = synth.kv_prefill(cfg, seed, prefill, max_seq)
         for li, (k, v) in enumerate(kv):
@@ -100,6 +104,37 @@ def run_parity(cfg, seed, wkind=4, lmkind=4, gs=32, prefill=0, steps=8, max_seq=
 ])
 def test_small_decoder_variants(cuda, variant):
     run_parity(small(), 5, prefill=37, steps=12, **variant)
+
+
+@pytest.mark.parametrize("layer_path", [False, True])
+def test_attention_cap_past_32768(cuda, layer_path):
+    """Steps at positions 32766..32771 of a 32832-position cache: the native step
+    scores only the first 32768 positions (decoder.rs:1179-1184), the per-layer
+    path (attention cap 0) every position; each against the oracle's same mode.
+    (Over a 32k-position cache the few positions past the cap move the logits
+    by about 1e-5, under the bar: the cap-40 case below is the sharp check.)"""
+    run_parity(small(), 23, prefill=32766, steps=6, max_seq=32832, layer_path=layer_path)
+
+
+def test_attention_cap_small(cuda):
+    """Cap 40 on a short cache, steps at positions 37..48 (the prefix and the
+    steps' own positions past 40 drop out of the scores): against the oracle
+    with the same cap, and far from the uncapped oracle."""
+    run_parity(small(), 29, prefill=37, steps=12, cap=40)
+    cfg = small()
+    w = synth.decoder_weights(cfg, 29, 4, 4, 32)
+    ocfg = dict(num_layers=2, hidden=256, intermediate=512, num_heads=4, num_kv_heads=2,
+                head_dim=64, vocab=1000, group_size=32, max_seq=256, rope_theta=1e6, eps=1e-6,
+                wkind=4, lmkind=4)
+    a, b = O.Decoder(w, ocfg, attention_cap=40), O.Decoder(w, ocfg)
+    kv = synth.kv_prefill(cfg, 29, 45, 256)
+    for li, (k, v) in enumerate(kv):
+        a.copy_kv(li, k, v, 45)
+        b.copy_kv(li, k, v, 45)
+    la, lb = a.step(3, 45), b.step(3, 45)
+    assert float(np.abs(la - lb).max() / np.abs(lb).max()) > 1e-3
+    a.close()
+    b.close()
 
 
 @pytest.mark.parametrize("variant", [

@@ -69,6 +69,17 @@ def test_quantize_weight_int4_bit_exact(cuda, n, k):
         tb.quantize_weight_int4(torch.randn(16, device=cuda))
 
 
+def test_quantize_weight_int4_non_finite(cuda):
+    """NaN and infinite weights give the reference's nibbles (NaN -> 8; an
+    infinite weight zeroes its row), bit-exact against the oracle."""
+    print("case quantize_weight_int4 non-finite", flush=True)
+    w = np.float32([[np.nan, 1.0, -7.0, 7.0], [np.inf, 1.0, -2.0, 0.5], [-np.inf, np.nan, 3.0, 0.0]])
+    qr, sr = O.quantize_int4_rows(w)
+    q, s = tb.quantize_weight_int4(T(w, cuda))
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(s.cpu().numpy(), sr)
+
+
 @pytest.mark.parametrize("m,n,k,gs", [
     (1, 300, 1000, 40),     # group 40, K % 32 != 0
     (2, 256, 4096, 128),    # power-of-two group 128 on the streaming GEMV

@@ -160,3 +160,33 @@ def test_capture_on_a_fresh_stream(cuda):
         torch.cuda.synchronize()
         ref = O.swiglu_mlp_w4(xv, gw, gsc, uw, usc, dw, dsc, group_size=32)
         assert rel(y.cpu().numpy(), ref) < 1e-4, rep
+
+
+def test_release_stream_workspace(cuda):
+    """A stream's workspace is freed on request (device memory comes back) and a
+    later call on the same stream gets a new one."""
+    print("case release_stream_workspace", flush=True)
+    g = synth.rng(57)
+    K, I = 4096, 14336
+    x = synth.activations(g, 8, K)
+    gw, gsc = w4(g, I, K)
+    uw, usc = w4(g, I, K)
+    dw, dsc = w4(g, K, I)
+    ref = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, group_size=32)
+    T = lambda a: torch.from_numpy(a).to(cuda)
+    args = [T(a) for a in (x, gw, gsc, uw, usc, dw, dsc)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y1 = tb.fused_swiglu_mlp_w4a32(args[0], args[1], args[2], None, args[3], args[4], None,
+                                       args[5], args[6], None, 32)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(cuda)[0]
+    tb.release_stream_workspace(s)
+    free1 = torch.cuda.mem_get_info(cuda)[0]
+    assert free1 > free0
+    tb.release_stream_workspace(s)   # nothing left: a no-op
+    with torch.cuda.stream(s):
+        y2 = tb.fused_swiglu_mlp_w4a32(args[0], args[1], args[2], None, args[3], args[4], None,
+                                       args[5], args[6], None, 32)
+    torch.cuda.synchronize()
+    assert rel(y1.cpu().numpy(), ref) < 1e-4 and rel(y2.cpu().numpy(), ref) < 1e-4

@@ -141,6 +141,31 @@ def test_vnni_semantics_g64(cuda, m, n, k):
     assert rel(y1, O.gemm_w4(x, w, s, bias, group_size=64)) > 10 * TOL
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 64, 20480), (1, 48, 1000), (3, 40, 20480)])
+def test_vnni_semantics_any_shape(cuda, m, n, k):
+    """Group-64 shapes outside the streaming kernels (K past the GEMV's split,
+    a short last group with K % 16 != 0) take the any-shape GEMV, and the W4A8
+    activation rounding applies there too (gemv.rs:1559-1563)."""
+    print(f"case vnni any-shape m={m} n={n} k={k}", flush=True)
+    g = synth.rng(97, m, n, k)
+    ng = (k + 63) // 64
+    nib = g.integers(0, 16, (n, k)).astype(np.uint8)
+    w = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    s = (np.abs(g.normal(0, 0.02, (n, ng))) + 1e-3).astype(np.float32)
+    x = synth.activations(g, m, k)
+    prev = tb.set_vnni_semantics(True)
+    try:
+        y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), None,
+                                    group_size=64).cpu().numpy()
+    finally:
+        tb.set_vnni_semantics(prev)
+    ref = O.gemm_w4a8_g64(x, w, s)
+    e = rel(y, ref)
+    print(f"max rel err {e:.3g}", flush=True)
+    assert e < TOL
+    assert rel(y, O.gemm_w4(x, w, s, None, group_size=64)) > 10 * TOL
+
+
 def test_vnni_semantics_leaves_g32_and_default(cuda):
     g = synth.rng(96)
     w, s = synth.int4_weight(g, 128, 512, 32)

@@ -289,6 +289,18 @@ def test_quantize_int4_rows_closed_form():
     assert list(O.unpack_int4(q, k)[2, :3]) == [7, 4, -4] and not O.unpack_int4(q, k)[1].any()
 
 
+def test_quantize_int4_rows_non_finite():
+    """A NaN skips the row maximum (`a > max_abs` is false), survives round and
+    clamp, and `as i8` makes it 0: nibble 8.  An infinite weight makes the scale
+    infinite and inv 0, so every element of its row becomes 0 * w: NaN for the
+    infinite one (nibble 8), 0 for the rest (fused_ops.rs:607-629)."""
+    w = np.float32([[np.nan, 1.0, -7.0, 7.0], [np.inf, 1.0, -2.0, 0.5], [-np.inf, np.nan, 3.0, 0.0]])
+    q, s = O.quantize_int4_rows(w)
+    assert s[0] == 1.0 and np.isinf(s[1]) and np.isinf(s[2])
+    assert O.unpack_int4(q, 4).tolist() == [[0, 1, -7, 7], [0, 0, 0, 0], [0, 0, 0, 0]]
+    assert q[0, 0] & 15 == 8
+
+
 # ------------------------------------------------------------------- int8 ---
 
 def test_dot_i8_reference_kat():
@@ -451,6 +463,31 @@ def test_attention_layer_vs_sdpa(hq, hkv, hd, seq):
     assert rel(out, ref) < 1e-5
     if seq == 1:
         assert np.array_equal(out, np.repeat(vc[:, 0], hq // hkv, 0))
+
+
+def test_attention_native_cap_32768():
+    """The native step scores only positions 0 .. min(seq_len, 32768) - 1
+    (decoder.rs:1179-1184); the per-layer path scores them all.  Keys past
+    32768 are made to dominate the scores, so an uncapped attention lands far
+    from SDPA over the first 32768 keys and a capped one within 1e-5."""
+    g = np.random.default_rng(32768)
+    hq, hkv, hd, seq = 4, 2, 64, 32800
+    q = g.standard_normal((hq, hd), dtype=np.float32) * np.float32(0.1)
+    kc = g.standard_normal((hkv, seq, hd), dtype=np.float32)
+    vc = g.standard_normal((hkv, seq, hd), dtype=np.float32)
+    kc[:, 32768:] = np.repeat(q[::hq // hkv, None, :] * 200, seq - 32768, 1)   # huge scores
+    vc[:, 32768:] = 1000.0
+    T = lambda a: torch.from_numpy(a.astype(np.float64))
+
+    def sdpa(n):
+        return F.scaled_dot_product_attention(T(q)[None, :, None], T(kc[:, :n])[None],
+                                              T(vc[:, :n])[None], enable_gqa=True)[0, :, 0].numpy()
+
+    first = sdpa(32768)
+    assert rel(O.attention(q, kc, vc, seq), first) < 1e-5
+    assert rel(O.attention(q, kc, vc, 32768), first) < 1e-5
+    whole = O.attention_layer(q, kc, vc, seq)
+    assert rel(whole, sdpa(seq)) < 1e-5 and rel(whole, first) > 1.0
 
 
 def test_attention_special_cases():

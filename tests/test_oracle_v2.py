@@ -152,11 +152,19 @@ def test_gemv_v2_reference_cases():
 # ------------------------------------------------------------------ W4A8 ---
 
 def test_quantize_act_closed_forms():
-    # s_x = 127 / 127 = 1 exactly: x on the integer grid maps to itself, ties to even
-    x = np.float32([127.0, -127.0, 0.0, 2.5, 3.5, -2.5, 1.49, 100.0])
+    # s_x = 127 / 127 = 1 exactly: x on the integer grid maps to itself.  The
+    # first 16 * (k / 16) elements round ties to even (cvtps_epi32), the tail
+    # rounds them away from zero (f32::round, gemv.rs:1383-1386).
+    vals = [127.0, -127.0, 0.0, 2.5, 3.5, -2.5, 1.49, 100.0]
+    x = np.float32(vals + vals + vals[:4] + [2.5, -2.5, 0.5, -0.5])   # k = 24: 16 + 8 tail
     u, sx = O.quantize_act_u8(x)
     assert sx == 1.0
-    assert list(u.astype(int) - 128) == [127, -127, 0, 2, 4, -2, 1, 100]
+    body = [127, -127, 0, 2, 4, -2, 1, 100]
+    assert list(u.astype(int) - 128) == body + body + [127, -127, 0, 3, 3, -3, 1, -1]
+    u8, _ = O.quantize_act_u8(np.float32(vals))   # k = 8: all tail
+    assert list(u8.astype(int) - 128) == [127, -127, 0, 3, 4, -3, 1, 100]
+    un, _ = O.quantize_act_u8(np.float32([np.nan] + (vals + vals)[:15] + [np.nan, 1.0]))
+    assert un[0] == 128 and un[16] == 128
     # the largest |x| maps to +-127 whatever its scale
     rng = np.random.default_rng(1)
     for _ in range(20):
@@ -188,6 +196,30 @@ def test_w4a8_gemv(n, k):
     yb = O.gemm_w4a8_g64(x, O.pack_v1_to_v2(wq, sc, k), None, bias, blocked=True)
     y16 = O.gemm_w4a8_g64(x, wq, _f16_round(sc), bias)
     assert np.array_equal(yb.view(np.uint32), y16.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(24, 1000), (9, 20504)])
+def test_w4a8_gemv_short_last_group(n, k):
+    """K % 64 != 0 (and K % 16 != 0 for 1000): the reference's VNNI row reads its
+    last group past the row (undefined); the oracle counts the missing elements
+    as zero.  Float64 over exact integer group sums, with the activation bytes
+    from the quantizer pinned above."""
+    rng = np.random.default_rng(k)
+    ng = (k + 63) // 64
+    nib = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    wq = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    sc = (np.abs(rng.normal(0, 0.02, (n, ng))) + 1e-3).astype(np.float32)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    y = O.gemm_w4a8_g64(x, wq, sc)
+    q = nib.astype(np.float64) - 8
+    for i in range(2):
+        u, sx = O.quantize_act_u8(x[i])
+        prod = q * (u.astype(np.float64) - 128)
+        pad = np.zeros((n, ng * 64))
+        pad[:, :k] = prod
+        grp = pad.reshape(n, ng, 64).sum(-1)
+        want = (grp * (np.float64(sx) * sc.astype(np.float64))).sum(-1)
+        assert rel(y[i], want) < 1e-6
 
 
 def test_w4a8_equals_w4a32_on_the_grid():

@@ -43,10 +43,12 @@ def call(name, t, m, k, inter, gs, dev):
 
 
 def test_noalloc_matches_allocating_entry(cuda):
-    # first a Llama-3-8B MLP at M = 8 (small-batch f16 MFMA), then smaller ones
-    # at M = 3 (same path) and M = 1 (the fused record path): the scratch keeps
-    # the previous call's contents.
-    for seed, m, k, inter in ((61, 8, 4096, 14336), (63, 3, 1024, 2048), (62, 1, 1024, 2048)):
+    # first Llama-3-8B MLPs at M = 16 and 8 (small-batch f16 MFMA; M = 16 needs
+    # 11.3 MB of the 16 MiB scratch), then smaller ones at M = 3 (same path) and
+    # M = 1 (the GEMV record path): the scratch keeps the previous call's
+    # contents.
+    for seed, m, k, inter in ((65, 16, 4096, 14336), (61, 8, 4096, 14336), (63, 3, 1024, 2048),
+                              (62, 1, 1024, 2048)):
         print(f"case noalloc mlp m={m} k={k} inter={inter}", flush=True)
         t, ref = mlp_case(cuda, seed, m, k, inter, 32)
         rc, got = call("tb_fused_swiglu_mlp_w4a32_noalloc", t, m, k, inter, 32, cuda)
@@ -60,8 +62,8 @@ def test_noalloc_matches_allocating_entry(cuda):
 
 
 def test_noalloc_rejects_oversized_scratch(cuda):
-    # M = 32 runs the FP32-MFMA pair, whose split-K partials exceed the 8 MiB scratch
-    m, k, inter = 32, 4096, 14336
+    # M = 64 runs the FP32-MFMA pair, whose split-K partials exceed the 16 MiB scratch
+    m, k, inter = 64, 4096, 14336
     print(f"case noalloc size limit m={m} k={k} inter={inter}", flush=True)
     dev = cuda
     x = torch.zeros((m, k), device=dev)
@@ -76,3 +78,29 @@ def test_noalloc_rejects_oversized_scratch(cuda):
         k, 32, torch.cuda.current_stream(dev).cuda_stream)
     assert rc == _lib.TB_ERR_UNSUPPORTED
     assert b"scratch" in _lib.lib().tb_last_error()
+
+
+def test_noalloc_allocates_nothing(cuda):
+    """Device memory is unchanged across a no-alloc call on a stream the library
+    has never seen (a new stream would get a fresh workspace from the
+    allocating entry).  The kernels are loaded first through the allocating
+    entry, and the output is allocated before the measurement."""
+    m, k, inter = 12, 4096, 14336
+    print(f"case noalloc memory check m={m} k={k} inter={inter}", flush=True)
+    t, ref = mlp_case(cuda, 66, m, k, inter, 32)
+    rc, _ = call("tb_fused_swiglu_mlp_w4a32", t, m, k, inter, 32, cuda)
+    _lib.check(rc)
+    x, gw, gsc, uw, usc, ub, dw, dsc, r = t
+    out = torch.empty((m, k), dtype=torch.float32, device=cuda)
+    stream = torch.cuda.Stream(cuda)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(cuda)[0]
+    P = lambda a: a.data_ptr()
+    rc = _lib.lib().tb_fused_swiglu_mlp_w4a32_noalloc(
+        P(x), P(gw), P(gsc), None, P(uw), P(usc), P(ub), P(dw), P(dsc), None, P(r), P(out), m, k,
+        inter, k, 32, stream.cuda_stream)
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info(cuda)[0]
+    assert free1 == free0, f"device memory changed by {free0 - free1} bytes"
+    assert rel(out.cpu().numpy(), ref) < 1e-4

@@ -28,6 +28,7 @@ from .quantization import (
     quantize_weight_int4_grouped_v2,
     quantize_weight_int8,
     set_vnni_semantics,
+    release_stream_workspace,
     unpack_rows_w4a32_group64_v2_to_v1,
     w4a32_grouped_linear,
     w4a32_grouped_linear_residual,
@@ -66,6 +67,7 @@ __all__ = [
     "dequantize_int4_grouped_v2",
     "pack_rows_w4a32_group64_v1_to_v2",
     "set_vnni_semantics",
+    "release_stream_workspace",
     "unpack_rows_w4a32_group64_v2_to_v1",
     "sample_logits",
     "sample_uniform",

@@ -45,6 +45,7 @@ _SIGS = {
     "tb_pack_rows_w4a32_group64_v1_to_v2": [_p, _p, _p, _i64, _i64, _p],
     "tb_dequantize_int4_grouped_v2": [_p, _p, _i64, _i64, _p],
     "tb_set_vnni_semantics": [C.c_int],
+    "tb_release_stream_workspace": [C.c_void_p],
     "tb_quantize_weight_int4_grouped": [_p, _p, _p, _i64, _i64, _i64, _p],
     "tb_quantize_weight_int8": [_p, _p, _p, _i64, _i64, _p],
     "tb_unpack_rows_w4a32_group64_v2_to_v1": [_p, _p, _p, _i64, _i64, _p],

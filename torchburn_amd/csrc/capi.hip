@@ -36,10 +36,12 @@ struct StreamScratch {
     std::mutex mu;        // held by the op enqueueing on this stream
     void *ptr = nullptr;
     size_t size = 0;
+    // buffers this workspace outgrew: a graph captured earlier may still read
+    // them, so they are kept until tb_release_stream_workspace or process exit
+    std::vector<void *> retired;
 };
-std::mutex g_ws_mu;       // guards the two containers below
+std::mutex g_ws_mu;       // guards g_ws
 std::map<std::pair<int, uintptr_t>, std::unique_ptr<StreamScratch>> g_ws;
-std::vector<void *> g_retired;   // replaced buffers: kept until the process exits
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -113,10 +115,7 @@ int workspace(size_t bytes, hipStream_t st, WsLease &out) {
         const hipError_t e = hipMalloc(&p, sz);
         TB_HIP(hipThreadExchangeStreamCaptureMode(&mode));
         TB_HIP(e);
-        if (sc->ptr) {
-            std::lock_guard<std::mutex> lk(g_ws_mu);
-            g_retired.push_back(sc->ptr);
-        }
+        if (sc->ptr) sc->retired.push_back(sc->ptr);
         sc->ptr = p;
         sc->size = sz;
     }
@@ -263,27 +262,36 @@ static int linear_w4(const float *x, const uint8_t *w, const float *s, bool v2,
     // form is faster, 25.7 against 30.2 us)
     const bool lb = !v2 && limb_fast(x, w, m, n, k, gs, scale_mode != 0, false) &&
                     !(m == 16 && n <= 4096 && k <= 4096);
-    if (!v2 && !lb && !w4_fast(x, w, m, k, gs, scale_mode != 0))
-        return generic(x, w, s, scale_mode, bias, nullptr, nullptr, 0, nullptr, res, out, m, n, k,
-                       scale_mode ? k : gs, 4, st);
+    const bool any_shape = !v2 && !lb && !w4_fast(x, w, m, k, gs, scale_mode != 0);
+    // W4A8 applies to every group-64 projection, whichever kernel takes the
+    // shape (gemv.rs:1559-1563).  With K % 64 != 0 the reference's VNNI row
+    // reads its last group past the row and the activation bytes (undefined);
+    // here the missing elements of that group count as zero.
     const bool a8 = gs == 64 && scale_mode == 0 && g_vnni.load(std::memory_order_relaxed) != 0;
     const size_t xb = a8 ? up256((size_t)m * (size_t)k * sizeof(float)) : 0;
     const int epi = res ? EPI_RESID : EPI_PLAIN;
-    const bool mf = !lb && m >= mfma_min_m();
-    const size_t rest = lb ? up256(limb_records_bytes((int)m, (int)k)) +
-                                 limb_partials_bytes((int)m, (int)n, (int)k, false)
-                           : mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
-                                : xq_bytes(m, k);
-    WsLease lease;
-    int rc = workspace(xb + rest, st, lease);
-    if (rc) return rc;
-    void *ws = lease.ptr;
+    const bool mf = !lb && !any_shape && m >= mfma_min_m();
+    const size_t rest = any_shape ? 0
+                        : lb ? up256(limb_records_bytes((int)m, (int)k)) +
+                                   limb_partials_bytes((int)m, (int)n, (int)k, false)
+                        : mf ? w4_mfma_partials_bytes((int)m, (int)n, (int)k, false)
+                             : xq_bytes(m, k);
     const float *xin = x;
-    if (a8) {
-        if ((rc = act_u8(x, static_cast<float *>(ws), m, k, st))) return rc;
-        xin = static_cast<const float *>(ws);
+    void *tail = nullptr;
+    int rc;
+    WsLease lease;
+    if (xb + rest) {
+        if ((rc = workspace(xb + rest, st, lease))) return rc;
+        void *ws = lease.ptr;
+        if (a8) {
+            if ((rc = act_u8(x, static_cast<float *>(ws), m, k, st))) return rc;
+            xin = static_cast<const float *>(ws);
+        }
+        tail = static_cast<char *>(ws) + xb;
     }
-    void *tail = static_cast<char *>(ws) + xb;
+    if (any_shape)
+        return generic(xin, w, s, scale_mode, bias, nullptr, nullptr, 0, nullptr, res, out, m, n,
+                       k, scale_mode ? k : gs, 4, st);
     if (lb) {
         uint8_t *rec = static_cast<uint8_t *>(tail);
         float *part =
@@ -502,7 +510,7 @@ static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
 // kNoAllocScratchBytes until the process ends.  `scratch` names the host-side
 // stand-in of the array; its device address (per device) comes from
 // hipGetSymbolAddress and is the only form passed to kernels.
-constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
@@ -687,6 +695,28 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     TB_HIP(hipStreamSynchronize(st));
     *token_out = ho.token;
     if (u_out) *u_out = ho.u;
+    return TB_OK;
+}
+
+int tb_release_stream_workspace(void *stream) {
+    int dev = 0;
+    TB_HIP(hipGetDevice(&dev));
+    std::unique_ptr<StreamScratch> sc;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        auto it = g_ws.find({dev, reinterpret_cast<uintptr_t>(stream)});
+        if (it == g_ws.end()) return TB_OK;
+        sc = std::move(it->second);
+        g_ws.erase(it);
+    }
+    {
+        // an op still enqueueing on this stream finishes first
+        std::lock_guard<std::mutex> lk(sc->mu);
+    }
+    // Work already enqueued on the stream may still read the buffers.
+    TB_HIP(hipDeviceSynchronize());
+    for (void *p : sc->retired) TB_HIP(hipFree(p));
+    if (sc->ptr) TB_HIP(hipFree(sc->ptr));
     return TB_OK;
 }
 

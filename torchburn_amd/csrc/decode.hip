@@ -168,14 +168,14 @@ __global__ __launch_bounds__(256) void k_attn(const DecState *__restrict__ st,
                                               const float *__restrict__ kc,
                                               const float *__restrict__ vc,
                                               float *__restrict__ part, int hq, int hkv,
-                                              int max_seq, int nsplit, float scale) {
+                                              int max_seq, int nsplit, float scale, int cap) {
     constexpr int T = kAttnTile, KP = HD + 4, C4 = HD / 4;
     constexpr int NV = T * C4 / 256;   // float4 of K (and of V) per thread
     static_assert(T <= 64 && NV >= 1, "tile of at most one wave of positions");
     extern __shared__ float sm[];
     const int kvh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
     const int G = hq / hkv;
-    const int seq = st->pos + 1;
+    const int seq = min(st->pos + 1, cap);
     const int t0 = sp * T;
     if (t0 >= seq) return;   // tile past the sequence: the merge never reads it
     const int tn = min(T, seq - t0);
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
                                                   const float *__restrict__ kc,
                                                   const float *__restrict__ vc,
                                                   float *__restrict__ part, int G, int max_seq,
-                                                  int nsplit, float scale) {
+                                                  int nsplit, float scale, int cap) {
     constexpr int T = kAttnTile;
     constexpr int PW = T / 4;              // positions per wave
     constexpr int C4 = HD / 4;             // lanes per position row
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
 #pragma unroll
     for (int g = 0; g < GP; ++g)
         qr[g] = g < G ? q4[(size_t)g * C4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    const int seq = st->pos + 1;
+    const int seq = min(st->pos + 1, cap);
     if ((int)blockIdx.y * T >= seq) return;   // no tile: the merge never reads this partial
     // the running (o, m, l) of this thread's (head, column) of the final fold
     // (G * C4 <= 256: one per thread at most)
@@ -458,14 +458,15 @@ template <int HD>
 __global__ __launch_bounds__(64) void k_attn_merge(const DecState *__restrict__ st,
                                                    const float *__restrict__ part,
                                                    float *__restrict__ out,
-                                                   uint32_t *__restrict__ xq, int nsplit) {
+                                                   uint32_t *__restrict__ xq, int nsplit,
+                                                   int cap) {
     constexpr int C4 = HD / 4;
     constexpr size_t rec = HD + 4;
     __shared__ float sw[kMaxTiles];
     __shared__ float sacc[2 * HD];
     __shared__ float so[HD];
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int used = (st->pos + 1 + kAttnTile - 1) / kAttnTile;
+    const int used = (min(st->pos + 1, cap) + kAttnTile - 1) / kAttnTile;
     const float *ph = part + (size_t)h * nsplit * rec;
     float M = -FLT_MAX;
     for (int s = tid; s < used; s += 64) M = fmaxf(M, ph[s * rec + HD]);
@@ -531,7 +532,8 @@ template <int HD>
 __global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restrict__ st,
                                                          const float *__restrict__ part,
                                                          float *__restrict__ out,
-                                                         uint32_t *__restrict__ xq, int nsplit) {
+                                                         uint32_t *__restrict__ xq, int nsplit,
+                                                         int cap) {
     constexpr int NSG = 8, NB = 12;
     constexpr size_t rec = HD + 4;
     __shared__ float4 so4[NSG][8];
@@ -539,7 +541,7 @@ __global__ __launch_bounds__(64) void k_attn_merge_chunk(const DecState *__restr
     const int h = blockIdx.x, ck = blockIdx.y, tid = threadIdx.x;
     const int c = tid & 7, sg = tid >> 3;
     // partials written: one per attention block that had a tile
-    const int used = min(nsplit, (st->pos + 1 + kAttnTile - 1) / kAttnTile);
+    const int used = min(nsplit, (min(st->pos + 1, cap) + kAttnTile - 1) / kAttnTile);
     const float *ph = part + (size_t)h * nsplit * rec;
     float M = -FLT_MAX, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1038,7 +1040,8 @@ int attn_nsplit(int max_seq) { return (max_seq + kAttnTile - 1) / kAttnTile; }
 
 int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
                      float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
-                     hipStream_t s) {
+                     int cap, hipStream_t s) {
+    TB_REQUIRE(cap >= 1, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: attention cap must be positive");
     const int ns = attn_nsplit(max_seq);
     TB_REQUIRE(ns <= kMaxTiles, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: max_seq_len above " + std::to_string(kMaxTiles * kAttnTile));
@@ -1055,7 +1058,7 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
         const int nb = std::min(ns, kAttnMaxSplits);
 #define TB_ATTN_REG(HD, GP)                                                                    \
     hipLaunchKernelGGL((k_attn_reg<HD, GP>), dim3(hkv, nb), dim3(256), 0, s, st, qkv, kc, vc, \
-                       part, G, max_seq, nb, scale)
+                       part, G, max_seq, nb, scale, cap)
         if (hd == 128) {
             if (gp == 1) TB_ATTN_REG(128, 1);
             else if (gp == 2) TB_ATTN_REG(128, 2);
@@ -1063,7 +1066,7 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
             else TB_ATTN_REG(128, 8);
             TB_LAUNCHED();
             hipLaunchKernelGGL(k_attn_merge_chunk<128>, dim3(hq, 4), dim3(64), 0, s, st, part, out,
-                               xq, nb);
+                               xq, nb, cap);
         } else {
             if (gp == 1) TB_ATTN_REG(64, 1);
             else if (gp == 2) TB_ATTN_REG(64, 2);
@@ -1071,19 +1074,21 @@ int launch_attention(const DecState *st, const float *qkv, const float *kc, cons
             else TB_ATTN_REG(64, 8);
             TB_LAUNCHED();
             hipLaunchKernelGGL(k_attn_merge_chunk<64>, dim3(hq, 2), dim3(64), 0, s, st, part, out,
-                               xq, nb);
+                               xq, nb, cap);
         }
 #undef TB_ATTN_REG
     } else if (hd == 128) {
         hipLaunchKernelGGL(k_attn<128>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc, part,
-                           hq, hkv, max_seq, ns, scale);
+                           hq, hkv, max_seq, ns, scale, cap);
         TB_LAUNCHED();
-        hipLaunchKernelGGL(k_attn_merge<128>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
+        hipLaunchKernelGGL(k_attn_merge<128>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns,
+                           cap);
     } else if (hd == 64) {
         hipLaunchKernelGGL(k_attn<64>, dim3(hkv, ns), dim3(256), lds, s, st, qkv, kc, vc, part,
-                           hq, hkv, max_seq, ns, scale);
+                           hq, hkv, max_seq, ns, scale, cap);
         TB_LAUNCHED();
-        hipLaunchKernelGGL(k_attn_merge<64>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns);
+        hipLaunchKernelGGL(k_attn_merge<64>, dim3(hq), dim3(64), 0, s, st, part, out, xq, ns,
+                           cap);
     } else {
         return fail(TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: head_dim must be 64 or 128");
     }

@@ -33,10 +33,14 @@ int launch_embed_rec(const DecState *st, const float *embed, float *x, const flo
 int launch_rope_kv(const DecState *st, float *qkv, const float *cos_t, const float *sin_t,
                    float *kc, float *vc, int hq, int hkv, int hd, int max_seq, hipStream_t s);
 int attn_nsplit(int max_seq);
-// part: [hq][attn_nsplit(max_seq)][hd + 4] floats of scratch.
+// part: [hq][attn_nsplit(max_seq)][hd + 4] floats of scratch.  The step at
+// position pos attends positions 0 .. min(pos + 1, cap) - 1: the native step
+// scores at most the first kNativeAttnCap positions (decoder.rs:1179-1184),
+// the per-layer path every position (cap = INT_MAX).
+constexpr int kNativeAttnCap = 32768;
 int launch_attention(const DecState *st, const float *qkv, const float *kc, const float *vc,
                      float *part, float *out, uint32_t *xq, int hq, int hkv, int hd, int max_seq,
-                     hipStream_t s);
+                     int cap, hipStream_t s);
 // Batched prefill: M consecutive positions start .. start+M-1.
 int launch_embed_rows(const int *tok, const float *embed, float *X, int M, int H, hipStream_t s);
 int launch_rmsnorm_rows(const float *X, const float *w, float *Xn, int M, int H, float eps,

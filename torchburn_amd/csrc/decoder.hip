@@ -14,6 +14,7 @@
 // final RMSNorm -> lm_head GEMV -> device argmax.  Token and position live in a
 // device state block, so the same graph replays for every step and a greedy
 // generation runs without host round trips.
+#include <limits.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -63,6 +64,10 @@ struct Decoder {
     // through the v1 GEMV, which streams faster than the 34-byte blocks.
     bool v2 = false;
     bool fused = true;   // RMSNorms fused into the GEMVs (TB_DECODER_UNFUSED=1: separate)
+    // A step at position p attends positions 0 .. min(p + 1, attn_cap) - 1:
+    // the native step's rule (decoder.rs:1179-1184) by default, INT_MAX for the
+    // per-layer path's every-position attention (tb_decoder_set_attention_cap).
+    int attn_cap = kNativeAttnCap;
     // Rows per GEMV block for QKV, O, gate/up, down, lm_head (0 = the GEMV's
     // default; TB_DECODER_J="qkv,o,gu,down,lm" overrides, for tuning sweeps).
     int rj[5] = {0, 0, 0, 0, 0};
@@ -271,7 +276,7 @@ struct Decoder {
                       H, EPI_ROPE, &ra, &fq, rj[0]);
             if (rc) return rc;
             rc = launch_attention(state, qkv, kcl, vcl, part, attn, q4 ? xq_a : nullptr, hq, hkv,
-                                  hd, max_seq, st);
+                                  hd, max_seq, attn_cap, st);
             if (rc) return rc;
             Fuse fo;
             fo.rec_out = q4 ? xq_h : nullptr;
@@ -325,7 +330,7 @@ struct Decoder {
                       tq, H, EPI_ROPE, &ra);
             if (rc) return rc;
             rc = launch_attention(state, qkv, kcl, vcl, part, attn, q4 ? xq_a : nullptr, hq, hkv,
-                                  hd, max_seq, st);
+                                  hd, max_seq, attn_cap, st);
             if (rc) return rc;
             rc = proj(wbits, attn, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H,
                       hq * hd, EPI_RESID);
@@ -372,6 +377,17 @@ struct Decoder {
     }
 
     int ensure_graph() { return exec ? TB_OK : capture(false, &graph, &exec); }
+
+    // Destroys the captured step graphs; the next step captures them again.
+    int drop_graphs() {
+        if (exec) TB_HIP(hipGraphExecDestroy(exec));
+        if (graph) TB_HIP(hipGraphDestroy(graph));
+        if (exec_s) TB_HIP(hipGraphExecDestroy(exec_s));
+        if (graph_s) TB_HIP(hipGraphDestroy(graph_s));
+        exec = exec_s = nullptr;
+        graph = graph_s = nullptr;
+        return TB_OK;
+    }
 
     // ---- Device sampling -----------------------------------------------------
     int sampler_alloc() {
@@ -533,9 +549,14 @@ struct Decoder {
         return w4_mfma(p, epi, pf_part, st);
     }
 
-    bool prefill_batchable(const int64_t *tokens, int64_t n) const {
+    // Positions start .. start + n - 1 attend every earlier position (the
+    // batched attention has no cap), so chunks reaching the cap take the step
+    // loop.
+    bool under_cap(int64_t start, int64_t n) const { return start + n <= (int64_t)attn_cap; }
+
+    bool prefill_batchable(const int64_t *tokens, int64_t n, int64_t start) const {
         static const bool loop_only = getenv("TB_PREFILL_LOOP") != nullptr;
-        if (loop_only || wbits != 4 || n < 16) return false;
+        if (loop_only || wbits != 4 || n < 16 || !under_cap(start, n)) return false;
         for (int64_t i = 0; i < n; ++i)
             if (tokens[i] < 0 || tokens[i] >= V) return false;   // the step's zero-logit rule
         return true;
@@ -1200,7 +1221,7 @@ int tb_decoder_verify(tb_decoder *d, int64_t start_offset, const int64_t *tokens
     TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
                "verify exceeds max_seq_len");
     if (n == 0) return TB_OK;
-    bool batch = d->wbits == 4 && n >= 2;
+    bool batch = d->wbits == 4 && n >= 2 && d->under_cap(start_offset, n);
     for (int64_t i = 0; i < n && batch; ++i) batch = tokens[i] >= 0 && tokens[i] < d->V;
     if (!batch) {
         for (int64_t i = 0; i < n; ++i) {
@@ -1258,7 +1279,7 @@ int tb_decoder_prefill(tb_decoder *d, const int64_t *tokens, int64_t n, int64_t 
     TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
                "prefill " + std::to_string(n) + " tokens at offset " + std::to_string(start_offset) +
                    " exceeds max_seq_len " + std::to_string(d->max_seq));
-    if (d->prefill_batchable(tokens, n)) {
+    if (d->prefill_batchable(tokens, n, start_offset)) {
         int rc = d->prefill_batched(tokens, n, start_offset);
         if (rc) return rc;
     } else {
@@ -1320,6 +1341,16 @@ int tb_decoder_set_seed(tb_decoder *d, uint64_t seed) {
     d->seed = seed;
     d->draws = 0;
     return TB_OK;
+}
+
+int tb_decoder_set_attention_cap(tb_decoder *d, int64_t cap) {
+    TB_REQUIRE(d, TB_ERR_VALUE, "null decoder");
+    TB_REQUIRE(cap >= 0, TB_ERR_VALUE, "attention cap must be >= 0 (0: none)");
+    const int c = (cap == 0 || cap > INT_MAX) ? INT_MAX : (int)cap;
+    if (c == d->attn_cap) return TB_OK;
+    TB_HIP(hipStreamSynchronize(d->st));
+    d->attn_cap = c;
+    return d->drop_graphs();   // the captured steps hold the old cap
 }
 
 int tb_decoder_set_rope_tables(tb_decoder *d, const float *cos_t, const float *sin_t,

@@ -11,6 +11,8 @@
 // DecState, set by a one-thread kernel so the sequence can be captured.
 #include <string>
 
+#include <limits.h>
+
 #include "decode.hpp"
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"
@@ -142,8 +144,9 @@ int attention_block(const Proj &qkv, const Proj &o, const float *x, const uint32
     int rc = project(qkv, x, xq, nullptr, nullptr, w.qkv, nq, H, gshift, EPI_ROPE, &ra, st);
     if (rc) return rc;
     const bool q4 = o.bits == 4;
+    // The per-layer path scores every position (no cap: fused_ops.rs:997-1040).
     rc = launch_attention(w.state, w.qkv, kc, vc, w.part, w.attn, q4 ? w.xq_a : nullptr, hq, hkv,
-                          hd, max_seq, st);
+                          hd, max_seq, INT_MAX, st);
     if (rc) return rc;
     return project(o, w.attn, w.xq_a, nullptr, res, out, H, (int64_t)hq * hd, gshift,
                    res ? EPI_RESID : EPI_PLAIN, nullptr, st);

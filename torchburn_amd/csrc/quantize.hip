@@ -140,8 +140,11 @@ __global__ __launch_bounds__(256) void k_quant_int4_rows(const float *__restrict
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int e = 2 * j + h;
-            // roundf: ties away from zero, as Rust's f32::round
-            const float q = e < k ? fminf(fmaxf(roundf(__fmul_rn(wr[e], inv)), -8.0f), 7.0f) : 0.f;
+            // roundf: ties away from zero, as Rust's f32::round; a NaN (a NaN
+            // weight, or an infinite one times inv = 0) stays NaN through
+            // Rust's clamp and casts to 0, so its nibble is 8
+            const float t = e < k ? roundf(__fmul_rn(wr[e], inv)) : 0.f;
+            const float q = __builtin_isnan(t) ? 0.f : fminf(fmaxf(t, -8.0f), 7.0f);
             nib[h] = (uint32_t)((int)q + 8) & 15u;
         }
         pr[j] = (uint8_t)(nib[0] | (nib[1] << 4));

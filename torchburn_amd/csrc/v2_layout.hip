@@ -97,9 +97,11 @@ __global__ __launch_bounds__(256) void k_dequant_v2(const uint8_t *__restrict__ 
 }
 
 // One block per activation row: s_x = max(max|x|, 1e-10) / 127, then
-// x' = q * s_x with q = rint(x * (1 / s_x)).  A NaN element gives q = 0 (the
-// reference's int conversion of NaN lands on byte 128, i.e. q = 0); fmaxf skips
-// NaN in the maximum.
+// x' = q * s_x with q = rint(x * (1 / s_x)) for the first 16 * (k / 16)
+// elements and, as the reference's scalar tail does (gemv.rs:1383-1386),
+// q = round-half-away(x / s_x) clamped to +-127 for the rest.  A NaN element
+// gives q = 0 (the reference's int conversion of NaN lands on byte 128, i.e.
+// q = 0); fmaxf skips NaN in the maximum.
 __global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
                                                 float *__restrict__ xo, int k) {
     __shared__ float red[4];
@@ -115,10 +117,15 @@ __global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
     if (mx < 1e-10f) mx = 1e-10f;
     const float sx = __fdiv_rn(mx, 127.0f);
     const float inv = __fdiv_rn(1.0f, sx);
+    const int body = k / 16 * 16;
     for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        const float t = __fmul_rn(xr[i], inv);
-        const float q = __builtin_isnan(t) ? 0.f : __builtin_rintf(t);
-        yr[i] = __fmul_rn(q, sx);
+        float q;
+        if (i < body) {
+            q = __builtin_rintf(__fmul_rn(xr[i], inv));
+        } else {
+            q = fminf(fmaxf(roundf(__fdiv_rn(xr[i], sx)), -127.f), 127.f);
+        }
+        yr[i] = __fmul_rn(__builtin_isnan(q) ? 0.f : q, sx);
     }
 }
 

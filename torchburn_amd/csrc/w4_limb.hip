@@ -557,11 +557,12 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
     }
 }
 
-// y = sum of the split partials (split order) + bias (+ residual).
+// y = sum of the split partials (split order) + bias (+ residual).  res may
+// be y (an in-place residual add): each element is read before it is written,
+// by the same thread, so neither pointer is restrict-qualified.
 __global__ __launch_bounds__(256) void k_limb_reduce(const float *__restrict__ part, int splits,
                                                      int m, int n, const float *__restrict__ b0,
-                                                     const float *__restrict__ res,
-                                                     float *__restrict__ y) {
+                                                     const float *res, float *y) {
     const size_t total = (size_t)m * n;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (size_t)gridDim.x * blockDim.x) {

@@ -180,12 +180,13 @@ __global__ __launch_bounds__(256) void k_w4_mfma(const float *__restrict__ x,
     }
 }
 
-// Sum of the split-K partials in split order, then the epilogue.
+// Sum of the split-K partials in split order, then the epilogue.  res may be
+// y (an in-place residual add; each element is read before the same thread
+// writes it), so neither pointer is restrict-qualified.
 __global__ __launch_bounds__(256) void k_mfma_reduce(const float *__restrict__ part, int splits,
                                                      int m, int n, const float *__restrict__ b0,
                                                      const float *__restrict__ b1,
-                                                     const float *__restrict__ res,
-                                                     float *__restrict__ y, int epi) {
+                                                     const float *res, float *y, int epi) {
     const size_t total = (size_t)m * n;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (size_t)gridDim.x * blockDim.x) {

@@ -54,6 +54,7 @@ def _bind():
         "tb_decoder_get_logits": [p, p],
         "tb_decoder_set_seed": [p, C.c_uint64],
         "tb_decoder_set_rope_tables": [p, p, p, i64, i64],
+        "tb_decoder_set_attention_cap": [p, i64],
         "tb_decoder_time_greedy": [p, i64, i64, i64, C.POINTER(C.c_float)],
         "tb_decoder_destroy": [p],
     }
@@ -95,7 +96,7 @@ def decoder_symbols() -> list:
             "tb_decoder_get_logits", "tb_decoder_set_seed", "tb_decoder_time_greedy",
             "tb_decoder_destroy", "tb_decoder_generate_sampled", "tb_decoder_verify",
             "tb_decoder_speculative_accept", "tb_speculative_accept_rows", "tb_spec_uniform",
-            "tb_decoder_set_rope_tables"]
+            "tb_decoder_set_rope_tables", "tb_decoder_set_attention_cap"]
 
 
 _NP_TO_TORCH = {"float32": "float32", "uint8": "uint8", "int8": "int8", "int64": "int64"}
@@ -261,6 +262,13 @@ class RustQwenDecoder:
         _lib.check(_bind().tb_decoder_set_rope_tables(self._h, cp, sp, self.max_seq_len,
                                                       self.head_dim))
         del ck, sk
+
+    def set_attention_cap(self, cap: int) -> None:
+        """Positions a step attends: 0 .. min(p + 1, cap) - 1 at position p.
+        The default, 32768, is RustQwenDecoder's native step (decoder.rs:1179-
+        1184); 0 scores every position, as the reference's per-layer Python
+        path does (no reference counterpart on RustQwenDecoder)."""
+        _lib.check(_bind().tb_decoder_set_attention_cap(self._h, int(cap)))
 
     # -- stepping -----------------------------------------------------------
 

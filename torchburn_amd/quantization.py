@@ -9,6 +9,7 @@ on the caller's device.  There is no CPU compute path.
 """
 from __future__ import annotations
 
+import ctypes as C
 import gc
 from typing import Any, List, Optional, Tuple
 
@@ -174,6 +175,15 @@ def dequantize_int4_grouped_v2(blocked: torch.Tensor, group_size: int = 64) -> t
     out = torch.empty((n, k), dtype=torch.float32, device=dev)
     _lib.call("tb_dequantize_int4_grouped_v2", _ptr(b), _ptr(out), n, k, _stream(dev))
     return out.to(blocked.device)
+
+
+def release_stream_workspace(stream=None) -> None:
+    """Frees the library's scratch for `stream` (default: the current torch
+    stream) on the current device: for streams created per request.  Waits for
+    the device; graphs captured on that stream must not be replayed afterwards.
+    No reference counterpart (the reference allocates per call)."""
+    s = stream if stream is not None else torch.cuda.current_stream()
+    _lib.check(_lib.lib().tb_release_stream_workspace(C.c_void_p(s.cuda_stream)))
 
 
 def set_vnni_semantics(enabled: bool) -> bool:
