@@ -166,13 +166,20 @@ TB_API float tb_sample_uniform(uint64_t seed, uint64_t counter);
 
 /*
  * Selects the reference's AVX-512 VNNI-tier semantics for group-64 INT4
- * projections (tb_w4a32_grouped_linear[_residual] at group 64 and
- * tb_w4a32_grouped_linear_v2): each activation row is quantized to bytes,
- * s_x = max(max|x|, 1e-10) / 127, q = round-half-even(x * (1 / s_x))
+ * projections: each activation row is quantized to bytes, s_x = max(max|x|,
+ * 1e-10) / 127, q = round-half-even(x * (1 / s_x)) for the first 16 * (K / 16)
+ * elements and round-half-away(x / s_x) for the rest
  * (src/quantization/gemv.rs:1353-1389), and contracted with the nibbles
- * (gemv.rs:1422-1473, packed_v2.rs:204-323).  The reference picks this by CPU
- * feature (gemv.rs:1541-1563); 0 (the default) is its exact W4A32 result.
- * Returns the previous setting.  Process-wide.
+ * (gemv.rs:1422-1473, packed_v2.rs:204-323).  It reaches every group-64 INT4
+ * projection the reference runs through those kernels: the linear entries
+ * (tb_w4a32_grouped_linear[_residual], _v2), the fused SwiGLU MLP (x before
+ * the gate / up pair, h before down: fused_ops.rs:215-232, 409-421), the
+ * per-layer steps (fused_ops.rs:932-1049, fused_transformer.rs:102-299) and the
+ * decoder (QKV, O, gate / up, down and an INT4 lm_head: decoder.rs:1029-1049,
+ * 1262-1282; a decoder re-captures its step when the setting changes, and
+ * prefills and verifies step by step while it is on).  The reference picks
+ * this by CPU feature (gemv.rs:1541-1563); 0 (the default) is its exact W4A32
+ * result.  Returns the previous setting.  Process-wide.
  */
 TB_API int tb_set_vnni_semantics(int enabled);
 

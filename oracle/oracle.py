@@ -49,6 +49,7 @@ def lib():
         L.orc_gemv_w4_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64]
         L.orc_swiglu_h_w4.argtypes = [_vp] * 8 + [_i64, _i64, _i64]
         L.orc_swiglu_mlp_w4.argtypes = [_vp] * 11 + [_i64] * 5
+        L.orc_swiglu_mlp_w4a8.argtypes = [_vp] * 11 + [_i64] * 4
         L.orc_gemv_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64]
         L.orc_quantize_int8.argtypes = [_f32p, _i8p, _f32p, _i64, _i64]
         L.orc_swiglu_h_w8.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
@@ -62,6 +63,7 @@ def lib():
         L.orc_decoder_set_rope_tables.argtypes = [_vp, _f32p, _f32p]
         L.orc_decoder_set_layer_path.argtypes = [_vp, C.c_int]
         L.orc_decoder_set_attention_cap.argtypes = [_vp, _i64]
+        L.orc_decoder_set_a8.argtypes = [_vp, C.c_int]
         L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float]
         L.orc_gemv_f32.argtypes = [_vp, _vp, _vp, _i64, _i64]
         L.orc_rope_tables.argtypes = [_f32p, _f32p, _i64, _i64, C.c_double]
@@ -284,6 +286,22 @@ def swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None, group
     return out.reshape(*x.shape[:-1], nout)
 
 
+def swiglu_mlp_w4a8(x, gw, gsc, uw, usc, dw, dsc, gb=None, ub=None, db=None):
+    """fused_swiglu_mlp_w4a32 at group 64 on an AVX-512 VNNI host: W4A8 gate / up
+    on x's bytes and W4A8 down on h's (fused_ops.rs:215-232, 409-421); no
+    residual."""
+    x = _c(x, np.float32)
+    k = x.shape[-1]
+    m = x.size // k
+    inter, nout = gw.shape[0], dw.shape[0]
+    arrs = [_c(a, dt) for a, dt in ((gw, np.uint8), (gsc, np.float32), (gb, np.float32),
+                                    (uw, np.uint8), (usc, np.float32), (ub, np.float32),
+                                    (dw, np.uint8), (dsc, np.float32), (db, np.float32))]
+    out = np.empty((m, nout), np.float32)
+    lib().orc_swiglu_mlp_w4a8(_p(x), *[_p(a) for a in arrs], _p(out), m, k, inter, nout)
+    return out.reshape(*x.shape[:-1], nout)
+
+
 def swiglu_h_w4(x, gw, gsc, uw, usc, gb=None, ub=None, group_size=32):
     x = _c(x, np.float32).reshape(-1)
     inter = gw.shape[0]
@@ -445,10 +463,11 @@ class Decoder:
     (orc_decoder_set_layer_path), which runs INT8 and fp32-lm_head models.
     attention_cap: positions the native step scores (the reference's 32768,
     decoder.rs:1179-1184, unless a test sets another).
+    a8: the W4A8 step of an AVX-512 VNNI host at group 64 (orc_decoder_set_a8).
     """
 
     def __init__(self, weights: dict, cfg: dict, rope_tables=None, layer_path=False,
-                 attention_cap=32768):
+                 attention_cap=32768, a8=False):
         self.cfg = cfg
         self.w = weights
         L = lib()
@@ -471,6 +490,7 @@ class Decoder:
             L.orc_decoder_set_rope_tables(self.h, c, sn)
         L.orc_decoder_set_layer_path(self.h, 1 if layer_path else 0)
         L.orc_decoder_set_attention_cap(self.h, int(attention_cap))
+        L.orc_decoder_set_a8(self.h, 1 if a8 else 0)
 
     def step(self, token: int, offset: int) -> np.ndarray:
         L = lib()

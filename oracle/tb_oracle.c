@@ -447,6 +447,34 @@ ORC_API void orc_swiglu_mlp_w4(const float *x, const uint8_t *gw, const float *g
     free(h);
 }
 
+/* The W4A8 form at group 64 on an AVX-512 VNNI host (fused_ops.rs:215-232,   */
+/* 409-421): x rounded to bytes per token; gate and up by                     */
+/* swiglu_neuron_w4a8_group64_vnni_avx512 (swiglu.rs:8-81: per matrix the      */
+/* lanes and per-group fma of gemv_row_w4a8_group64_vnni_avx512, w4a8_rows);   */
+/* h = silu(g + gb) * (u + ub); the down projection is a group-64 GEMV, so W4A8 */
+/* again on h.                                                                */
+ORC_API void orc_swiglu_mlp_w4a8(const float *x, const uint8_t *gw, const float *gsc,
+                                 const float *gb, const uint8_t *uw, const float *usc,
+                                 const float *ub, const uint8_t *dw, const float *dsc,
+                                 const float *db, float *out, int64_t m, int64_t k,
+                                 int64_t inter, int64_t nout) {
+    float *g = (float *)malloc((size_t)inter * sizeof(float));
+    float *u = (float *)malloc((size_t)inter * sizeof(float));
+    float *h = (float *)malloc((size_t)inter * sizeof(float));
+    for (int64_t t = 0; t < m; ++t) {
+        orc_gemv_w4a8_g64(x + t * k, gw, gsc, 0, NULL, g, inter, k);
+        orc_gemv_w4a8_g64(x + t * k, uw, usc, 0, NULL, u, inter, k);
+        for (int64_t j = 0; j < inter; ++j) {
+            float gv = g[j] + (gb ? gb[j] : 0.f), uv = u[j] + (ub ? ub[j] : 0.f);
+            h[j] = gv / (1.0f + expf(-gv)) * uv;
+        }
+        orc_gemv_w4a8_g64(h, dw, dsc, 0, db, out + t * nout, nout, inter);
+    }
+    free(g);
+    free(u);
+    free(h);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Per-channel INT4: w4a32_linear, gemv.rs:1066-1182 (the compile engine's    */
 /* d_quant.rs:109-125 and python/torchburn/quantization.py:219-243):           */
@@ -1060,6 +1088,7 @@ typedef struct {
     int use_v2;     /* decoder.rs:361-390 */
     int layer_path; /* numerics of the per-layer Python path (orc_decoder_set_layer_path) */
     int64_t attn_cap; /* native step: positions scored, 32768 (orc_decoder_set_attention_cap) */
+    int a8;         /* W4A8 on a VNNI host at group 64 (orc_decoder_set_a8)             */
     uint8_t *lm_w2;
     float eps;
     const float *embed, *final_norm;
@@ -1068,6 +1097,7 @@ typedef struct {
     orc_layer *layers;
     float *kc, *vc, *cos_t, *sin_t;
     float *x, *xn, *qkv, *att, *o, *h, *dn, *logits;
+    float *g; /* [I] gate row of the W4A8 SwiGLU */
     int64_t kv_used;
 } orc_decoder;
 
@@ -1107,6 +1137,7 @@ ORC_API orc_decoder *orc_decoder_create(int64_t L, int64_t H, int64_t I, int64_t
     d->qkv = (float *)calloc((size_t)tq, 4);
     d->att = (float *)calloc((size_t)(hq * hd), 4);
     d->o = (float *)calloc((size_t)H, 4);
+    d->g = (float *)calloc((size_t)I, 4);
     d->h = (float *)calloc((size_t)I, 4);
     d->dn = (float *)calloc((size_t)H, 4);
     d->logits = (float *)calloc((size_t)V, 4);
@@ -1142,7 +1173,7 @@ ORC_API void orc_decoder_destroy(orc_decoder *d) {
     }
     free(d->lm_w2);
     free(d->layers); free(d->kc); free(d->vc); free(d->cos_t); free(d->sin_t);
-    free(d->x); free(d->xn); free(d->qkv); free(d->att); free(d->o); free(d->h);
+    free(d->x); free(d->xn); free(d->qkv); free(d->att); free(d->o); free(d->h); free(d->g);
     free(d->dn); free(d->logits); free(d);
 }
 
@@ -1176,6 +1207,13 @@ ORC_API void orc_decoder_set_rope_tables(orc_decoder *d, const float *cos_t,
 /* kernels as the native step.  0 (default): RustQwenDecoder::step_internal. */
 ORC_API void orc_decoder_set_layer_path(orc_decoder *d, int on) { d->layer_path = on; }
 
+/* 1: the step of an AVX-512 VNNI host at group 64: every INT4 projection      */
+/* takes its input's bytes, W4A8 (decoder.rs:1262-1282 for the SwiGLU pair;   */
+/* projection_gemv, decoder.rs:1029-1049, into packed_v2.rs:366-370 for the   */
+/* v2 projections or gemv.rs:1559-1563 for v1).  Used when wkind == 4 and      */
+/* gs == 64; the lm_head too when lmkind == 4.                                */
+ORC_API void orc_decoder_set_a8(orc_decoder *d, int on) { d->a8 = on; }
+
 /* The native step scores positions 0 .. min(offset + 1, cap) - 1; the        */
 /* reference's cap is the constant 32768 (decoder.rs:1179-1184), the default. */
 /* Another value lets a test show the cap's effect on a short cache.          */
@@ -1197,6 +1235,20 @@ static void proj(const orc_decoder *d, int kind, const float *x, const void *w, 
     }
 }
 
+/* An INT4 projection of the step: v2 blocks (use_v2) or v1, W4A8 under a8.  */
+static void proj4(const orc_decoder *d, const float *x, const uint8_t *w1, const float *s1,
+                  const uint8_t *w2, const float *b, float *y, int64_t n, int64_t k) {
+    int a8 = d->a8 && d->gs == 64;
+    if (w2 && a8)
+        orc_gemv_w4a8_g64(x, w2, NULL, 1, b, y, n, k);
+    else if (w2)
+        orc_gemv_w4_v2(x, w2, b, y, n, k);
+    else if (a8)
+        orc_gemv_w4a8_g64(x, w1, s1, 0, b, y, n, k);
+    else
+        orc_gemv_w4(x, w1, s1, b, y, n, k, d->gs);
+}
+
 ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
     int64_t H = d->H, hd = d->hd, hq = d->hq, hkv = d->hkv;
     int64_t qd = hq * hd, kvd = hkv * hd, tq = qd + 2 * kvd, half = hd / 2;
@@ -1215,8 +1267,9 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
             orc_rms_norm_torch(d->x, y->in_norm, d->xn, H, d->eps);
         else
             orc_rms_norm(d->x, y->in_norm, d->xn, H, d->eps);
-        if (d->use_v2)
-            orc_gemv_w4_v2(d->xn, y->qkv_w2, y->qkv_b, d->qkv, tq, H);
+        if (d->wkind == 4)
+            proj4(d, d->xn, (const uint8_t *)y->qkv_w, y->qkv_s, d->use_v2 ? y->qkv_w2 : NULL,
+                  y->qkv_b, d->qkv, tq, H);
         else
             proj(d, d->wkind, d->xn, y->qkv_w, y->qkv_s, y->qkv_b, d->qkv, tq, H);
         float *q = d->qkv, *k = d->qkv + qd, *v = d->qkv + qd + kvd;
@@ -1229,8 +1282,9 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
         }
         attention_any(q, kc, vc, d->att, hq, hkv, hd, d->max_seq, offset + 1, d->layer_path,
                       d->attn_cap);
-        if (d->use_v2)
-            orc_gemv_w4_v2(d->att, y->o_w2, NULL, d->o, H, qd);
+        if (d->wkind == 4)
+            proj4(d, d->att, (const uint8_t *)y->o_w, y->o_s, d->use_v2 ? y->o_w2 : NULL, NULL,
+                  d->o, H, qd);
         else
             proj(d, d->wkind, d->att, y->o_w, y->o_s, NULL, d->o, H, qd);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->o[i];
@@ -1238,14 +1292,22 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
             orc_rms_norm_torch(d->x, y->post_norm, d->xn, H, d->eps);
         else
             orc_rms_norm(d->x, y->post_norm, d->xn, H, d->eps);
-        if (d->wkind == 4)
+        if (d->wkind == 4 && d->a8 && d->gs == 64) {
+            /* swiglu_neuron_w4a8_group64_vnni_avx512 (swiglu.rs:8-81): the W4A8  */
+            /* row of each matrix on the same bytes, then silu(g) * u             */
+            orc_gemv_w4a8_g64(d->xn, (const uint8_t *)y->gate_w, y->gate_s, 0, NULL, d->g, d->I,
+                              H);
+            orc_gemv_w4a8_g64(d->xn, (const uint8_t *)y->up_w, y->up_s, 0, NULL, d->h, d->I, H);
+            for (int64_t j = 0; j < d->I; ++j) d->h[j] = d->g[j] / (1.0f + expf(-d->g[j])) * d->h[j];
+        } else if (d->wkind == 4)
             orc_swiglu_h_w4(d->xn, (const uint8_t *)y->gate_w, y->gate_s, NULL,
                             (const uint8_t *)y->up_w, y->up_s, NULL, d->h, d->I, H, d->gs);
         else
             orc_swiglu_h_w8(d->xn, (const int8_t *)y->gate_w, y->gate_s, d->I, NULL,
                             (const int8_t *)y->up_w, y->up_s, d->I, NULL, d->h, d->I, H);
-        if (d->use_v2)
-            orc_gemv_w4_v2(d->h, y->down_w2, NULL, d->dn, H, d->I);
+        if (d->wkind == 4)
+            proj4(d, d->h, (const uint8_t *)y->down_w, y->down_s, d->use_v2 ? y->down_w2 : NULL,
+                  NULL, d->dn, H, d->I);
         else
             proj(d, d->wkind, d->h, y->down_w, y->down_s, NULL, d->dn, H, d->I);
         for (int64_t i = 0; i < H; ++i) d->x[i] += d->dn[i];
@@ -1254,8 +1316,8 @@ ORC_API void orc_decoder_step(orc_decoder *d, int64_t token, int64_t offset) {
         orc_rms_norm_torch(d->x, d->final_norm, d->xn, H, d->eps);
     else
         orc_rms_norm(d->x, d->final_norm, d->xn, H, d->eps);
-    if (d->lm_w2)
-        orc_gemv_w4_v2(d->xn, d->lm_w2, NULL, d->logits, d->V, H);
+    if (d->lmkind == 4)
+        proj4(d, d->xn, (const uint8_t *)d->lm_w, d->lm_s, d->lm_w2, NULL, d->logits, d->V, H);
     else
         proj(d, d->lmkind, d->xn, d->lm_w, d->lm_s, NULL, d->logits, d->V, H);
 }

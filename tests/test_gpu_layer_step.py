@@ -21,6 +21,10 @@ import torchburn_amd as tb
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-4
+# W4A8 steps round every projection input to bytes, intermediates included: an
+# element within ~1e-7 of a rounding boundary (f32 summation order) can land
+# one byte over, a one-quantum step in what follows
+A8_TOL = 3e-3
 
 
 def rel(a, b):
@@ -171,6 +175,67 @@ def test_transformer_layer_step_matches_oracle(cuda, H, I, hq, hkv, hd, max_seq,
     print(f"max rel err {err:.3g}", flush=True)
     assert err < TOL
     assert rel(kg.cpu().numpy()[0][:, offset], kc_ref[:, offset]) < 1e-4
+
+
+def a8proj(x, w, s, b):
+    return O.gemm_w4a8_g64(x.reshape(1, -1), w, s, b)[0]
+
+
+@pytest.mark.parametrize("H,I,hq,hkv,hd,max_seq,offset,eps", [
+    (896, 4864, 14, 2, 64, 2112, 2048, 1e-6),
+    (4096, 14336, 32, 8, 128, 4160, 4096, 1e-5),
+])
+def test_layer_steps_vnni_semantics(cuda, H, I, hq, hkv, hd, max_seq, offset, eps):
+    """Group 64 under W4A8 semantics (tb_set_vnni_semantics): every projection of
+    the attention step and the layer step contracts its input's bytes, as on the
+    reference's AVX-512 VNNI hosts (gemv.rs:1559-1563; the SwiGLU pair
+    fused_transformer.rs:299); against the oracle's W4A8 pieces, and far from
+    the exact steps."""
+    print(f"case layer steps vnni H={H} I={I} offset={offset}", flush=True)
+    g = synth.rng(86, H, I)
+    x, qkv, o, kc, vc, cr, sr = setup(g, H, hq, hkv, hd, max_seq, offset, 4, 64, 1e6)
+    in_w = (1.0 + g.normal(0, 0.1, H)).astype(np.float32)
+    post_w = (1.0 + g.normal(0, 0.1, H)).astype(np.float32)
+    gw, gsc = synth.int4_weight(g, I, H, 64)
+    uw, usc = synth.int4_weight(g, I, H, 64)
+    dw, dsc = synth.int4_weight(g, H, I, 64)
+    gb = g.normal(0, 0.02, I).astype(np.float32)
+    db = g.normal(0, 0.02, H).astype(np.float32)
+    # oracle: the attention step alone, then the layer step
+    ka, va = kc[0].copy(), vc[0].copy()
+    ref_att = oracle_attention_step(x[0], qkv, o, ka, va, cr, sr, offset, hq, hkv, hd, a8proj)
+    exact_att = oracle_attention_step(x[0], qkv, o, kc[0].copy(), vc[0].copy(), cr, sr, offset,
+                                      hq, hkv, hd, w4proj(64))
+    kr, vr = kc[0].copy(), vc[0].copy()
+    xr = x[0].copy()
+    xn = O.rms_norm(xr, in_w, eps)
+    xr = xr + oracle_attention_step(xn, qkv, o, kr, vr, cr, sr, offset, hq, hkv, hd, a8proj)
+    xn = O.rms_norm(xr, post_w, eps)
+    xr = xr + O.swiglu_mlp_w4a8(xn.reshape(1, -1), gw, gsc, uw, usc, dw, dsc, gb=gb, db=db)[0]
+    prev = tb.set_vnni_semantics(True)
+    try:
+        kg, vg = T(kc, cuda), T(vc, cuda)
+        out = tb.fused_attention_step_w4a32(T(x, cuda), *(T(a, cuda) for a in qkv),
+                                            *(T(a, cuda) for a in o), kg, vg, T(cr, cuda),
+                                            T(sr, cuda), offset, hq, hkv, hd, 64)
+        xg = T(x, cuda)
+        kl, vl = T(kc, cuda), T(vc, cuda)
+        tb.fused_transformer_layer_step_w4a32(
+            xg, T(in_w, cuda), *(T(a, cuda) for a in qkv), *(T(a, cuda) for a in o),
+            T(post_w, cuda), T(gw, cuda), T(gsc, cuda), T(gb, cuda), T(uw, cuda), T(usc, cuda),
+            None, T(dw, cuda), T(dsc, cuda), T(db, cuda), kl, vl, T(cr, cuda), T(sr, cuda),
+            offset, hq, hkv, hd, 64, eps)
+        torch.cuda.synchronize()
+    finally:
+        tb.set_vnni_semantics(prev)
+    e1 = rel(out.cpu().numpy()[0], ref_att)
+    e2 = rel(xg.cpu().numpy()[0], xr)
+    ex = rel(out.cpu().numpy()[0], exact_att)
+    print(f"max rel err attention step {e1:.3g}, layer step {e2:.3g}; the W4A32 attention "
+          f"step is off by {ex:.3g}", flush=True)
+    assert e1 < A8_TOL and e2 < A8_TOL
+    assert ex > 5 * max(e1, 1e-6)
+    assert rel(kg.cpu().numpy()[0][:, offset], ka[:, offset]) < 1e-4
 
 
 def test_layer_step_on_cpu_tensors_mutates_in_place(cuda):

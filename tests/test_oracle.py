@@ -514,15 +514,23 @@ def test_argmax_kat_and_ties():
 
 # ------------------------------------------------------------ decoder step ---
 
-def torch_step(w, cfg, kv, tok, pos, gs, f16=False, wkind=4, lmkind=4, tables=None):
+def torch_step(w, cfg, kv, tok, pos, gs, f16=False, wkind=4, lmkind=4, tables=None, a8=False):
     """One decoder step in float64 from torch library ops (independent of the
     oracle's C code): rms_norm, RoPE, SDPA with GQA, silu.  f16: QKV, O, down
     and lm_head use binary16-rounded scales (numpy's float16), the effect of the
     reference's v2 repack at group 64 (decoder.rs:361-390).  wkind / lmkind: 4
     INT4 grouped, 8 INT8 per-row, 32 fp32.  tables: (cos, sin) [max_seq, hd] for a
-    rotate-half RoPE (model.py:125-136); None = the exact complex rotation."""
+    rotate-half RoPE (model.py:125-136); None = the exact complex rotation.
+    a8: every INT4 projection contracts its input's bytes (u - 128) * s_x from
+    the pinned quantize_act_u8 (the W4A8 step of a VNNI host at group 64)."""
     D = lambda a: torch.from_numpy(np.asarray(a, np.float64))
     r16 = (lambda s: s.astype(np.float16).astype(np.float32)) if f16 else (lambda s: s)
+
+    def A(v, kind=4):   # a projection input, byte-rounded under a8
+        if not (a8 and kind == 4):
+            return v
+        u8, sx = O.quantize_act_u8(v.numpy().astype(np.float32))
+        return D((u8.astype(np.float64) - 128) * sx)
 
     def deq(wt, sc, k, kind, f16s=False):
         if kind == 4:
@@ -549,7 +557,7 @@ def torch_step(w, cfg, kv, tok, pos, gs, f16=False, wkind=4, lmkind=4, tables=No
     x = D(w["embed"][tok])
     for li, lw in enumerate(w["layers"]):
         xn = F.rms_norm(x, (H,), D(lw["in_norm"]), eps=cfg["eps"])
-        qkv = deq(lw["qkv_w"], lw["qkv_s"], H, wkind, True) @ xn
+        qkv = deq(lw["qkv_w"], lw["qkv_s"], H, wkind, True) @ A(xn, wkind)
         if lw.get("qkv_b") is not None:
             qkv = qkv + D(lw["qkv_b"])
         q = rope(qkv[:hq * hd].reshape(hq, hd))
@@ -560,13 +568,13 @@ def torch_step(w, cfg, kv, tok, pos, gs, f16=False, wkind=4, lmkind=4, tables=No
         vc[:, pos] = v
         att = F.scaled_dot_product_attention(q[None, :, None], kc[None, :, :pos + 1],
                                              vc[None, :, :pos + 1], enable_gqa=True)[0, :, 0]
-        x = x + deq(lw["o_w"], lw["o_s"], hq * hd, wkind, True) @ att.reshape(-1)
+        x = x + deq(lw["o_w"], lw["o_s"], hq * hd, wkind, True) @ A(att.reshape(-1), wkind)
         xn = F.rms_norm(x, (H,), D(lw["post_norm"]), eps=cfg["eps"])
-        h = F.silu(deq(lw["gate_w"], lw["gate_s"], H, wkind) @ xn) * \
-            (deq(lw["up_w"], lw["up_s"], H, wkind) @ xn)
-        x = x + deq(lw["down_w"], lw["down_s"], cfg["intermediate"], wkind, True) @ h
+        h = F.silu(deq(lw["gate_w"], lw["gate_s"], H, wkind) @ A(xn, wkind)) * \
+            (deq(lw["up_w"], lw["up_s"], H, wkind) @ A(xn, wkind))
+        x = x + deq(lw["down_w"], lw["down_s"], cfg["intermediate"], wkind, True) @ A(h, wkind)
     xn = F.rms_norm(x, (H,), D(w["final_norm"]), eps=cfg["eps"])
-    return (deq(w["lm_head_w"], w["lm_head_s"], H, lmkind, True) @ xn).numpy()
+    return (deq(w["lm_head_w"], w["lm_head_s"], H, lmkind, True) @ A(xn, lmkind)).numpy()
 
 
 @pytest.mark.parametrize("gs,vocab,v2", [(32, 300, False), (64, 300, False), (64, 320, True)])
@@ -602,6 +610,40 @@ def test_decoder_step_vs_torch_float64(gs, vocab, v2):
     # out-of-range token / position -> zeroed logits (decoder.rs:1066-1089)
     assert not dec.step(vocab, 3).any() and not dec.step(1, max_seq).any()
     dec.close()
+
+
+@pytest.mark.parametrize("vocab,v2", [(300, False), (320, True)])
+def test_decoder_step_a8_vs_torch_float64(vocab, v2):
+    """The W4A8 step of a VNNI host at group 64 (orc_decoder_set_a8): every INT4
+    projection input byte-rounded (the SwiGLU pair, decoder.rs:1262-1282; QKV,
+    O, down and the lm_head through projection_gemv, decoder.rs:1029-1049).
+    Against the float64 model on the same byte rounding (measured 1e-7; the
+    bar leaves room for an occasional rounding flip); the exact W4A32 step is
+    off by 2-4%."""
+    cfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
+               head_dim=64, vocab=vocab, eps=1e-6, rope_theta=1e6, qkv_bias=True)
+    max_seq, pre, gs = 24, 9, 64
+    w = synth.decoder_weights(cfg, 23, 4, 4, gs)
+    ocfg = dict(num_layers=2, hidden=128, intermediate=256, num_heads=4, num_kv_heads=2,
+                head_dim=64, vocab=vocab, group_size=gs, max_seq=max_seq, rope_theta=1e6,
+                eps=1e-6, wkind=4, lmkind=4)
+    dec, exact = O.Decoder(w, ocfg, a8=True), O.Decoder(w, ocfg)
+    kvp = synth.kv_prefill(cfg, 23, pre, max_seq)
+    tkv = []
+    for li, (k, v) in enumerate(kvp):
+        dec.copy_kv(li, k, v, pre)
+        exact.copy_kv(li, k, v, pre)
+        tkv.append((torch.from_numpy(k.astype(np.float64)), torch.from_numpy(v.astype(np.float64))))
+    tok = 5
+    for step in range(4):
+        pos = pre + step
+        lo = dec.step(tok, pos)
+        lt = torch_step(w, cfg, tkv, tok, pos, gs, f16=v2, a8=True)
+        assert rel(lo, lt) < 1e-4, f"step {step}"
+        assert rel(lo, exact.step(tok, pos)) > 1e-2
+        tok = O.argmax(lo)
+    dec.close()
+    exact.close()
 
 
 @pytest.mark.parametrize("wkind,lmkind,layer_path", [(4, 32, True), (8, 8, True), (8, 32, False),

@@ -233,3 +233,36 @@ def test_w4a8_equals_w4a32_on_the_grid():
     y8 = O.gemm_w4a8_g64(x, wq, sc)
     y32 = O.gemv_w4_f64(x[0], wq, sc, group_size=64)
     assert rel(y8[0], y32) < 1e-6
+
+
+def test_swiglu_mlp_w4a8_composition():
+    """The W4A8 fused MLP (fused_ops.rs:215-232, 409-421) is the pinned W4A8 GEMV
+    composed: h = silu(g + gb) * (u + ub) over the gate and up GEMVs on x's
+    bytes, then the down GEMV on h's bytes with its bias.  A float64 model with
+    the same byte rounding lands within the few-quantum slack of rounding h."""
+    rng = np.random.default_rng(77)
+    m, k, inter, nout = 2, 512, 192, 320
+    gw, gsc = O.quantize_int4_grouped(rng.standard_normal((inter, k)).astype(np.float32), 64)
+    uw, usc = O.quantize_int4_grouped(rng.standard_normal((inter, k)).astype(np.float32), 64)
+    dw, dsc = O.quantize_int4_grouped(rng.standard_normal((nout, inter)).astype(np.float32), 64)
+    gb, ub, db = (rng.standard_normal(n).astype(np.float32) for n in (inter, inter, nout))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = O.swiglu_mlp_w4a8(x, gw, gsc, uw, usc, dw, dsc, gb, ub, db)
+    g = O.gemm_w4a8_g64(x, gw, gsc) + gb
+    u = O.gemm_w4a8_g64(x, uw, usc) + ub
+    h = (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+    assert rel(y, O.gemm_w4a8_g64(h, dw, dsc, db)) < 1e-6
+    # float64: exact integer group sums of the bytes, f64 SwiGLU, then h's bytes
+    q = lambda w_, n_, kk: O.unpack_int4(w_, kk).astype(np.float64).reshape(n_, kk // 64, 64)
+    def a8(v, w_, s_, n_, kk):
+        u8, sx = O.quantize_act_u8(v)
+        xi = (u8.astype(np.float64) - 128).reshape(kk // 64, 64)
+        return ((q(w_, n_, kk) * xi).sum(-1) * (np.float64(sx) * s_.astype(np.float64))).sum(-1)
+    for i in range(m):
+        g64 = a8(x[i], gw, gsc, inter, k) + gb
+        u64 = a8(x[i], uw, usc, inter, k) + ub
+        h64 = g64 / (1 + np.exp(-g64)) * u64
+        want = a8(h64.astype(np.float32), dw, dsc, nout, inter) + db
+        assert rel(y[i], want) < 2e-3
+    y32 = O.swiglu_mlp_w4(x, gw, gsc, uw, usc, dw, dsc, gb, ub, db, group_size=64)
+    assert rel(y, y32) > 1e-2

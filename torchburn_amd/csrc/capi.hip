@@ -242,6 +242,8 @@ static int w4_rows(W4Params p, int epi, int64_t m, uint32_t *xq, bool build_xq,
 // exact W4A32 contraction of its scalar / AVX2 / AVX-512 tiers.
 std::atomic<int> g_vnni{0};
 
+bool vnni_semantics() { return g_vnni.load(std::memory_order_relaxed) != 0; }
+
 static size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // One INT4 projection y = x . deq(W)^T (+ bias) (+ residual) over m rows, with
@@ -421,7 +423,22 @@ static int mlp_w4_path(const MlpW4 &a) {
 
 // Scratch: h [m, inter] f32, then the MFMA split-K partials (path 1), the
 // chunk records of x and of h (path 2) or their f16-limb records (path 3).
+// W4A8 semantics (tb_set_vnni_semantics) at group 64: the reference rounds x to
+// bytes before the gate / up pair (fused_ops.rs:215-232) and h before the down
+// projection, which is itself a group-64 GEMV (fused_ops.rs:409-421).
+static bool mlp_a8(const MlpW4 &a) { return a.gs == 64 && vnni_semantics(); }
+
+static size_t mlp_w4_scratch_main(const MlpW4 &a);
+
+// [path scratch | x' (m x k) | h' (m x inter)], the last two under W4A8 only.
 static size_t mlp_w4_scratch_bytes(const MlpW4 &a) {
+    const size_t main = mlp_w4_scratch_main(a);
+    if (!mlp_a8(a)) return main;
+    return up256(main) + up256((size_t)a.m * (size_t)a.k * sizeof(float)) +
+           up256((size_t)a.m * (size_t)a.inter * sizeof(float));
+}
+
+static size_t mlp_w4_scratch_main(const MlpW4 &a) {
     const size_t hb = up256((size_t)a.m * (size_t)a.inter * sizeof(float));
     switch (mlp_w4_path(a)) {
         case 0: return hb;
@@ -448,59 +465,81 @@ static int mlp_w4_run(const MlpW4 &a, void *ws, hipStream_t st) {
     float *h = static_cast<float *>(ws);
     const size_t hb = up256((size_t)m * (size_t)inter * sizeof(float));
     const int path = mlp_w4_path(a);
+    // W4A8: x -> x' here, h -> h' before the down projection (the byte rounding
+    // of each activation row, written back as q * s_x).
+    const bool a8 = mlp_a8(a);
+    float *xa = nullptr, *ha = nullptr;
+    const float *x = a.x;
+    if (a8) {
+        xa = reinterpret_cast<float *>(static_cast<char *>(ws) + up256(mlp_w4_scratch_main(a)));
+        ha = reinterpret_cast<float *>(reinterpret_cast<char *>(xa) +
+                                       up256((size_t)m * (size_t)k * sizeof(float)));
+        if ((rc = act_u8(a.x, xa, m, k, st))) return rc;
+        x = xa;
+    }
+    const float *hin = a8 ? ha : h;   // the down projection's input
     if (path == 0) {
         // Shapes outside the streaming kernels: h by the any-shape GEMV, then the
         // down projection by whichever path its own shape takes.
-        rc = generic(a.x, a.gate_w, a.gate_s, 0, a.gate_b, a.up_w, a.up_s, 0, a.up_b, nullptr, h,
-                     m, inter, k, gs, 4, st);
+        rc = generic(x, a.gate_w, a.gate_s, 0, a.gate_b, a.up_w, a.up_s, 0, a.up_b, nullptr, h, m,
+                     inter, k, gs, 4, st);
         if (rc) return rc;
-        return generic(h, a.down_w, a.down_s, 0, a.down_b, nullptr, nullptr, 0, nullptr,
+        if (a8 && (rc = act_u8(h, ha, m, inter, st))) return rc;
+        return generic(hin, a.down_w, a.down_s, 0, a.down_b, nullptr, nullptr, 0, nullptr,
                        a.residual, a.out, m, n_out, inter, gs, 4, st);
     }
     if (path == 3) {
         // prep(x) -> gate/up + SwiGLU, which also writes h's records -> down
+        // (W4A8: h' and its records replace them)
         uint8_t *xr = static_cast<uint8_t *>(ws) + hb;
         uint8_t *hr = xr + up256(limb_records_bytes((int)m, (int)k));
         float *part =
             reinterpret_cast<float *>(hr + up256(limb_records_bytes((int)m, (int)inter)));
-        if ((rc = limb_prep(a.x, xr, (int)m, (int)k, st))) return rc;
-        LimbParams g = limb_params(a.x, xr, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+        if ((rc = limb_prep(x, xr, (int)m, (int)k, st))) return rc;
+        LimbParams g = limb_params(x, xr, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
         g.w1 = a.up_w; g.s1 = a.up_s; g.b1 = a.up_b;
         g.rec_out = hr;
         if ((rc = w4_limb(g, part, st))) return rc;
-        LimbParams d = limb_params(h, hr, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter,
+        if (a8 && ((rc = act_u8(h, ha, m, inter, st)) ||
+                   (rc = limb_prep(ha, hr, (int)m, (int)inter, st))))
+            return rc;
+        LimbParams d = limb_params(hin, hr, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter,
                                    gs);
         d.res = a.residual;
         return w4_limb(d, part, st);
     }
     if (path == 1) {
         float *part = reinterpret_cast<float *>(static_cast<char *>(ws) + hb);
-        MfmaParams g = mfma_params(a.x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+        MfmaParams g = mfma_params(x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
         g.w1 = a.up_w; g.s1 = a.up_s; g.b1 = a.up_b;
         if ((rc = w4_mfma(g, EPI_SWIGLU, part, st))) return rc;
-        MfmaParams d = mfma_params(h, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
+        if (a8 && (rc = act_u8(h, ha, m, inter, st))) return rc;
+        MfmaParams d = mfma_params(hin, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
         d.res = a.residual;
         return w4_mfma(d, a.residual ? EPI_RESID : EPI_PLAIN, part, st);
     }
     uint32_t *xq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb);
     uint32_t *hq = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + hb +
                                                 up256(xq_bytes(m, k)));
-    W4Params p = w4_params(a.x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
+    W4Params p = w4_params(x, a.gate_w, a.gate_s, a.gate_b, h, m, inter, k, gs);
     p.w1 = a.up_w; p.s1 = a.up_s; p.b1 = a.up_b;
-    W4Params d = w4_params(h, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
+    W4Params d = w4_params(hin, a.down_w, a.down_s, a.down_b, a.out, m, n_out, inter, gs);
     d.res = a.residual;
     const int depi = a.residual ? EPI_RESID : EPI_PLAIN;
     if (m == 1) {
         // One row: the gate/up epilogue writes h's chunk records as well, so the
-        // down projection needs no separate record pass.
-        if ((rc = xquant(a.x, xq, 1, (int)k, st))) return rc;
+        // down projection needs no separate record pass (W4A8: h' and its
+        // records in one pass instead).
+        if ((rc = xquant(x, xq, 1, (int)k, st))) return rc;
         p.xq = xq;
-        p.rec_out = hq;
+        p.rec_out = a8 ? nullptr : hq;
         if ((rc = w4_gemv(p, EPI_SWIGLU, st))) return rc;
+        if (a8 && (rc = act_rec(h, ha, hq, 1, inter, st))) return rc;
         d.xq = hq;
         return w4_gemv(d, depi, st);
     }
     if ((rc = w4_rows(p, EPI_SWIGLU, m, xq, true, st))) return rc;
+    if (a8 && (rc = act_u8(h, ha, m, inter, st))) return rc;
     return w4_rows(d, depi, m, hq, true, st);
 }
 

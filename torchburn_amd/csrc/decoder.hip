@@ -68,6 +68,9 @@ struct Decoder {
     // the native step's rule (decoder.rs:1179-1184) by default, INT_MAX for the
     // per-layer path's every-position attention (tb_decoder_set_attention_cap).
     int attn_cap = kNativeAttnCap;
+    // W4A8 semantics (tb_set_vnni_semantics) at group 64: the mode the step
+    // graphs were captured in (see enqueue_step_a8).
+    bool a8 = false;
     // Rows per GEMV block for QKV, O, gate/up, down, lm_head (0 = the GEMV's
     // default; TB_DECODER_J="qkv,o,gu,down,lm" overrides, for tuning sweeps).
     int rj[5] = {0, 0, 0, 0, 0};
@@ -83,6 +86,7 @@ struct Decoder {
     float *kc = nullptr, *vc = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *attn = nullptr, *h = nullptr;
     float *logits = nullptr, *part = nullptr, *am_v = nullptr;
+    float *xa = nullptr;   // W4A8: x' = q * s_x of the current projection input
     int *am_i = nullptr, *history = nullptr;
     uint32_t *xq_h = nullptr, *xq_a = nullptr, *xq_i = nullptr;
     float *ssq = nullptr;   // 16-element sums of squares of x (fused RMSNorm)
@@ -310,8 +314,61 @@ struct Decoder {
         return enqueue_tail(sampled);
     }
 
+    // The step under W4A8 semantics at group 64 (tb_set_vnni_semantics).  On
+    // an AVX-512 VNNI host the reference rounds the input of every group-64
+    // INT4 projection to bytes: the SwiGLU pair's (decoder.rs:1262-1282) and,
+    // through projection_gemv (decoder.rs:1029-1049 -> packed_v2.rs:366-370 or
+    // gemv.rs:1559-1563), QKV's, O's, down's and the INT4 lm_head's.  The
+    // RMSNorms run as separate kernels (the rounding takes the maximum of the
+    // normalised row), and one pass per projection input writes x' = q * s_x
+    // and its records.  The weights are those of the exact step (binary16
+    // scales where the reference repacks to v2 blocks).
+    bool a8_wanted() const { return wbits == 4 && gs == 64 && vnni_semantics(); }
+
+    int enqueue_step_a8(bool sampled) {
+        int rc;
+        const int qd = hq * hd;
+        for (int l = 0; l < L; ++l) {
+            const Layer &y = layers[l];
+            float *kcl = kc + (size_t)l * hkv * max_seq * hd;
+            float *vcl = vc + (size_t)l * hkv * max_seq * hd;
+            RopeArgs ra{&state->pos, cos_t, sin_t, kcl, vcl, hq, hkv, hd, max_seq, hd};
+            if ((rc = launch_rmsnorm(state, l == 0 ? embed : nullptr, x, y.in_norm, xn, nullptr, H,
+                                     eps, st)) ||
+                (rc = act_rec(xn, xa, xq_h, 1, H, st)) ||
+                (rc = proj(4, xa, xq_h, y.qkv_w, y.qkv_s, y.qkv_b, nullptr, nullptr, nullptr, qkv,
+                           tq, H, EPI_ROPE, &ra)) ||
+                (rc = launch_attention(state, qkv, kcl, vcl, part, attn, nullptr, hq, hkv, hd,
+                                       max_seq, attn_cap, st)) ||
+                (rc = act_rec(attn, xa, xq_a, 1, qd, st)) ||
+                (rc = proj(4, xa, xq_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, x, x, H, qd,
+                           EPI_RESID)) ||
+                (rc = launch_rmsnorm(state, nullptr, x, y.post_norm, xn, nullptr, H, eps, st)) ||
+                (rc = act_rec(xn, xa, xq_h, 1, H, st)) ||
+                (rc = proj(4, xa, xq_h, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, h,
+                           I, H, EPI_SWIGLU)) ||
+                (rc = act_rec(h, xa, xq_i, 1, I, st)) ||
+                (rc = proj(4, xa, xq_i, y.down_w, y.down_s, nullptr, nullptr, nullptr, x, x, H, I,
+                           EPI_RESID)))
+                return rc;
+        }
+        if ((rc = launch_rmsnorm(state, nullptr, x, final_norm, xn, nullptr, H, eps, st))) return rc;
+        const float *lin = xn;
+        const uint32_t *lq = nullptr;
+        if (lmbits == 4) {
+            if ((rc = act_rec(xn, xa, xq_h, 1, H, st))) return rc;
+            lin = xa;
+            lq = xq_h;
+        }
+        if ((rc = proj(lmbits, lin, lq, lm_w, lm_s, nullptr, nullptr, nullptr, nullptr, logits, V,
+                       H, EPI_PLAIN)))
+            return rc;
+        return enqueue_tail(sampled);
+    }
+
     // Enqueues one decoder step (reference step_internal) on `st`.
     int enqueue_step(bool sampled = false) {
+        if (a8) return enqueue_step_a8(sampled);
         const bool q4 = wbits == 4;
         // INT8 layers write no records, which an INT4 lm_head reads: that pair
         // keeps the separate final RMSNorm of the unfused step.
@@ -376,7 +433,22 @@ struct Decoder {
         return TB_OK;
     }
 
-    int ensure_graph() { return exec ? TB_OK : capture(false, &graph, &exec); }
+    // The step graphs follow the W4A8 switch: a change drops them.
+    int sync_a8() {
+        const bool want = a8_wanted();
+        if (want == a8) return TB_OK;
+        TB_HIP(hipStreamSynchronize(st));
+        int rc = drop_graphs();
+        if (rc) return rc;
+        a8 = want;
+        return TB_OK;
+    }
+
+    int ensure_graph() {
+        int rc = sync_a8();
+        if (rc) return rc;
+        return exec ? TB_OK : capture(false, &graph, &exec);
+    }
 
     // Destroys the captured step graphs; the next step captures them again.
     int drop_graphs() {
@@ -404,7 +476,7 @@ struct Decoder {
 
     int ensure_graph_s() {
         int rc = sampler_alloc();
-        if (rc) return rc;
+        if (rc || (rc = sync_a8())) return rc;
         return exec_s ? TB_OK : capture(true, &graph_s, &exec_s);
     }
 
@@ -556,7 +628,8 @@ struct Decoder {
 
     bool prefill_batchable(const int64_t *tokens, int64_t n, int64_t start) const {
         static const bool loop_only = getenv("TB_PREFILL_LOOP") != nullptr;
-        if (loop_only || wbits != 4 || n < 16 || !under_cap(start, n)) return false;
+        // W4A8 rounds each token's projection inputs: the step loop does that
+        if (loop_only || wbits != 4 || n < 16 || !under_cap(start, n) || a8_wanted()) return false;
         for (int64_t i = 0; i < n; ++i)
             if (tokens[i] < 0 || tokens[i] >= V) return false;   // the step's zero-logit rule
         return true;
@@ -856,6 +929,7 @@ int tb_decoder_create(const tb_decoder_config *cfg, const float *embed, const fl
         (rc = d->alloc(&d->x, d->H * 4)) || (rc = d->alloc(&d->xn, d->H * 4)) ||
         (rc = d->alloc(&d->qkv, d->tq * 4)) || (rc = d->alloc(&d->attn, d->hq * d->hd * 4)) ||
         (rc = d->alloc(&d->h, (size_t)d->I * 4)) || (rc = d->alloc(&d->logits, (size_t)d->V * 4)) ||
+        (rc = d->alloc(&d->xa, (size_t)std::max({d->H, d->hq * d->hd, d->I}) * 4)) ||
         (rc = d->alloc(&d->part, (size_t)d->hq * d->nsplit * (d->hd + 4) * 4)) ||
         (rc = d->alloc(&d->am_v, kArgmaxBlocks * 4)) || (rc = d->alloc(&d->am_i, kArgmaxBlocks * 4)) ||
         (rc = d->alloc(&d->history, (size_t)d->hist_cap * 4)) ||
@@ -1221,7 +1295,7 @@ int tb_decoder_verify(tb_decoder *d, int64_t start_offset, const int64_t *tokens
     TB_REQUIRE(start_offset >= 0 && start_offset + n <= d->max_seq, TB_ERR_VALUE,
                "verify exceeds max_seq_len");
     if (n == 0) return TB_OK;
-    bool batch = d->wbits == 4 && n >= 2 && d->under_cap(start_offset, n);
+    bool batch = d->wbits == 4 && n >= 2 && d->under_cap(start_offset, n) && !d->a8_wanted();
     for (int64_t i = 0; i < n && batch; ++i) batch = tokens[i] >= 0 && tokens[i] < d->V;
     if (!batch) {
         for (int64_t i = 0; i < n; ++i) {

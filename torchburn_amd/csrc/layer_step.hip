@@ -13,9 +13,12 @@
 
 #include <limits.h>
 
+#include <algorithm>
+
 #include "decode.hpp"
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"
+#include "v2_layout.hpp"
 #include "w4_gemv.hpp"
 
 namespace tb {
@@ -45,18 +48,20 @@ struct LayerWs {
     uint32_t *xq_h;   // records of xn (INT4)
     float *h;         // [I] SwiGLU output
     uint32_t *xq_i;   // records of h (INT4)
+    float *xa;        // W4A8: x' = q * s_x of the current projection input
 };
 
 int layer_ws(int64_t H, int64_t I, int hq, int hkv, int hd, int max_seq, LayerWs &w,
              WsLease &lease, hipStream_t st) {
     const size_t qkv_n = (size_t)(hq + 2 * hkv) * hd;
     const size_t part_n = (size_t)hq * attn_nsplit(max_seq) * (hd + 4);
-    size_t off[9], o = 0;
-    const size_t sz[9] = {up256(sizeof(DecState)), up256(qkv_n * 4), up256(part_n * 4),
-                          up256((size_t)hq * hd * 4), up256(recs((int64_t)hq * hd)),
-                          up256((size_t)H * 4), up256(recs(H)), up256((size_t)I * 4),
-                          up256(recs(I))};
-    for (int i = 0; i < 9; ++i) {
+    size_t off[10], o = 0;
+    const size_t xa_n = (size_t)std::max<int64_t>({H, (int64_t)hq * hd, I});
+    const size_t sz[10] = {up256(sizeof(DecState)), up256(qkv_n * 4), up256(part_n * 4),
+                           up256((size_t)hq * hd * 4), up256(recs((int64_t)hq * hd)),
+                           up256((size_t)H * 4), up256(recs(H)), up256((size_t)I * 4),
+                           up256(recs(I)), up256(xa_n * 4)};
+    for (int i = 0; i < 10; ++i) {
         off[i] = o;
         o += sz[i];
     }
@@ -72,8 +77,15 @@ int layer_ws(int64_t H, int64_t I, int hq, int hkv, int hd, int max_seq, LayerWs
     w.xq_h = reinterpret_cast<uint32_t *>(b + off[6]);
     w.h = reinterpret_cast<float *>(b + off[7]);
     w.xq_i = reinterpret_cast<uint32_t *>(b + off[8]);
+    w.xa = reinterpret_cast<float *>(b + off[9]);
     return TB_OK;
 }
+
+// W4A8 semantics (tb_set_vnni_semantics) at group 64: on an AVX-512 VNNI host
+// every group-64 projection of the reference's layer steps rounds its input
+// to bytes (gemv.rs:1559-1563 under fused_ops.rs:932-1049 and
+// fused_transformer.rs:102-241; the SwiGLU pair fused_transformer.rs:299).
+bool a8_on(int bits, int64_t gs) { return bits == 4 && gs == 64 && vnni_semantics(); }
 
 // Shape checks shared by the three entry points (the reference indexes its
 // slices with these sizes; it panics where this returns TB_UNSUPPORTED).
@@ -132,11 +144,12 @@ int project(const Proj &P, const float *x, const uint32_t *xq, const Proj *P2, c
 }
 
 // QKV (+bias, RoPE, KV append) -> attention -> O (+bias, + residual when res).
-// xq: records of x (INT4); out may alias res (in-place residual).
+// xq: records of x (INT4); out may alias res (in-place residual).  a8: the
+// attention output is byte-rounded (x' and its records) before O.
 int attention_block(const Proj &qkv, const Proj &o, const float *x, const uint32_t *xq,
                     float *kc, float *vc, const float *cos, const float *sin, const float *res,
                     float *out, int64_t H, int hq, int hkv, int hd, int max_seq, int gshift,
-                    const LayerWs &w, hipStream_t st) {
+                    bool a8, const LayerWs &w, hipStream_t st) {
     // cos / sin hold one position's row: a table stride of 0 makes every
     // position read it.
     RopeArgs ra{&w.state->pos, cos, sin, kc, vc, hq, hkv, hd, max_seq, 0};
@@ -145,10 +158,15 @@ int attention_block(const Proj &qkv, const Proj &o, const float *x, const uint32
     if (rc) return rc;
     const bool q4 = o.bits == 4;
     // The per-layer path scores every position (no cap: fused_ops.rs:997-1040).
-    rc = launch_attention(w.state, w.qkv, kc, vc, w.part, w.attn, q4 ? w.xq_a : nullptr, hq, hkv,
-                          hd, max_seq, INT_MAX, st);
+    rc = launch_attention(w.state, w.qkv, kc, vc, w.part, w.attn, q4 && !a8 ? w.xq_a : nullptr,
+                          hq, hkv, hd, max_seq, INT_MAX, st);
     if (rc) return rc;
-    return project(o, w.attn, w.xq_a, nullptr, res, out, H, (int64_t)hq * hd, gshift,
+    const float *ain = w.attn;
+    if (a8) {
+        if ((rc = act_rec(w.attn, w.xa, w.xq_a, 1, (int64_t)hq * hd, st))) return rc;
+        ain = w.xa;
+    }
+    return project(o, ain, w.xq_a, nullptr, res, out, H, (int64_t)hq * hd, gshift,
                    res ? EPI_RESID : EPI_PLAIN, nullptr, st);
 }
 
@@ -186,11 +204,18 @@ int attention_step(const char *what, int bits, const float *x, const void *qkv_w
     WsLease lease;
     if ((rc = layer_ws(H, 0, (int)hq, (int)hkv, (int)hd, (int)max_seq, w, lease, st))) return rc;
     if ((rc = set_pos(w, offset, st))) return rc;
-    if (bits == 4 && (rc = xquant(x, w.xq_h, 1, (int)H, st))) return rc;
+    const bool a8 = a8_on(bits, group_size);
+    const float *xin = x;
+    if (a8) {
+        if ((rc = act_rec(x, w.xa, w.xq_h, 1, H, st))) return rc;
+        xin = w.xa;
+    } else if (bits == 4 && (rc = xquant(x, w.xq_h, 1, (int)H, st))) {
+        return rc;
+    }
     const Proj qkv{bits, qkv_w, qkv_s, qkv_s_len, qkv_b};
     const Proj o{bits, o_w, o_s, o_s_len, o_b};
-    return attention_block(qkv, o, x, w.xq_h, k_cache, v_cache, cos, sin, nullptr, out, H,
-                           (int)hq, (int)hkv, (int)hd, (int)max_seq, gshift, w, st);
+    return attention_block(qkv, o, xin, w.xq_h, k_cache, v_cache, cos, sin, nullptr, out, H,
+                           (int)hq, (int)hkv, (int)hd, (int)max_seq, gshift, a8, w, st);
 }
 
 }  // namespace
@@ -262,23 +287,42 @@ int tb_fused_transformer_layer_step_w4a32(
     if ((rc = set_pos(w, offset, st))) return rc;
     const float e = (float)eps;
     const int H = (int)hidden, I = (int)intermediate;
+    const bool a8 = a8_on(4, group_size);
+    // The input of a projection: xn with its records, or under W4A8 x' and its records.
+    auto input = [&](const float *v, uint32_t *xq, int64_t k, const float **in) -> int {
+        *in = v;
+        if (!a8) return TB_OK;
+        *in = w.xa;
+        return act_rec(v, w.xa, xq, 1, k, st);
+    };
+    const float *in = nullptr;
     // 1. xn = RMSNorm(x) (+ its records), 2-6. attention block, x += O(attn)
-    if ((rc = launch_rmsnorm(w.state, nullptr, x, input_norm_w, w.xn, w.xq_h, H, e, st)))
+    if ((rc = launch_rmsnorm(w.state, nullptr, x, input_norm_w, w.xn, a8 ? nullptr : w.xq_h, H, e,
+                             st)) ||
+        (rc = input(w.xn, w.xq_h, H, &in)))
         return rc;
     const Proj qkv{4, qkv_w, qkv_s, 0, qkv_b}, o{4, o_w, o_s, 0, o_b};
-    rc = attention_block(qkv, o, w.xn, w.xq_h, k_cache, v_cache, cos, sin, x, x, hidden,
+    rc = attention_block(qkv, o, in, w.xq_h, k_cache, v_cache, cos, sin, x, x, hidden,
                          (int)num_heads, (int)num_kv_heads, (int)head_dim, (int)max_seq, gshift,
-                         w, st);
+                         a8, w, st);
     if (rc) return rc;
     // 8. xn = RMSNorm(x), 9. h = silu(gate xn + gb) * (up xn + ub), x += down h + db
-    if ((rc = launch_rmsnorm(w.state, nullptr, x, post_norm_w, w.xn, w.xq_h, H, e, st))) return rc;
+    if ((rc = launch_rmsnorm(w.state, nullptr, x, post_norm_w, w.xn, a8 ? nullptr : w.xq_h, H, e,
+                             st)) ||
+        (rc = input(w.xn, w.xq_h, H, &in)))
+        return rc;
     const Proj gate{4, gate_w, gate_s, 0, gate_b}, up{4, up_w, up_s, 0, up_b};
-    rc = project(gate, w.xn, w.xq_h, &up, nullptr, w.h, intermediate, hidden, gshift, EPI_SWIGLU,
+    rc = project(gate, in, w.xq_h, &up, nullptr, w.h, intermediate, hidden, gshift, EPI_SWIGLU,
                  nullptr, st);
     if (rc) return rc;
-    if ((rc = xquant(w.h, w.xq_i, 1, I, st))) return rc;
+    if (a8) {
+        if ((rc = input(w.h, w.xq_i, I, &in))) return rc;
+    } else {
+        if ((rc = xquant(w.h, w.xq_i, 1, I, st))) return rc;
+        in = w.h;
+    }
     const Proj down{4, down_w, down_s, 0, down_b};
-    return project(down, w.h, w.xq_i, nullptr, x, x, hidden, intermediate, gshift, EPI_RESID,
+    return project(down, in, w.xq_i, nullptr, x, x, hidden, intermediate, gshift, EPI_RESID,
                    nullptr, st);
 }
 

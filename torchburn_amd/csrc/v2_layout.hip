@@ -102,11 +102,8 @@ __global__ __launch_bounds__(256) void k_dequant_v2(const uint8_t *__restrict__ 
 // q = round-half-away(x / s_x) clamped to +-127 for the rest.  A NaN element
 // gives q = 0 (the reference's int conversion of NaN lands on byte 128, i.e.
 // q = 0); fmaxf skips NaN in the maximum.
-__global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
-                                                float *__restrict__ xo, int k) {
-    __shared__ float red[4];
-    const float *xr = x + (size_t)blockIdx.x * k;
-    float *yr = xo + (size_t)blockIdx.x * k;
+// s_x of one row: max(max|x|, 1e-10) / 127 (a 256-thread block).
+__device__ __forceinline__ float act_step(const float *xr, int k, float *red) {
     float mx = 0.f;
     for (int i = threadIdx.x; i < k; i += blockDim.x) mx = fmaxf(mx, fabsf(xr[i]));
 #pragma unroll
@@ -115,17 +112,57 @@ __global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     if (mx < 1e-10f) mx = 1e-10f;
-    const float sx = __fdiv_rn(mx, 127.0f);
+    return __fdiv_rn(mx, 127.0f);
+}
+
+// x' = q * s_x of element i of a row of k (body: the first 16 * (k / 16)).
+__device__ __forceinline__ float act_elem(float v, int i, int body, float sx, float inv) {
+    float q;
+    if (i < body) {
+        q = __builtin_rintf(__fmul_rn(v, inv));
+    } else {
+        q = fminf(fmaxf(roundf(__fdiv_rn(v, sx)), -127.f), 127.f);
+    }
+    return __fmul_rn(__builtin_isnan(q) ? 0.f : q, sx);
+}
+
+__global__ __launch_bounds__(256) void k_act_u8(const float *__restrict__ x,
+                                                float *__restrict__ xo, int k) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * k;
+    float *yr = xo + (size_t)blockIdx.x * k;
+    const float sx = act_step(xr, k, red);
     const float inv = __fdiv_rn(1.0f, sx);
     const int body = k / 16 * 16;
-    for (int i = threadIdx.x; i < k; i += blockDim.x) {
-        float q;
-        if (i < body) {
-            q = __builtin_rintf(__fmul_rn(xr[i], inv));
-        } else {
-            q = fminf(fmaxf(roundf(__fdiv_rn(xr[i], sx)), -127.f), 127.f);
-        }
-        yr[i] = __fmul_rn(__builtin_isnan(q) ? 0.f : q, sx);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) yr[i] = act_elem(xr[i], i, body, sx, inv);
+}
+
+// k_act_u8 that also writes the chunk records of x' (k % 32 == 0): eight lanes
+// per 32-element chunk, each with one float4 of x, so the GEMV input of a
+// W4A8 projection costs one pass instead of two.
+__global__ __launch_bounds__(256) void k_act_rec(const float *__restrict__ x,
+                                                 float *__restrict__ xo,
+                                                 uint32_t *__restrict__ xq, int k) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * k;
+    float *yr = xo + (size_t)blockIdx.x * k;
+    const int nc = k / 32;
+    uint32_t *qr = xq + (size_t)blockIdx.x * nc * kXRecDwords;
+    const float sx = act_step(xr, k, red);
+    const float inv = __fdiv_rn(1.0f, sx);
+    const int body = k / 16 * 16, n4 = k / 4;
+    // every thread runs the same number of rounds: the record build's quad
+    // exchanges need whole 8-lane groups
+    for (int e0 = 0; e0 < n4; e0 += blockDim.x) {
+        const int e = e0 + (int)threadIdx.x;
+        const bool live = e < n4;   // k % 32 == 0: whole 8-lane groups are live or not
+        float4 v = live ? reinterpret_cast<const float4 *>(xr)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v.x = act_elem(v.x, 4 * e, body, sx, inv);
+        v.y = act_elem(v.y, 4 * e + 1, body, sx, inv);
+        v.z = act_elem(v.z, 4 * e + 2, body, sx, inv);
+        v.w = act_elem(v.w, 4 * e + 3, body, sx, inv);
+        if (live) reinterpret_cast<float4 *>(yr)[e] = v;
+        build_xrec8(v, e & 7, live, qr, nc, live ? e >> 3 : 0);
     }
 }
 
@@ -162,6 +199,14 @@ int round_scales_f16(float *s, int64_t n, hipStream_t st) {
 int act_u8(const float *x, float *xo, int64_t m, int64_t k, hipStream_t st) {
     if (m == 0) return TB_OK;
     hipLaunchKernelGGL(k_act_u8, dim3((unsigned)m), dim3(256), 0, st, x, xo, (int)k);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int act_rec(const float *x, float *xo, uint32_t *xq, int64_t m, int64_t k, hipStream_t st) {
+    TB_REQUIRE(k % 32 == 0, TB_ERR_UNSUPPORTED, "TB_UNSUPPORTED: W4A8 records need K % 32 == 0");
+    if (m == 0) return TB_OK;
+    hipLaunchKernelGGL(k_act_rec, dim3((unsigned)m), dim3(256), 0, st, x, xo, xq, (int)k);
     TB_LAUNCHED();
     return TB_OK;
 }
