@@ -152,9 +152,10 @@ TB_API int tb_unpack_rows_w4a32_group64_v2_to_v1(const uint8_t *w_blocked, uint8
  * top_k == 1, else the top-k (ties: lower index first; non-finite logits as
  * -inf), softmax at the temperature, nucleus cut at top_p, one draw.  The
  * reference draws from an unseeded generator; here draw number `counter` of
- * `seed` is u = tb_sample_uniform(seed, counter).  top_k <= 128 and vocab <=
- * 262144.  Synchronizes the stream; *token_out and *u_out (or -1 when nothing
- * was drawn) are host values.
+ * `seed` is u = tb_sample_uniform(seed, counter).  Any top_k (above 128 one
+ * block takes the whole vocabulary and finds the cut and the draw by radix
+ * searches over the sorted mass); vocab <= 262144.  Synchronizes the stream;
+ * *token_out and *u_out (or -1 when nothing was drawn) are host values.
  */
 TB_API int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t top_k,
                             float top_p, float repetition_penalty, const int64_t *recent,
@@ -418,10 +419,10 @@ TB_API int tb_decoder_step(tb_decoder *d, int64_t token, int64_t offset, float *
 
 /* decode_and_sample (decoder.rs:752-777, 878-1020): repetition penalty over
  * `recent`, then greedy (temperature <= 0 or not finite, or top_k == 1) or
- * top-k / top-p sampling from the decoder's seeded generator.  top_k <= 128
- * samples on the device (tb_sample_logits, draws numbered from the last
- * tb_decoder_set_seed); larger top_k reads the logits back and samples on the
- * host. */
+ * top-k / top-p sampling from the decoder's seeded generator, on the device
+ * for any top_k (tb_sample_logits; draws numbered from the last
+ * tb_decoder_set_seed); vocabularies past 262144 read the logits back and
+ * sample on the host. */
 TB_API int tb_decoder_decode_and_sample(tb_decoder *d, int64_t token, int64_t offset,
                                         float temperature, int64_t top_k,
                                         float repetition_penalty, const int64_t *recent,
@@ -438,9 +439,9 @@ TB_API int tb_decoder_generate(tb_decoder *d, int64_t first_token, int64_t seq_l
 /* generate_loop with sampling (decoder.rs:788-832, window 859-876): the window
  * starts as the last 64 of recent_seed (n_seed ids, may be NULL when 0), each
  * step pushes its input token, applies the penalty over the window and samples
- * the next token.  With top_k <= 128 the steps inside the cache run as replays
- * of a graph whose tail samples on the device (no logits read back; with an
- * EOS token one 4-byte read per step).  Greedy without a penalty is
+ * the next token.  The steps inside the cache run as replays of a graph whose
+ * tail samples on the device (no logits read back; with an EOS token one
+ * 4-byte read per step), for any top_k.  Greedy without a penalty is
  * tb_decoder_generate. */
 TB_API int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_len,
                                        int64_t max_new_tokens, float temperature, int64_t top_k,

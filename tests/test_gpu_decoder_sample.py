@@ -51,7 +51,9 @@ def oracle_generate(ref, first, seq_len, n, T, k, top_p, pen, seed, recent_seed=
 
 
 @pytest.mark.parametrize("T,k,top_p,pen", [(0.8, 40, 0.9, 1.1), (1.2, 128, 1.0, 1.0),
-                                           (0.0, 40, 1.0, 1.3), (0.7, 2, 0.5, 1.05)])
+                                           (0.0, 40, 1.0, 1.3), (0.7, 2, 0.5, 1.05),
+                                           (0.9, 500, 0.95, 1.1), (1.0, 129, 1.0, 1.0),
+                                           (0.8, 5000, 0.9, 1.0)])
 def test_generate_sampled_matches_oracle(cuda, T, k, top_p, pen):
     print(f"case sampled generate T={T} top_k={k} top_p={top_p} penalty={pen}", flush=True)
     ref, dec = make(128)
@@ -94,12 +96,20 @@ def test_generate_sampled_eos_and_past_cache(cuda):
     dec.close()
 
 
-def test_host_sampler_beyond_device_top_k(cuda):
-    _, dec = make(64)
-    dec.set_seed(5)
-    a, _ = dec.generate_loop(11, 0, 8, temperature=0.8, top_k=500, repetition_penalty=1.1)
-    dec.reset_kv_cache()
-    dec.set_seed(5)
-    b, _ = dec.generate_loop(11, 0, 8, temperature=0.8, top_k=500, repetition_penalty=1.1)
-    assert a == b and all(0 <= t < 1000 for t in a)
+def test_sampler_paths_alternate_in_one_loop(cuda):
+    """top_k on either side of the slice path's 128 in one decoder: each path has
+    its own sampled-step graph, and switching back and forth keeps the draw
+    stream (seeded, the oracle's tokens)."""
+    ref, dec = make(128)
+    seed = 77
+    # each oracle run rewrites positions 0..7 in order before reading them
+    want_a = oracle_generate(ref, 11, 0, 8, 0.8, 40, 0.9, 1.1, seed)
+    want_b = oracle_generate(ref, 11, 0, 8, 0.8, 300, 0.9, 1.1, seed)
+    ref.close()
+    for k, want in ((40, want_a), (300, want_b), (40, want_a), (300, want_b)):
+        dec.reset_kv_cache()
+        dec.set_seed(seed)
+        got, _ = dec.generate_loop(11, 0, 8, temperature=0.8, top_k=k, top_p=0.9,
+                                   repetition_penalty=1.1)
+        assert got == want, k
     dec.close()

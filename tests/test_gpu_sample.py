@@ -1,7 +1,10 @@
 """The device sampler (tb_sample_logits) against the oracle's restatement of
 apply_repetition_penalty + sample_logits (decoder.rs:878-1020), pinned in
 tests/test_oracle_sample.py.  The draw u of (seed, counter) comes from the
-library's generator (tb_sample_uniform); given u the token must be identical.
+library's generator (tb_sample_uniform); given u the token must be identical
+for top_k <= 128 (sequential sums over at most 128 items, as the oracle's).
+Past that the masses are summed in a parallel order and the token must lie
+between the oracle's draws at u -/+ 2e-3.
 """
 import numpy as np
 import pytest
@@ -23,6 +26,13 @@ CASES = [
     (151936, 0.9, 1, 1.0, 1.3),        # top_k 1 -> greedy after the penalty
     (5000, 1.0, 0, 1.0, 1.0),          # top_k 0 -> one candidate
     (300, 2.0, 128, 0.95, 1.5),
+    # top_k past the slice path: one block over the whole vocabulary
+    (151936, 0.8, 500, 0.9, 1.1),
+    (128256, 1.0, 4096, 1.0, 1.0),
+    (1000, 0.7, 1000, 0.95, 1.0),       # k == V
+    (300, 2.0, 129, 1.0, 1.2),
+    (5000, 0.5, 200000, 0.8, 1.0),      # k > V
+    (151936, 1.0, 151936, 0.5, 1.0),    # the whole vocabulary, nucleus cut
 ]
 
 
@@ -52,8 +62,23 @@ def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
             assert u == uu
         else:
             assert u == -1.0
-        ref, _ = O.sample_logits(O.repetition_penalty(lg, recent, pen), T, k, top_p, uu)
-        assert tok == ref, (trial, tok, ref)
+        pl = O.repetition_penalty(lg, recent, pen)
+        ref, _ = O.sample_logits(pl, T, k, top_p, uu)
+        if greedy or k <= 128 or tok == ref:
+            assert tok == ref, (trial, tok, ref)
+            continue
+        # top_k > 128: the masses are summed in a parallel order, and over tens
+        # of thousands of f32 terms that moves the nucleus cut and the draw
+        # point by up to ~1e-4 of the mass.  The draw is monotone in u over the
+        # sorted order (value descending, index ascending), so the token must
+        # lie between the oracle's draws at u -/+ 2e-3.
+        key = np.where(np.isfinite(pl), pl, -np.inf)
+        order = np.lexsort((np.arange(V), -key.astype(np.float64)))
+        pos = np.empty(V, np.int64)
+        pos[order] = np.arange(V)
+        lo, _ = O.sample_logits(pl, T, k, top_p, max(0.0, uu - 2e-3))
+        hi, _ = O.sample_logits(pl, T, k, top_p, min(1.0 - 2 ** -24, uu + 2e-3))
+        assert pos[lo] <= pos[tok] <= pos[hi], (trial, tok, ref, pos[lo], pos[tok], pos[hi])
 
 
 def test_sampler_leaves_logits_and_limits(cuda):
@@ -61,8 +86,9 @@ def test_sampler_leaves_logits_and_limits(cuda):
     before = lg.clone()
     tb.sample_logits(lg, 0.7, 40, 1.0, 1.5, [1, 2, 3])
     assert torch.equal(lg, before)
-    with pytest.raises(tb.UnsupportedOpError, match="top_k"):
-        tb.sample_logits(lg, 0.7, 129)
+    tb.sample_logits(lg, 0.7, 129)   # any top_k on the device
+    with pytest.raises(tb.UnsupportedOpError, match="vocabulary"):
+        tb.sample_logits(torch.randn(262145, device=cuda), 0.7, 40)
 
 
 def test_sampler_seed_reproducible_and_distribution(cuda):

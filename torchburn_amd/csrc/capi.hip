@@ -697,8 +697,6 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     // decoder.rs:919-931: greedy when the temperature is not usable or top_k == 1
     const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
     const int64_t k = greedy ? 1 : std::max<int64_t>(1, std::min<int64_t>(top_k, vocab));
-    TB_REQUIRE(k <= kSampleMaxK, TB_ERR_UNSUPPORTED,
-               "TB_UNSUPPORTED: device sampling takes top_k <= " + std::to_string(kSampleMaxK));
     SampleParams prm{};
     prm.temperature = temperature;
     prm.top_p = top_p;
@@ -707,9 +705,9 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     prm.greedy = greedy ? 1 : 0;
     prm.seed = seed;
     prm.counter = counter;
-    const size_t cand = (size_t)kSampleCand;
+    const size_t cand = (size_t)sample_scratch_items(vocab);
     const size_t bytes = up256(sizeof(SampleParams)) + up256(sizeof(SampleOut)) +
-                         up256(cand * 4) + up256(cand * 4) + up256(kSampleMaxBlocks * 4);
+                         3 * up256(cand * 4) + up256(kSampleMaxBlocks * 4);
     WsLease lease;
     int rc = workspace(bytes, (hipStream_t)stream, lease);
     if (rc) return rc;
@@ -724,10 +722,13 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     w += up256(cand * 4);
     sc.idx = reinterpret_cast<int *>(w);
     w += up256(cand * 4);
+    sc.p = reinterpret_cast<float *>(w);
+    w += up256(cand * 4);
     sc.cnt = reinterpret_cast<int *>(w);
     hipStream_t st = (hipStream_t)stream;
     TB_HIP(hipMemcpyAsync(dprm, &prm, sizeof(prm), hipMemcpyHostToDevice, st));
-    rc = launch_sample(logits, (int)vocab, recent, (int)n_recent, dprm, sc, dout, st);
+    rc = launch_sample(logits, (int)vocab, recent, (int)n_recent, dprm, sc, dout, st,
+                       k > kSampleMaxK);
     if (rc) return rc;
     SampleOut ho{};
     TB_HIP(hipMemcpyAsync(&ho, dout, sizeof(ho), hipMemcpyDeviceToHost, st));

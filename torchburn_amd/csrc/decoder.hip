@@ -109,14 +109,19 @@ struct Decoder {
     int64_t *srec = nullptr;
     int64_t srec_cap = 0;
     uint64_t seed = 0x7B, draws = 0;
-    hipGraph_t graph_s = nullptr;
-    hipGraphExec_t exec_s = nullptr;
+    // sampled step graphs: [0] top_k <= kSampleMaxK (slice path), [1] beyond
+    hipGraph_t graph_s[2] = {nullptr, nullptr};
+    hipGraphExec_t exec_s[2] = {nullptr, nullptr};
+    bool tail_large = false;     // the sampler path enqueued by enqueue_tail
+    bool sample_large = false;   // the path of the parameters set last
 
     ~Decoder() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
-        if (exec_s) (void)hipGraphExecDestroy(exec_s);
-        if (graph_s) (void)hipGraphDestroy(graph_s);
+        for (int i = 0; i < 2; ++i) {
+            if (exec_s[i]) (void)hipGraphExecDestroy(exec_s[i]);
+            if (graph_s[i]) (void)hipGraphDestroy(graph_s[i]);
+        }
         if (st) (void)hipStreamSynchronize(st);
         for (void *p : allocs) (void)hipFree(p);
         if (hstate) (void)hipHostFree(hstate);
@@ -260,8 +265,8 @@ struct Decoder {
     // The step's tail: greedy argmax, or the device sampler over the window.
     int enqueue_tail(bool sampled) {
         if (!sampled) return launch_argmax(logits, V, am_v, am_i, state, history, hist_cap, st);
-        return launch_sample(logits, V, nullptr, 0, sprm, sws, sout, st, swin, state, history,
-                             hist_cap);
+        return launch_sample(logits, V, nullptr, 0, sprm, sws, sout, st, tail_large, swin, state,
+                             history, hist_cap);
     }
 
     int enqueue_step_fused(bool sampled) {
@@ -454,10 +459,14 @@ struct Decoder {
     int drop_graphs() {
         if (exec) TB_HIP(hipGraphExecDestroy(exec));
         if (graph) TB_HIP(hipGraphDestroy(graph));
-        if (exec_s) TB_HIP(hipGraphExecDestroy(exec_s));
-        if (graph_s) TB_HIP(hipGraphDestroy(graph_s));
-        exec = exec_s = nullptr;
-        graph = graph_s = nullptr;
+        for (int i = 0; i < 2; ++i) {
+            if (exec_s[i]) TB_HIP(hipGraphExecDestroy(exec_s[i]));
+            if (graph_s[i]) TB_HIP(hipGraphDestroy(graph_s[i]));
+            exec_s[i] = nullptr;
+            graph_s[i] = nullptr;
+        }
+        exec = nullptr;
+        graph = nullptr;
         return TB_OK;
     }
 
@@ -467,18 +476,24 @@ struct Decoder {
         int rc;
         if ((rc = alloc(&sprm, sizeof(SampleParams))) || (rc = alloc(&sout, sizeof(SampleOut))) ||
             (rc = alloc(&swin, sizeof(SampleWindow))) ||
-            (rc = alloc(&sws.key, (size_t)kSampleCand * 4)) ||
-            (rc = alloc(&sws.idx, (size_t)kSampleCand * 4)) ||
+            (rc = alloc(&sws.key, (size_t)sample_scratch_items(V) * 4)) ||
+            (rc = alloc(&sws.idx, (size_t)sample_scratch_items(V) * 4)) ||
+            (rc = alloc(&sws.p, (size_t)sample_scratch_items(V) * 4)) ||
             (rc = alloc(&sws.cnt, (size_t)kSampleMaxBlocks * 4)))
             return rc;
         return TB_OK;
     }
 
+    // The sampled step graph of the path the parameters set last call for.
     int ensure_graph_s() {
         int rc = sampler_alloc();
         if (rc || (rc = sync_a8())) return rc;
-        return exec_s ? TB_OK : capture(true, &graph_s, &exec_s);
+        const int i = sample_large ? 1 : 0;
+        if (exec_s[i]) return TB_OK;
+        tail_large = sample_large;
+        return capture(true, &graph_s[i], &exec_s[i]);
     }
+    hipGraphExec_t sampled_graph() const { return exec_s[sample_large ? 1 : 0]; }
 
     // Upload of the sampling parameters (the draw counter continues the stream).
     int set_sampler(float temperature, int64_t top_k, float top_p, float penalty) {
@@ -493,6 +508,7 @@ struct Decoder {
         p.greedy = greedy ? 1 : 0;
         p.seed = seed;
         p.counter = draws;
+        sample_large = p.k > kSampleMaxK;
         TB_HIP(hipMemcpyAsync(sprm, &p, sizeof(p), hipMemcpyHostToDevice, st));
         return TB_OK;
     }
@@ -509,11 +525,9 @@ struct Decoder {
         return TB_OK;
     }
 
-    bool device_samplable(float temperature, int64_t top_k) const {
-        const bool greedy = !std::isfinite(temperature) || temperature <= 0.f || top_k == 1;
-        const int64_t k = greedy ? 1 : std::max<int64_t>(1, std::min<int64_t>(top_k, V));
-        return k <= kSampleMaxK && V <= kSampleMaxBlocks * kSampleSlice;
-    }
+    // Every top_k samples on the device (top_k > kSampleMaxK on the one-block
+    // path); the host sampler remains for vocabularies past the slice grid.
+    bool device_samplable(float, int64_t) const { return V <= kSampleMaxBlocks * kSampleSlice; }
 
     // decode_and_sample on the device: one step, then the sampler over the
     // logits with the caller's recent tokens.
@@ -530,7 +544,7 @@ struct Decoder {
             TB_HIP(hipMemcpyAsync(srec, recent, (size_t)n_recent * 8, hipMemcpyHostToDevice, st));
         }
         if ((rc = launch_sample(logits, V, srec, penalty > 1.0f ? (int)n_recent : 0, sprm, sws,
-                                sout, st)))
+                                sout, st, sample_large)))
             return rc;
         return sampler_result(out);
     }
@@ -1067,8 +1081,9 @@ int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_
             next = tb::sample(d->host_logits, temperature, top_k, top_p, d->rng);
         }
     } else {
-        if ((rc = d->ensure_graph_s()) || (rc = d->set_sampler(temperature, top_k, top_p,
-                                                               repetition_penalty)))
+        // the parameters first: they pick the sampled graph's path
+        if ((rc = d->set_sampler(temperature, top_k, top_p, repetition_penalty)) ||
+            (rc = d->ensure_graph_s()))
             return rc;
         SampleWindow hw{};
         const int64_t w0 = std::min<int64_t>((int64_t)win.size(), kSampleWindow);
@@ -1084,7 +1099,7 @@ int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_
         if (valid > 0) {
             if ((rc = d->set_state((int)first_token, (int)seq_len))) return rc;
             if (eos_token_id < 0) {
-                for (int64_t i = 0; i < valid; ++i) TB_HIP(hipGraphLaunch(d->exec_s, d->st));
+                for (int64_t i = 0; i < valid; ++i) TB_HIP(hipGraphLaunch(d->sampled_graph(), d->st));
                 std::vector<int> hist((size_t)valid);
                 TB_HIP(hipMemcpyAsync(hist.data(), d->history, (size_t)valid * 4,
                                       hipMemcpyDeviceToHost, d->st));
@@ -1096,7 +1111,7 @@ int tb_decoder_generate_sampled(tb_decoder *d, int64_t first_token, int64_t seq_
             } else {
                 while (n < valid && next != eos_token_id) {
                     tokens_out[n++] = next;
-                    TB_HIP(hipGraphLaunch(d->exec_s, d->st));
+                    TB_HIP(hipGraphLaunch(d->sampled_graph(), d->st));
                     if ((rc = d->sampler_result(&next))) return rc;
                 }
             }

@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "decode.hpp"
+#include "gemv_common.hpp"
 #include "sample.hpp"
 #include "tb_common.hpp"
 
@@ -65,33 +66,48 @@ __device__ __forceinline__ int block_excl(int flag, int *s, int *total) {
     return base + below;
 }
 
-// The k-th largest (k >= 1) of the n keys in LDS; *need receives how many keys
-// equal to it belong to the top k.  hist: 256 ints of LDS; sh: 2 ints.
-__device__ uint32_t kth_largest(const uint32_t *keys, int n, int k, int *hist, int *sh,
-                                int *need) {
+// The k-th largest (k >= 1, k <= n) of n keys, key_at(i) for i < n, over an
+// NT-thread block; *need receives how many keys equal to it belong to the top
+// k.  Eight passes of 4-bit digits from the top; each thread counts its keys
+// per digit in registers (no atomics: logits crowd a few exponent digits, and
+// LDS atomics on one bin serialise), the 16 counts are summed across the wave
+// by a transpose reduction and across the waves through LDS (red: NT / 4
+// floats; counts stay exact in f32 below 2^24).
+template <int NT, class KeyAt>
+__device__ uint32_t kth_largest(KeyAt key_at, int n, int k, float *red, int *need) {
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t prefix = 0u, mask = 0u;
     int kk = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int i = threadIdx.x; i < 256; i += kThreads) hist[i] = 0;
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += kThreads) {
-            const uint32_t key = keys[i];
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+    for (int shift = 28; shift >= 0; shift -= 4) {
+        float c[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) c[j] = 0.f;
+        for (int i = threadIdx.x; i < n; i += NT) {
+            const uint32_t key = key_at(i);
+            const bool act = (key & mask) == prefix;
+            const uint32_t d = (key >> shift) & 15u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) c[j] += (act && d == (uint32_t)j) ? 1.f : 0.f;
         }
+        gemv::transpose_reduce<16>(c, lane, 6);   // lane 4b: digit b's wave count
+        if ((lane & 3) == 0) red[wave * 16 + ((lane >> 2) & 15)] = c[0];
         __syncthreads();
-        if (threadIdx.x == 0) {
-            int cum = 0, d = 255;
-            for (; d > 0; --d) {
-                if (cum + hist[d] >= kk) break;
-                cum += hist[d];
+        int cum = 0, dsel = 0, rem = kk;
+        for (int d = 15; d >= 0; --d) {
+            int t = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) t += (int)red[w * 16 + d];
+            if (cum + t >= kk) {
+                dsel = d;
+                rem = kk - cum;
+                break;
             }
-            sh[0] = d;
-            sh[1] = kk - cum;
+            cum += t;
         }
-        __syncthreads();
-        prefix |= (uint32_t)sh[0] << shift;
-        mask |= 255u << shift;
-        kk = sh[1];
+        prefix |= (uint32_t)dsel << shift;
+        mask |= 15u << shift;
+        kk = rem;
         __syncthreads();
     }
     *need = kk;
@@ -162,9 +178,10 @@ __global__ __launch_bounds__(kThreads) void k_topk_slice(const float *__restrict
     __shared__ uint32_t keys[kSampleSlice];
     __shared__ uint32_t okey[kSampleMaxK];
     __shared__ int oidx[kSampleMaxK];
-    __shared__ int hist[256];
+    __shared__ float red[kThreads / 4];
     __shared__ int sh[8];
     const int k = prm->k;
+    if (k > kSampleMaxK) return;   // the large-k path samples
     const bool greedy = prm->greedy != 0;
     const int b = blockIdx.x, base = b * kSampleSlice;
     const int n = min(kSampleSlice, V - base);
@@ -177,7 +194,8 @@ __global__ __launch_bounds__(kThreads) void k_topk_slice(const float *__restrict
     __syncthreads();
     const int kk = min(k, n);
     int need;
-    const uint32_t kth = kth_largest(keys, n, kk, hist, sh, &need);
+    const uint32_t kth =
+        kth_largest<kThreads>([&](int i) { return keys[i]; }, n, kk, red, &need);
     const int m = gather_top(keys, nullptr, n, kth, need, okey, oidx, sh + 4);
     __syncthreads();
     for (int i = threadIdx.x; i < m; i += kThreads) {
@@ -200,29 +218,40 @@ __global__ __launch_bounds__(kThreads) void k_topk_draw(const uint32_t *__restri
     __shared__ uint32_t tk[kSampleMaxK];
     __shared__ int ti[kSampleMaxK];
     __shared__ float p[kSampleMaxK];
-    __shared__ int hist[256];
+    __shared__ float red[kThreads / 4];
     __shared__ int sh[8];
     __shared__ int off[kSampleMaxBlocks + 1];
     const int k = prm->k;
-    if (threadIdx.x == 0) {
-        int o = 0;
-        for (int b = 0; b < nb; ++b) {
-            off[b] = o;
-            o += cnt[b];
+    if (k > kSampleMaxK) return;   // the large-k path samples
+    // slice offsets: an exclusive scan of the counts by wave 0 (nb <= 128)
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const int c0 = 2 * l < nb ? cnt[2 * l] : 0, c1 = 2 * l + 1 < nb ? cnt[2 * l + 1] : 0;
+        int incl = c0 + c1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o);
+            if (l >= o) incl += t;
         }
-        off[nb] = o;
+        const int ex = incl - c0 - c1;
+        if (2 * l < nb) off[2 * l] = ex;
+        if (2 * l + 1 < nb) off[2 * l + 1] = ex + c0;
+        if (l == 63) off[nb] = incl;
     }
     __syncthreads();
     const int n = off[nb];
-    for (int b = 0; b < nb; ++b)
-        for (int i = threadIdx.x; i < cnt[b]; i += kThreads) {
-            keys[off[b] + i] = cand_key[(size_t)b * kSampleMaxK + i];
-            idx[off[b] + i] = cand_idx[(size_t)b * kSampleMaxK + i];
+    for (int e = threadIdx.x; e < nb * kSampleMaxK; e += kThreads) {
+        const int b = e / kSampleMaxK, i = e - b * kSampleMaxK;
+        if (i < cnt[b]) {
+            keys[off[b] + i] = cand_key[e];
+            idx[off[b] + i] = cand_idx[e];
         }
+    }
     __syncthreads();
     const int kk = min(k, n);
     int need;
-    const uint32_t kth = kth_largest(keys, n, kk, hist, sh, &need);
+    const uint32_t kth =
+        kth_largest<kThreads>([&](int i) { return keys[i]; }, n, kk, red, &need);
     const int m = gather_top(keys, idx, n, kth, need, tk, ti, sh + 4);
     // bitonic sort of the m (<= 128) items: key descending, index ascending
     for (int i = m + threadIdx.x; i < kSampleMaxK; i += kThreads) {
@@ -301,6 +330,241 @@ __global__ __launch_bounds__(kThreads) void k_topk_draw(const uint32_t *__restri
     }
 }
 
+// ---- top_k > kSampleMaxK: one block over the whole vocabulary ----
+constexpr int kLargeThreads = 1024;
+
+// Exclusive scan of one value per thread over an NT-thread block in thread
+// order; *total gets the block's sum.  s: NT / 64 + 1 entries of LDS.
+template <int NT, class T>
+__device__ T block_scan_excl(T v, T *s, T *total) {
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    T incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) s[wave] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        T run = T(0);
+        for (int w = 0; w < NW; ++w) {
+            const T t = s[w];
+            s[w] = run;
+            run += t;
+        }
+        s[NW] = run;
+    }
+    __syncthreads();
+    const T ex = s[wave] + incl - v;
+    *total = s[NW];
+    __syncthreads();
+    return ex;
+}
+
+// The first item, in sorted order (key descending, then index ascending), at
+// which the running mass of p crosses M (strict: > M, else >= M).  Items
+// [0, n) are in index order.  Returns its position in the arrays (or -1 when
+// the whole mass does not cross) and *through the mass up to and including it.
+// The key of the crossing item comes from a radix search whose bins hold
+// masses instead of counts, then its rank among equal keys from a block scan
+// in index order.  red: NT / 4 floats; s: NT / 64 + 1 floats; si: 2 ints.
+template <int NT>
+__device__ int mass_cross(const uint32_t *keys, const float *p, int n, float M, bool strict,
+                          float *red, float *s, int *si, float *through) {
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    auto crosses = [&](float x) { return strict ? x > M : x >= M; };
+    uint32_t prefix = 0u, mask = 0u;
+    float above = 0.f;   // mass of the items whose key is above the prefix
+    for (int shift = 28; shift >= 0; shift -= 4) {
+        float c[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) c[j] = 0.f;
+        for (int i = threadIdx.x; i < n; i += NT) {
+            const uint32_t key = keys[i];
+            const bool act = (key & mask) == prefix;
+            const uint32_t d = (key >> shift) & 15u;
+            const float pi = p[i];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) c[j] += (act && d == (uint32_t)j) ? pi : 0.f;
+        }
+        gemv::transpose_reduce<16>(c, lane, 6);
+        if ((lane & 3) == 0) red[wave * 16 + ((lane >> 2) & 15)] = c[0];
+        __syncthreads();
+        int dsel = -1;
+        for (int d = 15; d >= 0; --d) {
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) t += red[w * 16 + d];
+            if (t > 0.f && crosses(above + t)) {
+                dsel = d;
+                break;
+            }
+            above += t;
+        }
+        __syncthreads();
+        if (dsel < 0) {
+            if (shift == 28) return -1;   // the whole mass stays on the near side of M
+            // summation order left the cut in the last bin: take its lowest digit
+            for (int d = 0; d < 16; ++d) {
+                float t = 0.f;
+                for (int w = 0; w < NW; ++w) t += red[w * 16 + d];
+                if (t > 0.f) {
+                    dsel = d;
+                    break;
+                }
+            }
+            dsel = dsel < 0 ? 0 : dsel;
+        }
+        prefix |= (uint32_t)dsel << shift;
+        mask |= 15u << shift;
+    }
+    // the crossing item among those with key == prefix, in index order
+    const int per = (n + NT - 1) / NT, lo = threadIdx.x * per, hi = min(n, lo + per);
+    float part = 0.f;
+    int last = -1;
+    for (int i = lo; i < hi; ++i)
+        if (keys[i] == prefix) {
+            part += p[i];
+            last = i;
+        }
+    float tot;
+    const float base = block_scan_excl<NT, float>(part, s, &tot);
+    if (threadIdx.x == 0) {
+        si[0] = 0x7FFFFFFF;
+        si[1] = -1;
+    }
+    __syncthreads();
+    atomicMax(&si[1], last);   // the group's last item, when rounding never crosses
+    float acc = above + base;
+    for (int i = lo; i < hi; ++i)
+        if (keys[i] == prefix) {
+            acc += p[i];
+            if (crosses(acc)) {
+                atomicMin(&si[0], i);
+                break;
+            }
+        }
+    __syncthreads();
+    const int pos = si[0] != 0x7FFFFFFF ? si[0] : si[1];
+    // the mass through pos: recomputed by the thread whose range holds it
+    if (pos >= lo && pos < hi) {
+        float a = above + base;
+        for (int i = lo; i <= pos; ++i)
+            if (keys[i] == prefix) a += p[i];
+        s[0] = a;
+    }
+    __syncthreads();
+    *through = s[0];
+    __syncthreads();
+    return pos;
+}
+
+// Top-k sampling for k > kSampleMaxK: the k-th largest key over the whole
+// vocabulary, the k items (in index order) into the scratch, p_i =
+// exp((v_i - v_0) / T), the nucleus cut (the first item whose mass before it,
+// normalised, exceeds top_p) and the draw (the first item whose running mass
+// reaches u * the kept mass), both in sorted order, as the small-k path and
+// the reference's sample_logits (decoder.rs:950-1019) visit them.  The masses
+// are summed in a parallel order, so an item within an f32 rounding of the
+// cut or the draw point may differ from a sequential sum's choice.
+__global__ __launch_bounds__(kLargeThreads) void k_topk_large(
+    const float *__restrict__ logits, int V, SampleParams *__restrict__ prm,
+    uint32_t *__restrict__ ikey, int *__restrict__ iidx, float *__restrict__ ip,
+    SampleOut *__restrict__ out, DecState *__restrict__ st, int *__restrict__ history,
+    int hist_cap) {
+    constexpr int NT = kLargeThreads, NW = NT / 64;
+    __shared__ float red[NT / 4];
+    __shared__ float sf[NW + 1];
+    __shared__ int sn[NW + 1];
+    __shared__ int si[2];
+    __shared__ uint32_t smax[2];
+    const int k = prm->k;
+    if (k <= kSampleMaxK) return;   // the small-k kernels sample
+    const int kk = min(k, V);
+    int need;
+    const uint32_t kth = kth_largest<NT>([&](int i) { return fkey(logits[i], false); }, V, kk,
+                                         red, &need);
+    // the k items in index order: each thread a contiguous range of the vocabulary
+    const int per = (V + NT - 1) / NT, lo = threadIdx.x * per, hi = min(V, lo + per);
+    int ng = 0, ne = 0;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t key = fkey(logits[i], false);
+        ng += key > kth;
+        ne += key == kth;
+    }
+    int tot;
+    const int eq_base = block_scan_excl<NT, int>(ne, sn, &tot);
+    const int eq_take = max(0, min(ne, need - eq_base));
+    const int base = block_scan_excl<NT, int>(ng + eq_take, sn, &tot);
+    int w = base, eq_seen = 0;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t key = fkey(logits[i], false);
+        const bool eq = key == kth;
+        if (key > kth || (eq && eq_seen < eq_take)) {
+            ikey[w] = key;
+            iidx[w] = i;
+            ++w;
+        }
+        eq_seen += eq;
+    }
+    __syncthreads();
+    const int n = tot;   // == kk
+    // the top item: the largest key, lowest index among equals (items in index order)
+    if (threadIdx.x == 0) smax[0] = 0u;
+    __syncthreads();
+    uint32_t mk = 0u;
+    for (int i = threadIdx.x; i < n; i += NT) mk = max(mk, ikey[i]);
+    atomicMax(&smax[0], mk);
+    __syncthreads();
+    const uint32_t kmax = smax[0];
+    if (threadIdx.x == 0) si[0] = 0x7FFFFFFF;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += NT)
+        if (ikey[i] == kmax) atomicMin(&si[0], i);
+    __syncthreads();
+    const int top = si[0];
+    __syncthreads();
+    const float T = prm->temperature, inv_t = 1.0f / T, vmax = kval(kmax);
+    float part = 0.f;
+    for (int i = threadIdx.x; i < n; i += NT) {
+        const float pi = expf((kval(ikey[i]) - vmax) * inv_t);
+        ip[i] = pi;
+        part += pi;
+    }
+    __syncthreads();
+    float pre;
+    (void)block_scan_excl<NT, float>(part, sf, &pre);
+    float ks = pre;
+    const float tp = prm->top_p;
+    if (tp > 0.f && tp < 1.f && n > 1 && pre > 0.f) {
+        float thr;
+        const int c = mass_cross<NT>(ikey, ip, n, tp * pre, true, red, sf, si, &thr);
+        if (c >= 0) ks = thr;
+    }
+    const uint64_t z = splitmix(prm->seed + (prm->counter + 1ull) * 0x9E3779B97F4A7C15ull);
+    const float u = (float)(z >> 40) * 5.9604644775390625e-8f;   // [0, 1), 24 bits
+    float dthr;
+    const int d = mass_cross<NT>(ikey, ip, n, u * ks, false, red, sf, si, &dthr);
+    if (threadIdx.x == 0) {
+        const int tok = iidx[d >= 0 ? d : top];
+        prm->counter += 1ull;
+        out->u = u;
+        out->token = tok;
+        out->kept = n;
+        if (st) {   // the decoder's next step, as the greedy argmax tail does
+            const int step = st->step;
+            if (history && step < hist_cap) history[step] = tok;
+            st->argmax = tok;
+            st->token = tok;
+            st->pos = st->pos + 1;
+            st->step = step + 1;
+        }
+    }
+}
+
 // Pushes the step's input token onto the recent-token window (the last
 // kSampleWindow tokens, decoder.rs:859-876) before its penalty is applied.
 __global__ void k_window_push(const DecState *__restrict__ st, SampleWindow *__restrict__ w) {
@@ -328,7 +592,7 @@ int sample_blocks(int V) { return (V + kSampleSlice - 1) / kSampleSlice; }
 
 int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
                   SampleParams *prm, const SampleScratch &ws, SampleOut *out, hipStream_t st,
-                  SampleWindow *win, DecState *dstate, int *history, int hist_cap) {
+                  bool large, SampleWindow *win, DecState *dstate, int *history, int hist_cap) {
     const int nb = sample_blocks(V);
     TB_REQUIRE(nb <= kSampleMaxBlocks, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: device sampling supports vocabularies up to " +
@@ -346,6 +610,12 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
         hipLaunchKernelGGL(k_penalty, dim3(1), dim3(kThreads), lds, st, logits, V, recent,
                            n_recent, (const int *)nullptr, prm);
         TB_LAUNCHED();
+    }
+    if (large) {
+        hipLaunchKernelGGL(k_topk_large, dim3(1), dim3(kLargeThreads), 0, st, logits, V, prm,
+                           ws.key, ws.idx, ws.p, out, dstate, history, hist_cap);
+        TB_LAUNCHED();
+        return TB_OK;
     }
     hipLaunchKernelGGL(k_topk_slice, dim3(nb), dim3(kThreads), 0, st, logits, V, prm, ws.key,
                        ws.idx, ws.cnt);

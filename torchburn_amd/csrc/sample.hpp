@@ -9,7 +9,7 @@ namespace tb {
 struct DecState;
 
 constexpr int kSampleSlice = 2048;     // logits per top-k block
-constexpr int kSampleMaxK = 128;       // largest top_k sampled on the device
+constexpr int kSampleMaxK = 128;       // largest top_k of the two-stage (slice) path
 constexpr int kSampleMaxBlocks = 128;  // vocabularies up to 262144
 constexpr int kSampleCand = kSampleMaxBlocks * kSampleMaxK;
 
@@ -42,12 +42,17 @@ struct SampleWindow {
     int64_t tok[kSampleWindow];
 };
 
-// Device scratch of the top-k candidates: [kSampleMaxBlocks][kSampleMaxK].
+// Device scratch of the sampler: the top-k candidates, [kSampleMaxBlocks]
+// [kSampleMaxK] (k <= kSampleMaxK), or the k items and their weights
+// (k > kSampleMaxK): key, idx and p each hold sample_scratch_items(V) entries.
 struct SampleScratch {
     uint32_t *key;
     int *idx;
+    float *p;
     int *cnt;
 };
+
+inline int64_t sample_scratch_items(int64_t V) { return V > kSampleCand ? V : kSampleCand; }
 
 int sample_blocks(int V);
 
@@ -56,12 +61,14 @@ float sample_uniform(uint64_t seed, uint64_t counter);
 
 // Penalty over `recent` (device int64, n_recent of them; logits modified in
 // place), then top-k / temperature / top-p / draw per *prm into *out.
+// large: the path for k > kSampleMaxK (prm->k must be on the same side; each
+// path's kernels return at once for the other's k).
 // Decoder form: with `win`, the step's input token (dstate->token) is pushed
 // onto the window and the penalty covers the window; with `dstate`, the drawn
 // token becomes the next step's input (history, token, pos, step), as the
 // greedy argmax tail does.  Capturable in a graph.
 int launch_sample(float *logits, int V, const int64_t *recent, int n_recent, SampleParams *prm,
-                  const SampleScratch &ws, SampleOut *out, hipStream_t st,
+                  const SampleScratch &ws, SampleOut *out, hipStream_t st, bool large,
                   SampleWindow *win = nullptr, DecState *dstate = nullptr,
                   int *history = nullptr, int hist_cap = 0);
 

@@ -307,8 +307,8 @@ class RustQwenDecoder:
                       repetition_penalty: float = 1.0, top_p: float = 1.0,
                       eos_token_id: Optional[int] = None,
                       recent_seed: Optional[Sequence[int]] = None) -> Tuple[List[int], int]:
-        """Whole decode loop in one call (decoder.rs:788-832).  Sampling with
-        top_k <= 128 runs on the device (see tb_decoder_generate_sampled)."""
+        """Whole decode loop in one call (decoder.rs:788-832).  Sampling runs on
+        the device for any top_k (see tb_decoder_generate_sampled)."""
         toks = np.empty(max(int(max_new_tokens), 1), np.int64)
         n, sl = C.c_int64(), C.c_int64()
         eos = -1 if eos_token_id is None else int(eos_token_id)
