@@ -26,8 +26,11 @@ CASES = [
     (151936, 0.9, 1, 1.0, 1.3),        # top_k 1 -> greedy after the penalty
     (5000, 1.0, 0, 1.0, 1.0),          # top_k 0 -> one candidate
     (300, 2.0, 128, 0.95, 1.5),
+    (32000, 0.8, 128, 0.95, 1.1),      # fewer waves than k: every listed item competes
+    (5000, 1.0, 100, 0.9, 1.0),        # lists too short for k: the exact select
     # top_k past the slice path: one block over the whole vocabulary
     (151936, 0.8, 500, 0.9, 1.1),
+    (151936, 0.8, 512, 0.9, 1.0),
     (128256, 1.0, 4096, 1.0, 1.0),
     (1000, 0.7, 1000, 0.95, 1.0),       # k == V
     (300, 2.0, 129, 1.0, 1.2),
@@ -105,3 +108,46 @@ def test_sampler_seed_reproducible_and_distribution(cuda):
     freq = np.array([a.count(o) for o in order]) / len(a)
     assert set(a) <= set(order)
     assert np.abs(freq - p).max() < 0.08
+
+
+def _wave_ids(V, b, w):
+    """The ids one wave of the list kernel holds: runs of 16 ids, block b of
+    nb takes runs b, b + nb, ..., and wave w the ids = w (mod 4) of each."""
+    nb = (V + 2047) // 2048
+    ids = [16 * (b + nb * ((l >> 2) + 16 * i)) + 4 * (l & 3) + w
+           for l in range(64) for i in range(8)]
+    return np.array([i for i in ids if i < V])
+
+
+@pytest.mark.parametrize("kind", ["low_ids", "bands", "few_finite", "finite_below_k", "one_wave"])
+def test_sampler_wave_list_edges(cuda, kind):
+    """Logits laid out against the list kernel's waves: top tokens crowded into
+    the lowest ids (waves re-read), into whole waves by descending bands (more
+    candidates than the select block holds: the exact select), or finite in a
+    few places only; tokens identical to the oracle for top_k <= 128."""
+    print(f"case wave lists {kind}", flush=True)
+    V = 151936
+    g = np.random.default_rng(len(kind))
+    for k in (40, 100, 128):
+        lg = g.standard_normal(V).astype(np.float32)
+        if kind == "low_ids":
+            lg[:94] += 10.0
+        elif kind == "bands":
+            for n in range(16):
+                ids = _wave_ids(V, n // 4, n % 4)
+                lg[ids] = 10 + 2 * n + g.random(len(ids)).astype(np.float32)
+        elif kind == "few_finite":
+            keep = g.choice(V, 300, replace=False)
+            lg[np.setdiff1d(np.arange(V), keep)] = -np.inf
+        elif kind == "finite_below_k":
+            keep = g.choice(V, 50, replace=False)
+            lg[np.setdiff1d(np.arange(V), keep)] = -np.inf
+        else:
+            ids = _wave_ids(V, 3, 1)
+            lg[ids] += 8.0
+        for c in range(3):
+            u = tb.sample_uniform(11, c)
+            tok = tb.sample_logits(torch.from_numpy(lg).to(cuda), 0.9, k, 0.95, seed=11,
+                                   counter=c)
+            ref, _ = O.sample_logits(lg, 0.9, k, 0.95, u)
+            assert tok == ref, (kind, k, c, tok, ref)

@@ -707,7 +707,7 @@ int tb_sample_logits(float *logits, int64_t vocab, float temperature, int64_t to
     prm.counter = counter;
     const size_t cand = (size_t)sample_scratch_items(vocab);
     const size_t bytes = up256(sizeof(SampleParams)) + up256(sizeof(SampleOut)) +
-                         3 * up256(cand * 4) + up256(kSampleMaxBlocks * 4);
+                         3 * up256(cand * 4) + up256(kSampleLists * 4);
     WsLease lease;
     int rc = workspace(bytes, (hipStream_t)stream, lease);
     if (rc) return rc;

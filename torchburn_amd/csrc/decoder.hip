@@ -479,7 +479,7 @@ struct Decoder {
             (rc = alloc(&sws.key, (size_t)sample_scratch_items(V) * 4)) ||
             (rc = alloc(&sws.idx, (size_t)sample_scratch_items(V) * 4)) ||
             (rc = alloc(&sws.p, (size_t)sample_scratch_items(V) * 4)) ||
-            (rc = alloc(&sws.cnt, (size_t)kSampleMaxBlocks * 4)))
+            (rc = alloc(&sws.cnt, (size_t)kSampleLists * 4)))
             return rc;
         return TB_OK;
     }

@@ -8,10 +8,12 @@
 //     when positive, multiplied otherwise (a bitmap over the vocabulary in LDS
 //     makes "distinct" one atomicOr per token);
 //   * greedy (temperature not finite or <= 0, or top_k <= 1) is the top-1;
-//   * top-k: logits become order-preserving 32-bit keys (non-finite -> -inf);
-//     each of NB blocks radix-selects the k-th largest key of its 2048-element
-//     slice in LDS and writes its k best (ties: lower index first) in index
-//     order; one block radix-selects the global top-k among those candidates;
+//   * top-k: logits become order-preserving 32-bit keys (non-finite -> -inf),
+//     packed with their index into 64-bit items that order as the sampler
+//     does (key descending, then index ascending); for k <= kSampleMaxK every
+//     wave of a wide launch lists its best 8 items, one block takes the items
+//     at or above the k-th best wave maximum and ranks them (k_topk_select);
+//     for larger k one block radix-selects over the whole vocabulary;
 //   * the k items are sorted (value descending, index ascending), p_i =
 //     exp((v_i - v_0) / T), the nucleus keeps items while the mass before them
 //     is <= top_p, and r = u * (kept mass) picks the first item whose running
@@ -38,8 +40,8 @@ constexpr int kThreads = 256;
 // -inf (decoder.rs:951-997); greedy keeps +inf (the reference's argmax compares
 // raw values) and never picks a NaN past index 0.
 __device__ __forceinline__ uint32_t fkey(float f, bool greedy) {
-    if (greedy ? isnan(f) : !isfinite(f)) f = -INFINITY;
-    const uint32_t b = __float_as_uint(f);
+    const bool drop = greedy ? isnan(f) : !isfinite(f);
+    const uint32_t b = drop ? 0xFF800000u : __float_as_uint(f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
@@ -47,23 +49,27 @@ __device__ __forceinline__ float kval(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// Exclusive prefix sum of a 0/1 flag over the block (256 threads, 4 waves),
-// in thread order; *total gets the block's count.  Uses s[0..4].
-__device__ __forceinline__ int block_excl(int flag, int *s, int *total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const unsigned long long m = __ballot(flag);
-    const int below = __popcll(m & ((1ull << lane) - 1ull));
-    if (lane == 0) s[w] = __popcll(m);
-    __syncthreads();
-    int base = 0, tot = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        base += i < w ? s[i] : 0;
-        tot += s[i];
-    }
-    __syncthreads();
-    *total = tot;
-    return base + below;
+// The key the sampler ranks logit v at index id by.  Greedy scans from
+// logits[0] with strict > (decoder.rs:914-925): a NaN there is never
+// replaced, so it takes the largest key.
+__device__ __forceinline__ uint32_t sample_key(float v, int id, bool greedy) {
+    return (greedy && id == 0 && isnan(v)) ? 0xFFFFFFFFu : fkey(v, greedy);
+}
+
+// An item: key in the high word, the complement of the index in the low word,
+// so that larger items come first in the sampler's order.  0 is no item.
+__device__ __forceinline__ uint64_t pack_item(uint32_t key, int id) {
+    return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)id);
+}
+__device__ __forceinline__ uint32_t item_key(uint64_t it) { return (uint32_t)(it >> 32); }
+__device__ __forceinline__ int item_index(uint64_t it) {
+    return (int)(0xFFFFFFFFu - (uint32_t)it);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const int lo = __shfl_xor((int)(uint32_t)v, m);
+    const int hi = __shfl_xor((int)(uint32_t)(v >> 32), m);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
 // The k-th largest (k >= 1, k <= n) of n keys, key_at(i) for i < n, over an
@@ -114,31 +120,6 @@ __device__ uint32_t kth_largest(KeyAt key_at, int n, int k, float *red, int *nee
     return prefix;
 }
 
-// Writes, in index order, the keys > kth and the first `need` keys == kth
-// (lowest positions) of keys[0..n) to ok/oi; returns the count (= k).
-__device__ int gather_top(const uint32_t *keys, const int *idx, int n, uint32_t kth, int need,
-                          uint32_t *ok, int *oi, int *s) {
-    // (k <= kSampleMaxK items are taken; the bound below only guards ok / oi)
-    int taken = 0, eq_seen = 0;
-    for (int base = 0; base < n; base += kThreads) {
-        const int i = base + threadIdx.x;
-        const uint32_t key = i < n ? keys[i] : 0u;
-        const int eq = (i < n && key == kth) ? 1 : 0;
-        int eq_tot;
-        const int eq_rank = eq_seen + block_excl(eq, s, &eq_tot);
-        const int take = (i < n && (key > kth || (eq && eq_rank < need))) ? 1 : 0;
-        int take_tot;
-        const int pos = taken + block_excl(take, s, &take_tot);
-        if (take && pos < kSampleMaxK) {
-            ok[pos] = key;
-            oi[pos] = idx ? idx[i] : i;
-        }
-        taken += take_tot;
-        eq_seen += eq_tot;
-    }
-    return min(taken, kSampleMaxK);
-}
-
 __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
@@ -146,186 +127,42 @@ __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
 }
 
 // Penalty over the distinct tokens of `recent` (n of them, tokens outside the
-// vocabulary skipped), in place.  One block; the vocabulary bitmap lives in LDS.
+// vocabulary skipped), in place.  With `win`, the step's input token is first
+// pushed onto the recent-token window (the last kSampleWindow tokens,
+// decoder.rs:859-876) and the penalty covers the window.  One block; a
+// vocabulary bitmap in LDS (only the words the tokens touch are cleared) makes
+// "distinct" one atomicOr per token.
 __global__ __launch_bounds__(kThreads) void k_penalty(float *__restrict__ logits, int V,
-                                                      const int64_t *__restrict__ recent, int n,
-                                                      const int *__restrict__ n_dev,
+                                                      const int64_t *recent, int n,
+                                                      SampleWindow *__restrict__ win,
+                                                      const DecState *__restrict__ dstate,
                                                       const SampleParams *__restrict__ prm) {
     extern __shared__ uint32_t bits[];
+    __shared__ int64_t wtok[kSampleWindow];
+    const int tid = threadIdx.x;
+    if (win) {
+        const int c = win->n, drop = c == kSampleWindow ? 1 : 0, nn = c - drop + 1;
+        if (tid < nn) wtok[tid] = tid < c - drop ? win->tok[tid + drop] : (int64_t)dstate->token;
+        __syncthreads();   // every old entry is read before any is replaced
+        if (tid < nn) win->tok[tid] = wtok[tid];
+        if (tid == 0) win->n = nn;
+        recent = wtok;
+        n = nn;
+    }
     const float pen = prm->penalty;
-    if (n_dev) n = *n_dev;
     if (!(pen > 1.0f) || n <= 0) return;
-    const int words = (V + 31) / 32;
-    for (int i = threadIdx.x; i < words; i += kThreads) bits[i] = 0u;
+    for (int i = tid; i < n; i += kThreads) {
+        const int64_t t = recent[i];
+        if (t >= 0 && t < V) bits[t >> 5] = 0u;
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kThreads) {
+    for (int i = tid; i < n; i += kThreads) {
         const int64_t t = recent[i];
         if (t < 0 || t >= V) continue;
         const uint32_t bit = 1u << (t & 31);
         if ((atomicOr(&bits[t >> 5], bit) & bit) == 0u) {
             const float l = logits[t];
             logits[t] = l > 0.f ? l / pen : l * pen;
-        }
-    }
-}
-
-// Per-block top-k of a 2048-element slice: cand_key/idx [NB][kmax], cnt [NB].
-__global__ __launch_bounds__(kThreads) void k_topk_slice(const float *__restrict__ logits, int V,
-                                                         const SampleParams *__restrict__ prm,
-                                                         uint32_t *__restrict__ cand_key,
-                                                         int *__restrict__ cand_idx,
-                                                         int *__restrict__ cnt) {
-    __shared__ uint32_t keys[kSampleSlice];
-    __shared__ uint32_t okey[kSampleMaxK];
-    __shared__ int oidx[kSampleMaxK];
-    __shared__ float red[kThreads / 4];
-    __shared__ int sh[8];
-    const int k = prm->k;
-    if (k > kSampleMaxK) return;   // the large-k path samples
-    const bool greedy = prm->greedy != 0;
-    const int b = blockIdx.x, base = b * kSampleSlice;
-    const int n = min(kSampleSlice, V - base);
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-        const float v = logits[base + i];
-        // greedy scans from logits[0] with strict > (decoder.rs:914-925): a NaN
-        // there is never replaced, so it takes the largest key
-        keys[i] = (greedy && base + i == 0 && isnan(v)) ? 0xFFFFFFFFu : fkey(v, greedy);
-    }
-    __syncthreads();
-    const int kk = min(k, n);
-    int need;
-    const uint32_t kth =
-        kth_largest<kThreads>([&](int i) { return keys[i]; }, n, kk, red, &need);
-    const int m = gather_top(keys, nullptr, n, kth, need, okey, oidx, sh + 4);
-    __syncthreads();
-    for (int i = threadIdx.x; i < m; i += kThreads) {
-        cand_key[(size_t)b * kSampleMaxK + i] = okey[i];
-        cand_idx[(size_t)b * kSampleMaxK + i] = base + oidx[i];
-    }
-    if (threadIdx.x == 0) cnt[b] = m;
-}
-
-// Global top-k from the slices' candidates, the draw, and the result.
-__global__ __launch_bounds__(kThreads) void k_topk_draw(const uint32_t *__restrict__ cand_key,
-                                                        const int *__restrict__ cand_idx,
-                                                        const int *__restrict__ cnt, int nb,
-                                                        SampleParams *__restrict__ prm,
-                                                        SampleOut *__restrict__ out,
-                                                        DecState *__restrict__ st,
-                                                        int *__restrict__ history, int hist_cap) {
-    __shared__ uint32_t keys[kSampleCand];
-    __shared__ int idx[kSampleCand];
-    __shared__ uint32_t tk[kSampleMaxK];
-    __shared__ int ti[kSampleMaxK];
-    __shared__ float p[kSampleMaxK];
-    __shared__ float red[kThreads / 4];
-    __shared__ int sh[8];
-    __shared__ int off[kSampleMaxBlocks + 1];
-    const int k = prm->k;
-    if (k > kSampleMaxK) return;   // the large-k path samples
-    // slice offsets: an exclusive scan of the counts by wave 0 (nb <= 128)
-    if (threadIdx.x < 64) {
-        const int l = threadIdx.x;
-        const int c0 = 2 * l < nb ? cnt[2 * l] : 0, c1 = 2 * l + 1 < nb ? cnt[2 * l + 1] : 0;
-        int incl = c0 + c1;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o);
-            if (l >= o) incl += t;
-        }
-        const int ex = incl - c0 - c1;
-        if (2 * l < nb) off[2 * l] = ex;
-        if (2 * l + 1 < nb) off[2 * l + 1] = ex + c0;
-        if (l == 63) off[nb] = incl;
-    }
-    __syncthreads();
-    const int n = off[nb];
-    for (int e = threadIdx.x; e < nb * kSampleMaxK; e += kThreads) {
-        const int b = e / kSampleMaxK, i = e - b * kSampleMaxK;
-        if (i < cnt[b]) {
-            keys[off[b] + i] = cand_key[e];
-            idx[off[b] + i] = cand_idx[e];
-        }
-    }
-    __syncthreads();
-    const int kk = min(k, n);
-    int need;
-    const uint32_t kth =
-        kth_largest<kThreads>([&](int i) { return keys[i]; }, n, kk, red, &need);
-    const int m = gather_top(keys, idx, n, kth, need, tk, ti, sh + 4);
-    // bitonic sort of the m (<= 128) items: key descending, index ascending
-    for (int i = m + threadIdx.x; i < kSampleMaxK; i += kThreads) {
-        tk[i] = 0u;
-        ti[i] = 0x7FFFFFFF;
-    }
-    __syncthreads();
-    for (int size = 2; size <= kSampleMaxK; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const int i = threadIdx.x;
-            if (i < kSampleMaxK) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const uint32_t a = tk[i], c = tk[j];
-                    const int ia = ti[i], ic = ti[j];
-                    const bool a_first = a > c || (a == c && ia < ic);
-                    if (a_first != desc) {
-                        tk[i] = c; tk[j] = a;
-                        ti[i] = ic; ti[j] = ia;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    if (threadIdx.x == 0) {
-        int tok = ti[0];
-        const float T = prm->temperature;
-        float u = -1.f;
-        if (!prm->greedy && m > 1) {
-            const float vmax = kval(tk[0]), inv_t = 1.0f / T;
-            float pre = 0.f;
-            for (int i = 0; i < m; ++i) {
-                p[i] = expf((kval(tk[i]) - vmax) * inv_t);
-                pre += p[i];
-            }
-            int kept = m;
-            const float tp = prm->top_p;
-            if (tp > 0.f && tp < 1.f && pre > 0.f) {
-                const float inv = 1.0f / pre;
-                float cum = 0.f;
-                for (int i = 0; i < m; ++i) {
-                    if (cum > tp) {
-                        kept = i;
-                        break;
-                    }
-                    cum += p[i] * inv;
-                }
-            }
-            float ks = 0.f;
-            for (int i = 0; i < kept; ++i) ks += p[i];
-            const uint64_t z = splitmix(prm->seed + (prm->counter + 1ull) * 0x9E3779B97F4A7C15ull);
-            u = (float)(z >> 40) * 5.9604644775390625e-8f;   // [0, 1), 24 bits
-            prm->counter += 1ull;
-            const float r = u * ks;
-            float acc = 0.f;
-            for (int i = 0; i < kept; ++i) {
-                acc += p[i];
-                if (acc >= r) {
-                    tok = ti[i];
-                    break;
-                }
-            }
-        }
-        out->u = u;
-        out->token = tok;
-        out->kept = m;
-        if (st) {   // the decoder's next step, as the greedy argmax tail does
-            const int step = st->step;
-            if (history && step < hist_cap) history[step] = tok;
-            st->argmax = tok;
-            st->token = tok;
-            st->pos = st->pos + 1;
-            st->step = step + 1;
         }
     }
 }
@@ -361,6 +198,34 @@ __device__ T block_scan_excl(T v, T *s, T *total) {
     *total = s[NW];
     __syncthreads();
     return ex;
+}
+
+// The top items of n keys given the k-th largest key kth and how many keys
+// equal to it belong (need): emit(w, key, i) for the keys above kth and the
+// first `need` equal to it, w = 0, 1, ... in index order (each thread takes a
+// contiguous range of the indices).  Returns the count.  sn: NT / 64 + 1 ints.
+template <int NT, class KeyAt, class Emit>
+__device__ int gather_top(KeyAt key_at, int n, uint32_t kth, int need, int *sn, Emit emit) {
+    const int per = (n + NT - 1) / NT, lo = min(n, (int)threadIdx.x * per), hi = min(n, lo + per);
+    int ng = 0, ne = 0;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t key = key_at(i);
+        ng += key > kth;
+        ne += key == kth;
+    }
+    int tot;
+    const int eq_base = block_scan_excl<NT, int>(ne, sn, &tot);
+    const int eq_take = max(0, min(ne, need - eq_base));
+    const int base = block_scan_excl<NT, int>(ng + eq_take, sn, &tot);
+    int w = base, eq_seen = 0;
+    for (int i = lo; i < hi; ++i) {
+        const uint32_t key = key_at(i);
+        const bool eq = key == kth;
+        if (key > kth || (eq && eq_seen < eq_take)) emit(w++, key, i);
+        eq_seen += eq;
+    }
+    __syncthreads();
+    return tot;
 }
 
 // The first item, in sorted order (key descending, then index ascending), at
@@ -487,31 +352,11 @@ __global__ __launch_bounds__(kLargeThreads) void k_topk_large(
     int need;
     const uint32_t kth = kth_largest<NT>([&](int i) { return fkey(logits[i], false); }, V, kk,
                                          red, &need);
-    // the k items in index order: each thread a contiguous range of the vocabulary
-    const int per = (V + NT - 1) / NT, lo = threadIdx.x * per, hi = min(V, lo + per);
-    int ng = 0, ne = 0;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t key = fkey(logits[i], false);
-        ng += key > kth;
-        ne += key == kth;
-    }
-    int tot;
-    const int eq_base = block_scan_excl<NT, int>(ne, sn, &tot);
-    const int eq_take = max(0, min(ne, need - eq_base));
-    const int base = block_scan_excl<NT, int>(ng + eq_take, sn, &tot);
-    int w = base, eq_seen = 0;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t key = fkey(logits[i], false);
-        const bool eq = key == kth;
-        if (key > kth || (eq && eq_seen < eq_take)) {
-            ikey[w] = key;
-            iidx[w] = i;
-            ++w;
-        }
-        eq_seen += eq;
-    }
-    __syncthreads();
-    const int n = tot;   // == kk
+    const int n = gather_top<NT>([&](int i) { return fkey(logits[i], false); }, V, kth, need, sn,
+                                 [&](int w, uint32_t key, int i) {
+                                     ikey[w] = key;
+                                     iidx[w] = i;
+                                 });   // == kk
     // the top item: the largest key, lowest index among equals (items in index order)
     if (threadIdx.x == 0) smax[0] = 0u;
     __syncthreads();
@@ -565,17 +410,431 @@ __global__ __launch_bounds__(kLargeThreads) void k_topk_large(
     }
 }
 
-// Pushes the step's input token onto the recent-token window (the last
-// kSampleWindow tokens, decoder.rs:859-876) before its penalty is applied.
-__global__ void k_window_push(const DecState *__restrict__ st, SampleWindow *__restrict__ w) {
-    if (threadIdx.x != 0) return;
-    int n = w->n;
-    if (n == kSampleWindow) {
-        for (int i = 1; i < kSampleWindow; ++i) w->tok[i - 1] = w->tok[i];
-        n -= 1;
+// ---- top_k <= kSampleMaxK: wave lists, a threshold, ranks ----
+//
+// k_topk_lists (nb blocks of 4 waves, E = list_per_lane(V) ids per lane):
+// the vocabulary is cut into runs of kRun ids; block b takes runs b, b + nb,
+// b + 2 nb, ..., and in each run wave w takes the ids = w (mod 4), so a
+// wave's 64 E ids are spread over the vocabulary and neighbouring ids (which
+// related tokens often are) fall to different waves.  Each wave writes its
+// best q = min(k, kListQ) items, best first (0 past its count), and its count.
+//
+// k_topk_select (one block): the pool is the best j = ceil(k / W) listed
+// items of each of the W waves; T = the k-th best of the pool (every item
+// when the pool holds fewer than k).  At least k items are >= T, so the top k
+// all are.  The candidates are the listed items >= T; a candidate's rank
+// among them is its place in the sorted order.  A wave whose q-th item ranks
+// before the (m-1)-th candidate may hold more of the top m than it listed; if
+// one does, its ids are read again and those of its items at or above the
+// m-th candidate that it did not list join.  The candidates' top m is then the
+// global top m: a top item x missing from the lists sits below its wave's q
+// listed items, all of which lie above x, so above the m-th best item, so
+// above the m-th candidate, and the rescan takes x.  Past kCandCap
+// candidates, an exact radix select over the vocabulary takes over.
+constexpr int kRun = 16;
+constexpr int kListQ = 8;
+constexpr int kCandCap = 2048;
+constexpr int kPoolCap = 512;
+constexpr int kSelThreads = 1024;
+constexpr int kMaxFlagged = kSampleMaxK / kListQ;
+static_assert(kSampleLists * kListQ * 8 <= kSampleCand * 4, "wave lists fit the key scratch");
+
+// ids per lane of the list kernel: 16 past 65536 logits (at most 256 waves
+// for the select block to rank), else 8 (at most 128 waves)
+inline int list_per_lane(int V) { return V > 65536 ? 16 : 8; }
+inline int list_blocks(int V) {
+    const int per_block = 256 * list_per_lane(V);
+    return (V + per_block - 1) / per_block;
+}
+
+// The id that item i of lane l in wave w of block b (of nb) stands for; ids
+// >= V are no item.
+__device__ __forceinline__ int list_id(int b, int nb, int w, int l, int i) {
+    return kRun * (b + nb * ((l >> 2) + 16 * i)) + 4 * (l & 3) + w;
+}
+
+__device__ __forceinline__ void cas_desc(uint64_t &a, uint64_t &b) {
+    const uint64_t x = a, y = b;
+    const bool s = x < y;
+    a = s ? y : x;
+    b = s ? x : y;
+}
+
+// Batcher's odd-even merge network over 8 items, best first.
+__device__ __forceinline__ void sort8_desc(uint64_t (&v)[8]) {
+    cas_desc(v[0], v[1]); cas_desc(v[2], v[3]); cas_desc(v[4], v[5]); cas_desc(v[6], v[7]);
+    cas_desc(v[0], v[2]); cas_desc(v[1], v[3]); cas_desc(v[4], v[6]); cas_desc(v[5], v[7]);
+    cas_desc(v[1], v[2]); cas_desc(v[5], v[6]);
+    cas_desc(v[0], v[4]); cas_desc(v[1], v[5]); cas_desc(v[2], v[6]); cas_desc(v[3], v[7]);
+    cas_desc(v[2], v[4]); cas_desc(v[3], v[5]);
+    cas_desc(v[1], v[2]); cas_desc(v[3], v[4]); cas_desc(v[5], v[6]);
+}
+
+// v = the best 8 of a and b (each sorted best first), sorted best first: the
+// pairwise maxima of a and reversed b form a bitonic sequence, which three
+// half-cleaner stages sort.
+__device__ __forceinline__ void merge8_desc(const uint64_t (&a)[8], const uint64_t (&b)[8],
+                                            uint64_t (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = a[i] > b[7 - i] ? a[i] : b[7 - i];
+    cas_desc(v[0], v[4]); cas_desc(v[1], v[5]); cas_desc(v[2], v[6]); cas_desc(v[3], v[7]);
+    cas_desc(v[0], v[2]); cas_desc(v[1], v[3]); cas_desc(v[4], v[6]); cas_desc(v[5], v[7]);
+    cas_desc(v[0], v[1]); cas_desc(v[2], v[3]); cas_desc(v[4], v[5]); cas_desc(v[6], v[7]);
+}
+
+// x from another lane of the same row or the row before, by a DPP move
+// (lanes outside row_mask keep old).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// The wave's maximum, uniform: quad swaps and row mirrors leave every lane
+// with its 16-lane row's maximum, row broadcasts carry rows 0-2 into row 3,
+// and lane 63 is read.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, dpp_u32<0xB1, 0xF>(x, x));    // quad_perm [1,0,3,2]
+    x = max(x, dpp_u32<0x4E, 0xF>(x, x));    // quad_perm [2,3,0,1]
+    x = max(x, dpp_u32<0x141, 0xF>(x, x));   // row_half_mirror
+    x = max(x, dpp_u32<0x140, 0xF>(x, x));   // row_mirror
+    x = max(x, dpp_u32<0x142, 0xA>(x, x));   // row_bcast:15 into rows 1 and 3
+    x = max(x, dpp_u32<0x143, 0xC>(x, x));   // row_bcast:31 into rows 2 and 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// The wave's best item among the lanes' x (0: none), uniform: the best key,
+// then, only when several lanes hold it, the best index among them.
+__device__ __forceinline__ uint64_t wave_best(uint64_t x) {
+    const uint32_t hk = (uint32_t)(x >> 32), mk = wave_max_u32(hk);
+    const unsigned long long at = __ballot(hk == mk && x != 0ull);
+    if (__popcll(at) == 1) {
+        const int src = __ffsll((long long)at) - 1;
+        return ((uint64_t)mk << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, src);
     }
-    w->tok[n] = st->token;
-    w->n = n + 1;
+    const uint32_t ml = wave_max_u32(hk == mk ? (uint32_t)x : 0u);
+    return ((uint64_t)mk << 32) | ml;
+}
+
+template <int E>
+__global__ __launch_bounds__(kThreads) void k_topk_lists(const float *__restrict__ logits, int V,
+                                                         const SampleParams *__restrict__ prm,
+                                                         uint64_t *__restrict__ lists,
+                                                         int *__restrict__ wcnt) {
+    static_assert(E == 8 || E == 16, "8 or 16 ids per lane");
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nb = gridDim.x;
+    float x[E];
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {   // every load issued at once (ids past V read logits[V-1])
+        const int id = list_id(blockIdx.x, nb, w, l, i);
+        x[i] = logits[min(id, V - 1)];
+        n += __popcll(__ballot(id < V));
+    }
+    // (the k test comes last, so that the loads above need not wait for it)
+    const int k = prm->k;
+    const bool greedy = prm->greedy != 0;
+    const int q = min(k, kListQ);
+    auto item = [&](int i) {
+        const int id = list_id(blockIdx.x, nb, w, l, i);
+        const uint64_t it = pack_item(sample_key(x[i], id, greedy), id);
+        return id < V ? it : 0ull;
+    };
+    uint64_t v[kListQ];
+    if constexpr (E == 8) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = item(i);
+        sort8_desc(v);
+    } else {
+        uint64_t a[8], b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            a[i] = item(i);
+            b[i] = item(8 + i);
+        }
+        sort8_desc(a);
+        sort8_desc(b);
+        merge8_desc(a, b, v);
+    }
+    // q rounds: the wave's best head leaves its lane (items are distinct)
+    uint64_t mine = 0ull;
+    for (int t = 0; t < q; ++t) {
+        const uint64_t best = wave_best(v[0]);
+        if (l == t) mine = best;
+        if (best != 0ull && v[0] == best) {
+#pragma unroll
+            for (int i = 0; i + 1 < kListQ; ++i) v[i] = v[i + 1];
+            v[kListQ - 1] = 0ull;
+        }
+    }
+    if (k > kSampleMaxK) return;   // the large-k path samples
+    const int gw = blockIdx.x * 4 + w;
+    if (l < kListQ) lists[(size_t)gw * kListQ + l] = mine;
+    if (l == 0) wcnt[gw] = n;
+}
+
+// Appends `it` (and tag) where keep holds to buf / tags (positions from
+// *count; past cap only counted).  Called by every active lane of a wave.
+__device__ __forceinline__ void wave_append(bool keep, uint64_t it, int tag, uint64_t *buf,
+                                            int *tags, int cap, int *count) {
+    const unsigned long long b = __ballot(keep);
+    if (b == 0ull) return;
+    const int lane = threadIdx.x & 63, leader = __ffsll((long long)b) - 1;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(count, __popcll(b));
+    base = __shfl(base, leader);
+    if (keep) {
+        const int pos = base + __popcll(b & ((1ull << lane) - 1ull));
+        if (pos < cap) {
+            buf[pos] = it;
+            if (tags) tags[pos] = tag;
+        }
+    }
+}
+
+// rank[c] += how many of a[0..n) are greater than a[c] (rank zero on entry):
+// a holds distinct nonzero items and zeros up to the next multiple of 8
+// (16-byte aligned).  Each wave takes 64 items against a share of a (waves
+// left over split a between them and add their counts); ends with a barrier.
+template <int NT>
+__device__ void rank_items(const uint64_t *a, int n, int *rank) {
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int groups = (n + 63) / 64, parts = groups >= NW ? 1 : NW / groups;
+    const int n8 = (n + 7) & ~7, chunk = ((n8 + parts - 1) / parts + 7) & ~7;
+    for (int u = wave; u < groups * parts; u += NW) {
+        const int g = u / parts, pt = u - g * parts, c = g * 64 + lane;
+        const uint64_t me = c < n ? a[c] : ~0ull;
+        const int j1 = min(n8, (pt + 1) * chunk);
+        int r = 0;
+        for (int j = pt * chunk; j < j1; j += 8) {
+            const ulonglong2 x0 = *reinterpret_cast<const ulonglong2 *>(a + j);
+            const ulonglong2 x1 = *reinterpret_cast<const ulonglong2 *>(a + j + 2);
+            const ulonglong2 x2 = *reinterpret_cast<const ulonglong2 *>(a + j + 4);
+            const ulonglong2 x3 = *reinterpret_cast<const ulonglong2 *>(a + j + 6);
+            r += (x0.x > me) + (x0.y > me) + (x1.x > me) + (x1.y > me) + (x2.x > me) +
+                 (x2.y > me) + (x3.x > me) + (x3.y > me);
+        }
+        if (c < n && r) atomicAdd(&rank[c], r);
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kSelThreads) void k_topk_select(
+    const float *__restrict__ logits, int V, int nb, const uint64_t *__restrict__ lists,
+    const int *__restrict__ wcnt, SampleParams *__restrict__ prm, SampleOut *__restrict__ out,
+    DecState *__restrict__ st, int *__restrict__ history, int hist_cap) {
+    constexpr int NT = kSelThreads, NW = NT / 64;
+    constexpr int kPer = kSampleLists * kListQ / NT;   // list slots per thread
+    __shared__ __align__(16) uint64_t cand[kCandCap];
+    __shared__ int ctag[kCandCap];
+    __shared__ int crank[kCandCap];
+    __shared__ __align__(16) uint64_t pool[kPoolCap];
+    __shared__ uint64_t top[kSampleMaxK];
+    __shared__ __align__(16) float p[kSampleMaxK];
+    __shared__ __align__(16) float cp[kSampleMaxK];
+    __shared__ __align__(16) float cb[kSampleMaxK];
+    __shared__ int prank[kPoolCap];
+    __shared__ float red[NT / 4];
+    __shared__ int sn[NW + 1];
+    __shared__ int flagged[kMaxFlagged];
+    __shared__ uint64_t s_t;
+    __shared__ int n_cand, n_pool, n_flag, s_lim;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int W = 4 * nb, slots = W * kListQ;
+    uint64_t li[kPer];
+    int lc[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int e = tid + r * NT;
+        li[r] = e < slots ? lists[e] : 0ull;
+        lc[r] = e < slots ? wcnt[e / kListQ] : 0;
+    }
+    const int k = prm->k;
+    if (k > kSampleMaxK) return;   // the large-k path samples
+    const bool greedy = prm->greedy != 0;
+    const int E = V > 65536 ? 16 : 8;
+    const int q = min(k, kListQ), m = min(k, V), jp = min(q, (k + W - 1) / W);
+    if (tid == 0) {
+        n_cand = 0;
+        n_pool = 0;
+        n_flag = 0;
+        s_t = 1ull;   // every item
+    }
+    for (int i = tid; i < kCandCap; i += NT) crank[i] = 0;
+    for (int i = tid; i < kPoolCap; i += NT) prank[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int e = tid + r * NT;
+        wave_append(li[r] != 0ull && (e & (kListQ - 1)) < jp, li[r], 0, pool, nullptr, kPoolCap,
+                    &n_pool);
+    }
+    __syncthreads();
+    const int np = n_pool;
+    if (np >= k) {   // T = the k-th best of the pool
+        if (tid < 8) pool[np + tid] = 0ull;   // np + 8 <= kPoolCap: np < W + k
+        __syncthreads();
+        rank_items<NT>(pool, np, prank);
+        for (int c = tid; c < np; c += NT)
+            if (prank[c] == k - 1) s_t = pool[c];
+        __syncthreads();
+    }
+    const uint64_t T = s_t;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int e = tid + r * NT, slot = e & (kListQ - 1);
+        const int tag = (slot == q - 1 && lc[r] > q) ? e / kListQ : -1;
+        wave_append(li[r] >= T && slot < q, li[r], tag, cand, ctag, kCandCap, &n_cand);
+    }
+    __syncthreads();
+    int nc = n_cand;
+    // ranks -> top[0..m); a short wave's q-th item ranked before m - 1 flags it
+    auto order = [&](bool flags) {
+        if (tid < 8) cand[nc + tid] = 0ull;   // nc + 8 <= kCandCap: see callers
+        if (!flags)
+            for (int c = tid; c < nc; c += NT) crank[c] = 0;
+        __syncthreads();
+        rank_items<NT>(cand, nc, crank);
+        for (int c = tid; c < nc; c += NT) {
+            const int r = crank[c];
+            if (r < m) top[r] = cand[c];
+            if (flags && ctag[c] >= 0 && r < m - 1) {
+                const int f = atomicAdd(&n_flag, 1);
+                if (f < kMaxFlagged) flagged[f] = ctag[c];
+            }
+        }
+        __syncthreads();
+    };
+    bool exact = nc > kCandCap - 8;
+    if (!exact) {
+        order(true);
+        const int nf = n_flag;
+        if (nf > kMaxFlagged) {
+            exact = true;
+        } else if (nf > 0) {
+            const uint64_t thr = nc >= m ? top[m - 1] : 1ull;
+            for (int f = wave; f < nf; f += NW) {
+                const int L = flagged[f], b = L >> 2, w = L & 3;
+                const uint64_t last = lists[(size_t)L * kListQ + q - 1];
+                for (int i = 0; i < E; ++i) {
+                    const int id = list_id(b, nb, w, lane, i);
+                    const uint64_t it =
+                        id < V ? pack_item(sample_key(logits[id], id, greedy), id) : 0ull;
+                    wave_append(it < last && it >= thr, it, -1, cand, ctag, kCandCap, &n_cand);
+                }
+            }
+            __syncthreads();
+            nc = n_cand;
+            exact = nc > kCandCap - 8;
+            if (!exact) order(false);
+        }
+    }
+    if (exact) {   // the m best over the whole vocabulary, then their order
+        int need;
+        const uint32_t kth = kth_largest<NT>(
+            [&](int i) { return sample_key(logits[i], i, greedy); }, V, m, red, &need);
+        nc = gather_top<NT>([&](int i) { return sample_key(logits[i], i, greedy); }, V, kth, need,
+                            sn, [&](int w, uint32_t key, int i) { cand[w] = pack_item(key, i); });
+        order(false);
+    }
+    // the draw over top[0..m), in order; sums run in sequence, as the
+    // reference's loops do, and the nucleus step is not contracted
+    const bool draw = !greedy && m > 1;
+    if (draw) {
+        const float vmax = kval(item_key(top[0])), inv_t = 1.0f / prm->temperature;
+        for (int i = tid; i < kSampleMaxK; i += NT)
+            p[i] = i < m ? expf((kval(item_key(top[i])) - vmax) * inv_t) : 0.f;
+        __syncthreads();
+        if (tid == 0) {   // running masses in chunks of 16, the next chunk's loads in flight
+            const float4 *p4 = reinterpret_cast<const float4 *>(p);
+            float4 *cp4 = reinterpret_cast<float4 *>(cp);
+            float4 *cb4 = reinterpret_cast<float4 *>(cb);
+            float4 a[4], nx[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] = p4[t];
+            float pre = 0.f;
+            for (int c = 0; c < m; c += 16) {   // cp[i]: the mass through item i
+#pragma unroll
+                for (int t = 0; t < 4; ++t) nx[t] = p4[min((c >> 2) + 4 + t, kSampleMaxK / 4 - 1)];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float4 o;
+                    pre += a[t].x; o.x = pre;
+                    pre += a[t].y; o.y = pre;
+                    pre += a[t].z; o.z = pre;
+                    pre += a[t].w; o.w = pre;
+                    cp4[(c >> 2) + t] = o;
+                    a[t] = nx[t];
+                }
+            }
+            int lim = m;   // cb[i] (the normalised mass before item i) is written for i < lim
+            const float tp = prm->top_p;
+            if (tp > 0.f && tp < 1.f && pre > 0.f) {
+                const float inv = 1.0f / pre;
+                float cum = 0.f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[t] = p4[t];
+                for (int c = 0; c < m; c += 16) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) nx[t] = p4[min((c >> 2) + 4 + t, kSampleMaxK / 4 - 1)];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        float4 o;
+                        o.x = cum; cum = __fadd_rn(cum, __fmul_rn(a[t].x, inv));
+                        o.y = cum; cum = __fadd_rn(cum, __fmul_rn(a[t].y, inv));
+                        o.z = cum; cum = __fadd_rn(cum, __fmul_rn(a[t].z, inv));
+                        o.w = cum; cum = __fadd_rn(cum, __fmul_rn(a[t].w, inv));
+                        cb4[(c >> 2) + t] = o;
+                        a[t] = nx[t];
+                    }
+                    if (cum > tp) {   // the cut lies at or before item c + 16
+                        lim = min(m, c + 16);
+                        break;
+                    }
+                }
+            } else {
+                lim = 0;   // no cut
+            }
+            s_lim = lim;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tok = item_index(top[0]);
+        float u = -1.f;
+        if (draw) {
+            // kept: the first item whose normalised mass before it exceeds top_p
+            const int lim = s_lim;
+            const float tp = prm->top_p;
+            const unsigned long long c0 = __ballot(lane < lim && cb[lane] > tp);
+            const unsigned long long c1 = __ballot(lane + 64 < lim && cb[lane + 64] > tp);
+            const int kept = c0 ? __ffsll((long long)c0) - 1
+                             : c1 ? 64 + __ffsll((long long)c1) - 1
+                                  : (lim > 0 && lim < m ? lim : m);
+            const uint64_t z = splitmix(prm->seed + (prm->counter + 1ull) * 0x9E3779B97F4A7C15ull);
+            u = (float)(z >> 40) * 5.9604644775390625e-8f;   // [0, 1), 24 bits
+            const float r = u * cp[kept - 1];   // u times the mass of the kept items
+            // the first kept item whose running mass reaches r
+            const unsigned long long b0 = __ballot(lane < kept && cp[lane] >= r);
+            const unsigned long long b1 = __ballot(lane + 64 < kept && cp[lane + 64] >= r);
+            const int d = b0 ? __ffsll((long long)b0) - 1 : b1 ? 64 + __ffsll((long long)b1) - 1 : 0;
+            tok = item_index(top[d]);
+        }
+        if (lane == 0) {
+            if (draw) prm->counter += 1ull;
+            out->u = u;
+            out->token = tok;
+            out->kept = m;
+            if (st) {   // the decoder's next step, as the greedy argmax tail does
+                const int step = st->step;
+                if (history && step < hist_cap) history[step] = tok;
+                st->argmax = tok;
+                st->token = tok;
+                st->pos = st->pos + 1;
+                st->step = step + 1;
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -600,15 +859,9 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
     const size_t lds = (size_t)((V + 31) / 32) * 4;
     TB_REQUIRE(lds <= 64 * 1024, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: repetition penalty bitmap exceeds LDS");
-    if (win) {
-        hipLaunchKernelGGL(k_window_push, dim3(1), dim3(64), 0, st, dstate, win);
-        TB_LAUNCHED();
-        hipLaunchKernelGGL(k_penalty, dim3(1), dim3(kThreads), lds, st, logits, V, win->tok, 0,
-                           &win->n, prm);
-        TB_LAUNCHED();
-    } else if (recent && n_recent > 0) {
-        hipLaunchKernelGGL(k_penalty, dim3(1), dim3(kThreads), lds, st, logits, V, recent,
-                           n_recent, (const int *)nullptr, prm);
+    if (win || (recent && n_recent > 0)) {
+        hipLaunchKernelGGL(k_penalty, dim3(1), dim3(kThreads), lds, st, logits, V,
+                           win ? nullptr : recent, win ? 0 : n_recent, win, dstate, prm);
         TB_LAUNCHED();
     }
     if (large) {
@@ -617,11 +870,17 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
         TB_LAUNCHED();
         return TB_OK;
     }
-    hipLaunchKernelGGL(k_topk_slice, dim3(nb), dim3(kThreads), 0, st, logits, V, prm, ws.key,
-                       ws.idx, ws.cnt);
+    uint64_t *lists = reinterpret_cast<uint64_t *>(ws.key);
+    const int nbl = list_blocks(V);
+    if (list_per_lane(V) == 16)
+        hipLaunchKernelGGL(k_topk_lists<16>, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm,
+                           lists, ws.cnt);
+    else
+        hipLaunchKernelGGL(k_topk_lists<8>, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm,
+                           lists, ws.cnt);
     TB_LAUNCHED();
-    hipLaunchKernelGGL(k_topk_draw, dim3(1), dim3(kThreads), 0, st, ws.key, ws.idx, ws.cnt, nb,
-                       prm, out, dstate, history, hist_cap);
+    hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kSelThreads), 0, st, logits, V, nbl, lists,
+                       ws.cnt, prm, out, dstate, history, hist_cap);
     TB_LAUNCHED();
     return TB_OK;
 }

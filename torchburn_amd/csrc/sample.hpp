@@ -12,6 +12,7 @@ constexpr int kSampleSlice = 2048;     // logits per top-k block
 constexpr int kSampleMaxK = 128;       // largest top_k of the two-stage (slice) path
 constexpr int kSampleMaxBlocks = 128;  // vocabularies up to 262144
 constexpr int kSampleCand = kSampleMaxBlocks * kSampleMaxK;
+constexpr int kSampleLists = 4 * kSampleMaxBlocks;   // one per wave of the list kernel
 
 // Device-resident sampling parameters.  k: candidates (1 for greedy);
 // greedy: take the top-1 of the raw logits; counter advances once per draw.
@@ -42,9 +43,10 @@ struct SampleWindow {
     int64_t tok[kSampleWindow];
 };
 
-// Device scratch of the sampler: the top-k candidates, [kSampleMaxBlocks]
-// [kSampleMaxK] (k <= kSampleMaxK), or the k items and their weights
-// (k > kSampleMaxK): key, idx and p each hold sample_scratch_items(V) entries.
+// Device scratch of the sampler: key, idx and p each hold
+// sample_scratch_items(V) entries, cnt kSampleLists.  k <= kSampleMaxK: key
+// holds the wave lists (64-bit items, kSampleLists x 8) and cnt their wave
+// counts; k > kSampleMaxK: the k items and their weights.
 struct SampleScratch {
     uint32_t *key;
     int *idx;
