@@ -15,10 +15,10 @@
 //     would spread one instruction over 64 cache lines (fp32 lm_head: 2.2
 //     TB/s);
 //   * x stays in VGPRs as f32 (32 per activation row), loaded from x directly;
-//   * INT8: two non-temporal 16-byte loads per chunk; w ^ 0x80808080 turns each
-//     signed byte into w + 128, which v_cvt_f32_ubyte{0..3} converts in one
-//     instruction; the +128 is removed once per chunk via 128 * sum(x_chunk);
-//     the per-channel scale multiplies the row dot in the epilogue
+//   * INT8: two non-temporal 16-byte loads per chunk; each signed byte becomes
+//     a float in one instruction (v_cvt_f32_i32 with a sign-extending byte
+//     select), so the row dot is summed over w * x itself, without an offset
+//     to cancel; the per-channel scale multiplies the row dot in the epilogue
 //     (y = dot * s + b, as gemv.rs:777-785);
 //   * FP32: eight 16-byte loads per chunk, one FMA per element.
 #include "gemv_common.hpp"
@@ -53,7 +53,6 @@ struct DenseGemv {
     int piece[LD];        // the lane's pieces (clamped into the row)
     uint32_t pmask;       // bit i: piece i lies inside K
     float xr[M][32];
-    float xs[M];   // 128 * sum of the lane's elements (INT8 offset correction)
 
     __device__ __forceinline__ DenseGemv(const DenseParams &pp, const Layout &ll) : p(pp), L(ll) {
         lane = threadIdx.x & 63;
@@ -94,14 +93,11 @@ struct DenseGemv {
     __device__ __forceinline__ void unpack_x(const float4 (&raw)[M][8]) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            float s = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float4 t = raw[m][i];
                 xr[m][4 * i] = t.x; xr[m][4 * i + 1] = t.y; xr[m][4 * i + 2] = t.z; xr[m][4 * i + 3] = t.w;
-                s += (t.x + t.y) + (t.z + t.w);
             }
-            xs[m] = 128.0f * s;
         }
     }
 
@@ -139,9 +135,11 @@ struct DenseGemv {
                                                  bt.q[d][j][i].w};
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const uint32_t u = xor_opaque(dw4[k], 0x80808080u);
-                            const float f[4] = {(float)(u & 0xFFu), (float)((u >> 8) & 0xFFu),
-                                                (float)((u >> 16) & 0xFFu), (float)(u >> 24)};
+                            const uint32_t u = dw4[k];
+                            const float f[4] = {(float)(int8_t)(u & 0xFFu),
+                                                (float)(int8_t)((u >> 8) & 0xFFu),
+                                                (float)(int8_t)((u >> 16) & 0xFFu),
+                                                (float)(int8_t)(u >> 24)};
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -149,8 +147,6 @@ struct DenseGemv {
                                     acc[m] = fmaf(f[e], xr[m][16 * i + 4 * k + e], acc[m]);
                         }
                     }
-#pragma unroll
-                    for (int m = 0; m < M; ++m) acc[m] -= xs[m];
                 } else {
 #pragma unroll
                     for (int i = 0; i < LD; ++i) {
