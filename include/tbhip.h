@@ -511,24 +511,7 @@ TB_API int tb_decoder_set_rope_tables(tb_decoder *d, const float *cos_t, const f
  * prefill and verify chunks that reach the cap run step by step. */
 TB_API int tb_decoder_set_attention_cap(tb_decoder *d, int64_t cap);
 
-/* Benchmark helper (no reference counterpart): n_steps greedy steps from
- * (first_token, offset) as back-to-back graph replays, timed with HIP events on
- * the decoder's stream. */
-TB_API int tb_decoder_time_greedy(tb_decoder *d, int64_t first_token, int64_t offset,
-                                  int64_t n_steps, float *ms_out);
-
 TB_API int tb_decoder_destroy(tb_decoder *d);
-
-/* Measurement aid (no reference counterpart): one plain streaming read of
- * device memory, for the benchmark to set each GEMV's bandwidth beside what a
- * read of the same byte count reaches on this GPU.  `blocks` blocks of 256
- * threads each read a contiguous share of buf (16-byte aligned) in passes of
- * `loads` (4, 8 or 16) non-temporal 16-byte loads per thread (the last pass
- * masked), and write one xor-folded word per thread to out[blocks * 256]
- * (device memory).  bytes is rounded down to a multiple of 16; the bytes read
- * go to *bytes_read (host). */
-TB_API int tb_read_probe(const void *buf, int64_t bytes, int64_t blocks, int64_t loads,
-                         uint32_t *out, int64_t *bytes_read, void *stream);
 
 #ifdef __cplusplus
 }

@@ -13,8 +13,8 @@ from torchburn_amd import decoder as tbdec
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_symbols():
-    txt = open(os.path.join(ROOT, "include", "tbhip.h")).read()
+def header_symbols(names=("tbhip.h", "tbhip_bench.h")):
+    txt = "".join(open(os.path.join(ROOT, "include", n)).read() for n in names)
     return sorted(set(re.findall(r"TB_API\s+[\w\s\*]*?\b(tb_\w+)\s*\(", txt)))
 
 
@@ -22,6 +22,10 @@ def test_header_declares_entry_points():
     syms = header_symbols()
     assert "tb_w4a32_grouped_linear" in syms and "tb_decoder_step" in syms
     assert len(syms) >= 21
+    # the measurement entry points stay out of the product header
+    product = header_symbols(("tbhip.h",))
+    assert "tb_read_probe" not in product and "tb_decoder_time_greedy" not in product
+    assert "tbhip_bench.h" not in open(os.path.join(ROOT, "include", "tbhip.h")).read()
 
 
 def test_library_exports_every_declared_symbol():

@@ -25,6 +25,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/tbhip_bench.h"
 #include "decode.hpp"
 #include "gemv_dense.hpp"
 #include "tb_common.hpp"

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 
+#include "../../include/tbhip_bench.h"
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
 
