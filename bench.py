@@ -475,7 +475,7 @@ def decode_run(torch, name, steps, prefill_tokens=0):
         "qwen64": (synth.QWEN_0_5B, 4, 4, 2048, 0x7B + 4),
     }[name]
     gs = 64 if name == "qwen64" else 32
-    max_seq = kvlen + steps
+    max_seq = kvlen + max(steps, 8)   # room for the 5-position verify at any step count
     w = synth.decoder_weights_torch(cfg, seed, wk, lk, gs)
     dec = decoder_from_weights(w, cfg, group_size=gs, max_seq_len=max_seq)
     del w
