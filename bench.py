@@ -312,6 +312,16 @@ def int4_set(torch, dev, gen, n, k, gs=32):
     return w, s
 
 
+def batched_kernel(M, N, K):
+    """The kernel tb_w4a32_grouped_linear runs for an M x N x K v1 projection
+    (the selection in csrc/capi.hip linear_w4): M = 3..16 takes the f16-MFMA
+    limb kernel (exact f32 products from f16 limbs of x), except M = 16 with N
+    and K at most 4096, which stays on FP32 MFMA like every M > 16."""
+    if 3 <= M <= 16 and not (M == 16 and N <= 4096 and K <= 4096):
+        return "k_limb_prep + k_w4_limb (f16 MFMA on exact limbs of x) + k_limb_reduce"
+    return "k_w4_mfma (FP32 MFMA) + k_mfma_reduce"
+
+
 def batched_section(torch, args, dev):
     """Config 3: Y[M, N] = X[M, 4096] . deq(W)^T on FP32 MFMA, M in {16, 64}."""
     from torchburn_amd import _lib
@@ -337,7 +347,8 @@ def batched_section(torch, args, dev):
         us = ms * 1e3 / len(sets)
         flops = 2.0 * M * N * K
         wbytes = N * K // 2 + 4 * N * (K // GS)
-        out[f"m{M}_n{N}"] = {"us": round(us, 3), "tflops": round(flops / us / 1e6, 2),
+        out[f"m{M}_n{N}"] = {"kernel": batched_kernel(M, N, K),
+                             "us": round(us, 3), "tflops": round(flops / us / 1e6, 2),
                              "frac_fp32_mfma_peak": round(flops / us / 1e6 / MFMA_F32_PEAK, 4),
                              "weight_gbs": round(wbytes / us / 1e3, 1),
                              "weight_copies_rotated": copies}
