@@ -2,9 +2,10 @@
 apply_repetition_penalty + sample_logits (decoder.rs:878-1020), pinned in
 tests/test_oracle_sample.py.  The draw u of (seed, counter) comes from the
 library's generator (tb_sample_uniform); given u the token must be identical
-for top_k <= 128 (sequential sums over at most 128 items, as the oracle's).
-Past that the masses are summed in a parallel order and the token must lie
-between the oracle's draws at u -/+ 2e-3.
+for top_k <= 1024 (the list / select path sums the masses of its at most 1024
+items in sequence, as the oracle does).  Past that the one-block path sums them
+in a parallel order and the token must lie between the oracle's draws at
+u -/+ 2e-3.
 """
 import numpy as np
 import pytest
@@ -31,6 +32,9 @@ CASES = [
     # top_k past the slice path: one block over the whole vocabulary
     (151936, 0.8, 500, 0.9, 1.1),
     (151936, 0.8, 512, 0.9, 1.0),
+    (151936, 1.1, 1024, 0.95, 1.0),     # the largest k of the list / select path
+    (32000, 0.9, 700, 0.9, 1.1),        # fewer waves than k, past 128
+    (151936, 0.9, 1025, 0.9, 1.0),      # the first k of the one-block path
     (128256, 1.0, 4096, 1.0, 1.0),
     (1000, 0.7, 1000, 0.95, 1.0),       # k == V
     (300, 2.0, 129, 1.0, 1.2),
@@ -67,10 +71,10 @@ def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
             assert u == -1.0
         pl = O.repetition_penalty(lg, recent, pen)
         ref, _ = O.sample_logits(pl, T, k, top_p, uu)
-        if greedy or k <= 128 or tok == ref:
+        if greedy or k <= 1024 or tok == ref:
             assert tok == ref, (trial, tok, ref)
             continue
-        # top_k > 128: the masses are summed in a parallel order, and over tens
+        # top_k > 1024: the masses are summed in a parallel order, and over tens
         # of thousands of f32 terms that moves the nucleus cut and the draw
         # point by up to ~1e-4 of the mass.  The draw is monotone in u over the
         # sorted order (value descending, index ascending), so the token must
@@ -128,7 +132,7 @@ def test_sampler_wave_list_edges(cuda, kind):
     print(f"case wave lists {kind}", flush=True)
     V = 151936
     g = np.random.default_rng(len(kind))
-    for k in (40, 100, 128):
+    for k in (40, 128, 600):
         lg = g.standard_normal(V).astype(np.float32)
         if kind == "low_ids":
             lg[:94] += 10.0

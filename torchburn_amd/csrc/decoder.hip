@@ -110,7 +110,7 @@ struct Decoder {
     int64_t *srec = nullptr;
     int64_t srec_cap = 0;
     uint64_t seed = 0x7B, draws = 0;
-    // sampled step graphs: [0] top_k <= kSampleMaxK (slice path), [1] beyond
+    // sampled step graphs: [0] top_k <= kSampleMaxK (list / select path), [1] beyond
     hipGraph_t graph_s[2] = {nullptr, nullptr};
     hipGraphExec_t exec_s[2] = {nullptr, nullptr};
     bool tail_large = false;     // the sampler path enqueued by enqueue_tail
@@ -527,7 +527,7 @@ struct Decoder {
     }
 
     // Every top_k samples on the device (top_k > kSampleMaxK on the one-block
-    // path); the host sampler remains for vocabularies past the slice grid.
+    // path); the host sampler remains for vocabularies past 262144 tokens.
     bool device_samplable(float, int64_t) const { return V <= kSampleMaxBlocks * kSampleSlice; }
 
     // decode_and_sample on the device: one step, then the sampler over the

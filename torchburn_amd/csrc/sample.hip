@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kLargeThreads) void k_topk_large(
 constexpr int kRun = 16;
 constexpr int kListQ = 8;
 constexpr int kCandCap = 2048;
-constexpr int kPoolCap = 512;
+constexpr int kPoolCap = 1536;   // W * ceil(k / W) < W + k <= 256 + kSampleMaxK, + 8 zeros
 constexpr int kSelThreads = 1024;
 constexpr int kMaxFlagged = kSampleMaxK / kListQ;
 static_assert(kSampleLists * kListQ * 8 <= kSampleCand * 4, "wave lists fit the key scratch");
@@ -628,12 +628,15 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
     __shared__ __align__(16) uint64_t cand[kCandCap];
     __shared__ int ctag[kCandCap];
     __shared__ int crank[kCandCap];
-    __shared__ __align__(16) uint64_t pool[kPoolCap];
     __shared__ uint64_t top[kSampleMaxK];
-    __shared__ __align__(16) float p[kSampleMaxK];
-    __shared__ __align__(16) float cp[kSampleMaxK];
-    __shared__ __align__(16) float cb[kSampleMaxK];
-    __shared__ int prank[kPoolCap];
+    // the pool and its ranks, then (once T is known) the draw's masses
+    constexpr int kPoolBytes = kPoolCap * 12, kDrawBytes = 3 * kSampleMaxK * 4;
+    __shared__ __align__(16) unsigned char scratch[kPoolBytes > kDrawBytes ? kPoolBytes : kDrawBytes];
+    uint64_t *pool = reinterpret_cast<uint64_t *>(scratch);
+    int *prank = reinterpret_cast<int *>(scratch + kPoolCap * 8);
+    float *p = reinterpret_cast<float *>(scratch);
+    float *cp = p + kSampleMaxK;
+    float *cb = cp + kSampleMaxK;
     __shared__ float red[NT / 4];
     __shared__ int sn[NW + 1];
     __shared__ int flagged[kMaxFlagged];
@@ -672,7 +675,7 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
     __syncthreads();
     const int np = n_pool;
     if (np >= k) {   // T = the k-th best of the pool
-        if (tid < 8) pool[np + tid] = 0ull;   // np + 8 <= kPoolCap: np < W + k
+        if (tid < 8) pool[np + tid] = 0ull;   // np + 8 <= kPoolCap
         __syncthreads();
         rank_items<NT>(pool, np, prank);
         for (int c = tid; c < np; c += NT)
@@ -806,18 +809,26 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
             // kept: the first item whose normalised mass before it exceeds top_p
             const int lim = s_lim;
             const float tp = prm->top_p;
-            const unsigned long long c0 = __ballot(lane < lim && cb[lane] > tp);
-            const unsigned long long c1 = __ballot(lane + 64 < lim && cb[lane + 64] > tp);
-            const int kept = c0 ? __ffsll((long long)c0) - 1
-                             : c1 ? 64 + __ffsll((long long)c1) - 1
-                                  : (lim > 0 && lim < m ? lim : m);
+            int kept = lim > 0 && lim < m ? lim : m;
+            for (int c = 0; c < lim; c += 64) {
+                const unsigned long long b = __ballot(c + lane < lim && cb[c + lane] > tp);
+                if (b) {
+                    kept = c + __ffsll((long long)b) - 1;
+                    break;
+                }
+            }
             const uint64_t z = splitmix(prm->seed + (prm->counter + 1ull) * 0x9E3779B97F4A7C15ull);
             u = (float)(z >> 40) * 5.9604644775390625e-8f;   // [0, 1), 24 bits
             const float r = u * cp[kept - 1];   // u times the mass of the kept items
             // the first kept item whose running mass reaches r
-            const unsigned long long b0 = __ballot(lane < kept && cp[lane] >= r);
-            const unsigned long long b1 = __ballot(lane + 64 < kept && cp[lane + 64] >= r);
-            const int d = b0 ? __ffsll((long long)b0) - 1 : b1 ? 64 + __ffsll((long long)b1) - 1 : 0;
+            int d = 0;
+            for (int c = 0; c < kept; c += 64) {
+                const unsigned long long b = __ballot(c + lane < kept && cp[c + lane] >= r);
+                if (b) {
+                    d = c + __ffsll((long long)b) - 1;
+                    break;
+                }
+            }
             tok = item_index(top[d]);
         }
         if (lane == 0) {

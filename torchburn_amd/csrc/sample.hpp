@@ -9,10 +9,10 @@ namespace tb {
 struct DecState;
 
 constexpr int kSampleSlice = 2048;     // logits per top-k block
-constexpr int kSampleMaxK = 128;       // largest top_k of the two-stage (slice) path
+constexpr int kSampleMaxK = 1024;      // largest top_k of the list / select path
 constexpr int kSampleMaxBlocks = 128;  // vocabularies up to 262144
-constexpr int kSampleCand = kSampleMaxBlocks * kSampleMaxK;
 constexpr int kSampleLists = 4 * kSampleMaxBlocks;   // one per wave of the list kernel
+constexpr int kSampleCand = kSampleLists * 8 * 2;     // u32 words of the wave lists
 
 // Device-resident sampling parameters.  k: candidates (1 for greedy);
 // greedy: take the top-1 of the raw logits; counter advances once per draw.
