@@ -412,10 +412,10 @@ __global__ __launch_bounds__(kLargeThreads) void k_topk_large(
 
 // ---- top_k <= kSampleMaxK: wave lists, a threshold, ranks ----
 //
-// k_topk_lists (nb blocks of 4 waves, E = list_per_lane(V) ids per lane):
-// the vocabulary is cut into runs of kRun ids; block b takes runs b, b + nb,
+// k_topk_lists (nb = ceil(V / 2048) blocks of 4 waves, 8 ids per lane): the
+// vocabulary is cut into runs of kRun ids; block b takes runs b, b + nb,
 // b + 2 nb, ..., and in each run wave w takes the ids = w (mod 4), so a
-// wave's 64 E ids are spread over the vocabulary and neighbouring ids (which
+// wave's 512 ids are spread over the vocabulary and neighbouring ids (which
 // related tokens often are) fall to different waves.  Each wave writes its
 // best q = min(k, kListQ) items, best first (0 past its count), and its count.
 //
@@ -434,18 +434,13 @@ __global__ __launch_bounds__(kLargeThreads) void k_topk_large(
 constexpr int kRun = 16;
 constexpr int kListQ = 8;
 constexpr int kCandCap = 2048;
-constexpr int kPoolCap = 1536;   // W * ceil(k / W) < W + k <= 256 + kSampleMaxK, + 8 zeros
+constexpr int kPoolCap = kSampleLists + kSampleMaxK + 8;   // W * ceil(k / W) < W + k, + 8 zeros
 constexpr int kSelThreads = 1024;
 constexpr int kMaxFlagged = kSampleMaxK / kListQ;
 static_assert(kSampleLists * kListQ * 8 <= kSampleCand * 4, "wave lists fit the key scratch");
 
-// ids per lane of the list kernel: 16 past 65536 logits (at most 256 waves
-// for the select block to rank), else 8 (at most 128 waves)
-inline int list_per_lane(int V) { return V > 65536 ? 16 : 8; }
-inline int list_blocks(int V) {
-    const int per_block = 256 * list_per_lane(V);
-    return (V + per_block - 1) / per_block;
-}
+// Blocks of the list kernel (2048 ids each: 4 waves x 64 lanes x kListQ).
+inline int list_blocks(int V) { return (V + 2047) / 2048; }
 
 // The id that item i of lane l in wave w of block b (of nb) stands for; ids
 // >= V are no item.
@@ -468,18 +463,6 @@ __device__ __forceinline__ void sort8_desc(uint64_t (&v)[8]) {
     cas_desc(v[0], v[4]); cas_desc(v[1], v[5]); cas_desc(v[2], v[6]); cas_desc(v[3], v[7]);
     cas_desc(v[2], v[4]); cas_desc(v[3], v[5]);
     cas_desc(v[1], v[2]); cas_desc(v[3], v[4]); cas_desc(v[5], v[6]);
-}
-
-// v = the best 8 of a and b (each sorted best first), sorted best first: the
-// pairwise maxima of a and reversed b form a bitonic sequence, which three
-// half-cleaner stages sort.
-__device__ __forceinline__ void merge8_desc(const uint64_t (&a)[8], const uint64_t (&b)[8],
-                                            uint64_t (&v)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = a[i] > b[7 - i] ? a[i] : b[7 - i];
-    cas_desc(v[0], v[4]); cas_desc(v[1], v[5]); cas_desc(v[2], v[6]); cas_desc(v[3], v[7]);
-    cas_desc(v[0], v[2]); cas_desc(v[1], v[3]); cas_desc(v[4], v[6]); cas_desc(v[5], v[7]);
-    cas_desc(v[0], v[1]); cas_desc(v[2], v[3]); cas_desc(v[4], v[5]); cas_desc(v[6], v[7]);
 }
 
 // x from another lane of the same row or the row before, by a DPP move
@@ -515,17 +498,15 @@ __device__ __forceinline__ uint64_t wave_best(uint64_t x) {
     return ((uint64_t)mk << 32) | ml;
 }
 
-template <int E>
 __global__ __launch_bounds__(kThreads) void k_topk_lists(const float *__restrict__ logits, int V,
                                                          const SampleParams *__restrict__ prm,
                                                          uint64_t *__restrict__ lists,
                                                          int *__restrict__ wcnt) {
-    static_assert(E == 8 || E == 16, "8 or 16 ids per lane");
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nb = gridDim.x;
-    float x[E];
+    float x[kListQ];
     int n = 0;
 #pragma unroll
-    for (int i = 0; i < E; ++i) {   // every load issued at once (ids past V read logits[V-1])
+    for (int i = 0; i < kListQ; ++i) {   // every load issued at once (ids past V read logits[V-1])
         const int id = list_id(blockIdx.x, nb, w, l, i);
         x[i] = logits[min(id, V - 1)];
         n += __popcll(__ballot(id < V));
@@ -534,27 +515,14 @@ __global__ __launch_bounds__(kThreads) void k_topk_lists(const float *__restrict
     const int k = prm->k;
     const bool greedy = prm->greedy != 0;
     const int q = min(k, kListQ);
-    auto item = [&](int i) {
+    uint64_t v[kListQ];
+#pragma unroll
+    for (int i = 0; i < kListQ; ++i) {
         const int id = list_id(blockIdx.x, nb, w, l, i);
         const uint64_t it = pack_item(sample_key(x[i], id, greedy), id);
-        return id < V ? it : 0ull;
-    };
-    uint64_t v[kListQ];
-    if constexpr (E == 8) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = item(i);
-        sort8_desc(v);
-    } else {
-        uint64_t a[8], b[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            a[i] = item(i);
-            b[i] = item(8 + i);
-        }
-        sort8_desc(a);
-        sort8_desc(b);
-        merge8_desc(a, b, v);
+        v[i] = id < V ? it : 0ull;
     }
+    sort8_desc(v);
     // q rounds: the wave's best head leaves its lane (items are distinct)
     uint64_t mine = 0ull;
     for (int t = 0; t < q; ++t) {
@@ -655,7 +623,6 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
     const int k = prm->k;
     if (k > kSampleMaxK) return;   // the large-k path samples
     const bool greedy = prm->greedy != 0;
-    const int E = V > 65536 ? 16 : 8;
     const int q = min(k, kListQ), m = min(k, V), jp = min(q, (k + W - 1) / W);
     if (tid == 0) {
         n_cand = 0;
@@ -669,8 +636,8 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
         const int e = tid + r * NT;
-        wave_append(li[r] != 0ull && (e & (kListQ - 1)) < jp, li[r], 0, pool, nullptr, kPoolCap,
-                    &n_pool);
+        wave_append(li[r] != 0ull && (e & (kListQ - 1)) < jp, li[r], 0, pool, nullptr,
+                    kPoolCap - 8, &n_pool);
     }
     __syncthreads();
     const int np = n_pool;
@@ -719,7 +686,7 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
             for (int f = wave; f < nf; f += NW) {
                 const int L = flagged[f], b = L >> 2, w = L & 3;
                 const uint64_t last = lists[(size_t)L * kListQ + q - 1];
-                for (int i = 0; i < E; ++i) {
+                for (int i = 0; i < kListQ; ++i) {
                     const int id = list_id(b, nb, w, lane, i);
                     const uint64_t it =
                         id < V ? pack_item(sample_key(logits[id], id, greedy), id) : 0ull;
@@ -883,12 +850,8 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
     }
     uint64_t *lists = reinterpret_cast<uint64_t *>(ws.key);
     const int nbl = list_blocks(V);
-    if (list_per_lane(V) == 16)
-        hipLaunchKernelGGL(k_topk_lists<16>, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm,
-                           lists, ws.cnt);
-    else
-        hipLaunchKernelGGL(k_topk_lists<8>, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm,
-                           lists, ws.cnt);
+    hipLaunchKernelGGL(k_topk_lists, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm, lists,
+                       ws.cnt);
     TB_LAUNCHED();
     hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kSelThreads), 0, st, logits, V, nbl, lists,
                        ws.cnt, prm, out, dstate, history, hist_cap);
