@@ -140,14 +140,26 @@ __global__ __launch_bounds__(kThreads) void k_penalty(float *__restrict__ logits
     extern __shared__ uint32_t bits[];
     __shared__ int64_t wtok[kSampleWindow];
     const int tid = threadIdx.x;
-    if (win) {
-        const int c = win->n, drop = c == kSampleWindow ? 1 : 0, nn = c - drop + 1;
-        if (tid < nn) wtok[tid] = tid < c - drop ? win->tok[tid + drop] : (int64_t)dstate->token;
-        __syncthreads();   // every old entry is read before any is replaced
-        if (tid < nn) win->tok[tid] = wtok[tid];
-        if (tid == 0) win->n = nn;
+    if (win) {   // push onto the ring, then the live slots are the window
+        const int c = win->n, head = win->head;
+        const int slot = c < kSampleWindow ? (head + c) % kSampleWindow : head;
+        if (tid < kSampleWindow)
+            wtok[tid] = tid == slot ? (int64_t)dstate->token : win->tok[tid];
+        __syncthreads();   // every thread read the ring before thread 0 changes it
+        if (tid == 0) {
+            win->tok[slot] = wtok[slot];
+            win->head = c < kSampleWindow ? head : (head + 1) % kSampleWindow;
+            win->n = c < kSampleWindow ? c + 1 : c;
+        }
+        // the live slots: all of them once full, else slots head .. head + c
+        n = c < kSampleWindow ? c + 1 : kSampleWindow;
+        if (n < kSampleWindow && tid < kSampleWindow) {
+            const int rel = (tid - head + kSampleWindow) % kSampleWindow;
+            if (rel >= n) wtok[tid] = -1;   // not live: skipped below
+        }
+        __syncthreads();
         recent = wtok;
-        n = nn;
+        n = kSampleWindow;
     }
     const float pen = prm->penalty;
     if (!(pen > 1.0f) || n <= 0) return;
@@ -498,10 +510,20 @@ __device__ __forceinline__ uint64_t wave_best(uint64_t x) {
     return ((uint64_t)mk << 32) | ml;
 }
 
-__global__ __launch_bounds__(kThreads) void k_topk_lists(const float *__restrict__ logits, int V,
+// With `win` (the decoder's step), the repetition penalty of the window as it
+// stands after the step's input token (dstate->token) is pushed: every block
+// finds the distinct window tokens it holds (the inverse of list_id), and the
+// thread holding one divides or multiplies its copy (decoder.rs:878-899) and
+// writes it back, so the select kernel's re-reads see it.  The push itself is
+// the select kernel's, after every block here has read the ring.
+__global__ __launch_bounds__(kThreads) void k_topk_lists(float *__restrict__ logits, int V,
                                                          const SampleParams *__restrict__ prm,
                                                          uint64_t *__restrict__ lists,
-                                                         int *__restrict__ wcnt) {
+                                                         int *__restrict__ wcnt,
+                                                         const SampleWindow *__restrict__ win,
+                                                         const DecState *__restrict__ dstate) {
+    __shared__ int pen_n;
+    __shared__ int pen_e[kSampleWindow + 1];
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nb = gridDim.x;
     float x[kListQ];
     int n = 0;
@@ -510,6 +532,52 @@ __global__ __launch_bounds__(kThreads) void k_topk_lists(const float *__restrict
         const int id = list_id(blockIdx.x, nb, w, l, i);
         x[i] = logits[min(id, V - 1)];
         n += __popcll(__ballot(id < V));
+    }
+    if (win) {
+        const float pen = prm->penalty;
+        if (threadIdx.x == 0) pen_n = 0;
+        __syncthreads();
+        if (w == 0 && pen > 1.0f) {
+            // lane l: ring slot l if live after the push; the pushed token
+            // replaces the slot it lands in (the oldest one when full)
+            const int c = win->n, head = win->head;
+            const int slot = c < kSampleWindow ? (head + c) % kSampleWindow : head;
+            const int live_n = c < kSampleWindow ? c + 1 : kSampleWindow;
+            const int64_t tin = dstate->token;
+            const int64_t t = l == slot ? tin : win->tok[l];
+            const bool live = (l - head + kSampleWindow) % kSampleWindow < live_n;
+            const bool ok = live && t >= 0 && t < V;
+            const int r = ok ? (int)(t / kRun) : 0, o = ok ? (int)(t % kRun) : 0;
+            const bool own = ok && r % nb == (int)blockIdx.x;
+            unsigned long long ob = __ballot(own);
+            while (ob) {   // usually none or one: 64 tokens over nb blocks
+                const int j = __ffsll((long long)ob) - 1;
+                ob &= ob - 1ull;
+                const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)t, j);
+                const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)t >> 32), j);
+                const int64_t tj = (int64_t)(((uint64_t)hi << 32) | lo);
+                // the first live slot holding tj applies it
+                if (__ballot(ok && l < j && t == tj) == 0ull && l == j) {
+                    const int jj = r / nb;
+                    const int e = ((o & 3) << 16) | ((((jj & 15) << 2) | (o >> 2)) << 8) | (jj >> 4);
+                    pen_e[atomicAdd(&pen_n, 1)] = e;
+                }
+            }
+        }
+        __syncthreads();
+        const int ne = pen_n;
+        for (int ei = 0; ei < ne; ++ei) {
+            const int e = pen_e[ei];
+            if ((e >> 16) != w || ((e >> 8) & 255) != l) continue;
+            const int item = e & 255;
+#pragma unroll
+            for (int i = 0; i < kListQ; ++i)
+                if (i == item) {
+                    const float v = x[i];
+                    x[i] = v > 0.f ? v / pen : v * pen;
+                    logits[list_id(blockIdx.x, nb, w, l, i)] = x[i];
+                }
+        }
     }
     // (the k test comes last, so that the loads above need not wait for it)
     const int k = prm->k;
@@ -590,7 +658,8 @@ __device__ void rank_items(const uint64_t *a, int n, int *rank) {
 __global__ __launch_bounds__(kSelThreads) void k_topk_select(
     const float *__restrict__ logits, int V, int nb, const uint64_t *__restrict__ lists,
     const int *__restrict__ wcnt, SampleParams *__restrict__ prm, SampleOut *__restrict__ out,
-    DecState *__restrict__ st, int *__restrict__ history, int hist_cap) {
+    DecState *__restrict__ st, int *__restrict__ history, int hist_cap,
+    SampleWindow *__restrict__ win) {
     constexpr int NT = kSelThreads, NW = NT / 64;
     constexpr int kPer = kSampleLists * kListQ / NT;   // list slots per thread
     __shared__ __align__(16) uint64_t cand[kCandCap];
@@ -803,6 +872,12 @@ __global__ __launch_bounds__(kSelThreads) void k_topk_select(
             out->u = u;
             out->token = tok;
             out->kept = m;
+            if (win) {   // the step's input token onto the ring (the lists applied it)
+                const int c = win->n, head = win->head;
+                win->tok[c < kSampleWindow ? (head + c) % kSampleWindow : head] = st->token;
+                win->head = c < kSampleWindow ? head : (head + 1) % kSampleWindow;
+                win->n = c < kSampleWindow ? c + 1 : c;
+            }
             if (st) {   // the decoder's next step, as the greedy argmax tail does
                 const int step = st->step;
                 if (history && step < hist_cap) history[step] = tok;
@@ -837,7 +912,10 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
     const size_t lds = (size_t)((V + 31) / 32) * 4;
     TB_REQUIRE(lds <= 64 * 1024, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: repetition penalty bitmap exceeds LDS");
-    if (win || (recent && n_recent > 0)) {
+    // the decoder's window on the list path: the list kernel applies the
+    // penalty and the select kernel pushes the token
+    const bool fused_window = win && !large;
+    if ((win && !fused_window) || (!win && recent && n_recent > 0)) {
         hipLaunchKernelGGL(k_penalty, dim3(1), dim3(kThreads), lds, st, logits, V,
                            win ? nullptr : recent, win ? 0 : n_recent, win, dstate, prm);
         TB_LAUNCHED();
@@ -851,10 +929,10 @@ int launch_sample(float *logits, int V, const int64_t *recent, int n_recent,
     uint64_t *lists = reinterpret_cast<uint64_t *>(ws.key);
     const int nbl = list_blocks(V);
     hipLaunchKernelGGL(k_topk_lists, dim3(nbl), dim3(kThreads), 0, st, logits, V, prm, lists,
-                       ws.cnt);
+                       ws.cnt, fused_window ? win : nullptr, dstate);
     TB_LAUNCHED();
     hipLaunchKernelGGL(k_topk_select, dim3(1), dim3(kSelThreads), 0, st, logits, V, nbl, lists,
-                       ws.cnt, prm, out, dstate, history, hist_cap);
+                       ws.cnt, prm, out, dstate, history, hist_cap, fused_window ? win : nullptr);
     TB_LAUNCHED();
     return TB_OK;
 }

@@ -35,11 +35,13 @@ struct SampleOut {
 };
 
 // The repetition-penalty window of a generation loop: the last kSampleWindow
-// tokens (decoder.rs:859-876), on the device.
+// tokens (decoder.rs:859-876), on the device, as a ring: the n live tokens
+// sit in slots head, head + 1, ... (mod kSampleWindow).  The penalty only needs
+// the set, so a push writes one slot instead of shifting the window.
 constexpr int kSampleWindow = 64;
 struct SampleWindow {
     int n;
-    int pad;
+    int head;
     int64_t tok[kSampleWindow];
 };
 
