@@ -35,6 +35,11 @@ CASES = [
     (151936, 1.1, 1024, 0.95, 1.0),     # the largest k of the list / select path
     (32000, 0.9, 700, 0.9, 1.1),        # fewer waves than k, past 128
     (151936, 0.9, 1025, 0.9, 1.0),      # the first k of the one-block path
+    (1, 0.8, 40, 0.9, 1.1),             # tiny vocabularies: empty waves, k clamped to V
+    (3, 0.8, 2, 0.9, 1.1),
+    (7, 1.0, 7, 1.0, 1.0),
+    (2049, 0.8, 64, 0.9, 1.0),          # a second list block with one logit
+    (65537, 0.9, 300, 0.95, 1.1),
     (128256, 1.0, 4096, 1.0, 1.0),
     (1000, 0.7, 1000, 0.95, 1.0),       # k == V
     (300, 2.0, 129, 1.0, 1.2),
@@ -58,7 +63,8 @@ def test_sampler_matches_oracle(cuda, V, T, k, top_p, pen):
             lg[:] = 0.0                           # all equal
         if trial == 4:
             lg[0] = np.nan                        # greedy keeps index 0 (decoder.rs:914-925)
-            lg[g.integers(1, V, 3)] = np.nan
+            if V > 1:
+                lg[g.integers(1, V, 3)] = np.nan
         recent = list(g.integers(0, V, 30)) + [V + 5, -1]
         seed, counter = int(g.integers(0, 2 ** 63)), int(g.integers(0, 1000))
         tok, u = tb.sample_logits(torch.from_numpy(lg).to(cuda), T, k, top_p, pen, recent,
