@@ -21,13 +21,13 @@ namespace {
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    for (int o = 32; o >= 1; o >>= 1) v += shfl_xor_u(v, o);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, shfl_xor_u(v, o));
     return v;
 }
 
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
         }
 #pragma unroll
         for (int j = 0; j < 6; ++j)
-            if (j < RB || j >= RB + LGP) m = fmaxf(m, __shfl_xor(m, 1 << j));
+            if (j < RB || j >= RB + LGP) m = fmaxf(m, shfl_xor_u(m, 1 << j));
         float l = 0.f;
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
         }
 #pragma unroll
         for (int j = 0; j < 6; ++j)
-            if (j < RB || j >= RB + LGP) l += __shfl_xor(l, 1 << j);
+            if (j < RB || j >= RB + LGP) l += shfl_xor_u(l, 1 << j);
         if (rg == 0 && rep && vi < GP) {
             sml[wave][g][0] = m;
             sml[wave][g][1] = l;
@@ -400,10 +400,10 @@ __global__ __launch_bounds__(256) void k_attn_reg(const DecState *__restrict__ s
         for (int j = B; j < 6; ++j)
 #pragma unroll
             for (int h = 0; h < GP; ++h) {
-                acc[h].x += __shfl_xor(acc[h].x, 1 << j);
-                acc[h].y += __shfl_xor(acc[h].y, 1 << j);
-                acc[h].z += __shfl_xor(acc[h].z, 1 << j);
-                acc[h].w += __shfl_xor(acc[h].w, 1 << j);
+                acc[h].x += shfl_xor_u(acc[h].x, 1 << j);
+                acc[h].y += shfl_xor_u(acc[h].y, 1 << j);
+                acc[h].z += shfl_xor_u(acc[h].z, 1 << j);
+                acc[h].w += shfl_xor_u(acc[h].w, 1 << j);
             }
         if (rg == 0) {
 #pragma unroll

@@ -108,28 +108,87 @@ __device__ __forceinline__ float select_bits(float a, float b, uint32_t mask_b) 
     return __uint_as_float((__float_as_uint(a) & ~mask_b) | (__float_as_uint(b) & mask_b));
 }
 
-// Reduce V per-lane values over the lanes of bits [0, b) of the lane id
-// (halving exchanges through ds_bpermute: V - 1 exchanges for V values instead
-// of log2(64) per value).  After the call, lane l holds in v[0] the full sum of
-// value index (l >> (b - log2 V)) & (V - 1) over its 2^b-lane span.
-// Requires V <= 2^b.
-template <int V>
-__device__ __forceinline__ void transpose_reduce(float (&v)[V], int lane, int b) {
+// v from lane (lane ^ MASK) of the wave, in VALU moves instead of an
+// LDS-crossbar permute: quad permutes for 1 and 2, the row shifts by 4 either
+// way picked by lane bit 2, a row rotation by 8 (which swaps the row's
+// halves), and gfx950's 16- and 32-lane swaps.
+template <int MASK>
+__device__ __forceinline__ float shfl_xor_c(float v) {
+    static_assert(MASK == 1 || MASK == 2 || MASK == 4 || MASK == 8 || MASK == 16 || MASK == 32,
+                  "a power of two below 64");
+    const int lane = threadIdx.x & 63;
+    const int iv = __float_as_int(v);
+    if constexpr (MASK == 1) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false));
+    } else if constexpr (MASK == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false));
+    } else if constexpr (MASK == 4) {
+        const int up = __builtin_amdgcn_update_dpp(iv, iv, 0x104, 0xF, 0xF, false);   // i + 4
+        const int dn = __builtin_amdgcn_update_dpp(iv, iv, 0x114, 0xF, 0xF, false);   // i - 4
+        return __int_as_float((lane & 4) ? dn : up);
+    } else if constexpr (MASK == 8) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(iv, iv, 0x128, 0xF, 0xF, false));
+    } else if constexpr (MASK == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)iv, (unsigned)iv, false, false);
+        return __uint_as_float((lane & 16) ? r[0] : r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)iv, (unsigned)iv, false, false);
+        return __uint_as_float((lane & 32) ? r[0] : r[1]);
+    }
+}
+
+// The same for a mask known only at run time (wave-uniform; a constant after
+// unrolling folds the switch away).
+__device__ __forceinline__ float shfl_xor_u(float v, int mask) {
+    switch (mask) {
+    case 1: return shfl_xor_c<1>(v);
+    case 2: return shfl_xor_c<2>(v);
+    case 4: return shfl_xor_c<4>(v);
+    case 8: return shfl_xor_c<8>(v);
+    case 16: return shfl_xor_c<16>(v);
+    case 32: return shfl_xor_c<32>(v);
+    default: return __shfl_xor(v, mask);
+    }
+}
+
+// Reduce V per-lane values over the lanes of bits [0, B) of the lane id
+// (halving exchanges: V - 1 exchanges for V values instead of log2(64) per
+// value).  After the call, lane l holds in v[0] the full sum of value index
+// (l >> (B - log2 V)) & (V - 1) over its 2^B-lane span.  Requires V <= 2^B.
+template <int V, int B>
+__device__ __forceinline__ void transpose_reduce_c(float (&v)[V], int lane) {
     constexpr int LOGV = Log2<V>::value;
+    static_assert(LOGV <= B && B <= 6, "V <= 2^B <= 64");
 #pragma unroll
     for (int s = 0; s < LOGV; ++s) {
         const int h = (V >> s) >> 1;
-        const int mask = 1 << (b - 1 - s);
+        const int mask = 1 << (B - 1 - s);
         const uint32_t up = (lane & mask) ? 0xFFFFFFFFu : 0u;
 #pragma unroll
         for (int i = 0; i < h; ++i) {
             const float lo = v[i], hi = v[i + h];
             const float keep = select_bits(lo, hi, up);
             const float send = select_bits(hi, lo, up);
-            v[i] = keep + __shfl_xor(send, mask);
+            v[i] = keep + shfl_xor_u(send, mask);
         }
     }
-    for (int sh = b - LOGV - 1; sh >= 0; --sh) v[0] += __shfl_xor(v[0], 1 << sh);
+#pragma unroll
+    for (int sh = B - LOGV - 1; sh >= 0; --sh) v[0] += shfl_xor_u(v[0], 1 << sh);
+}
+
+// transpose_reduce_c for a lane-bit count b known at run time (wave-uniform).
+template <int V>
+__device__ __forceinline__ void transpose_reduce(float (&v)[V], int lane, int b) {
+    constexpr int LOGV = Log2<V>::value;
+    switch (b) {
+    case 6: transpose_reduce_c<V, 6>(v, lane); break;
+    case 5: if constexpr (LOGV <= 5) transpose_reduce_c<V, 5>(v, lane); break;
+    case 4: if constexpr (LOGV <= 4) transpose_reduce_c<V, 4>(v, lane); break;
+    case 3: if constexpr (LOGV <= 3) transpose_reduce_c<V, 3>(v, lane); break;
+    case 2: if constexpr (LOGV <= 2) transpose_reduce_c<V, 2>(v, lane); break;
+    case 1: if constexpr (LOGV <= 1) transpose_reduce_c<V, 1>(v, lane); break;
+    default: if constexpr (LOGV == 0) transpose_reduce_c<V, 0>(v, lane); break;
+    }
 }
 
 // silu(g) = g / (1 + exp(-g)), as the reference writes it
@@ -357,7 +416,7 @@ __device__ __forceinline__ void reduce_and_store(float (&v)[V], float *red, EpiS
         for (int u = 0; u < kMaxSsqPerThread; ++u)
             if ((int)threadIdx.x + u * nt < e.ssq_n) t += in_raw.ssq[u];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+        for (int o = 32; o >= 1; o >>= 1) t += shfl_xor_u(t, o);
         if (lane == 0) sh.ssq[wave] = t;
     }
     __syncthreads();
