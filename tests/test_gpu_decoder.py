@@ -239,9 +239,19 @@ def test_decoder_from_empty_cache(cuda):
     small(num_heads=6, num_kv_heads=2, head_dim=64, hidden=384, num_layers=1),  # G = 3
     small(num_heads=16, num_kv_heads=2, head_dim=128, hidden=2048, num_layers=1),  # G = 8
     small(num_heads=16, num_kv_heads=1, head_dim=64, hidden=1024, num_layers=1),   # G = 16
+    small(num_heads=16, num_kv_heads=16, head_dim=64, hidden=1024, num_layers=1),  # 16 KV heads
+    small(num_heads=24, num_kv_heads=12, head_dim=64, hidden=1536, num_layers=1),  # 12 KV heads
 ])
 def test_decoder_head_layouts(cuda, cfg):
+    """Head layouts, including more KV heads than XCDs (12 and 16)."""
     run_parity(cfg, 7, prefill=130, steps=6, max_seq=200)
+
+
+def test_decoder_long_cache_folded_tiles(cuda):
+    """9000 positions: 128 attention blocks per KV head, each folding two
+    tiles, then the in-kernel merge of the 128 partials."""
+    run_parity(small(num_heads=14, num_kv_heads=2, head_dim=64, hidden=896, intermediate=1024,
+                     num_layers=1), 8, prefill=9000, steps=6, max_seq=9100)
 
 
 def test_decoder_cache_boundaries(cuda):
