@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="batched prefill timed on the llama4 decoder (0: skip)")
     ap.add_argument("--batched", default="16x4096,16x14336,64x4096,64x14336",
-                    help="config 3 MxN projections (K=4096) on FP32 MFMA, or 'none'")
+                    help="config 3 MxN projections (K=4096), or 'none'")
     ap.add_argument("--mlp-batches", default="4,8",
                     help="config 2 batch sizes M > 1 for the fused MLP, or 'none'")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -313,17 +313,22 @@ def int4_set(torch, dev, gen, n, k, gs=32):
 
 
 def batched_kernel(M, N, K):
-    """The kernel tb_w4a32_grouped_linear runs for an M x N x K v1 projection
-    (the selection in csrc/capi.hip linear_w4): M = 3..16 takes the f16-MFMA
-    limb kernel (exact f32 products from f16 limbs of x), except M = 16 with N
-    and K at most 4096, which stays on FP32 MFMA like every M > 16."""
+    """The kernel tb_w4a32_grouped_linear runs for an M x N x K v1 g32
+    projection (the selection in csrc/capi.hip linear_w4 and csrc/w4_mfma.hip
+    w4_mfma): M = 3..16 takes the small-batch f16-MFMA limb kernel (exact
+    products from f16 limbs of x), except M = 16 with N and K at most 4096,
+    which stays on FP32 MFMA; from M = 17 (K a multiple of 128) the batched
+    limb GEMM.  Every entry's frac_fp32_mfma_peak is its f32-contraction rate
+    over the FP32-MFMA peak; the limb kernels get there on f16 MFMA."""
     if 3 <= M <= 16 and not (M == 16 and N <= 4096 and K <= 4096):
         return "k_limb_prep + k_w4_limb (f16 MFMA on exact limbs of x) + k_limb_reduce"
+    if M >= 17 and K % 128 == 0:
+        return "k_lgemm_prep + k_w4_lgemm (f16 MFMA on exact limbs of x, 16-row slabs) + k_mfma_reduce"
     return "k_w4_mfma (FP32 MFMA) + k_mfma_reduce"
 
 
 def batched_section(torch, args, dev):
-    """Config 3: Y[M, N] = X[M, 4096] . deq(W)^T on FP32 MFMA, M in {16, 64}."""
+    """Config 3: Y[M, N] = X[M, 4096] . deq(W)^T, M in {16, 64}."""
     from torchburn_amd import _lib
     K, GS = 4096, 32
     gen = torch.Generator(device=dev)
@@ -578,7 +583,9 @@ def prefill_run(dec, cfg, n):
     fl = synth.prefill_flops(cfg, n)
     return {"tokens": n, "ms": round(sec * 1e3, 3), "tok_s": round(n / sec, 1),
             "tflops": round(fl / sec / 1e12, 2), "flops": fl,
-            "mfma_fp32_frac": round(fl / sec / 1e12 / MFMA_F32_PEAK, 4)}
+            "mfma_fp32_frac": round(fl / sec / 1e12 / MFMA_F32_PEAK, 4),
+            "kernel": "k_w4_lgemm (f16 MFMA on exact limbs of x) for the projections; "
+                      "mfma_fp32_frac is the f32-contraction rate over the FP32-MFMA peak"}
 
 
 def main():

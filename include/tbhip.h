@@ -236,12 +236,12 @@ TB_API int tb_fused_swiglu_mlp_w4a32(const float *x, const uint8_t *gate_w, cons
  * tb_fused_swiglu_mlp_w4a32 without any allocation, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * intermediates (h, the x / h chunk records or the MFMA split-K partials) live
- * in a 16 MiB static device array, one per GPU, instead of the per-stream
- * workspace: shapes needing more return TB_ERR_UNSUPPORTED with the byte count
- * before any GPU work (the Llama-3-8B MLP fits at M = 1..58 and 65..97; M =
- * 59..64 and M >= 98 are refused: the FP32-MFMA split-K partials grow with
- * the row tiles).  Every call on one GPU shares that array, so calls that overlap on
+ * intermediates (h, the x / h records, the split-K partials) live in a 16 MiB
+ * static device array, one per GPU, instead of the per-stream workspace:
+ * shapes needing more return TB_ERR_UNSUPPORTED with the byte count before any
+ * GPU work (the Llama-3-8B MLP fits at M = 1..54 and 65..88; M = 55..64 and
+ * M >= 89 are refused: the split-K partials and the records of the batched
+ * projection grow with the row tiles).  Every call on one GPU shares that array, so calls that overlap on
  * one GPU (two streams, or two threads) race; nothing in it needs clearing
  * between calls.  Same arguments and results as tb_fused_swiglu_mlp_w4a32.
  */

@@ -102,8 +102,8 @@ def test_product_path_never_touches_the_oracle():
 
 def test_noalloc_scratch_limit_before_any_gpu_call():
     """tb_fused_swiglu_mlp_w4a32_noalloc checks the 16 MiB static scratch before
-    any GPU work: the Llama-3-8B MLP (K 4096, I 14336) fits at M = 1..58 and
-    65..97 and is refused with the byte count at M = 59..64 and from 98.  The
+    any GPU work: the Llama-3-8B MLP (K 4096, I 14336) fits at M = 1..54 and
+    65..88 and is refused with the byte count at M = 55..64 and from 89.  The
     pointers are placeholders: a shape that fits goes on to the device (none
     here) and fails with a HIP error, a refused one never gets there."""
     L = _lib.lib()
@@ -115,8 +115,8 @@ def test_noalloc_scratch_limit_before_any_gpu_call():
                                                    C.c_int64(14336), C.c_int64(4096),
                                                    C.c_int64(32), None)
 
-    for m in (1, 8, 12, 16, 58, 65, 97):
+    for m in (1, 8, 12, 16, 54, 65, 88):
         assert call(m) != _lib.TB_ERR_UNSUPPORTED, m
-    for m in (59, 64, 98, 128):
+    for m in (55, 64, 89, 128):
         assert call(m) == _lib.TB_ERR_UNSUPPORTED, m
         assert b"static scratch holds 16777216" in L.tb_last_error()

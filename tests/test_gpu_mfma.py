@@ -155,8 +155,11 @@ def test_mfma_special_cases(cuda):
         np.testing.assert_allclose(y, np.broadcast_to(want, (m, n)), rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("m", [16, 6])
+@pytest.mark.parametrize("m", [16, 6, 40, 70])
 def test_mfma_non_finite_propagate(cuda, m):
+    """NaN / Inf in one 16-row slab take the f32 path for that slab's batch
+    (M = 40: the third slab of a block; M = 70: the fifth slab, a second block
+    along M); the other slabs stay on the limbs."""
     g = synth.rng(34, m)
     n, k = 128, 1024
     w, s = synth.int4_weight(g, n, k, 32)

@@ -358,21 +358,8 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
     // weight MFMAs; the batch's partial sum takes the batch exponent once.
     auto compute = [&](int k0, const u32x4 (&wv)[R], const f32x4 (&st)[R]) {
         const uint8_t *rg = lrec + (size_t)((k0 - ks) / kBatch) * BS;
-        h8 A[4][T];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int u = 0; u < T; ++u)
-                A[t][u] = *reinterpret_cast<const h8 *>(rg + (t * T + u) * kTile + lane * 16);
         // exponent bytes of A-rows 4 q .. 4 q + 3, both halves
         const uint2 pw = *reinterpret_cast<const uint2 *>(rg + 4 * T * kTile + 8 * q);
-        f32x4 off[4][T];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int u = 0; u < T; ++u)
-                off[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    A[t][u], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         float pf[2][4];   // 2^(24 - e) of the lane's four A-rows, per half
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -381,22 +368,38 @@ void k_w4_limb(LimbParams p, float *__restrict__ part, int ksl, int ntot) {
                 pf[h][r] = __builtin_bit_cast(
                     float, __builtin_amdgcn_ubfe(r < 2 ? pw.x : pw.y, 16 * (r & 1) + 8 * h, 8)
                                << 23);
+        // one half batch (groups 2 h, 2 h + 1) at a time: half the A tiles and
+        // offsets live at once
 #pragma unroll
-        for (int rb = 0; rb < R; ++rb) {
-            f32x4 D[4];
+        for (int h = 0; h < 2; ++h) {
+            h8 A[2][T];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const h8 B = expand_nibbles(wv[rb][t]);
-                D[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][0], B, off[t][0], 0, 0, 0);
-                if (T == 2)
-                    D[t] += __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][T - 1], B, off[t][T - 1],
-                                                                   0, 0, 0);
-            }
+            for (int g = 0; g < 2; ++g)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                f32x4 bs = D[2 * h] * st[rb][2 * h];
+                for (int u = 0; u < T; ++u)
+                    A[g][u] =
+                        *reinterpret_cast<const h8 *>(rg + ((2 * h + g) * T + u) * kTile + lane * 16);
+            f32x4 off[2][T];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[2 * h + 1][r], st[rb][2 * h + 1], bs[r]);
+            for (int g = 0; g < 2; ++g)
+#pragma unroll
+                for (int u = 0; u < T; ++u)
+                    off[g][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        A[g][u], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                f32x4 D[2];
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const h8 B = expand_nibbles(wv[rb][2 * h + g]);
+                    D[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[g][0], B, off[g][0], 0, 0, 0);
+                    if (T == 2)
+                        D[g] += __builtin_amdgcn_mfma_f32_16x16x32_f16(A[g][T - 1], B,
+                                                                       off[g][T - 1], 0, 0, 0);
+                }
+                f32x4 bs = D[0] * st[rb][2 * h];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[1][r], st[rb][2 * h + 1], bs[r]);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[rb][r] = fmaf(bs[r], pf[h][r], acc[rb][r]);
             }
@@ -736,7 +739,212 @@ __global__ __launch_bounds__(256) void k_limb_prep(const float *__restrict__ x,
     limb_prep_body<T>(x, rec, m, k, batches);
 }
 
+
+// ---------------------------------------------------------------------------
+// Batched projection for M >= 17 on the same exact limbs: the tiling of the
+// FP32-MFMA kernel (w4_mfma.hip) with its f32 operands replaced.  A block (4
+// waves) owns 64 weight rows (16 per wave) x MT 16-row slabs of activation
+// rows x a K range (split-K; the partials go to k_mfma_reduce in the FP32
+// kernel's layout, so the epilogues are shared).  Per 128-element batch:
+//   * the MT slab records of the batch (limb_prep's two-tile format, built
+//     per 16-row slab by lgemm_prep) are staged in LDS through registers,
+//     loaded one batch ahead, and read by all four waves;
+//   * each lane loads one 16-byte chunk of its weight row (group q of the
+//     batch) and its scale; a 4x4 transpose across the lane quarters leaves
+//     dword q of group t in register t, expanded to the f16 B operand;
+//   * per slab and group: two offset MFMAs (the -8 of every weight, against
+//     the limbs) and two weight MFMAs (one per limb), each exact; the group's
+//     result takes the row's group scale, and each half batch its 2^(24 - e);
+//   * a slab whose half batch is flagged (NaN / Inf, or out of range) takes
+//     the f32 path on the raw activations for that batch.
+// The f16 matrix cores run 16x the FP32 rate, and two limbs plus the offset
+// MFMAs cost 4 instructions per group and slab against 8 of
+// v_mfma_f32_16x16x4_f32 at a quarter of the K each.
+template <int MT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_w4_lgemm(LGemmArgs a) {
+    constexpr int BS = rec_stride(2);             // 8224 bytes per slab and batch
+    constexpr int ACH = 4 * 2 * kTile / 16;       // 16-byte chunks of a slab's A tiles (512)
+    constexpr int AV = MT * ACH / 256;            // A chunks per thread per batch
+    static_assert(MT * ACH % 256 == 0, "whole chunks per thread");
+    __shared__ __align__(16) uint8_t lr[MT * BS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 15, q = lane >> 4;
+    int bx = blockIdx.x;
+    const int second = bx >= a.nbx ? 1 : 0;   // dual launch: blocks of the up projection
+    bx -= second * a.nbx;
+    const uint8_t *w = second ? a.w1 : a.w0;
+    const float *s = second ? a.s1 : a.s0;
+    const int sb = blockIdx.z * MT;                   // first slab of the block
+    const int ms = min(MT, a.nslabs - sb);            // slabs that exist
+    const int kb = blockIdx.y * a.klen;
+    const int ke = min(a.k, kb + a.klen);
+    const int row = bx * 64 + wave * 16 + i;
+    const bool rok = row < a.n;
+    const uint8_t *wrow = w + (size_t)(rok ? row : 0) * (size_t)(a.k >> 1);
+    const float *srow = s + (size_t)(rok ? row : 0) * (size_t)a.scols;
+    const size_t slab_bytes = (size_t)a.batches * BS;
+
+    u32x4 ar[AV];   // the next batch's record chunks
+    u32x4 tr;       // its exponent tail chunk (threads < 2 MT)
+    u32x4 wr;
+    float sr;
+    auto load_step = [&](int k0) {
+        const int bt = k0 / kBatch;
+#pragma unroll
+        for (int v = 0; v < AV; ++v) {
+            const int f = tid + 256 * v, mt = f / ACH, c = f - mt * ACH;
+            ar[v] = mt < ms ? *reinterpret_cast<const u32x4 *>(a.rec + (size_t)(sb + mt) * slab_bytes +
+                                                               (size_t)bt * BS + 16 * c)
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+        {
+            const int mt = tid >> 1;
+            tr = (tid < 2 * MT && mt < ms)
+                     ? *reinterpret_cast<const u32x4 *>(a.rec + (size_t)(sb + mt) * slab_bytes +
+                                                        (size_t)bt * BS + 8 * kTile + 16 * (tid & 1))
+                     : u32x4{0u, 0u, 0u, 0u};
+        }
+        const int kk = k0 + 32 * q;
+        wr = rok ? load_nt16(wrow + (kk >> 1)) : u32x4{0u, 0u, 0u, 0u};
+        sr = rok ? srow[kk >> a.gshift] : 0.f;
+    };
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const h8 boff = offset_operand();
+
+    load_step(kb);
+    for (int k0 = kb; k0 < ke; k0 += kBatch) {
+        __syncthreads();   // the previous batch's readers are done with lr
+#pragma unroll
+        for (int v = 0; v < AV; ++v) {
+            const int f = tid + 256 * v, mt = f / ACH, c = f - mt * ACH;
+            *reinterpret_cast<u32x4 *>(lr + mt * BS + 16 * c) = ar[v];
+        }
+        if (tid < 2 * MT) *reinterpret_cast<u32x4 *>(lr + (tid >> 1) * BS + 8 * kTile + 16 * (tid & 1)) = tr;
+        u32x4 cw = wr;
+        const float sc = sr;
+        __syncthreads();
+        if (k0 + kBatch < ke) load_step(k0 + kBatch);
+        transpose4(cw);
+        float st[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) st[t] = __shfl(sc, i + 16 * t);
+        h8 B[4];
+        B[0] = expand_nibbles(cw.x);
+        B[1] = expand_nibbles(cw.y);
+        B[2] = expand_nibbles(cw.z);
+        B[3] = expand_nibbles(cw.w);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if (mt >= ms) break;
+            const uint8_t *rg = lr + mt * BS;
+            if (flagged(rg + 8 * kTile)) {
+                // f32 path: tokens of the slab's rows, raw activations
+                const int tok = (sb + mt) * 16 + i;
+                const bool live = tok < a.m;
+                const float *xrow = a.x + (size_t)(live ? tok : 0) * a.k;
+                const uint32_t dw[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float *xp = xrow + k0 + 32 * t + 8 * q;
+                    const float4 a0 = *reinterpret_cast<const float4 *>(xp);
+                    const float4 a1 = *reinterpret_cast<const float4 *>(xp + 4);
+                    const float xv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        D = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            live ? xv[e] : 0.f, (float)((dw[t] >> (4 * e)) & 15u) - 8.0f, D, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(D[r], st[t], acc[mt][r]);
+                }
+                continue;
+            }
+            const uint2 pw = *reinterpret_cast<const uint2 *>(rg + 8 * kTile + 8 * q);
+            // one half batch (groups 2 h, 2 h + 1) at a time
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                h8 A[2][2];
+#pragma unroll
+                for (int g = 0; g < 2; ++g)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+                        A[g][u] = *reinterpret_cast<const h8 *>(rg + ((2 * h + g) * 2 + u) * kTile +
+                                                                lane * 16);
+                f32x4 D[2];
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const f32x4 o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        A[g][0], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const f32x4 o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        A[g][1], boff, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    D[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[g][0], B[2 * h + g], o0, 0, 0, 0);
+                    D[g] += __builtin_amdgcn_mfma_f32_16x16x32_f16(A[g][1], B[2 * h + g], o1, 0, 0, 0);
+                }
+                f32x4 bs = D[0] * st[2 * h];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bs[r] = fmaf(D[1][r], st[2 * h + 1], bs[r]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pf = __builtin_bit_cast(
+                        float, __builtin_amdgcn_ubfe(r < 2 ? pw.x : pw.y, 16 * (r & 1) + 8 * h, 8) << 23);
+                    acc[mt][r] = fmaf(bs[r], pf, acc[mt][r]);
+                }
+            }
+        }
+    }
+
+    const int col = bx * 64 + wave * 16 + i;
+    if (col >= a.n) return;
+    float *pb = a.part + (size_t)(second * a.splits + blockIdx.y) * (size_t)a.m * a.n;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mr = (sb + mt) * 16 + 4 * q + r;
+            if (mr < a.m) pb[(size_t)mr * a.n + col] = acc[mt][r];
+        }
+    }
+}
+
+// Records of x [m, k] as 16-row slabs in the two-tile format: slab s at
+// rec + s * (k / 128) * rec_stride(2).
+__global__ __launch_bounds__(256) void k_lgemm_prep(const float *__restrict__ x,
+                                                    uint8_t *__restrict__ rec, int m, int k,
+                                                    int batches) {
+    const int sl = blockIdx.y;
+    limb_prep_body<2>(x + (size_t)sl * 16 * k, rec + (size_t)sl * batches * rec_stride(2),
+                      min(16, m - 16 * sl), k, batches);
+}
+
 }  // namespace
+
+size_t lgemm_records_bytes(int m, int k) {
+    return (size_t)((m + 15) / 16) * (size_t)(k / kBatch) * (size_t)rec_stride(2);
+}
+
+int lgemm_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st) {
+    TB_REQUIRE(m >= 1 && k % kBatch == 0, TB_ERR_UNSUPPORTED,
+               "TB_UNSUPPORTED: slab records need K % 128 == 0");
+    const int batches = k / kBatch;
+    const dim3 grid((unsigned)((2 * batches + 3) / 4), (unsigned)((m + 15) / 16));
+    hipLaunchKernelGGL(k_lgemm_prep, grid, dim3(256), 0, st, x, rec, m, k, batches);
+    TB_LAUNCHED();
+    return TB_OK;
+}
+
+int lgemm_launch(const LGemmArgs &a, int mt, dim3 grid, hipStream_t st) {
+    switch (mt) {
+        case 1: hipLaunchKernelGGL(k_w4_lgemm<1>, grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(k_w4_lgemm<2>, grid, dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL(k_w4_lgemm<3>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(k_w4_lgemm<4>, grid, dim3(256), 0, st, a); break;
+    }
+    TB_LAUNCHED();
+    return TB_OK;
+}
 
 size_t limb_records_bytes(int m, int k) {
     return (size_t)(k / kBatch) * (size_t)rec_stride(tiles_of(m));

@@ -45,4 +45,24 @@ bool limb_shape_ok(int64_t m, int64_t n, int64_t k, bool pair);
 // part: device scratch of limb_partials_bytes().
 int w4_limb(const LimbParams &p, float *part, hipStream_t st);
 
+// Batched projection for larger M on the exact limbs (k_w4_lgemm): the FP32-MFMA
+// kernel's tiling and split-K partial layout (w4_mfma.hip reduces them).
+struct LGemmArgs {
+    const float *x;         // [m, k] raw activations (the f32 path of flagged batches)
+    const uint8_t *rec;     // lgemm_prep records: ceil(m / 16) slabs
+    const uint8_t *w0;      // [n, k/2] nibbles (gate when dual)
+    const float *s0;
+    const uint8_t *w1;      // up projection of a SwiGLU pair, or null
+    const float *s1;
+    float *part;            // [dual + 1][splits][m][n] partials
+    int m, n, k;
+    int scols, gshift;      // scale of (row, kk) at s[row * scols + (kk >> gshift)]
+    int klen, nbx, splits;  // K per split (a multiple of 128), 64-row blocks per matrix
+    int batches, nslabs;    // k / 128, ceil(m / 16)
+};
+size_t lgemm_records_bytes(int m, int k);
+int lgemm_prep(const float *x, uint8_t *rec, int m, int k, hipStream_t st);
+// grid: (nbx * (dual + 1), splits, ceil(nslabs / mt)); mt slabs per block (1..4).
+int lgemm_launch(const LGemmArgs &a, int mt, dim3 grid, hipStream_t st);
+
 }  // namespace tb

@@ -41,6 +41,7 @@
 #include "gemv_common.hpp"
 #include "tb_common.hpp"
 #include "w4_gemv.hpp"
+#include "w4_limb.hpp"
 #include "w4_mfma.hpp"
 
 namespace tb {
@@ -236,11 +237,29 @@ Plan plan(int m, int n, int k, bool dual) {
     return pl;
 }
 
+// From 17 rows the projection runs on the exact f16 limbs of x (k_w4_lgemm,
+// w4_limb.hip) when K is whole 128-element batches and a 32-element group has
+// one scale (16-row projections measured 14.7 against 14.4 us on FP32 MFMA);
+// TB_MFMA_LIMB=0 keeps the FP32-MFMA kernel (measurement only).
+bool use_limbs(int m, int k, bool v2, int scale_mode, int gshift) {
+    static const bool on = [] {
+        const char *e = getenv("TB_MFMA_LIMB");
+        return !(e && e[0] == '0');
+    }();
+    return on && m >= 17 && !v2 && k % kBK == 0 && (scale_mode != 0 || gshift >= 5);
+}
+
+size_t partials_only(int m, int n, int k, bool dual) {
+    const Plan pl = plan(m, n, k, dual);
+    return (size_t)(dual ? 2 : 1) * pl.splits * (size_t)m * n * sizeof(float);
+}
+
 }  // namespace
 
 size_t w4_mfma_partials_bytes(int m, int n, int k, bool dual) {
-    const Plan pl = plan(m, n, k, dual);
-    return (size_t)(dual ? 2 : 1) * pl.splits * (size_t)m * n * sizeof(float);
+    // partials, then (256-byte aligned) room for the limb records of x
+    const size_t pb = (partials_only(m, n, k, dual) + 255) & ~(size_t)255;
+    return pb + (m >= 17 && k % kBK == 0 ? lgemm_records_bytes(m, k) : 0);
 }
 
 int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
@@ -258,6 +277,22 @@ int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
     dim3 grid(pl.nbx * (dual ? 2 : 1), pl.splits, pl.mz);
     const int scols = p.scale_mode == 0 ? p.k >> p.gshift : (p.scale_mode == 1 ? 1 : 0);
     const int gsh = p.scale_mode == 0 ? p.gshift : 31;
+    if (use_limbs(p.m, p.k, p.v2, p.scale_mode, p.gshift)) {
+        LGemmArgs a;
+        a.x = p.x;
+        a.rec = reinterpret_cast<uint8_t *>(part) +
+                ((partials_only(p.m, p.n, p.k, dual) + 255) & ~(size_t)255);
+        a.w0 = p.w0; a.s0 = p.s0; a.w1 = p.w1; a.s1 = p.s1;
+        a.part = part;
+        a.m = p.m; a.n = p.n; a.k = p.k;
+        a.scols = scols; a.gshift = gsh;
+        a.klen = pl.klen; a.nbx = pl.nbx; a.splits = pl.splits;
+        a.batches = p.k / kBK;
+        a.nslabs = (p.m + 15) / 16;
+        int rc = lgemm_prep(p.x, const_cast<uint8_t *>(a.rec), p.m, p.k, st);
+        if (rc) return rc;
+        if ((rc = lgemm_launch(a, pl.mt, grid, st))) return rc;
+    } else {
 #define TB_MFMA_LAUNCH(MT)                                                                   \
     if (p.v2)                                                                                \
         hipLaunchKernelGGL((k_w4_mfma<MT, true>), grid, dim3(256), 0, st, p.x, p.w0, p.s0,   \
@@ -275,6 +310,7 @@ int w4_mfma(const MfmaParams &p, int epi, float *part, hipStream_t st) {
     }
 #undef TB_MFMA_LAUNCH
     TB_LAUNCHED();
+    }
     const size_t total = (size_t)p.m * p.n;
     size_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
