@@ -596,7 +596,8 @@ struct Decoder {
             (rc = alloc(&pf_q, (size_t)R * hq * hd * 4)) ||
             (rc = alloc(&pf_a, (size_t)R * hq * hd * 4)) || (rc = alloc(&pf_h, (size_t)R * I * 4)) ||
             (rc = alloc(&pf_part, part)) || (rc = alloc(&pf_tok, (size_t)R * 4)) ||
-            (lb && (rc = alloc(&pf_limb, lb))))
+            (lb && (rc = alloc(&pf_limb, lb))) ||
+            (lb && (rc = alloc(&pf_hrec, limb_records_bytes(kLimbMaxM, I)))))
             return rc;
         pf_limb_bytes = lb;
         return TB_OK;
@@ -604,24 +605,49 @@ struct Decoder {
 
     // The small-batch projection (records of x, then w4_limb) when it takes
     // the shape and the buffer holds its scratch; false: use the GEMM.
+    // rec_out (a SwiGLU pair): the pair also writes the records of h there;
+    // rec_in: records of xin already built (by such a pair), no record pass.
     uint8_t *pf_limb = nullptr;
+    uint8_t *pf_hrec = nullptr;   // records of h, [kLimbMaxM, I]
     size_t pf_limb_bytes = 0;
     bool limb_gemm(const float *xin, const void *w, const float *s, const float *b,
                    const void *w2, const float *s2, const float *res, float *y, int m, int n,
-                   int k, int &rc) {
+                   int k, int &rc, uint8_t *rec_out = nullptr, const uint8_t *rec_in = nullptr) {
         const bool pair = w2 != nullptr;
         if (!pf_limb || m < 3 || m > kLimbMaxM || !limb_shape_ok(m, n, k, pair)) return false;
         const size_t rb = up256(limb_records_bytes(m, k));
         if (rb + limb_partials_bytes(m, n, k, pair) > pf_limb_bytes) return false;
         LimbParams p{};
-        p.x = xin; p.rec = pf_limb;
+        p.x = xin; p.rec = rec_in ? rec_in : pf_limb;
         p.w0 = static_cast<const uint8_t *>(w); p.s0 = s; p.b0 = b;
         p.w1 = static_cast<const uint8_t *>(w2); p.s1 = s2;
         p.res = res; p.y = y; p.m = m; p.n = n; p.k = k;
         p.scols = k / gs; p.gshift = gshift(gs);
-        if ((rc = limb_prep(xin, pf_limb, m, k, st))) return true;
+        p.rec_out = pair ? rec_out : nullptr;
+        if (!rec_in && (rc = limb_prep(xin, pf_limb, m, k, st))) return true;
         rc = w4_limb(p, reinterpret_cast<float *>(pf_limb + rb), st);
         return true;
+    }
+
+    // The SwiGLU pair then the down projection (+ residual): on the
+    // small-batch path the pair writes h's records and the down projection
+    // reads them (no record pass for h).
+    int mlp_rows(const Layer &y, int M) {
+        int rc = TB_OK;
+        if (pf_hrec && limb_gemm(pf_xn, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr,
+                                 pf_h, M, I, H, rc, pf_hrec)) {
+            if (rc) return rc;
+            if (limb_gemm(pf_h, y.down_w, y.down_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H,
+                          I, rc, nullptr, pf_hrec))
+                return rc;
+            return gemm(pf_h, y.down_w, y.down_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H, I,
+                        EPI_RESID);
+        }
+        if ((rc = gemm(pf_xn, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, pf_h, M, I,
+                       H, EPI_SWIGLU)))
+            return rc;
+        return gemm(pf_h, y.down_w, y.down_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H, I,
+                    EPI_RESID);
     }
 
     int gemm(const float *xin, const void *w, const float *s, const float *b, const void *w2,
@@ -721,10 +747,7 @@ struct Decoder {
                     (rc = gemm(pf_a, y.o_w, y.o_s, nullptr, nullptr, nullptr, pf_x, pf_x, M, H,
                                hq * hd, EPI_RESID)) ||
                     (rc = launch_rmsnorm_rows(pf_x, y.post_norm, pf_xn, M, H, eps, st)) ||
-                    (rc = gemm(pf_xn, y.gate_w, y.gate_s, nullptr, y.up_w, y.up_s, nullptr, pf_h,
-                               M, I, H, EPI_SWIGLU)) ||
-                    (rc = gemm(pf_h, y.down_w, y.down_s, nullptr, nullptr, nullptr, pf_x, pf_x, M,
-                               H, I, EPI_RESID)))
+                    (rc = mlp_rows(y, M)))
                     return rc;
             }
             if (rows_out) {
