@@ -38,6 +38,8 @@ def T(a, dev):
     (1, 77, 1001, False),       # odd K: any-shape GEMV
     (2, 50, 31, True),          # K below one chunk
     (1, 256, 20480, False),     # K past one GEMV pass
+    (24, 512, 4096, False),     # limb GEMM (M >= 17), one scale per row
+    (40, 300, 1024, True),      # limb GEMM, one per-tensor scale, ragged N
 ])
 def test_w4a32_linear_per_channel(cuda, m, n, k, scalar):
     print(f"case w4a32_linear m={m} n={n} k={k} scalar={scalar}", flush=True)
@@ -87,6 +89,8 @@ def test_quantize_weight_int4_non_finite(cuda):
     (1, 128, 28672, 32),    # K past one GEMV pass (Llama-70B intermediate)
     (1, 64, 1001, 32),      # odd K, short last group
     (5, 96, 100, 20),       # 5 rows, odd shape: any-shape GEMV
+    (40, 256, 4096, 128),   # group 128 on the limb GEMM (M >= 17)
+    (18, 130, 384, 64),     # group 64, two slabs (one of 2 rows), ragged N
 ])
 def test_w4_grouped_general_shapes(cuda, m, n, k, gs):
     print(f"case w4a32_grouped_linear m={m} n={n} k={k} gs={gs}", flush=True)
