@@ -67,6 +67,50 @@ def test_mfma_linear_matches_oracle(cuda, m, n, k, gs):
     assert err < TOL
 
 
+# Up to 16 rows in shapes the small-batch limb path does not take (K % 128 != 0,
+# or M = 16 with N, K <= 4096): the FP32-MFMA split-K projection, with and
+# without the residual epilogue.
+SMALL_M_SHAPES = [
+    # (m, n, k, gs)
+    (11, 300, 4064, 32),      # ragged N, K % 128 != 0
+    (16, 4096, 1056, 32),     # 8.25 steps: the last K split ends inside a step
+    (13, 77, 2112, 64),       # group 64
+    (5, 2000, 160, 32),       # 2 steps
+    (16, 4160, 4000, 32),     # N past 4096 with K % 128 != 0
+    (16, 33, 4096, 128),      # group 128, one row block
+]
+
+
+@pytest.mark.parametrize("m,n,k,gs", SMALL_M_SHAPES)
+def test_mfma_small_m_matches_oracle(cuda, m, n, k, gs):
+    print(f"case mfma small-M m={m} n={n} k={k} gs={gs}", flush=True)
+    g = synth.rng(35, m, n, k, gs)
+    x = synth.activations(g, m, k)
+    w, s = synth.int4_weight(g, n, k, gs)
+    bias = g.normal(0, 0.1, n).astype(np.float32)
+    r = synth.activations(g, m, n)
+    ref = O.gemm_w4(x, w, s, bias, group_size=gs)
+    y = tb.w4a32_grouped_linear(T(x, cuda), T(w, cuda), T(s, cuda), T(bias, cuda), group_size=gs)
+    yr = tb.w4a32_grouped_linear_residual(T(x, cuda), T(w, cuda), T(s, cuda), T(r, cuda),
+                                          T(bias, cuda), group_size=gs)
+    torch.cuda.synchronize()
+    err = rel(y.cpu().numpy(), ref)
+    print(f"max rel err {err:.3g}", flush=True)
+    assert err < TOL
+    assert rel(yr.cpu().numpy(), ref + r) < TOL
+
+
+def test_mfma_split_k_deterministic(cuda):
+    """The K splits are summed in split order: repeated calls agree bit for bit."""
+    g = synth.rng(36)
+    m, n, k = 16, 4096, 4096
+    x = T(synth.activations(g, m, k), cuda)
+    w, s = synth.int4_weight(g, n, k, 32)
+    w, s = T(w, cuda), T(s, cuda)
+    ys = [tb.w4a32_grouped_linear(x, w, s, None, group_size=32).cpu().numpy() for _ in range(3)]
+    assert np.array_equal(ys[0], ys[1]) and np.array_equal(ys[0], ys[2])
+
+
 @pytest.mark.parametrize("m", [16, 64])
 def test_mfma_residual_matches_oracle(cuda, m):
     print(f"case mfma residual m={m}", flush=True)
@@ -83,7 +127,9 @@ def test_mfma_residual_matches_oracle(cuda, m):
 
 
 @pytest.mark.parametrize("m,k,inter,gs", [(16, 4096, 14336, 32), (64, 4096, 14336, 32),
-                                          (24, 896, 4864, 32), (16, 512, 1024, 64)])
+                                          (24, 896, 4864, 32), (16, 512, 1024, 64),
+                                          (12, 1056, 1120, 32),   # K % 128 != 0: FP32 MFMA
+                                          (16, 2112, 3136, 64)])
 def test_mfma_swiglu_mlp_matches_oracle(cuda, m, k, inter, gs):
     print(f"case mfma fused_swiglu_mlp m={m} k={k} inter={inter} gs={gs}", flush=True)
     g = synth.rng(33, m, k, inter)

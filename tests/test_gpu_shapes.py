@@ -40,6 +40,8 @@ def T(a, dev):
     (1, 256, 20480, False),     # K past one GEMV pass
     (24, 512, 4096, False),     # limb GEMM (M >= 17), one scale per row
     (40, 300, 1024, True),      # limb GEMM, one per-tensor scale, ragged N
+    (16, 1000, 4064, False),    # FP32-MFMA projection (K % 128 != 0), one scale per row
+    (9, 300, 2080, True),       # FP32-MFMA projection (K % 128 != 0), one per-tensor scale
 ])
 def test_w4a32_linear_per_channel(cuda, m, n, k, scalar):
     print(f"case w4a32_linear m={m} n={n} k={k} scalar={scalar}", flush=True)
