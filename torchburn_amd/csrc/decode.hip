@@ -757,174 +757,289 @@ __global__ void k_rope_rows(const float *__restrict__ qkv, int nq, float *__rest
 }
 
 // Causal GQA attention of M consecutive query positions start .. start+M-1
-// over the cache (query at position p sees keys 0..p; decoder.rs:1148-1213).
+// over the cache (query at position p sees keys 0..p; decoder.rs:1148-1213),
+// on FP32 MFMA (v_mfma_f32_16x16x4f32).  out [M][hq * HD].
 //
-// A block owns one KV head and a tile of QT = 16 * RPT query rows, where the
-// rows of a KV head are its (position m, head g of the group) pairs, i = m * G
-// + g: every query head that shares the KV head reads each K / V tile from
-// the same LDS copy, and a short verify chunk (M * G rows) fills one small
-// tile instead of padding a position tile per head.  K and V tiles of KT = 16
-// * KPT positions are staged in LDS (zero past the last position the tile
-// needs); thread (rg, kg) scores rows RPT * rg + r against keys kg + 16 j and
-// owns output columns 64 c + 4 kg .. + 3 of its rows (consecutive lanes read
-// LDS rows HD + 4 floats apart, or consecutive float4s: no bank conflicts);
-// online softmax with a running max and sum per row, then 1 / max(sum,
-// 1e-30).  out [M][hq * HD].
+// A block owns one KV head and a tile of query rows, where the rows of a KV
+// head are its (position m, head g of the group) pairs, i = m * G + g: every
+// query head that shares the KV head reads each K / V tile from the same LDS
+// copy, and a short verify chunk (M * G rows) fills one small tile instead of
+// padding a position tile per head.  K and V tiles of KT positions are staged
+// in LDS (zero past the last position the tile needs); online softmax with a
+// running max and sum per row, then 1 / max(sum, 1e-30).
 //
 // Key-range split (blockIdx.z of nsplit, tps tiles each): with nsplit > 1 the
 // block writes its unnormalised o, running max and sum to part / pml and
 // k_prefill_merge combines the splits, so few query rows over a long cache
 // (verify_tokens, short chunks after a long prefix) still fill the chip.
-template <int HD, int RPT, int KPT>
-__global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ q,
-                                                      const float *__restrict__ kc,
-                                                      const float *__restrict__ vc,
-                                                      float *__restrict__ out, int start, int M,
-                                                      int hq, int hkv, int max_seq, float scale,
-                                                      int tps, float *__restrict__ part,
-                                                      float *__restrict__ pml) {
-    constexpr int QT = 16 * RPT, KT = 16 * KPT, HP = HD + 4, OC = HD / 16, C4 = HD / 4;
-    // unroll of the score and PV loops: none for the 64 x 64 tile (122 VGPRs;
-    // unrolled it grows past 150 or spills), by 4 for the small ones
-    constexpr int DU = RPT == 4 ? 1 : 4, JU = RPT == 4 ? 1 : 4;
-    __shared__ __attribute__((aligned(16))) float sq[QT][HP];
-    __shared__ __attribute__((aligned(16))) float sk[KT][HP];
-    __shared__ __attribute__((aligned(16))) float sv[KT][HD];
-    __shared__ float sp[QT][KT + 1];
+//
+// Query tiles of 64 / KG rows.  The four waves take the tile's 16-row blocks
+// and, with KG > 1 (few rows: verify_tokens, short chunks), KG groups of each
+// key tile's positions: wave w takes row block w % (4 / KG) and key group
+// w / (4 / KG), keeps its own online softmax over the key tiles of its split,
+// and the key groups' (o, m, l) meet in LDS at the end.  MFMA operands: lane
+// (g, c) = (lane / 16, lane % 16) supplies A[c][g] and B[g][c], and gets
+// D[4g + r][c] in register r; lane group g takes the contiguous quarter
+// g * (K / 4) .. of each contraction, so its operands are 16-byte LDS reads.
+// Per tile and wave:
+//   S (16 x KT / KG) = Q K^T: A = the wave's q rows (registers, from the
+//     start), B = its keys (LDS, every read issued before the MFMAs, the key
+//     blocks' chains interleaved);
+//   causal mask, scale and the online softmax in the MFMA result layout
+//     (lane (g, c) holds rows 4g..4g+3 at key c of every 16-key block): row
+//     max and sum by DPP butterflies over the 16 lanes of a row group, and
+//     each row's rescale of o lands in the lane's own registers;
+//   P goes through the wave's own LDS rows from the result to the A layout;
+//   O (16 x HD) += P V: A = P, B = its values (LDS, read ahead of the MFMAs,
+//     one chain per 16 output columns).
+// The next tile's K / V loads are in flight during the MFMAs.  A wave whose
+// rows are all padding only helps load the tiles.
+template <int HD, int KT, int KG>
+__global__ __launch_bounds__(256) void k_prefill_attn_mfma(const float *__restrict__ q,
+                                                           const float *__restrict__ kc,
+                                                           const float *__restrict__ vc,
+                                                           float *__restrict__ out, int start,
+                                                           int M, int hq, int hkv, int max_seq,
+                                                           float scale, int tps,
+                                                           float *__restrict__ part,
+                                                           float *__restrict__ pml) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    constexpr int RB = 4 / KG;             // row blocks of 16 per tile
+    constexpr int QT = 16 * RB, KW = KT / KG;   // query rows per tile, keys per wave per tile
+    constexpr int KP = HD + 4, NB = KW / 16, NS = HD / 4, OB = HD / 16, C4 = HD / 4;
+    constexpr int KS = KW / 4;   // keys per lane group in the P V contraction
+    static_assert(KW >= 16, "a wave takes whole 16-key blocks");
+    __shared__ __attribute__((aligned(16))) float sk[KT > QT ? KT : QT][KP];
+    __shared__ __attribute__((aligned(16))) float sv[KT][KP];
+    __shared__ __attribute__((aligned(16))) float sp[4][16][KW + 4];
     const int G = hq / hkv, NR = M * G;
     const int kvh = blockIdx.y, i0 = blockIdx.x * QT;
-    const int t = threadIdx.x, rg = t >> 4, kg = t & 15;   // rows RPT*rg.., keys KPT*kg..
-    for (int i = t; i < QT * C4; i += 256) {
-        const int r = i / C4, c4 = i - r * C4, ii = i0 + r;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (ii < NR) {
-            const int m = ii / G, h = kvh * G + (ii - m * G);
-            v = reinterpret_cast<const float4 *>(q + ((size_t)m * hq + h) * HD)[c4];
-        }
-        *reinterpret_cast<float4 *>(&sq[r][4 * c4]) = v;
-    }
-    float mrun[RPT], lrun[RPT], o[RPT][OC];
-    int pq[RPT];
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        mrun[r] = -INFINITY;
-        lrun[r] = 0.f;
-        pq[r] = start + (i0 + RPT * rg + r) / G;   // past `last` for padding rows: finite scores
-#pragma unroll
-        for (int c = 0; c < OC; ++c) o[r][c] = 0.f;
-    }
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 4, c = lane & 15;
+    const int rb = wave % RB, kg = wave / RB;   // row block, key group
+    const int w0 = i0 + 16 * rb;   // first row of this wave
+    const bool busy = w0 < NR;       // wave-uniform
     const int last = start + (min(i0 + QT, NR) - 1) / G;   // last position any row sees
     const int ntiles = last / KT + 1;
     const int kt0 = blockIdx.z * tps, kt1 = min(ntiles, kt0 + tps);
     const float *kb = kc + (size_t)kvh * max_seq * HD, *vb = vc + (size_t)kvh * max_seq * HD;
+    // A tile's K and V rows go global -> registers -> LDS; the next tile's
+    // loads are in flight while the current one is multiplied (rows past
+    // `last` read row `last` and are stored as zeros).
+    constexpr int NL = KT * C4 / 256;
+    float4 kv[NL], vv[NL];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = t + 256 * u, j = i / C4, c4 = i - j * C4;
+            const int p = min(kt * KT + j, last);
+            kv[u] = reinterpret_cast<const float4 *>(kb + (size_t)p * HD)[c4];
+        }
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = t + 256 * u, j = i / C4, c4 = i - j * C4;
+            const int p = min(kt * KT + j, last);
+            vv[u] = reinterpret_cast<const float4 *>(vb + (size_t)p * HD)[c4];
+        }
+    };
+    // the tile's q rows through LDS into the A-operand registers, loaded
+    // together with the first K / V tile
+    {
+        constexpr int NQ = QT * C4 / 256;
+        float4 v[NQ];
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            const int i = t + 256 * u, r = i / C4, c4 = i - r * C4, ii = i0 + r;
+            const int iq = ii < NR ? ii : 0;
+            const int m = iq / G, h = kvh * G + (iq - m * G);
+            v[u] = reinterpret_cast<const float4 *>(q + ((size_t)m * hq + h) * HD)[c4];
+            if (ii >= NR) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (kt0 < kt1) load_tile(kt0);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            const int i = t + 256 * u, r = i / C4, c4 = i - r * C4;
+            *reinterpret_cast<float4 *>(&sk[r][4 * c4]) = v[u];
+        }
+    }
+    __syncthreads();
+    float qa[NS];   // q[row w0 + c][g * NS + s]
+#pragma unroll
+    for (int s = 0; s < NS; s += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(&sk[16 * rb + c][g * NS + s]);
+        qa[s] = v.x; qa[s + 1] = v.y; qa[s + 2] = v.z; qa[s + 3] = v.w;
+    }
+    float mrun[4], lrun[4];
+    int pq[4];
+    f32x4_t o[OB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        mrun[r] = -INFINITY;
+        lrun[r] = 0.f;
+        pq[r] = start + (w0 + 4 * g + r) / G;   // past `last` for padding rows: finite scores
+    }
+#pragma unroll
+    for (int b = 0; b < OB; ++b) o[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     for (int kt = kt0; kt < kt1; ++kt) {
+        __syncthreads();   // every wave is done with sk / sv (and the q rows)
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = t + 256 * u, j = i / C4, c4 = i - j * C4;
+            const bool in = kt * KT + j <= last;
+            *reinterpret_cast<float4 *>(&sk[j][4 * c4]) =
+                in ? kv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4 *>(&sv[j][4 * c4]) =
+                in ? vv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         __syncthreads();
-        for (int i = t; i < KT * C4; i += 256) {
-            const int j = i / C4, c4 = i - j * C4;
-            const int p = kt * KT + j;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (p <= last) {
-                kv = reinterpret_cast<const float4 *>(kb + (size_t)p * HD)[c4];
-                vv = reinterpret_cast<const float4 *>(vb + (size_t)p * HD)[c4];
+        if (kt + 1 < kt1) load_tile(kt + 1);
+        if (!busy) continue;
+        // S = Q K^T over the wave's keys kg * KW .. of the tile: the keys
+        // first, then the MFMAs
+        float kr[NB][NS];   // k[key kg * KW + 16 b + c][g * NS + s]
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int s = 0; s < NS; s += 4) {
+                const float4 v =
+                    *reinterpret_cast<const float4 *>(&sk[kg * KW + 16 * b + c][g * NS + s]);
+                kr[b][s] = v.x; kr[b][s + 1] = v.y; kr[b][s + 2] = v.z; kr[b][s + 3] = v.w;
             }
-            *reinterpret_cast<float4 *>(&sk[j][4 * c4]) = kv;
-            *reinterpret_cast<float4 *>(&sv[j][4 * c4]) = vv;
-        }
-        __syncthreads();
-        float s[RPT][KPT];
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4_t sacc[NB];
 #pragma unroll
-        for (int r = 0; r < RPT; ++r)
+        for (int b = 0; b < NB; ++b) sacc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < KPT; ++j) s[r][j] = 0.f;
-#pragma unroll DU
-        for (int d = 0; d < HD; d += 4) {
-            float4 qa[RPT], kk[KPT];
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int r = 0; r < RPT; ++r)
-                qa[r] = *reinterpret_cast<const float4 *>(&sq[RPT * rg + r][d]);
+            for (int b = 0; b < NB; ++b)
+                sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kr[b][s], sacc[b], 0, 0, 0);
+        // sacc[b][r] = S[row 4 g + r][key kg * KW + 16 b + c]
 #pragma unroll
-            for (int j = 0; j < KPT; ++j)
-                kk[j] = *reinterpret_cast<const float4 *>(&sk[kg + 16 * j][d]);
-#pragma unroll
-            for (int r = 0; r < RPT; ++r)
-#pragma unroll
-                for (int j = 0; j < KPT; ++j) {
-                    s[r][j] = fmaf(qa[r].x, kk[j].x, s[r][j]);
-                    s[r][j] = fmaf(qa[r].y, kk[j].y, s[r][j]);
-                    s[r][j] = fmaf(qa[r].z, kk[j].z, s[r][j]);
-                    s[r][j] = fmaf(qa[r].w, kk[j].w, s[r][j]);
-                }
-        }
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) {
+        for (int r = 0; r < 4; ++r) {
+            float sc[NB];
             float mt = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < KPT; ++j) {
-                const int pk = kt * KT + kg + 16 * j;
-                s[r][j] = pk <= pq[r] ? s[r][j] * scale : -INFINITY;
-                mt = fmaxf(mt, s[r][j]);
+            for (int b = 0; b < NB; ++b) {
+                const int pk = kt * KT + kg * KW + 16 * b + c;
+                sc[b] = pk <= pq[r] ? sacc[b][r] * scale : -INFINITY;
+                mt = fmaxf(mt, sc[b]);
             }
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
+            for (int off = 1; off < 16; off <<= 1) mt = fmaxf(mt, shfl_xor_u(mt, off));
             const float mn = fmaxf(mrun[r], mt);
             // all-masked so far: nothing to rescale, every p is 0
             const float alpha = mn == -INFINITY ? 1.f : expf(mrun[r] - mn);
             float ls = 0.f;
 #pragma unroll
-            for (int j = 0; j < KPT; ++j) {
-                const float pj = mn == -INFINITY ? 0.f : expf(s[r][j] - mn);
-                sp[RPT * rg + r][kg + 16 * j] = pj;
+            for (int b = 0; b < NB; ++b) {
+                const float pj = mn == -INFINITY ? 0.f : expf(sc[b] - mn);
+                sp[wave][4 * g + r][16 * b + c] = pj;
                 ls += pj;
             }
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) ls += __shfl_xor(ls, off);
+            for (int off = 1; off < 16; off <<= 1) ls += shfl_xor_u(ls, off);
             lrun[r] = lrun[r] * alpha + ls;
             mrun[r] = mn;
 #pragma unroll
-            for (int c = 0; c < OC; ++c) o[r][c] *= alpha;
+            for (int b = 0; b < OB; ++b) o[b][r] *= alpha;
         }
+        // the wave's P rows: written above by their owners, read below across lanes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // O += P V: P[row c][key g * KS + s] and V[key kg * KW + g * KS + s][col 16 b + c]
+        float pa[KS];
+#pragma unroll
+        for (int s = 0; s < KS; s += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(&sp[wave][c][g * KS + s]);
+            pa[s] = v.x; pa[s + 1] = v.y; pa[s + 2] = v.z; pa[s + 3] = v.w;
+        }
+        constexpr int OG = OB < 4 ? OB : 4;   // output column blocks per batch of reads
+#pragma unroll
+        for (int b0 = 0; b0 < OB; b0 += OG) {
+            float vr[OG][KS];
+#pragma unroll
+            for (int bb = 0; bb < OG; ++bb)
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+                    vr[bb][s] = sv[kg * KW + g * KS + s][16 * (b0 + bb) + c];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int bb = 0; bb < OG; ++bb)
+                    o[b0 + bb] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vr[bb][s],
+                                                                      o[b0 + bb], 0, 0, 0);
+        }
+        // the next tile's P writes wait for these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (KG > 1) {
+        // key groups 1.. hand their (o, m, l) to group 0 through LDS (sk)
         __syncthreads();
-#pragma unroll JU
-        for (int j = 0; j < KT; ++j) {
-            float pv[RPT];
+        float *xo = &sk[0][0];                          // [KG - 1][RB][16][HD]
+        float *xm = xo + (KG - 1) * RB * 16 * HD;       // [KG - 1][RB][16][2]
+        if (kg > 0 && busy) {
 #pragma unroll
-            for (int r = 0; r < RPT; ++r) pv[r] = sp[RPT * rg + r][j];
+            for (int r = 0; r < 4; ++r) {
+                float *row = xo + (((kg - 1) * RB + rb) * 16 + 4 * g + r) * HD;
 #pragma unroll
-            for (int c = 0; c < OC; c += 4) {
-                const float4 vv = *reinterpret_cast<const float4 *>(&sv[j][16 * c + 4 * kg]);
-#pragma unroll
-                for (int r = 0; r < RPT; ++r) {
-                    o[r][c] = fmaf(pv[r], vv.x, o[r][c]);
-                    o[r][c + 1] = fmaf(pv[r], vv.y, o[r][c + 1]);
-                    o[r][c + 2] = fmaf(pv[r], vv.z, o[r][c + 2]);
-                    o[r][c + 3] = fmaf(pv[r], vv.w, o[r][c + 3]);
+                for (int b = 0; b < OB; ++b) row[16 * b + c] = o[b][r];
+                if (c == 0) {
+                    float *ml = xm + (((kg - 1) * RB + rb) * 16 + 4 * g + r) * 2;
+                    ml[0] = mrun[r];
+                    ml[1] = lrun[r];
                 }
             }
         }
-    }
+        __syncthreads();
+        if (kg > 0) return;
+        if (busy) {
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int ii = i0 + RPT * rg + r;
+            for (int r = 0; r < 4; ++r) {
+                float mg = mrun[r];
+#pragma unroll
+                for (int j = 1; j < KG; ++j)
+                    mg = fmaxf(mg, xm[(((j - 1) * RB + rb) * 16 + 4 * g + r) * 2]);
+                // every group all-masked: keep o = 0, l = 0 (m = -inf)
+                const float a0 = mg == -INFINITY ? 1.f : expf(mrun[r] - mg);
+                float l = lrun[r] * a0;
+#pragma unroll
+                for (int b = 0; b < OB; ++b) o[b][r] *= a0;
+#pragma unroll
+                for (int j = 1; j < KG; ++j) {
+                    const int slot = ((j - 1) * RB + rb) * 16 + 4 * g + r;
+                    const float mj = xm[slot * 2];
+                    const float aj = mg == -INFINITY ? 0.f : expf(mj - mg);
+                    l = fmaf(xm[slot * 2 + 1], aj, l);
+#pragma unroll
+                    for (int b = 0; b < OB; ++b) o[b][r] = fmaf(xo[slot * HD + 16 * b + c], aj, o[b][r]);
+                }
+                mrun[r] = mg;
+                lrun[r] = l;
+            }
+        }
+    }
+    if (!busy) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int ii = w0 + 4 * g + r;
         if (ii >= NR) continue;
         const int m = ii / G, h = kvh * G + (ii - m * G);
         if (part) {   // one split of several: unnormalised o, max and sum
             const size_t row = ((size_t)blockIdx.z * M + m) * hq + h;
-            float *dst = part + row * HD + 4 * kg;
 #pragma unroll
-            for (int c = 0; c < OC; c += 4)
-                *reinterpret_cast<float4 *>(dst + 16 * c) =
-                    make_float4(o[r][c], o[r][c + 1], o[r][c + 2], o[r][c + 3]);
-            if (kg == 0) {
+            for (int b = 0; b < OB; ++b) part[row * HD + 16 * b + c] = o[b][r];
+            if (c == 0) {
                 pml[row * 2] = mrun[r];
                 pml[row * 2 + 1] = lrun[r];
             }
         } else {
             const float inv = 1.0f / fmaxf(lrun[r], 1e-30f);
-            float *dst = out + ((size_t)m * hq + h) * HD + 4 * kg;
 #pragma unroll
-            for (int c = 0; c < OC; c += 4)
-                *reinterpret_cast<float4 *>(dst + 16 * c) = make_float4(
-                    o[r][c] * inv, o[r][c + 1] * inv, o[r][c + 2] * inv, o[r][c + 3] * inv);
+            for (int b = 0; b < OB; ++b) out[((size_t)m * hq + h) * HD + 16 * b + c] = o[b][r] * inv;
         }
     }
 }
@@ -1131,43 +1246,60 @@ int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const flo
 
 namespace {
 
-// Query rows per tile (RPT) and key positions per tile (KPT), in sixteens, for
-// M positions x G heads per KV head: the smallest row tile that holds a short
-// chunk, with 32-key tiles for the small ones (44 / 54 KB of LDS, several
-// blocks per CU) and 64 x 64 tiles for long prompts.
-struct AttnShape {
-    int rpt, kpt;
-};
-AttnShape attn_shape(int M, int G) {
-    const int nr = M * G;
-    if (nr <= 16) return {1, 2};
-    if (nr <= 32) return {2, 2};
-    return {4, 4};
+// Key positions per tile of the prefill attention: 32, or 64 for four key
+// groups (TB_PREFILL_ATTN_KT=64 takes 64 throughout, measurement only).
+int mfma_attn_kt() {
+    static const int v = [] {
+        const char *e = getenv("TB_PREFILL_ATTN_KT");
+        return e && atoi(e) == 64 ? 64 : 32;
+    }();
+    return v;
 }
 
+// Key groups per tile of the MFMA prefill attention: few rows share the four
+// waves between row blocks and key groups.
+int mfma_attn_kg(int M, int G) {
+    const int nr = M * G;
+    return nr <= 16 ? 4 : nr <= 32 ? 2 : 1;
+}
+
+// Key positions per tile for kg key groups (each wave takes whole 16-key blocks).
+int mfma_attn_tile(int kg) { return kg == 4 ? 64 : mfma_attn_kt(); }
+
 template <int HD>
-void launch_attn_tiles(AttnShape sh, dim3 grid, hipStream_t s, const float *q, const float *kc,
-                       const float *vc, float *out, int start, int M, int hq, int hkv,
-                       int max_seq, float scale, int tps, float *part, float *pml) {
-    if (sh.rpt == 1)
-        hipLaunchKernelGGL((k_prefill_attn<HD, 1, 2>), grid, dim3(256), 0, s, q, kc, vc, out,
-                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
-    else if (sh.rpt == 2)
-        hipLaunchKernelGGL((k_prefill_attn<HD, 2, 2>), grid, dim3(256), 0, s, q, kc, vc, out,
-                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
-    else
-        hipLaunchKernelGGL((k_prefill_attn<HD, 4, 4>), grid, dim3(256), 0, s, q, kc, vc, out,
-                           start, M, hq, hkv, max_seq, scale, tps, part, pml);
+void launch_attn_mfma(int kt, int kg, dim3 grid, hipStream_t s, const float *q, const float *kc,
+                      const float *vc, float *out, int start, int M, int hq, int hkv, int max_seq,
+                      float scale, int tps, float *part, float *pml) {
+#define TB_PA(KT, KG)                                                                         \
+    hipLaunchKernelGGL((k_prefill_attn_mfma<HD, KT, KG>), grid, dim3(256), 0, s, q, kc, vc, out, \
+                       start, M, hq, hkv, max_seq, scale, tps, part, pml)
+    if (kg == 4) TB_PA(64, 4);
+    else if (kt == 32 && kg == 2) TB_PA(32, 2);
+    else if (kt == 32) TB_PA(32, 1);
+    else if (kg == 2) TB_PA(64, 2);
+    else TB_PA(64, 1);
+#undef TB_PA
 }
 
 }  // namespace
 
 int prefill_attention_splits(int start, int M, int hq, int hkv) {
-    const AttnShape sh = attn_shape(M, hq / hkv);
-    const int rtiles = (M * (hq / hkv) + 16 * sh.rpt - 1) / (16 * sh.rpt);
-    const int tiles = (start + M - 1) / (16 * sh.kpt) + 1;   // key tiles of the last row
-    const int want = (2048 + rtiles * hkv - 1) / (rtiles * hkv);   // ~8 blocks per CU
-    return std::max(1, std::min(want, tiles));
+    // 64 / kg-row tiles; about 256 blocks (one or two per CU at their LDS;
+    // TB_PREFILL_ATTN_BLOCKS overrides, measurement only), every split with at
+    // least one key tile
+    static const int target = [] {
+        const char *e = getenv("TB_PREFILL_ATTN_BLOCKS");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 256;
+    }();
+    const int kg = mfma_attn_kg(M, hq / hkv);
+    const int rows = 64 / kg, tile = mfma_attn_tile(kg);
+    const int rtiles = (M * (hq / hkv) + rows - 1) / rows;
+    const int tiles = (start + M - 1) / tile + 1;
+    const int want = (target + rtiles * hkv - 1) / (rtiles * hkv);
+    const int ns = std::max(1, std::min(want, tiles));
+    const int tps = (tiles + ns - 1) / ns;
+    return (tiles + tps - 1) / tps;
 }
 
 size_t prefill_attention_scratch(int M, int hq, int hd, int nsplit) {
@@ -1181,21 +1313,23 @@ int launch_prefill_attention(const float *q, const float *kc, const float *vc, f
                "TB_UNSUPPORTED: num_heads must be a multiple of num_kv_heads");
     TB_REQUIRE(hd == 64 || hd == 128, TB_ERR_UNSUPPORTED,
                "TB_UNSUPPORTED: head_dim must be 64 or 128");
-    const AttnShape sh = attn_shape(M, hq / hkv);
+    const int kg = mfma_attn_kg(M, hq / hkv);
+    const int kt = mfma_attn_tile(kg);
     const int nsplit = scratch ? prefill_attention_splits(start, M, hq, hkv) : 1;
-    const int tiles = (start + M - 1) / (16 * sh.kpt) + 1;
+    const int tiles = (start + M - 1) / kt + 1;
     const int tps = (tiles + nsplit - 1) / nsplit;
     float *part = nsplit > 1 ? scratch : nullptr;
     float *pml = nsplit > 1 ? scratch + (size_t)nsplit * M * hq * hd : nullptr;
-    const int rtiles = (M * (hq / hkv) + 16 * sh.rpt - 1) / (16 * sh.rpt);
+    const int rows = 64 / kg;
+    const int rtiles = (M * (hq / hkv) + rows - 1) / rows;
     const dim3 grid(rtiles, hkv, nsplit);
     const float scale = 1.0f / sqrtf((float)hd);
     if (hd == 128)
-        launch_attn_tiles<128>(sh, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale, tps,
-                               part, pml);
+        launch_attn_mfma<128>(kt, kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
+                              tps, part, pml);
     else
-        launch_attn_tiles<64>(sh, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale, tps,
-                              part, pml);
+        launch_attn_mfma<64>(kt, kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
+                             tps, part, pml);
     TB_LAUNCHED();
     if (nsplit > 1) {
         if (hd == 128)
