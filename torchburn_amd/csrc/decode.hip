@@ -1246,16 +1246,6 @@ int launch_rope_rows(const float *qkv, float *q, float *kc, float *vc, const flo
 
 namespace {
 
-// Key positions per tile of the prefill attention: 32, or 64 for four key
-// groups (TB_PREFILL_ATTN_KT=64 takes 64 throughout, measurement only).
-int mfma_attn_kt() {
-    static const int v = [] {
-        const char *e = getenv("TB_PREFILL_ATTN_KT");
-        return e && atoi(e) == 64 ? 64 : 32;
-    }();
-    return v;
-}
-
 // Key groups per tile of the MFMA prefill attention: few rows share the four
 // waves between row blocks and key groups.
 int mfma_attn_kg(int M, int G) {
@@ -1263,21 +1253,20 @@ int mfma_attn_kg(int M, int G) {
     return nr <= 16 ? 4 : nr <= 32 ? 2 : 1;
 }
 
-// Key positions per tile for kg key groups (each wave takes whole 16-key blocks).
-int mfma_attn_tile(int kg) { return kg == 4 ? 64 : mfma_attn_kt(); }
+// Key positions per tile for kg key groups: 32, or 64 for four key groups
+// (each wave takes whole 16-key blocks).
+int mfma_attn_tile(int kg) { return kg == 4 ? 64 : 32; }
 
 template <int HD>
-void launch_attn_mfma(int kt, int kg, dim3 grid, hipStream_t s, const float *q, const float *kc,
+void launch_attn_mfma(int kg, dim3 grid, hipStream_t s, const float *q, const float *kc,
                       const float *vc, float *out, int start, int M, int hq, int hkv, int max_seq,
                       float scale, int tps, float *part, float *pml) {
 #define TB_PA(KT, KG)                                                                         \
     hipLaunchKernelGGL((k_prefill_attn_mfma<HD, KT, KG>), grid, dim3(256), 0, s, q, kc, vc, out, \
                        start, M, hq, hkv, max_seq, scale, tps, part, pml)
     if (kg == 4) TB_PA(64, 4);
-    else if (kt == 32 && kg == 2) TB_PA(32, 2);
-    else if (kt == 32) TB_PA(32, 1);
-    else if (kg == 2) TB_PA(64, 2);
-    else TB_PA(64, 1);
+    else if (kg == 2) TB_PA(32, 2);
+    else TB_PA(32, 1);
 #undef TB_PA
 }
 
@@ -1325,10 +1314,10 @@ int launch_prefill_attention(const float *q, const float *kc, const float *vc, f
     const dim3 grid(rtiles, hkv, nsplit);
     const float scale = 1.0f / sqrtf((float)hd);
     if (hd == 128)
-        launch_attn_mfma<128>(kt, kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
+        launch_attn_mfma<128>(kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
                               tps, part, pml);
     else
-        launch_attn_mfma<64>(kt, kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
+        launch_attn_mfma<64>(kg, grid, s, q, kc, vc, out, start, M, hq, hkv, max_seq, scale,
                              tps, part, pml);
     TB_LAUNCHED();
     if (nsplit > 1) {
